@@ -1,0 +1,335 @@
+#!/usr/bin/env python3
+"""Throughput of the routed relation path on one MI355X.
+
+Step = one pass of the cfg2 prefill workload (B=8, T=512, d=512, block 32,
+local 64, top 4, K=8, bf16 activations / fp32 scores, relation hidden 512):
+    expanded-cache projection -> relation_select (all 4096 queries)
+    -> relation hidden -> second linear -> LayerNorm / softmax / partner sum.
+`value` is queries per second with every input resident in HBM.
+
+Also reported:
+  * per-kernel average duration (HIP events on the launch stream) and the
+    HBM roofline fraction of the dominant kernel at its operator-contract bytes;
+  * decode-step latency (cfg3: packed 576->512 projection, cache-row writes,
+    select, reduce) at B=1 and B=8, eager and replayed from a HIP graph;
+  * the CPU oracle timed on this host's cores on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "relation-lm_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--kernel-repeats", type=int, default=50)
+    ap.add_argument("--decode-steps", type=int, default=200)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only-chain", action="store_true",
+                    help="run only the timed chain (for profiler runs)")
+    return ap.parse_args()
+
+
+def algorithmic_bytes(cfg):
+    """Operator-contract bytes per launch (inputs at unique footprint + outputs)."""
+    b, t, e, k = cfg.batch, cfg.context, cfg.exact_dim, cfg.k_out
+    rd = cfg.heads * cfg.head_dim
+    r, h, d = cfg.relation_dim, cfg.hidden_dim, cfg.d_model
+    q = b * t
+    s = 2  # bf16 activations
+    nb = cfg.blocks
+    return {
+        "expanded_projection": q * r * s + 2 * h * r * s + 2 * h * s + q * 2 * h * s,
+        "relation_select": (q * (2 * e + 2 * rd) * s + b * (t * (3 * e + rd) * s + 4 * nb * rd * 4)
+                            + q * (8 + 8 * k)),
+        "relation_hidden": b * t * (2 * h + r) * s + h * r * s + q * k * h * 4 + q * (1 + k) * 4,
+        "second_linear": q * k * h * 4 + d * h * s + d * s + q * k * d * 4,
+        "norm_reduce": q * k * d * 4 + q * k * 4 + 2 * d * s + q * d * 4,
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the routed relation path is batch-separable; "
+              f"see DESIGN.md for the sharding plan); got --gpus {args.gpus}", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from relation_lm.kernels.relation_reduce import (
+        relation_hidden_cache_update,
+        relation_hidden_cached,
+        relation_hidden_cached_seq,
+        relation_linear,
+        relation_norm_reduce,
+        relation_norm_reduce_seq,
+    )
+    from relation_lm.kernels.relation_select import (
+        relation_select_packed,
+        relation_select_packed_seq,
+    )
+    from relation_lm.inference import pack_sparse_cache_projection_weights
+    from relation_lm.workloads import (
+        CONFIGS,
+        RelationConfig,
+        packed_projection_inputs,
+        reduce_inputs,
+        select_args,
+        selection_inputs,
+    )
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    cfg = CONFIGS["cfg2"]
+    sel = selection_inputs(cfg, device=device)
+    red = reduce_inputs(cfg, device=device)
+    sargs = select_args(sel, cfg)
+    positions = sel["positions"]
+    operand = red["operand_cache"]
+
+    def run_expanded():
+        return relation_linear(operand, red["expanded_weight"], red["expanded_bias"])
+
+    def run_select():
+        return relation_select_packed_seq(*sargs)
+
+    def run_hidden(expanded, a, p):
+        return relation_hidden_cached_seq(expanded, operand, a, p, red["product_weight"])
+
+    def run_second(hidden):
+        return relation_linear(hidden, red["second_weight"], red["second_bias"],
+                               out_dtype=torch.float32)
+
+    def run_norm(raw, ps):
+        return relation_norm_reduce_seq(raw, ps, red["norm_weight"], red["norm_bias"], positions,
+                                        1e-5)
+
+    def step():
+        expanded = run_expanded()
+        a, s, p, ps = run_select()
+        hidden = run_hidden(expanded, a, p)
+        raw = run_second(hidden)
+        return run_norm(raw, ps)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    if args.only_chain:
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        print(json.dumps({"only_chain": True, "steps": args.steps}), flush=True)
+        return 0
+
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(end) / args.steps
+    queries = cfg.queries
+    value = queries / (ms_per_step / 1e3)
+
+    # Per-kernel average duration on the launch stream (torch's current stream).
+    expanded = run_expanded()
+    a, s, p, ps = run_select()
+    hidden = run_hidden(expanded, a, p)
+    raw = run_second(hidden)
+    kernels = {
+        "expanded_projection": run_expanded,
+        "relation_select": run_select,
+        "relation_hidden": lambda: run_hidden(expanded, a, p),
+        "second_linear": lambda: run_second(hidden),
+        "norm_reduce": lambda: run_norm(raw, ps),
+    }
+    per_kernel_us = {}
+    for name, fn in kernels.items():
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(args.kernel_repeats):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        per_kernel_us[name] = start.elapsed_time(end) * 1e3 / args.kernel_repeats
+    nbytes = algorithmic_bytes(cfg)
+    dominant = max(per_kernel_us, key=per_kernel_us.get)
+    achieved = nbytes[dominant] / (per_kernel_us[dominant] * 1e-6) / 1e9
+    trio = ("relation_select", "relation_hidden", "norm_reduce")
+    trio_bytes = sum(nbytes[k] for k in trio)
+    trio_us = sum(per_kernel_us[k] for k in trio)
+    chain_bytes = sum(nbytes.values())
+
+    # Decode step (cfg3) at B=1 and B=8.
+    decode = {}
+    for batch in (1, 8):
+        dcfg = RelationConfig(**{**CONFIGS["cfg3"].__dict__, "batch": batch})
+        dsel = selection_inputs(dcfg, queries=1, device=device)
+        dred = reduce_inputs(dcfg, device=device)
+        dexp = relation_linear(dred["operand_cache"], dred["expanded_weight"],
+                               dred["expanded_bias"])
+        memory, weights = packed_projection_inputs(dcfg, device=device)
+        projection = pack_sparse_cache_projection_weights(weights)
+        dargs = select_args(dsel, dcfg)
+        t = dcfg.context - 1
+        position = dsel["position"]
+
+        def decode_step(dsel=dsel, dred=dred, dexp=dexp, memory=memory, projection=projection,
+                        dargs=dargs, t=t, position=position, batch=batch):
+            parts = projection.project(memory)
+            dsel["anchor_keys"][:, t] = parts[0]
+            dsel["partner_keys"][:, t] = parts[1]
+            dred["operand_cache"][:, t] = parts[2]
+            dsel["partner_anchor_cache"][:, t] = parts[3]
+            a_, s_, p_, ps_ = relation_select_packed(*dargs)
+            if batch == 1:
+                hid = relation_hidden_cache_update(
+                    dexp, dred["operand_cache"], a_, p_, dred["anchor_weight"],
+                    dred["partner_weight"], dred["product_weight"], dred["first_bias"], position)
+            else:
+                row = relation_linear(dred["operand_cache"][:, t], dred["expanded_weight"],
+                                      dred["expanded_bias"])
+                dexp[:, t] = row
+                hid = relation_hidden_cached(dexp, dred["operand_cache"], a_, p_,
+                                             dred["product_weight"])
+            raw_ = relation_linear(hid, dred["second_weight"], dred["second_bias"],
+                                   out_dtype=torch.float32)
+            return relation_norm_reduce(raw_, ps_, dred["norm_weight"], dred["norm_bias"],
+                                        position, 1e-5)
+
+        for _ in range(20):
+            decode_step()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(args.decode_steps):
+            decode_step()
+        end.record()
+        torch.cuda.synchronize()
+        eager_us = start.elapsed_time(end) * 1e3 / args.decode_steps
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            decode_step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            decode_step()
+        for _ in range(10):
+            graph.replay()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(args.decode_steps):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        graph_us = start.elapsed_time(end) * 1e3 / args.decode_steps
+        decode[f"B{batch}"] = {"eager_us": round(eager_us, 2), "graph_us": round(graph_us, 2)}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(cfg, sel, red, torch)
+
+    result = {
+        "metric": "relation_select+reduce queries/s @B8 ctx512; decode-step us; % HBM roofline",
+        "value": round(value, 1),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations/caches, N(0,1/fan_in) weights)",
+        "config": {
+            "workload": "cfg2 prefill: B=8 T=512 d=512 block32 local64 top4 K=8 hidden512 "
+                        "(expanded projection + select + hidden + linear2 + norm-reduce)",
+            "batch": cfg.batch, "context": cfg.context, "d_model": cfg.d_model,
+            "queries_per_step": queries, "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dominant,
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes": nbytes[dominant],
+        },
+        "per_kernel_us": {k: round(v, 2) for k, v in per_kernel_us.items()},
+        "select_hidden_norm_frac": round(trio_bytes / (trio_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "chain_frac": round(chain_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "decode_step_us": decode,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def cpu_baseline(cfg, sel, red, torch):
+    """The float64 oracle chain on a bounded sample of cfg2 queries (one batch row)."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import reduce as ored
+    from oracle import select as osel
+
+    def h(t):
+        return t.detach().float().cpu().numpy() if t.dtype.is_floating_point else t.cpu().numpy()
+
+    sample_rows = cfg.batch
+    hs = {k: h(v)[:sample_rows] if v.dim() >= 2 and v.size(0) == cfg.batch else h(v)
+          for k, v in sel.items()}
+    hr = {k: h(v) for k, v in red.items()}
+    operand = hr["operand_cache"][:sample_rows]
+    keys = ("anchor_query", "anchor_keys", "anchor_router_query", "anchor_block_mean",
+            "anchor_block_std", "anchor_gamma", "anchor_bias", "partner_base",
+            "partner_anchor_cache", "partner_keys", "partner_block_mean", "partner_block_std",
+            "partner_gamma", "partner_bias")
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        expanded = ored.linear(operand, hr["expanded_weight"], hr["expanded_bias"])
+        a, s, p, ps = osel.relation_select_packed_seq(
+            *[hs[k] for k in keys], hs["positions"], cfg.local_window, cfg.top_blocks, cfg.k_out,
+            False)
+        hidden = ored.relation_hidden_cached_seq(expanded, operand, a, p, hr["product_weight"])
+        raw = ored.linear(hidden, hr["second_weight"], hr["second_bias"])
+        ctx = ored.relation_norm_reduce_seq(raw, ps, hr["norm_weight"], hr["norm_bias"],
+                                            hs["positions"], 1e-5)
+        elapsed = time.perf_counter() - t0
+    assert np.isfinite(ctx).all()
+    n = sample_rows * cfg.context
+    return {
+        "value": round(n / elapsed, 1),
+        "unit": "queries/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"cfg2 chain (expanded projection, select, hidden, linear2, norm-reduce) on "
+                  f"{n} queries (all {sample_rows} batch rows x 512 positions), float64 numpy oracle, "
+                  f"{elapsed:.1f} s",
+        "host_cpus": os.cpu_count(),
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,238 @@
+/*
+ * relation_lm_hip.h -- C ABI of the MI355X (gfx950) routed relation path.
+ *
+ * Every entry point mirrors one operator of the reference package
+ * (Ahmet2001/relation-lm, src/relation_lm/...) argument for argument: the
+ * tensors arrive as plain descriptors (pointer, dtype, shape, strides), the
+ * scalar arguments keep their reference names and meaning, outputs are
+ * caller-allocated descriptors, and the call is enqueued on `stream`.
+ *
+ * Conventions shared by every entry point
+ *  - Return value: hipSuccess (0) or a hipError_t.  Argument errors return
+ *    hipErrorInvalidValue and leave a message for rlm_last_error(); nothing
+ *    is launched in that case.
+ *  - No entry point allocates device memory, synchronises the stream or
+ *    reads device memory on the host: `position` stays on the device, so
+ *    every call can be captured into a HIP graph.
+ *  - Positions and indices that fall outside [0, max_t) are never
+ *    dereferenced: the kernels treat such rows as invalid / all-zero.
+ *  - Inputs are borrowed.  Only the tensors documented as mutated are
+ *    written besides the outputs.
+ */
+#ifndef RELATION_LM_HIP_H
+#define RELATION_LM_HIP_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types understood by the library. */
+enum rlm_dtype {
+  RLM_F32 = 0,
+  RLM_BF16 = 1,
+  RLM_F16 = 2,
+  RLM_I32 = 3,
+  RLM_I64 = 4,
+};
+
+#define RLM_MAX_DIMS 4
+
+/* A strided view of device memory.  Strides are in elements. */
+typedef struct rlm_tensor {
+  void* data;
+  int32_t dtype;                 /* enum rlm_dtype */
+  int32_t ndim;                  /* 0..RLM_MAX_DIMS */
+  int64_t shape[RLM_MAX_DIMS];
+  int64_t stride[RLM_MAX_DIMS];
+} rlm_tensor;
+
+/* Message describing the last failed call on this host thread ("" if none). */
+const char* rlm_last_error(void);
+
+/* Library version string. */
+const char* rlm_version(void);
+
+/* ------------------------------------------------------------------------
+ * Routed selection
+ * ---------------------------------------------------------------------- */
+
+/*
+ * Replaces relation_lm::relation_select_packed
+ *   (src/relation_lm/kernels/relation_select.py:311-382).
+ * Anchor block scoring, exact top-1 anchor, factorized partner query,
+ * partner block routing and exact top-k partners for one query per batch
+ * row at the shared 0-d device `position`.
+ *   anchor_query [B,E], anchor_keys [B,T,E], anchor_router_query [B,RD],
+ *   anchor_block_mean/std [B,NB,H,HD], anchor_gamma [H], anchor_bias [H,RB],
+ *   partner_base [B,2E], partner_anchor_cache [B,T,2E], partner_keys [B,T,E],
+ *   partner_block_mean/std [B,NB,H,HD], partner_gamma [H], partner_bias [H,RB],
+ *   position: 0-d int64/int32.  RD = H*HD must equal E.
+ * Outputs: out_anchor int32 [B], out_anchor_score f32 [B],
+ *          out_partner int32 [B,K], out_partner_score f32 [B,K].
+ */
+hipError_t rlm_relation_select_packed(
+    const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
+    const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
+    const rlm_tensor* anchor_block_std, const rlm_tensor* anchor_gamma,
+    const rlm_tensor* anchor_bias, const rlm_tensor* partner_base,
+    const rlm_tensor* partner_anchor_cache, const rlm_tensor* partner_keys,
+    const rlm_tensor* partner_block_mean, const rlm_tensor* partner_block_std,
+    const rlm_tensor* partner_gamma, const rlm_tensor* partner_bias,
+    const rlm_tensor* position, int64_t local_window, int64_t top_blocks,
+    int64_t k_out, int32_t strict_valid, const rlm_tensor* out_anchor,
+    const rlm_tensor* out_anchor_score, const rlm_tensor* out_partner,
+    const rlm_tensor* out_partner_score, hipStream_t stream);
+
+/*
+ * Sequence (prefill) form of rlm_relation_select_packed: no reference
+ * counterpart; the reference op is its Tq=1 case.  Query-side tensors gain a
+ * query axis ([B,Tq,E], [B,Tq,RD], [B,Tq,2E]) and `position` holds one
+ * position per query, shaped [Tq] (shared by all rows) or [B,Tq].
+ * Outputs: int32 [B,Tq], f32 [B,Tq], int32 [B,Tq,K], f32 [B,Tq,K].
+ */
+hipError_t rlm_relation_select_packed_seq(
+    const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
+    const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
+    const rlm_tensor* anchor_block_std, const rlm_tensor* anchor_gamma,
+    const rlm_tensor* anchor_bias, const rlm_tensor* partner_base,
+    const rlm_tensor* partner_anchor_cache, const rlm_tensor* partner_keys,
+    const rlm_tensor* partner_block_mean, const rlm_tensor* partner_block_std,
+    const rlm_tensor* partner_gamma, const rlm_tensor* partner_bias,
+    const rlm_tensor* positions, int64_t local_window, int64_t top_blocks,
+    int64_t k_out, int32_t strict_valid, const rlm_tensor* out_anchor,
+    const rlm_tensor* out_anchor_score, const rlm_tensor* out_partner,
+    const rlm_tensor* out_partner_score, hipStream_t stream);
+
+/*
+ * Replaces relationlex::anchor_select
+ *   (src/relation_lm/kernels/triton_select.py:255-295).
+ *   anchor_query [B,E], anchor_keys [B,T,E], router_query [B,RD],
+ *   block_mean/std [B,NB,H,HD], gamma [H], bias [H,RB], position 0-d.
+ * Outputs: out_index int32 [B], out_score f32 [B].
+ */
+hipError_t rlm_anchor_select(
+    const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
+    const rlm_tensor* router_query, const rlm_tensor* block_mean,
+    const rlm_tensor* block_std, const rlm_tensor* gamma,
+    const rlm_tensor* bias, const rlm_tensor* position, int64_t local_window,
+    int64_t top_blocks, int32_t strict_valid, const rlm_tensor* out_index,
+    const rlm_tensor* out_score, hipStream_t stream);
+
+/*
+ * Replaces relationlex::partner_topk
+ *   (src/relation_lm/kernels/triton_select.py:298-346).
+ *   partner_query [B,E], partner_keys [B,T,E], router_query [B,RD],
+ *   block_mean/std [B,NB,H,HD], gamma [H], bias [H,RB], position 0-d,
+ *   anchor_index int32/int64 [B].
+ * Outputs: out_index int32 [B,K], out_score f32 [B,K].
+ */
+hipError_t rlm_partner_topk(
+    const rlm_tensor* partner_query, const rlm_tensor* partner_keys,
+    const rlm_tensor* router_query, const rlm_tensor* block_mean,
+    const rlm_tensor* block_std, const rlm_tensor* gamma,
+    const rlm_tensor* bias, const rlm_tensor* position,
+    const rlm_tensor* anchor_index, int64_t local_window, int64_t top_blocks,
+    int64_t k_out, int32_t strict_valid, const rlm_tensor* out_index,
+    const rlm_tensor* out_score, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Relation reduce
+ * ---------------------------------------------------------------------- */
+
+/*
+ * Replaces relation_lm::relation_hidden_cached
+ *   (src/relation_lm/kernels/relation_reduce.py:149-183).
+ *   hidden[b,k,:] = GELU(W_m (op[a_b] * op[p_bk]) + X[a_b,0:H] + X[p_bk,H:2H])
+ *   expanded_cache X [B,T,2H], operand_cache op [B,T,R],
+ *   anchor_index [B], partner_index [B,K] (int32/int64), product_weight W_m [H,R].
+ * Output: out f32 [B,K,H].
+ */
+hipError_t rlm_relation_hidden_cached(
+    const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
+    const rlm_tensor* anchor_index, const rlm_tensor* partner_index,
+    const rlm_tensor* product_weight, const rlm_tensor* out,
+    hipStream_t stream);
+
+/*
+ * Sequence form of rlm_relation_hidden_cached (no reference counterpart):
+ * anchor_index [B,Tq], partner_index [B,Tq,K]; output f32 [B,Tq,K,H].
+ */
+hipError_t rlm_relation_hidden_cached_seq(
+    const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
+    const rlm_tensor* anchor_index, const rlm_tensor* partner_index,
+    const rlm_tensor* product_weight, const rlm_tensor* out,
+    hipStream_t stream);
+
+/*
+ * Replaces relation_lm::relation_hidden_cache_update
+ *   (src/relation_lm/kernels/relation_reduce.py:312-357).
+ * Writes expanded_cache[b, position] = [W_a op[t] + b1, W_p op[t]] (the only
+ * mutated input) and returns the hidden of rlm_relation_hidden_cached, using
+ * the fresh row wherever an index equals `position`.
+ *   anchor_weight, partner_weight, product_weight [H,R], first_bias [H].
+ */
+hipError_t rlm_relation_hidden_cache_update(
+    const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
+    const rlm_tensor* anchor_index, const rlm_tensor* partner_index,
+    const rlm_tensor* anchor_weight, const rlm_tensor* partner_weight,
+    const rlm_tensor* product_weight, const rlm_tensor* first_bias,
+    const rlm_tensor* position, const rlm_tensor* out, hipStream_t stream);
+
+/*
+ * Replaces relation_lm::relation_norm_reduce
+ *   (src/relation_lm/kernels/relation_reduce.py:420-450).
+ *   ctx[b] = sum_k p_k * LayerNorm(raw[b,k]),  p = active-K masked softmax.
+ *   raw [B,K,D], partner_scores f32 [B,K], norm_weight/bias [D], position 0-d.
+ * Output: out f32 [B,D].
+ */
+hipError_t rlm_relation_norm_reduce(
+    const rlm_tensor* raw, const rlm_tensor* partner_scores,
+    const rlm_tensor* norm_weight, const rlm_tensor* norm_bias,
+    const rlm_tensor* position, double norm_eps, const rlm_tensor* out,
+    hipStream_t stream);
+
+/*
+ * Sequence form of rlm_relation_norm_reduce (no reference counterpart):
+ * raw [B,Tq,K,D], partner_scores [B,Tq,K], positions [Tq] or [B,Tq];
+ * output f32 [B,Tq,D].
+ */
+hipError_t rlm_relation_norm_reduce_seq(
+    const rlm_tensor* raw, const rlm_tensor* partner_scores,
+    const rlm_tensor* norm_weight, const rlm_tensor* norm_bias,
+    const rlm_tensor* positions, double norm_eps, const rlm_tensor* out,
+    hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Dense projections (MFMA)
+ * ---------------------------------------------------------------------- */
+
+/*
+ * Replaces the F.linear inside PackedSparseCacheProjection.project
+ *   (src/relation_lm/inference/packed_cache.py:52-57).
+ *   memory [M,Din] (any leading shape flattened by the caller), weight [Dout,Din].
+ * Output: out [M,Dout], same dtype as memory.
+ */
+hipError_t rlm_packed_sparse_cache_projection(
+    const rlm_tensor* memory, const rlm_tensor* weight, const rlm_tensor* out,
+    hipStream_t stream);
+
+/*
+ * out = input @ weight^T (+ bias), the library GEMM behind the expanded-cache
+ * projection (tests/test_relation_reduce_gpu.py:64-68 in the reference) and
+ * the relation MLP's second linear (benchmarks/benchmark_relation_reduce.py:63).
+ *   input [M,Kd] (f32/bf16/f16), weight [N,Kd] (same dtype), bias [N] or NULL.
+ * Output: out [M,N] (f32/bf16/f16).  bf16/f16 inputs use MFMA with fp32
+ * accumulation; f32 inputs use fp32 arithmetic throughout.
+ */
+hipError_t rlm_linear(const rlm_tensor* input, const rlm_tensor* weight,
+                      const rlm_tensor* bias, const rlm_tensor* out,
+                      hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RELATION_LM_HIP_H */

@@ -1,0 +1,178 @@
+// Shared device helpers and host-side argument validation for the gfx950
+// routed relation path.  Everything here is CDNA4-specific: wave64, LDS
+// ordering within a wave, bf16 as raw 16-bit storage.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "relation_lm_hip.h"
+
+namespace rlm {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Element types
+// ---------------------------------------------------------------------------
+
+struct bf16 {
+  uint16_t bits;
+};
+using f16 = _Float16;
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16 v) {
+  return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
+}
+__device__ __forceinline__ float to_f32(f16 v) { return static_cast<float>(v); }
+
+// Round-to-nearest-even float -> bf16 (NaN kept quiet).
+__device__ __forceinline__ bf16 f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  bf16 out;
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    out.bits = 0x7fc0;
+    return out;
+  }
+  u += 0x7fffu + ((u >> 16) & 1u);
+  out.bits = static_cast<uint16_t>(u >> 16);
+  return out;
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v);
+template <>
+__device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ bf16 from_f32<bf16>(float v) { return f32_to_bf16(v); }
+template <>
+__device__ __forceinline__ f16 from_f32<f16>(float v) { return static_cast<f16>(v); }
+
+// Four consecutive elements starting at p (p aligned to 4 elements).
+__device__ __forceinline__ float4 load4(const float* p) {
+  return *reinterpret_cast<const float4*>(p);
+}
+__device__ __forceinline__ float4 load4(const bf16* p) {
+  uint2 raw = *reinterpret_cast<const uint2*>(p);
+  return make_float4(__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
+                     __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u));
+}
+__device__ __forceinline__ float4 load4(const f16* p) {
+  const f16* q = p;
+  return make_float4(static_cast<float>(q[0]), static_cast<float>(q[1]),
+                     static_cast<float>(q[2]), static_cast<float>(q[3]));
+}
+
+// Scalar element of a runtime-typed tensor (small parameter tensors only).
+__device__ __forceinline__ float load_any_f(const void* p, int dtype, int64_t i) {
+  switch (dtype) {
+    case RLM_BF16:
+      return to_f32(static_cast<const bf16*>(p)[i]);
+    case RLM_F16:
+      return to_f32(static_cast<const f16*>(p)[i]);
+    default:
+      return static_cast<const float*>(p)[i];
+  }
+}
+__device__ __forceinline__ int64_t load_any_i(const void* p, int dtype, int64_t i) {
+  return dtype == RLM_I64 ? static_cast<const int64_t*>(p)[i]
+                          : static_cast<int64_t>(static_cast<const int32_t*>(p)[i]);
+}
+
+// ---------------------------------------------------------------------------
+// Wave-level primitives (wave64)
+// ---------------------------------------------------------------------------
+
+// Orders LDS traffic between lanes of one wave: a wave's LDS operations are
+// executed in issue order, so only compiler reordering has to be fenced.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint64_t o = __shfl_xor(static_cast<unsigned long long>(v), off, kWave);
+    v = v > o ? v : o;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// Order-preserving map float -> uint32 (+0.0 and -0.0 map to the same key,
+// so they tie as they do under float comparison).
+__device__ __forceinline__ uint32_t ordered_key(float f) {
+  const uint32_t u = (f == 0.0f) ? 0u : __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+  const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+// 64-bit selection key: larger score first, then the smaller tie index.
+__device__ __forceinline__ uint64_t select_key(float score, uint32_t tie_index) {
+  return (static_cast<uint64_t>(ordered_key(score)) << 32) |
+         static_cast<uint64_t>(0xffffffffu - tie_index);
+}
+__device__ __forceinline__ uint32_t key_index(uint64_t key) {
+  return 0xffffffffu - static_cast<uint32_t>(key & 0xffffffffu);
+}
+__device__ __forceinline__ float key_score(uint64_t key) {
+  return key_to_float(static_cast<uint32_t>(key >> 32));
+}
+
+// ---------------------------------------------------------------------------
+// Host-side validation
+// ---------------------------------------------------------------------------
+
+void set_error(const char* fmt, ...);
+void clear_error();
+
+inline bool is_float_dtype(int d) { return d == RLM_F32 || d == RLM_BF16 || d == RLM_F16; }
+inline bool is_index_dtype(int d) { return d == RLM_I32 || d == RLM_I64; }
+const char* dtype_name(int d);
+
+// Checks that `t` is a non-null, contiguous tensor of the given rank.
+bool check_tensor(const rlm_tensor* t, const char* name, int ndim);
+// Checks t->shape[dim] == value.
+bool check_dim(const rlm_tensor* t, const char* name, int dim, int64_t value);
+bool check_dtype_float(const rlm_tensor* t, const char* name);
+bool check_dtype_is(const rlm_tensor* t, const char* name, int dtype);
+bool check_same_dtype(const rlm_tensor* a, const char* an, const rlm_tensor* b, const char* bn);
+
+#define RLM_REQUIRE(cond, ...)      \
+  do {                              \
+    if (!(cond)) {                  \
+      ::rlm::set_error(__VA_ARGS__); \
+      return hipErrorInvalidValue;  \
+    }                               \
+  } while (0)
+
+#define RLM_TRY(expr)                              \
+  do {                                             \
+    if (!(expr)) return hipErrorInvalidValue;      \
+  } while (0)
+
+// Launch status of the last kernel, with the error message recorded.
+hipError_t launch_status(const char* what);
+
+}  // namespace rlm

@@ -1,0 +1,412 @@
+// PyTorch-ROCm operator registration over the C ABI of librlm_hip.so.
+//
+// Registers the reference's operator names and schemas
+//   relation_lm::relation_select_packed      (relation_select.py:311)
+//   relationlex::anchor_select               (triton_select.py:255)
+//   relationlex::partner_topk                (triton_select.py:298)
+//   relation_lm::relation_hidden_cached      (relation_reduce.py:149)
+//   relation_lm::relation_hidden_cache_update(relation_reduce.py:312)
+//   relation_lm::relation_norm_reduce        (relation_reduce.py:420)
+// plus the sequence forms, the packed sparse-cache projection and the linear.
+// Only a CUDA-key (ROCm device) implementation exists: CPU tensors raise.
+// Outputs are allocated with the caching allocator on the input device and
+// every kernel is enqueued on the current HIP stream, so the ops compose
+// with graph capture.
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include <initializer_list>
+#include <tuple>
+
+#include "relation_lm_hip.h"
+
+namespace {
+
+int32_t dtype_code(at::ScalarType s) {
+  switch (s) {
+    case at::kFloat: return RLM_F32;
+    case at::kBFloat16: return RLM_BF16;
+    case at::kHalf: return RLM_F16;
+    case at::kInt: return RLM_I32;
+    case at::kLong: return RLM_I64;
+    default: return -1;
+  }
+}
+
+rlm_tensor desc(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.defined(), name, ": tensor is undefined");
+  TORCH_CHECK(t.dim() <= RLM_MAX_DIMS, name, ": at most ", RLM_MAX_DIMS, " dims supported");
+  const int32_t code = dtype_code(t.scalar_type());
+  TORCH_CHECK(code >= 0, name, ": unsupported dtype ", t.scalar_type());
+  rlm_tensor d{};
+  d.data = t.data_ptr();
+  d.dtype = code;
+  d.ndim = static_cast<int32_t>(t.dim());
+  for (int64_t i = 0; i < t.dim(); ++i) {
+    d.shape[i] = t.size(i);
+    d.stride[i] = t.stride(i);
+  }
+  return d;
+}
+
+// All tensors must live on one ROCm device; returns its current stream.
+hipStream_t device_stream(const char* op, std::initializer_list<const at::Tensor*> tensors) {
+  const at::Tensor* first = *tensors.begin();
+  TORCH_CHECK(first->is_cuda(), op, ": relation_lm HIP ops need tensors on a ROCm device, got ",
+              first->device());
+  for (const at::Tensor* t : tensors) {
+    if (!t->defined()) continue;
+    TORCH_CHECK(t->is_cuda() && t->device() == first->device(), op,
+                ": all tensors must be on ", first->device(), ", found one on ", t->device());
+  }
+  return c10::hip::getCurrentHIPStream(first->device().index()).stream();
+}
+
+void check(hipError_t err, const char* op) {
+  TORCH_CHECK(err == hipSuccess, op, " failed (hipError ", static_cast<int>(err), "): ",
+              rlm_last_error());
+}
+
+at::TensorOptions f32(const at::Tensor& like) { return like.options().dtype(at::kFloat); }
+at::TensorOptions i32(const at::Tensor& like) { return like.options().dtype(at::kInt); }
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> select_packed_common(
+    bool seq, const at::Tensor& anchor_query, const at::Tensor& anchor_keys,
+    const at::Tensor& anchor_router_query, const at::Tensor& anchor_block_mean,
+    const at::Tensor& anchor_block_std, const at::Tensor& anchor_gamma,
+    const at::Tensor& anchor_bias, const at::Tensor& partner_base,
+    const at::Tensor& partner_anchor_cache, const at::Tensor& partner_keys,
+    const at::Tensor& partner_block_mean, const at::Tensor& partner_block_std,
+    const at::Tensor& partner_gamma, const at::Tensor& partner_bias, const at::Tensor& position,
+    int64_t local_window, int64_t top_blocks, int64_t k_out, bool strict_valid) {
+  const char* op = seq ? "relation_lm::relation_select_packed_seq"
+                       : "relation_lm::relation_select_packed";
+  c10::DeviceGuard guard(anchor_query.device());
+  hipStream_t stream = device_stream(
+      op, {&anchor_query, &anchor_keys, &anchor_router_query, &anchor_block_mean,
+           &anchor_block_std, &anchor_gamma, &anchor_bias, &partner_base, &partner_anchor_cache,
+           &partner_keys, &partner_block_mean, &partner_block_std, &partner_gamma, &partner_bias,
+           &position});
+  TORCH_CHECK(anchor_query.dim() == (seq ? 3 : 2), op, ": anchor_query must be ",
+              seq ? "[B,Tq,E]" : "[B,E]");
+  TORCH_CHECK(k_out >= 0, op, ": k_out must be non-negative");
+  std::vector<int64_t> qshape{anchor_query.size(0)};
+  if (seq) qshape.push_back(anchor_query.size(1));
+  std::vector<int64_t> kshape = qshape;
+  kshape.push_back(k_out);
+  at::Tensor out_anchor = at::empty(qshape, i32(anchor_query));
+  at::Tensor out_anchor_score = at::empty(qshape, f32(anchor_query));
+  at::Tensor out_partner = at::empty(kshape, i32(anchor_query));
+  at::Tensor out_partner_score = at::empty(kshape, f32(anchor_query));
+  rlm_tensor d[19] = {
+      desc(anchor_query, "anchor_query"), desc(anchor_keys, "anchor_keys"),
+      desc(anchor_router_query, "anchor_router_query"),
+      desc(anchor_block_mean, "anchor_block_mean"), desc(anchor_block_std, "anchor_block_std"),
+      desc(anchor_gamma, "anchor_gamma"), desc(anchor_bias, "anchor_bias"),
+      desc(partner_base, "partner_base"), desc(partner_anchor_cache, "partner_anchor_cache"),
+      desc(partner_keys, "partner_keys"), desc(partner_block_mean, "partner_block_mean"),
+      desc(partner_block_std, "partner_block_std"), desc(partner_gamma, "partner_gamma"),
+      desc(partner_bias, "partner_bias"), desc(position, "position"),
+      desc(out_anchor, "out_anchor"), desc(out_anchor_score, "out_anchor_score"),
+      desc(out_partner, "out_partner"), desc(out_partner_score, "out_partner_score")};
+  auto fn = seq ? rlm_relation_select_packed_seq : rlm_relation_select_packed;
+  check(fn(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7], &d[8], &d[9], &d[10], &d[11],
+           &d[12], &d[13], &d[14], local_window, top_blocks, k_out, strict_valid ? 1 : 0, &d[15],
+           &d[16], &d[17], &d[18], stream),
+        op);
+  return {out_anchor, out_anchor_score, out_partner, out_partner_score};
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> relation_select_packed(
+    const at::Tensor& anchor_query, const at::Tensor& anchor_keys,
+    const at::Tensor& anchor_router_query, const at::Tensor& anchor_block_mean,
+    const at::Tensor& anchor_block_std, const at::Tensor& anchor_gamma,
+    const at::Tensor& anchor_bias, const at::Tensor& partner_base,
+    const at::Tensor& partner_anchor_cache, const at::Tensor& partner_keys,
+    const at::Tensor& partner_block_mean, const at::Tensor& partner_block_std,
+    const at::Tensor& partner_gamma, const at::Tensor& partner_bias, const at::Tensor& position,
+    int64_t local_window, int64_t top_blocks, int64_t k_out, bool strict_valid) {
+  return select_packed_common(false, anchor_query, anchor_keys, anchor_router_query,
+                              anchor_block_mean, anchor_block_std, anchor_gamma, anchor_bias,
+                              partner_base, partner_anchor_cache, partner_keys,
+                              partner_block_mean, partner_block_std, partner_gamma, partner_bias,
+                              position, local_window, top_blocks, k_out, strict_valid);
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> relation_select_packed_seq(
+    const at::Tensor& anchor_query, const at::Tensor& anchor_keys,
+    const at::Tensor& anchor_router_query, const at::Tensor& anchor_block_mean,
+    const at::Tensor& anchor_block_std, const at::Tensor& anchor_gamma,
+    const at::Tensor& anchor_bias, const at::Tensor& partner_base,
+    const at::Tensor& partner_anchor_cache, const at::Tensor& partner_keys,
+    const at::Tensor& partner_block_mean, const at::Tensor& partner_block_std,
+    const at::Tensor& partner_gamma, const at::Tensor& partner_bias, const at::Tensor& positions,
+    int64_t local_window, int64_t top_blocks, int64_t k_out, bool strict_valid) {
+  return select_packed_common(true, anchor_query, anchor_keys, anchor_router_query,
+                              anchor_block_mean, anchor_block_std, anchor_gamma, anchor_bias,
+                              partner_base, partner_anchor_cache, partner_keys,
+                              partner_block_mean, partner_block_std, partner_gamma, partner_bias,
+                              positions, local_window, top_blocks, k_out, strict_valid);
+}
+
+std::tuple<at::Tensor, at::Tensor> anchor_select(
+    const at::Tensor& anchor_query, const at::Tensor& anchor_keys, const at::Tensor& router_query,
+    const at::Tensor& block_mean, const at::Tensor& block_std, const at::Tensor& gamma,
+    const at::Tensor& bias, const at::Tensor& position, int64_t local_window, int64_t top_blocks,
+    bool strict_valid) {
+  const char* op = "relationlex::anchor_select";
+  c10::DeviceGuard guard(anchor_query.device());
+  hipStream_t stream = device_stream(op, {&anchor_query, &anchor_keys, &router_query,
+                                          &block_mean, &block_std, &gamma, &bias, &position});
+  TORCH_CHECK(anchor_query.dim() == 2, op, ": anchor_query must be [B,E]");
+  at::Tensor out_index = at::empty({anchor_query.size(0)}, i32(anchor_query));
+  at::Tensor out_score = at::empty({anchor_query.size(0)}, f32(anchor_query));
+  rlm_tensor d[10] = {desc(anchor_query, "anchor_query"), desc(anchor_keys, "anchor_keys"),
+                      desc(router_query, "router_query"), desc(block_mean, "block_mean"),
+                      desc(block_std, "block_std"),       desc(gamma, "gamma"),
+                      desc(bias, "bias"),                 desc(position, "position"),
+                      desc(out_index, "out_index"),       desc(out_score, "out_score")};
+  check(rlm_anchor_select(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7], local_window,
+                          top_blocks, strict_valid ? 1 : 0, &d[8], &d[9], stream),
+        op);
+  return {out_index, out_score};
+}
+
+std::tuple<at::Tensor, at::Tensor> partner_topk(
+    const at::Tensor& partner_query, const at::Tensor& partner_keys,
+    const at::Tensor& router_query, const at::Tensor& block_mean, const at::Tensor& block_std,
+    const at::Tensor& gamma, const at::Tensor& bias, const at::Tensor& position,
+    const at::Tensor& anchor_index, int64_t local_window, int64_t top_blocks, int64_t k_out,
+    bool strict_valid) {
+  const char* op = "relationlex::partner_topk";
+  c10::DeviceGuard guard(partner_query.device());
+  hipStream_t stream =
+      device_stream(op, {&partner_query, &partner_keys, &router_query, &block_mean, &block_std,
+                         &gamma, &bias, &position, &anchor_index});
+  TORCH_CHECK(partner_query.dim() == 2, op, ": partner_query must be [B,E]");
+  TORCH_CHECK(k_out >= 0, op, ": k_out must be non-negative");
+  at::Tensor out_index = at::empty({partner_query.size(0), k_out}, i32(partner_query));
+  at::Tensor out_score = at::empty({partner_query.size(0), k_out}, f32(partner_query));
+  rlm_tensor d[11] = {desc(partner_query, "partner_query"), desc(partner_keys, "partner_keys"),
+                      desc(router_query, "router_query"),   desc(block_mean, "block_mean"),
+                      desc(block_std, "block_std"),         desc(gamma, "gamma"),
+                      desc(bias, "bias"),                   desc(position, "position"),
+                      desc(anchor_index, "anchor_index"),   desc(out_index, "out_index"),
+                      desc(out_score, "out_score")};
+  check(rlm_partner_topk(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7], &d[8],
+                         local_window, top_blocks, k_out, strict_valid ? 1 : 0, &d[9], &d[10],
+                         stream),
+        op);
+  return {out_index, out_score};
+}
+
+at::Tensor hidden_common(bool seq, const at::Tensor& expanded_cache,
+                         const at::Tensor& operand_cache, const at::Tensor& anchor_index,
+                         const at::Tensor& partner_index, const at::Tensor& product_weight) {
+  const char* op = seq ? "relation_lm::relation_hidden_cached_seq"
+                       : "relation_lm::relation_hidden_cached";
+  c10::DeviceGuard guard(operand_cache.device());
+  hipStream_t stream = device_stream(
+      op, {&operand_cache, &expanded_cache, &anchor_index, &partner_index, &product_weight});
+  TORCH_CHECK(partner_index.dim() == (seq ? 3 : 2), op, ": partner_index must be ",
+              seq ? "[B,Tq,K]" : "[B,K]");
+  TORCH_CHECK(product_weight.dim() == 2, op, ": product_weight must be [H,R]");
+  std::vector<int64_t> shape = partner_index.sizes().vec();
+  shape.push_back(product_weight.size(0));
+  at::Tensor out = at::empty(shape, f32(operand_cache));
+  rlm_tensor d[6] = {desc(expanded_cache, "expanded_cache"), desc(operand_cache, "operand_cache"),
+                     desc(anchor_index, "anchor_index"),     desc(partner_index, "partner_index"),
+                     desc(product_weight, "product_weight"), desc(out, "out")};
+  auto fn = seq ? rlm_relation_hidden_cached_seq : rlm_relation_hidden_cached;
+  check(fn(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], stream), op);
+  return out;
+}
+
+at::Tensor relation_hidden_cached(const at::Tensor& expanded_cache,
+                                  const at::Tensor& operand_cache,
+                                  const at::Tensor& anchor_index,
+                                  const at::Tensor& partner_index,
+                                  const at::Tensor& product_weight) {
+  return hidden_common(false, expanded_cache, operand_cache, anchor_index, partner_index,
+                       product_weight);
+}
+
+at::Tensor relation_hidden_cached_seq(const at::Tensor& expanded_cache,
+                                      const at::Tensor& operand_cache,
+                                      const at::Tensor& anchor_index,
+                                      const at::Tensor& partner_index,
+                                      const at::Tensor& product_weight) {
+  return hidden_common(true, expanded_cache, operand_cache, anchor_index, partner_index,
+                       product_weight);
+}
+
+at::Tensor relation_hidden_cache_update(at::Tensor& expanded_cache,
+                                        const at::Tensor& operand_cache,
+                                        const at::Tensor& anchor_index,
+                                        const at::Tensor& partner_index,
+                                        const at::Tensor& anchor_weight,
+                                        const at::Tensor& partner_weight,
+                                        const at::Tensor& product_weight,
+                                        const at::Tensor& first_bias,
+                                        const at::Tensor& position) {
+  const char* op = "relation_lm::relation_hidden_cache_update";
+  c10::DeviceGuard guard(operand_cache.device());
+  hipStream_t stream = device_stream(
+      op, {&operand_cache, &expanded_cache, &anchor_index, &partner_index, &anchor_weight,
+           &partner_weight, &product_weight, &first_bias, &position});
+  TORCH_CHECK(partner_index.dim() == 2, op, ": partner_index must be [B,K]");
+  TORCH_CHECK(product_weight.dim() == 2, op, ": product_weight must be [H,R]");
+  at::Tensor out = at::empty({partner_index.size(0), partner_index.size(1),
+                              product_weight.size(0)},
+                             f32(operand_cache));
+  rlm_tensor d[10] = {desc(expanded_cache, "expanded_cache"), desc(operand_cache, "operand_cache"),
+                      desc(anchor_index, "anchor_index"),     desc(partner_index, "partner_index"),
+                      desc(anchor_weight, "anchor_weight"),   desc(partner_weight, "partner_weight"),
+                      desc(product_weight, "product_weight"), desc(first_bias, "first_bias"),
+                      desc(position, "position"),             desc(out, "out")};
+  check(rlm_relation_hidden_cache_update(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7],
+                                         &d[8], &d[9], stream),
+        op);
+  return out;
+}
+
+at::Tensor norm_common(bool seq, const at::Tensor& raw, const at::Tensor& partner_scores,
+                       const at::Tensor& norm_weight, const at::Tensor& norm_bias,
+                       const at::Tensor& position, double norm_eps) {
+  const char* op = seq ? "relation_lm::relation_norm_reduce_seq"
+                       : "relation_lm::relation_norm_reduce";
+  c10::DeviceGuard guard(raw.device());
+  hipStream_t stream =
+      device_stream(op, {&raw, &partner_scores, &norm_weight, &norm_bias, &position});
+  TORCH_CHECK(raw.dim() == (seq ? 4 : 3), op, ": raw must be ", seq ? "[B,Tq,K,D]" : "[B,K,D]");
+  std::vector<int64_t> shape{raw.size(0)};
+  if (seq) shape.push_back(raw.size(1));
+  shape.push_back(raw.size(raw.dim() - 1));
+  at::Tensor out = at::empty(shape, f32(raw));
+  rlm_tensor d[6] = {desc(raw, "raw"),           desc(partner_scores, "partner_scores"),
+                     desc(norm_weight, "norm_weight"), desc(norm_bias, "norm_bias"),
+                     desc(position, "position"), desc(out, "out")};
+  auto fn = seq ? rlm_relation_norm_reduce_seq : rlm_relation_norm_reduce;
+  check(fn(&d[0], &d[1], &d[2], &d[3], &d[4], norm_eps, &d[5], stream), op);
+  return out;
+}
+
+at::Tensor relation_norm_reduce(const at::Tensor& raw, const at::Tensor& partner_scores,
+                                const at::Tensor& norm_weight, const at::Tensor& norm_bias,
+                                const at::Tensor& position, double norm_eps) {
+  return norm_common(false, raw, partner_scores, norm_weight, norm_bias, position, norm_eps);
+}
+
+at::Tensor relation_norm_reduce_seq(const at::Tensor& raw, const at::Tensor& partner_scores,
+                                    const at::Tensor& norm_weight, const at::Tensor& norm_bias,
+                                    const at::Tensor& positions, double norm_eps) {
+  return norm_common(true, raw, partner_scores, norm_weight, norm_bias, positions, norm_eps);
+}
+
+at::Tensor linear_common(const char* op, const at::Tensor& input, const at::Tensor& weight,
+                         const c10::optional<at::Tensor>& bias, at::ScalarType out_dtype,
+                         bool packed) {
+  c10::DeviceGuard guard(input.device());
+  at::Tensor b = bias.has_value() ? *bias : at::Tensor();
+  hipStream_t stream = device_stream(op, {&input, &weight, &b});
+  TORCH_CHECK(weight.dim() == 2, op, ": weight must be 2-D");
+  TORCH_CHECK(input.dim() >= 1 && input.size(-1) == weight.size(1), op,
+              ": input width does not match weight");
+  at::Tensor x = input.reshape({-1, input.size(-1)});
+  std::vector<int64_t> shape = input.sizes().vec();
+  shape.back() = weight.size(0);
+  at::Tensor out = at::empty({x.size(0), weight.size(0)}, input.options().dtype(out_dtype));
+  rlm_tensor dx = desc(x, "input"), dw = desc(weight, "weight"), dout = desc(out, "out");
+  hipError_t err;
+  if (packed) {
+    err = rlm_packed_sparse_cache_projection(&dx, &dw, &dout, stream);
+  } else {
+    rlm_tensor db{};
+    if (b.defined()) db = desc(b, "bias");
+    err = rlm_linear(&dx, &dw, b.defined() ? &db : nullptr, &dout, stream);
+  }
+  check(err, op);
+  return out.view(shape);
+}
+
+at::Tensor packed_sparse_cache_projection(const at::Tensor& memory, const at::Tensor& weight) {
+  return linear_common("relation_lm::packed_sparse_cache_projection", memory, weight,
+                       c10::nullopt, memory.scalar_type(), true);
+}
+
+at::Tensor relation_linear(const at::Tensor& input, const at::Tensor& weight,
+                           const c10::optional<at::Tensor>& bias,
+                           c10::optional<at::ScalarType> out_dtype) {
+  return linear_common("relation_lm::relation_linear", input, weight, bias,
+                       out_dtype.value_or(input.scalar_type()), false);
+}
+
+}  // namespace
+
+TORCH_LIBRARY(relation_lm, m) {
+  m.def(
+      "relation_select_packed(Tensor anchor_query, Tensor anchor_keys, Tensor "
+      "anchor_router_query, Tensor anchor_block_mean, Tensor anchor_block_std, Tensor "
+      "anchor_gamma, Tensor anchor_bias, Tensor partner_base, Tensor partner_anchor_cache, "
+      "Tensor partner_keys, Tensor partner_block_mean, Tensor partner_block_std, Tensor "
+      "partner_gamma, Tensor partner_bias, Tensor position, SymInt local_window, SymInt "
+      "top_blocks, SymInt k_out, bool strict_valid) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def(
+      "relation_select_packed_seq(Tensor anchor_query, Tensor anchor_keys, Tensor "
+      "anchor_router_query, Tensor anchor_block_mean, Tensor anchor_block_std, Tensor "
+      "anchor_gamma, Tensor anchor_bias, Tensor partner_base, Tensor partner_anchor_cache, "
+      "Tensor partner_keys, Tensor partner_block_mean, Tensor partner_block_std, Tensor "
+      "partner_gamma, Tensor partner_bias, Tensor positions, SymInt local_window, SymInt "
+      "top_blocks, SymInt k_out, bool strict_valid) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def(
+      "relation_hidden_cached(Tensor expanded_cache, Tensor operand_cache, Tensor anchor_index, "
+      "Tensor partner_index, Tensor product_weight) -> Tensor");
+  m.def(
+      "relation_hidden_cached_seq(Tensor expanded_cache, Tensor operand_cache, Tensor "
+      "anchor_index, Tensor partner_index, Tensor product_weight) -> Tensor");
+  m.def(
+      "relation_hidden_cache_update(Tensor(a!) expanded_cache, Tensor operand_cache, Tensor "
+      "anchor_index, Tensor partner_index, Tensor anchor_weight, Tensor partner_weight, Tensor "
+      "product_weight, Tensor first_bias, Tensor position) -> Tensor");
+  m.def(
+      "relation_norm_reduce(Tensor raw, Tensor partner_scores, Tensor norm_weight, Tensor "
+      "norm_bias, Tensor position, float norm_eps) -> Tensor");
+  m.def(
+      "relation_norm_reduce_seq(Tensor raw, Tensor partner_scores, Tensor norm_weight, Tensor "
+      "norm_bias, Tensor positions, float norm_eps) -> Tensor");
+  m.def("packed_sparse_cache_projection(Tensor memory, Tensor weight) -> Tensor");
+  m.def(
+      "relation_linear(Tensor input, Tensor weight, Tensor? bias=None, ScalarType? "
+      "out_dtype=None) -> Tensor");
+}
+
+TORCH_LIBRARY(relationlex, m) {
+  m.def(
+      "anchor_select(Tensor anchor_query, Tensor anchor_keys, Tensor router_query, Tensor "
+      "block_mean, Tensor block_std, Tensor gamma, Tensor bias, Tensor position, SymInt "
+      "local_window, SymInt top_blocks, bool strict_valid) -> (Tensor, Tensor)");
+  m.def(
+      "partner_topk(Tensor partner_query, Tensor partner_keys, Tensor router_query, Tensor "
+      "block_mean, Tensor block_std, Tensor gamma, Tensor bias, Tensor position, Tensor "
+      "anchor_index, SymInt local_window, SymInt top_blocks, SymInt k_out, bool strict_valid) "
+      "-> (Tensor, Tensor)");
+}
+
+TORCH_LIBRARY_IMPL(relation_lm, CUDA, m) {
+  m.impl("relation_select_packed", TORCH_FN(relation_select_packed));
+  m.impl("relation_select_packed_seq", TORCH_FN(relation_select_packed_seq));
+  m.impl("relation_hidden_cached", TORCH_FN(relation_hidden_cached));
+  m.impl("relation_hidden_cached_seq", TORCH_FN(relation_hidden_cached_seq));
+  m.impl("relation_hidden_cache_update", TORCH_FN(relation_hidden_cache_update));
+  m.impl("relation_norm_reduce", TORCH_FN(relation_norm_reduce));
+  m.impl("relation_norm_reduce_seq", TORCH_FN(relation_norm_reduce_seq));
+  m.impl("packed_sparse_cache_projection", TORCH_FN(packed_sparse_cache_projection));
+  m.impl("relation_linear", TORCH_FN(relation_linear));
+}
+
+TORCH_LIBRARY_IMPL(relationlex, CUDA, m) {
+  m.impl("anchor_select", TORCH_FN(anchor_select));
+  m.impl("partner_topk", TORCH_FN(partner_topk));
+}

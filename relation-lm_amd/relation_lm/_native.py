@@ -1,0 +1,86 @@
+"""Loads the HIP operator library and registers fake (meta) kernels.
+
+Importing this module makes ``torch.ops.relation_lm.*`` and
+``torch.ops.relationlex.*`` available.  There is no fallback: when the built
+library is missing the import fails with instructions to build it, and calling
+an op with CPU tensors raises (only the ROCm-device implementation exists).
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+
+LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
+TORCH_LIBRARY = os.path.join(LIB_DIR, "_rlm_torch.so")
+C_LIBRARY = os.path.join(LIB_DIR, "librlm_hip.so")
+
+_loaded = False
+
+
+def load() -> None:
+    """Load the operator library once (idempotent)."""
+    global _loaded
+    if _loaded:
+        return
+    if not os.path.exists(TORCH_LIBRARY) or not os.path.exists(C_LIBRARY):
+        raise ImportError(
+            "relation_lm HIP library not built: expected "
+            f"{TORCH_LIBRARY} and {C_LIBRARY}. Run `make -C relation-lm_amd/csrc` "
+            "(or __graft_entry__.build()) first.")
+    torch.ops.load_library(TORCH_LIBRARY)
+    _register_fakes()
+    _loaded = True
+
+
+def _register_fakes() -> None:
+    def fake_select(anchor_query, *rest):
+        k_out = rest[-2]
+        seq = anchor_query.dim() == 3
+        qshape = tuple(anchor_query.shape[:2] if seq else anchor_query.shape[:1])
+        return (anchor_query.new_empty(qshape, dtype=torch.int32),
+                anchor_query.new_empty(qshape, dtype=torch.float32),
+                anchor_query.new_empty(qshape + (k_out,), dtype=torch.int32),
+                anchor_query.new_empty(qshape + (k_out,), dtype=torch.float32))
+
+    torch.library.register_fake("relation_lm::relation_select_packed")(fake_select)
+    torch.library.register_fake("relation_lm::relation_select_packed_seq")(fake_select)
+
+    @torch.library.register_fake("relationlex::anchor_select")
+    def _(anchor_query, *rest):
+        b = anchor_query.shape[0]
+        return (anchor_query.new_empty((b,), dtype=torch.int32),
+                anchor_query.new_empty((b,), dtype=torch.float32))
+
+    @torch.library.register_fake("relationlex::partner_topk")
+    def _(partner_query, *rest):
+        b, k_out = partner_query.shape[0], rest[-2]
+        return (partner_query.new_empty((b, k_out), dtype=torch.int32),
+                partner_query.new_empty((b, k_out), dtype=torch.float32))
+
+    def fake_hidden(expanded_cache, operand_cache, anchor_index, partner_index, product_weight,
+                    *rest):
+        return operand_cache.new_empty(tuple(partner_index.shape) + (product_weight.shape[0],),
+                                       dtype=torch.float32)
+
+    torch.library.register_fake("relation_lm::relation_hidden_cached")(fake_hidden)
+    torch.library.register_fake("relation_lm::relation_hidden_cached_seq")(fake_hidden)
+    torch.library.register_fake("relation_lm::relation_hidden_cache_update")(fake_hidden)
+
+    def fake_norm(raw, *rest):
+        return raw.new_empty(tuple(raw.shape[:-2]) + (raw.shape[-1],), dtype=torch.float32)
+
+    torch.library.register_fake("relation_lm::relation_norm_reduce")(fake_norm)
+    torch.library.register_fake("relation_lm::relation_norm_reduce_seq")(fake_norm)
+
+    @torch.library.register_fake("relation_lm::packed_sparse_cache_projection")
+    def _(memory, weight):
+        return memory.new_empty(tuple(memory.shape[:-1]) + (weight.shape[0],))
+
+    @torch.library.register_fake("relation_lm::relation_linear")
+    def _(input, weight, bias=None, out_dtype=None):
+        return input.new_empty(tuple(input.shape[:-1]) + (weight.shape[0],),
+                               dtype=out_dtype or input.dtype)
+
+
+load()

@@ -1,0 +1,148 @@
+"""Factorized relation reduce on gfx950.
+
+Mirrors src/relation_lm/kernels/relation_reduce.py:
+  * ``FactorizedRelationWeights`` / ``factor_relation_first_layer`` (:11-57) --
+    host-side weight algebra, pure torch, identical contract and errors;
+  * ``recommended_relation_cache_mode`` (:60-69);
+  * ``relation_hidden_cached`` (:149-183), ``relation_hidden_cache_update``
+    (:312-357) and ``relation_norm_reduce`` (:420-450) -- HIP kernels behind the
+    same ``torch.ops.relation_lm`` schemas;
+plus the sequence forms ``relation_hidden_cached_seq`` /
+``relation_norm_reduce_seq`` and ``relation_linear`` (the MFMA GEMM used for the
+expanded-cache projection and the relation MLP's second linear).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor
+
+from relation_lm import _native  # noqa: F401  (registers torch.ops.relation_lm)
+
+
+@dataclass(frozen=True)
+class FactorizedRelationWeights:
+    """First Relation-MLP layer split into reusable token contributions."""
+
+    anchor_weight: Tensor
+    partner_weight: Tensor
+    product_weight: Tensor
+    first_bias: Tensor
+    expanded_weight: Tensor
+    expanded_bias: Tensor
+
+
+def factor_relation_first_layer(
+    first_weight: Tensor,
+    first_bias: Tensor,
+    relation_dim: int,
+) -> FactorizedRelationWeights:
+    """Factor ``W[a,p,a*p,a-p]+b`` into anchor, partner, and product terms.
+
+    ``(W_a + W_d) a + (W_p - W_d) p + W_m (a * p) + b`` equals the unfactorized
+    layer exactly in real arithmetic.  ``expanded_weight`` = ``[W_a+W_d; W_p-W_d]``
+    projects a cached operand into ``[anchor_base, partner_base]``;
+    ``expanded_bias`` = ``[b; 0]`` applies the bias once.
+    """
+    if first_weight.ndim != 2 or first_bias.ndim != 1:
+        raise ValueError("first_weight must be 2D and first_bias must be 1D")
+    relation_dim = int(relation_dim)
+    if first_weight.size(1) != 4 * relation_dim:
+        raise ValueError("first_weight input dimension must equal 4 * relation_dim")
+    blocks = first_weight.split(relation_dim, dim=1)
+    anchor_weight = (blocks[0] + blocks[3]).contiguous()
+    partner_weight = (blocks[1] - blocks[3]).contiguous()
+    product_weight = blocks[2].contiguous()
+    return FactorizedRelationWeights(
+        anchor_weight=anchor_weight,
+        partner_weight=partner_weight,
+        product_weight=product_weight,
+        first_bias=first_bias.contiguous(),
+        expanded_weight=torch.cat((anchor_weight, partner_weight), dim=0).contiguous(),
+        expanded_bias=torch.cat((first_bias, torch.zeros_like(first_bias)), dim=0).contiguous(),
+    )
+
+
+def recommended_relation_cache_mode(batch_size: int) -> str:
+    """Cache-update policy for decode: fuse the current-row update at batch 1.
+
+    Same contract as the reference (relation_reduce.py:60-69): "fused_update"
+    for batch 1, "separate_update" otherwise, ValueError for batch < 1.
+    """
+    if batch_size < 1:
+        raise ValueError("batch_size must be positive")
+    return "fused_update" if batch_size == 1 else "separate_update"
+
+
+def relation_hidden_cached(
+    expanded_cache: Tensor,
+    operand_cache: Tensor,
+    anchor_index: Tensor,
+    partner_index: Tensor,
+    product_weight: Tensor,
+) -> Tensor:
+    """GELU(W_m (op[a] * op[p]) + X[a, :H] + X[p, H:]) -> f32 [B, K, H]."""
+    return torch.ops.relation_lm.relation_hidden_cached(
+        expanded_cache, operand_cache, anchor_index, partner_index, product_weight)
+
+
+def relation_hidden_cached_seq(
+    expanded_cache: Tensor,
+    operand_cache: Tensor,
+    anchor_index: Tensor,
+    partner_index: Tensor,
+    product_weight: Tensor,
+) -> Tensor:
+    """Sequence form: anchor [B,Tq], partner [B,Tq,K] -> f32 [B,Tq,K,H]."""
+    return torch.ops.relation_lm.relation_hidden_cached_seq(
+        expanded_cache, operand_cache, anchor_index, partner_index, product_weight)
+
+
+def relation_hidden_cache_update(
+    expanded_cache: Tensor,
+    operand_cache: Tensor,
+    anchor_index: Tensor,
+    partner_index: Tensor,
+    anchor_weight: Tensor,
+    partner_weight: Tensor,
+    product_weight: Tensor,
+    first_bias: Tensor,
+    position: Tensor,
+) -> Tensor:
+    """Writes ``expanded_cache[:, position]`` and returns the relation hidden f32 [B,K,H]."""
+    return torch.ops.relation_lm.relation_hidden_cache_update(
+        expanded_cache, operand_cache, anchor_index, partner_index, anchor_weight,
+        partner_weight, product_weight, first_bias, position)
+
+
+def relation_norm_reduce(
+    raw: Tensor,
+    partner_scores: Tensor,
+    norm_weight: Tensor,
+    norm_bias: Tensor,
+    position: Tensor,
+    norm_eps: float,
+) -> Tensor:
+    """Per-partner LayerNorm, active-K softmax and weighted sum -> f32 [B, D]."""
+    return torch.ops.relation_lm.relation_norm_reduce(
+        raw, partner_scores, norm_weight, norm_bias, position, float(norm_eps))
+
+
+def relation_norm_reduce_seq(
+    raw: Tensor,
+    partner_scores: Tensor,
+    norm_weight: Tensor,
+    norm_bias: Tensor,
+    positions: Tensor,
+    norm_eps: float,
+) -> Tensor:
+    """Sequence form: raw [B,Tq,K,D], scores [B,Tq,K], positions [Tq] or [B,Tq] -> f32 [B,Tq,D]."""
+    return torch.ops.relation_lm.relation_norm_reduce_seq(
+        raw, partner_scores, norm_weight, norm_bias, positions, float(norm_eps))
+
+
+def relation_linear(input: Tensor, weight: Tensor, bias: Tensor | None = None,
+                    out_dtype: torch.dtype | None = None) -> Tensor:
+    """``input @ weight.T + bias`` on MFMA (bf16/f16 weights) or fp32 FMA (fp32 weights)."""
+    return torch.ops.relation_lm.relation_linear(input, weight, bias, out_dtype)

@@ -1,0 +1,79 @@
+"""Packed relation selection on gfx950.
+
+``relation_select_packed`` keeps the signature and semantics of the reference
+op ``relation_lm::relation_select_packed``
+(src/relation_lm/kernels/relation_select.py:311-382): anchor block scoring,
+exact top-1 anchor (ties to the lowest position), factorized partner query,
+partner block routing and exact top-k partners (ties to the lowest candidate
+lane) with anchor exclusion and strict/compat remote-block validity.
+
+``relation_select_packed_seq`` is the sequence (prefill) form: query-side
+tensors carry a query axis and ``positions`` holds one position per query.
+"""
+from __future__ import annotations
+
+from torch import Tensor
+
+from relation_lm import _native  # noqa: F401  (registers torch.ops.relation_lm)
+import torch
+
+
+def relation_select_packed(
+    anchor_query: Tensor,
+    anchor_keys: Tensor,
+    anchor_router_query: Tensor,
+    anchor_block_mean: Tensor,
+    anchor_block_std: Tensor,
+    anchor_gamma: Tensor,
+    anchor_bias: Tensor,
+    partner_base: Tensor,
+    partner_anchor_cache: Tensor,
+    partner_keys: Tensor,
+    partner_block_mean: Tensor,
+    partner_block_std: Tensor,
+    partner_gamma: Tensor,
+    partner_bias: Tensor,
+    position: Tensor,
+    local_window: int,
+    top_blocks: int,
+    k_out: int,
+    strict_valid: bool,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Returns (anchor int32 [B], anchor_score f32 [B], partner int32 [B,K], partner_score f32 [B,K])."""
+    return torch.ops.relation_lm.relation_select_packed(
+        anchor_query, anchor_keys, anchor_router_query, anchor_block_mean, anchor_block_std,
+        anchor_gamma, anchor_bias, partner_base, partner_anchor_cache, partner_keys,
+        partner_block_mean, partner_block_std, partner_gamma, partner_bias, position,
+        local_window, top_blocks, k_out, strict_valid)
+
+
+def relation_select_packed_seq(
+    anchor_query: Tensor,
+    anchor_keys: Tensor,
+    anchor_router_query: Tensor,
+    anchor_block_mean: Tensor,
+    anchor_block_std: Tensor,
+    anchor_gamma: Tensor,
+    anchor_bias: Tensor,
+    partner_base: Tensor,
+    partner_anchor_cache: Tensor,
+    partner_keys: Tensor,
+    partner_block_mean: Tensor,
+    partner_block_std: Tensor,
+    partner_gamma: Tensor,
+    partner_bias: Tensor,
+    positions: Tensor,
+    local_window: int,
+    top_blocks: int,
+    k_out: int,
+    strict_valid: bool,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Sequence form: anchor_query [B,Tq,E] ..., positions [Tq] or [B,Tq].
+
+    Returns (anchor [B,Tq], anchor_score [B,Tq], partner [B,Tq,K], partner_score [B,Tq,K]).
+    """
+    return torch.ops.relation_lm.relation_select_packed_seq(
+        anchor_query, anchor_keys, anchor_router_query, anchor_block_mean, anchor_block_std,
+        anchor_gamma, anchor_bias, partner_base, partner_anchor_cache, partner_keys,
+        partner_block_mean, partner_block_std, partner_gamma, partner_bias, positions,
+        local_window, top_blocks, k_out, strict_valid)

@@ -1,0 +1,167 @@
+"""Seeded synthetic workloads of the routed relation path.
+
+Shapes follow the benchmark configurations of the routed relation path:
+
+  cfg1  B=1  T=128  d=256, block 16 (8 blocks), local 32, top 2, K=8, fp32
+  cfg2  B=8  T=512  d=512, block 32 (16 blocks), local 64, top 4, K=8, bf16
+        activations / fp32 scores, relation hidden 512 (full sequence)
+  cfg3  decode at t=511 against a 512-row cache, block 32, local 64, top 4,
+        K=8, packed 576->512 bf16 projection, R=128 H=2304 D=576, B in {1, 8}
+  cfg4  B=8  T=2048 d=512, K=8, hidden 1024 (reduce in isolation)
+
+Every tensor is drawn on the CPU from one ``torch.Generator`` in a fixed order
+and then copied to the device, so a CPU checker sees the same bits as the GPU.
+Activations and caches ~ N(0,1); weights ~ N(0, 1/fan_in); gamma and bias ~
+N(0,1); block statistics are the mean and biased std of seeded router keys
+(the DistilledBlockRouter.block_statistics definition).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from relation_lm.kernels.relation_reduce import factor_relation_first_layer
+
+
+@dataclass(frozen=True)
+class RelationConfig:
+    name: str
+    batch: int
+    context: int
+    d_model: int
+    block_size: int
+    local_window: int
+    top_blocks: int
+    k_out: int
+    dtype: torch.dtype
+    relation_dim: int = 128
+    hidden_dim: int = 1024
+    exact_dim: int = 64
+    heads: int = 4
+    head_dim: int = 16
+    rel_buckets: int = 16
+    strict_valid: bool = False
+    seed: int = 20261201
+
+    @property
+    def blocks(self) -> int:
+        return self.context // self.block_size
+
+    @property
+    def queries(self) -> int:
+        return self.batch * self.context
+
+
+CONFIGS = {
+    "cfg1": RelationConfig("cfg1", 1, 128, 256, 16, 32, 2, 8, torch.float32, hidden_dim=1024,
+                           seed=20261201),
+    "cfg2": RelationConfig("cfg2", 8, 512, 512, 32, 64, 4, 8, torch.bfloat16, hidden_dim=512,
+                           seed=20261202),
+    "cfg3": RelationConfig("cfg3", 8, 512, 576, 32, 64, 4, 8, torch.bfloat16, hidden_dim=2304,
+                           seed=20261203),
+    "cfg4": RelationConfig("cfg4", 8, 2048, 512, 64, 128, 4, 8, torch.bfloat16, hidden_dim=1024,
+                           seed=20261204),
+}
+
+
+def _gen(seed: int) -> torch.Generator:
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return g
+
+
+def _randn(g, *shape, scale: float = 1.0, dtype=torch.float32) -> torch.Tensor:
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def block_statistics(keys: torch.Tensor, block_size: int, heads: int, head_dim: int):
+    """Per-block mean and biased std, [B, NB, heads, head_dim] (block_router.py:54-68)."""
+    batch, length, _ = keys.shape
+    grouped = keys.float().view(batch, length // block_size, block_size, heads, head_dim)
+    return grouped.mean(2).contiguous(), grouped.std(2, unbiased=False).contiguous()
+
+
+def selection_inputs(cfg: RelationConfig, *, queries: int | None = None,
+                     device: torch.device | str = "cpu", seed: int | None = None) -> dict:
+    """Inputs of relation_select_packed(_seq).
+
+    ``queries=None`` gives the sequence form (one query per cache position, query
+    tensors [B,T,*]); ``queries=1`` gives the decode form (query tensors [B,*]).
+    """
+    g = _gen(cfg.seed if seed is None else seed)
+    b, t, e = cfg.batch, cfg.context, cfg.exact_dim
+    rd = cfg.heads * cfg.head_dim
+    q = t if queries is None else queries
+    qshape = (b, q) if queries is None else (b,)
+    act = cfg.dtype
+    out = {
+        "anchor_query": _randn(g, *qshape, e, dtype=act),
+        "anchor_keys": _randn(g, b, t, e, dtype=act),
+        "anchor_router_query": _randn(g, *qshape, rd, dtype=act),
+        "partner_base": _randn(g, *qshape, 2 * e, dtype=act),
+        "partner_anchor_cache": _randn(g, b, t, 2 * e, dtype=act),
+        "partner_keys": _randn(g, b, t, e, dtype=act),
+    }
+    for side in ("anchor", "partner"):
+        router_keys = _randn(g, b, t, rd, dtype=act)
+        mean, std = block_statistics(router_keys, cfg.block_size, cfg.heads, cfg.head_dim)
+        out[f"{side}_block_mean"] = mean
+        out[f"{side}_block_std"] = std
+        out[f"{side}_gamma"] = _randn(g, cfg.heads)
+        out[f"{side}_bias"] = _randn(g, cfg.heads, cfg.rel_buckets)
+    if queries is None:
+        out["positions"] = torch.arange(t, dtype=torch.int64)
+    else:
+        out["position"] = torch.tensor(t - 1, dtype=torch.int64)
+    return {k: v.to(device) for k, v in out.items()}
+
+
+SELECT_ORDER = ("anchor_query", "anchor_keys", "anchor_router_query", "anchor_block_mean",
+                "anchor_block_std", "anchor_gamma", "anchor_bias", "partner_base",
+                "partner_anchor_cache", "partner_keys", "partner_block_mean",
+                "partner_block_std", "partner_gamma", "partner_bias")
+
+
+def select_args(inputs: dict, cfg: RelationConfig) -> tuple:
+    """Positional arguments of relation_select_packed(_seq) in reference order."""
+    position = inputs["positions"] if "positions" in inputs else inputs["position"]
+    return tuple(inputs[k] for k in SELECT_ORDER) + (
+        position, cfg.local_window, cfg.top_blocks, cfg.k_out, cfg.strict_valid)
+
+
+def reduce_inputs(cfg: RelationConfig, *, device: torch.device | str = "cpu",
+                  seed: int | None = None) -> dict:
+    """Operand cache, factorized first layer, second linear and LayerNorm parameters."""
+    g = _gen((cfg.seed if seed is None else seed) + 7919)
+    b, t, r, h, d = cfg.batch, cfg.context, cfg.relation_dim, cfg.hidden_dim, cfg.d_model
+    act = cfg.dtype
+    operand = _randn(g, b, t, r, dtype=act)
+    first_weight = _randn(g, h, 4 * r, scale=(4 * r) ** -0.5)
+    first_bias = _randn(g, h, scale=0.01)
+    factors = factor_relation_first_layer(first_weight, first_bias, r)
+    out = {
+        "operand_cache": operand,
+        "first_weight": first_weight.to(act),
+        "first_bias": first_bias.to(act),
+        "anchor_weight": factors.anchor_weight.to(act),
+        "partner_weight": factors.partner_weight.to(act),
+        "product_weight": factors.product_weight.to(act),
+        "expanded_weight": factors.expanded_weight.to(act),
+        "expanded_bias": factors.expanded_bias.to(act),
+        "second_weight": _randn(g, d, h, scale=h ** -0.5, dtype=act),
+        "second_bias": _randn(g, d, scale=0.01, dtype=act),
+        "norm_weight": (1.0 + _randn(g, d, scale=0.05)).to(act),
+        "norm_bias": _randn(g, d, scale=0.01, dtype=act),
+    }
+    return {k: v.to(device) for k, v in out.items()}
+
+
+def packed_projection_inputs(cfg: RelationConfig, *, device="cpu", seed: int | None = None):
+    """Memory rows [B, 576] and the six packed weights (widths 64,64,128,128,64,64)."""
+    g = _gen((cfg.seed if seed is None else seed) + 104729)
+    widths = (64, 64, 128, 128, 64, 64)
+    memory = _randn(g, cfg.batch, cfg.d_model, dtype=cfg.dtype)
+    weights = tuple(_randn(g, w, cfg.d_model, scale=cfg.d_model ** -0.5, dtype=cfg.dtype)
+                    for w in widths)
+    return memory.to(device), tuple(w.to(device) for w in weights)
