@@ -153,6 +153,9 @@ const char* dtype_name(int d);
 
 // Checks that `t` is a non-null, contiguous tensor of the given rank.
 bool check_tensor(const rlm_tensor* t, const char* name, int ndim);
+// Checks that `t` is a non-null 2-d tensor of unit column stride whose row
+// stride is at least its width (row-strided views such as cache[:, t]).
+bool check_rows(const rlm_tensor* t, const char* name);
 // Checks t->shape[dim] == value.
 bool check_dim(const rlm_tensor* t, const char* name, int dim, int64_t value);
 bool check_dtype_float(const rlm_tensor* t, const char* name);

@@ -27,6 +27,7 @@ constexpr int kPad = 8;  // 16-bit elements of padding per LDS row
 
 struct GemmParams {
   int64_t M, N, K;
+  int64_t lda;  // input row stride in elements (>= K)
   const void* a;
   const void* w;
   const void* bias;
@@ -104,7 +105,7 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmParams p) {
     {
       const int64_t m = m0 + lrow;
       uint4 va = make_uint4(0, 0, 0, 0);
-      if (m < p.M) va = load_a8<TA, W>(A + m * p.K, k0 + lk, p.K);
+      if (m < p.M) va = load_a8<TA, W>(A + m * p.lda, k0 + lk, p.K);
       *reinterpret_cast<uint4*>(&As[lrow][lk]) = va;
       const int64_t n = n0 + lrow;
       uint4 vb = make_uint4(0, 0, 0, 0);
@@ -168,7 +169,7 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(const GemmParams p) {
       const int r = idx / kBK;
       const int k = idx % kBK;
       const int64_t m = m0 + r, n = n0 + r, kk = k0 + k;
-      As[k][r] = (m < p.M && kk < p.K) ? A[m * p.K + kk] : 0.0f;
+      As[k][r] = (m < p.M && kk < p.K) ? A[m * p.lda + kk] : 0.0f;
       Bs[k][r] = (n < p.N && kk < p.K) ? Wt[n * p.K + kk] : 0.0f;
     }
     __syncthreads();
@@ -214,7 +215,7 @@ hipError_t launch_mfma_out(const GemmParams& p, int out_dtype, dim3 grid, hipStr
 
 hipError_t linear_impl(const rlm_tensor* input, const rlm_tensor* weight, const rlm_tensor* bias,
                        const rlm_tensor* out, hipStream_t stream, const char* what) {
-  RLM_TRY(check_tensor(input, "input", 2));
+  RLM_TRY(check_rows(input, "input"));
   RLM_TRY(check_tensor(weight, "weight", 2));
   RLM_TRY(check_tensor(out, "out", 2));
   RLM_TRY(check_dtype_float(input, "input"));
@@ -233,6 +234,7 @@ hipError_t linear_impl(const rlm_tensor* input, const rlm_tensor* weight, const 
   p.M = M;
   p.N = N;
   p.K = K;
+  p.lda = M > 1 ? input->stride[0] : K;
   p.a = input->data;
   p.w = weight->data;
   p.bias = bias ? bias->data : nullptr;
@@ -253,7 +255,9 @@ hipError_t linear_impl(const rlm_tensor* input, const rlm_tensor* weight, const 
       hipLaunchKernelGGL((gemm_f32_kernel<f16>), grid, dim3(256), 0, stream, p);
     return launch_status(what);
   }
-  RLM_REQUIRE(K % 8 == 0, "%s: reduction dim must be a multiple of 8 for 16-bit weights", what);
+  RLM_REQUIRE(K % 8 == 0 && p.lda % 8 == 0,
+              "%s: reduction dim and input row stride must be multiples of 8 for 16-bit weights",
+              what);
   RLM_REQUIRE((reinterpret_cast<uintptr_t>(input->data) & 15u) == 0 &&
                   (reinterpret_cast<uintptr_t>(weight->data) & 15u) == 0,
               "%s: input and weight must be 16-byte aligned", what);

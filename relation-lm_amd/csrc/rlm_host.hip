@@ -60,6 +60,35 @@ bool check_tensor(const rlm_tensor* t, const char* name, int ndim) {
   return true;
 }
 
+bool check_rows(const rlm_tensor* t, const char* name) {
+  if (t == nullptr) {
+    set_error("%s: missing tensor", name);
+    return false;
+  }
+  if (t->ndim != 2) {
+    set_error("%s: expected a 2-d tensor, got %d-d", name, t->ndim);
+    return false;
+  }
+  if (t->shape[0] < 0 || t->shape[1] < 0) {
+    set_error("%s: negative size", name);
+    return false;
+  }
+  if (t->shape[0] * t->shape[1] > 0 && t->data == nullptr) {
+    set_error("%s: null data pointer", name);
+    return false;
+  }
+  if (t->shape[1] > 1 && t->stride[1] != 1) {
+    set_error("%s: columns must be unit-stride (got stride %lld)", name, (long long)t->stride[1]);
+    return false;
+  }
+  if (t->shape[0] > 1 && t->stride[0] < t->shape[1]) {
+    set_error("%s: row stride %lld is smaller than the row width %lld", name,
+              (long long)t->stride[0], (long long)t->shape[1]);
+    return false;
+  }
+  return true;
+}
+
 bool check_dim(const rlm_tensor* t, const char* name, int dim, int64_t value) {
   if (t->shape[dim] != value) {
     set_error("%s: size %lld in dim %d does not match the expected %lld", name,

@@ -314,7 +314,11 @@ at::Tensor linear_common(const char* op, const at::Tensor& input, const at::Tens
   TORCH_CHECK(weight.dim() == 2, op, ": weight must be 2-D");
   TORCH_CHECK(input.dim() >= 1 && input.size(-1) == weight.size(1), op,
               ": input width does not match weight");
+  // Row-strided 2-d views (a cache column such as cache[:, t]) pass through
+  // as they are; anything else is compacted first.
   at::Tensor x = input.reshape({-1, input.size(-1)});
+  if ((x.size(1) > 1 && x.stride(1) != 1) || (x.size(0) > 1 && x.stride(0) % 8 != 0))
+    x = x.contiguous();
   std::vector<int64_t> shape = input.sizes().vec();
   shape.back() = weight.size(0);
   at::Tensor out = at::empty({x.size(0), weight.size(0)}, input.options().dtype(out_dtype));
