@@ -32,16 +32,19 @@ __device__ __forceinline__ float to_f32(bf16 v) {
 }
 __device__ __forceinline__ float to_f32(f16 v) { return static_cast<float>(v); }
 
-// Round-to-nearest-even float -> bf16 (NaN kept quiet).
+// Two floats -> two bf16 (lo in bits 0..15), round-to-nearest-even, in one
+// v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+// Round-to-nearest-even float -> bf16.
 __device__ __forceinline__ bf16 f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
   bf16 out;
-  if ((u & 0x7fffffffu) > 0x7f800000u) {
-    out.bits = 0x7fc0;
-    return out;
-  }
-  u += 0x7fffu + ((u >> 16) & 1u);
-  out.bits = static_cast<uint16_t>(u >> 16);
+  out.bits = static_cast<uint16_t>(pack_bf16x2(f, 0.0f));
   return out;
 }
 
@@ -83,6 +86,76 @@ __device__ __forceinline__ float load_any_f(const void* p, int dtype, int64_t i)
 __device__ __forceinline__ int64_t load_any_i(const void* p, int dtype, int64_t i) {
   return dtype == RLM_I64 ? static_cast<const int64_t*>(p)[i]
                           : static_cast<int64_t>(static_cast<const int32_t*>(p)[i]);
+}
+
+// ---------------------------------------------------------------------------
+// Range-checked buffer access
+// ---------------------------------------------------------------------------
+//
+// Raw buffer loads/stores through a resource descriptor whose size is the
+// tensor's byte size: an access past the end reads zero / is dropped by the
+// hardware, so a gather with an invalid index needs no branch -- its offset is
+// set to kNoOffset.  Every buffer addressed this way is smaller than 2 GiB
+// (checked on the host), so kNoOffset plus any in-row offset stays past it.
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kNoOffset = 0x80000000u;
+constexpr int kRawBufferWord3 = 0x00020000;  // gfx9 family: raw (untyped) buffer
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           kRawBufferWord3);
+}
+__device__ __forceinline__ uint4 buf_load_b128(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t buf_load_b32(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint16_t buf_load_b16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+__device__ __forceinline__ void buf_store_f32(float v, rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+}
+// One element of type T at byte offset `off`, as float.
+template <typename T>
+__device__ __forceinline__ float buf_load_elem(rsrc_t r, uint32_t off);
+template <>
+__device__ __forceinline__ float buf_load_elem<float>(rsrc_t r, uint32_t off) {
+  return __uint_as_float(buf_load_b32(r, off));
+}
+template <>
+__device__ __forceinline__ float buf_load_elem<bf16>(rsrc_t r, uint32_t off) {
+  return __uint_as_float(static_cast<uint32_t>(buf_load_b16(r, off)) << 16);
+}
+template <>
+__device__ __forceinline__ float buf_load_elem<f16>(rsrc_t r, uint32_t off) {
+  return static_cast<float>(__builtin_bit_cast(f16, buf_load_b16(r, off)));
+}
+
+// ---------------------------------------------------------------------------
+// Elementwise math
+// ---------------------------------------------------------------------------
+
+// erf(x) by Abramowitz & Stegun, Handbook of Mathematical Functions, 7.1.26:
+// 1 - (a1 t + ... + a5 t^5) exp(-x^2), t = 1/(1 + p|x|), odd extension;
+// |error| <= 1.5e-7 for all x.
+__device__ __forceinline__ float erf_as7126(float x) {
+  const float ax = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, ax, 1.0f));
+  float y = fmaf(1.061405429f, t, -1.453152027f);
+  y = fmaf(y, t, 1.421413741f);
+  y = fmaf(y, t, -0.284496736f);
+  y = fmaf(y, t, 0.254829592f);
+  y *= t;
+  const float r = fmaf(-y, __expf(-ax * ax), 1.0f);
+  return copysignf(r, x);
+}
+
+// Exact (erf) GELU, x * Phi(x) (relation_reduce.py:139).
+__device__ __forceinline__ float gelu_erf(float x) {
+  return 0.5f * x * (1.0f + erf_as7126(x * 0.70710678118654752440f));
 }
 
 // ---------------------------------------------------------------------------

@@ -4,12 +4,25 @@
 // (src/relation_lm/inference/packed_cache.py:52-57), the expanded-cache
 // projection and the relation MLP's second linear of the reference's callers.
 //
-// 16-bit weights (bf16/f16): v_mfma_f32_16x16x32_{bf16,f16} with fp32
-//   accumulation.  A 64x64 workgroup tile is four waves of 32x32 (2x2 MFMA
-//   tiles); A and W k-slices of 32 are staged in LDS.  A may be fp32 (the
-//   relation hidden); it is rounded to the weight type while staging.
-// fp32 weights: fp32 FMA on the same tiling (4x4 outputs per thread), so the
-//   fp32 mode never passes through reduced precision.
+// 16-bit weights (bf16/f16): v_mfma_f32_16x16x32_{bf16,f16}, fp32 accumulation.
+// A may be fp32 (the relation hidden); it is rounded to the weight type while
+// it is staged, so the MFMA sees the same operand a bf16 F.linear would.
+//
+//   tile_kernel   (M > 64)   BMxBN workgroup tile (128x128 or 64x128), four
+//                 waves in 2x2, each a (BM/2)x(BN/2) grid of 16x16 MFMA tiles.
+//                 A and W k-slices of 32 are double-buffered in LDS: the
+//                 global loads of slice k+1 are in flight while slice k runs
+//                 on the matrix cores.  Workgroups are renumbered so that the
+//                 tiles sharing an A row-block run on the same XCD (one L2),
+//                 which keeps A's HBM traffic at one read.
+//   skinny_kernel (M <= 64)  decode shapes.  A workgroup owns 16 output columns
+//                 and every row; its four waves split K, each streaming its
+//                 W and A slices straight from global memory in MFMA operand
+//                 layout, and the partial sums meet once in LDS.
+//
+// fp32 weights: f32_tile_kernel, 64x64 tiles on v_mfma_f32_16x16x4f32 (fp32
+// operands, fp32 accumulation), so fp32 mode never passes through reduced
+// precision.
 #include "rlm_common.hpp"
 
 namespace rlm {
@@ -20,10 +33,9 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kBM = 64;
-constexpr int kBN = 64;
-constexpr int kBK = 32;
-constexpr int kPad = 8;  // 16-bit elements of padding per LDS row
+constexpr int kBK = 32;   // k-slice of the 16-bit path
+constexpr int kPad = 8;   // 16-bit elements of padding per LDS row (conflict-free b128 reads)
+constexpr int kSkinnyM = 64;
 
 struct GemmParams {
   int64_t M, N, K;
@@ -39,31 +51,32 @@ struct GemmParams {
 template <typename W>
 __device__ __forceinline__ uint16_t to_bits(float v);
 template <>
-__device__ __forceinline__ uint16_t to_bits<bf16>(float v) { return f32_to_bf16(v).bits; }
-template <>
 __device__ __forceinline__ uint16_t to_bits<f16>(float v) {
   const f16 h = static_cast<f16>(v);
   return __builtin_bit_cast(uint16_t, h);
 }
 
-// Eight consecutive A elements as W bit patterns (zero past K).
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
+  return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+}
+
+// Eight consecutive elements starting at row[k] as W bit patterns.  The
+// caller guarantees k + 8 <= K and 16-byte alignment of 16-bit rows.
 template <typename TA, typename W>
-__device__ __forceinline__ uint4 load_a8(const TA* row, int64_t k, int64_t K) {
-  uint16_t v[8];
-  if constexpr (sizeof(TA) == 2 && sizeof(W) == 2 && __is_same(TA, W)) {
-    if (k + 8 <= K) return *reinterpret_cast<const uint4*>(row + k);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = k + i < K ? reinterpret_cast<const uint16_t*>(row)[k + i] : 0;
+__device__ __forceinline__ uint4 load8(const TA* row, int64_t k) {
+  if constexpr (sizeof(TA) == 2) {
+    return *reinterpret_cast<const uint4*>(row + k);
+  } else if constexpr (__is_same(W, bf16)) {
+    const float4 x = *reinterpret_cast<const float4*>(row + k);
+    const float4 y = *reinterpret_cast<const float4*>(row + k + 4);
+    return make_uint4(pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w), pack_bf16x2(y.x, y.y),
+                      pack_bf16x2(y.z, y.w));
   } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = k + i < K ? to_bits<W>(to_f32(row[k + i])) : 0;
+    const float4 x = *reinterpret_cast<const float4*>(row + k);
+    const float4 y = *reinterpret_cast<const float4*>(row + k + 4);
+    return make_uint4(pack2(to_bits<W>(x.x), to_bits<W>(x.y)), pack2(to_bits<W>(x.z), to_bits<W>(x.w)),
+                      pack2(to_bits<W>(y.x), to_bits<W>(y.y)), pack2(to_bits<W>(y.z), to_bits<W>(y.w)));
   }
-  uint4 r;
-  r.x = v[0] | (static_cast<uint32_t>(v[1]) << 16);
-  r.y = v[2] | (static_cast<uint32_t>(v[3]) << 16);
-  r.z = v[4] | (static_cast<uint32_t>(v[5]) << 16);
-  r.w = v[6] | (static_cast<uint32_t>(v[7]) << 16);
-  return r;
 }
 
 template <typename W>
@@ -79,138 +92,285 @@ __device__ __forceinline__ f32x4 mfma16<f16>(const u16x8& a, const u16x8& b, f32
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-template <typename TA, typename W, typename TO>
-__global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmParams p) {
-  __shared__ __align__(16) uint16_t As[kBM][kBK + kPad];
-  __shared__ __align__(16) uint16_t Bs[kBN][kBK + kPad];
+// Renumbers workgroup `i` of `count` so that each XCD (the hardware deals
+// workgroups round-robin over 8 XCDs) receives a contiguous range of logical
+// tile ids.
+__device__ __forceinline__ int64_t xcd_tile(int64_t i, int64_t count) {
+  constexpr int kXcd = 8;
+  const int64_t per = count / kXcd, rem = count % kXcd;
+  const int64_t x = i % kXcd;
+  return x * per + (x < rem ? x : rem) + i / kXcd;
+}
+
+// Stores one 16x16 MFMA accumulator (lane holds rows 4*(lane/16)+e of column
+// lane%16) plus bias.
+template <typename TO>
+__device__ __forceinline__ void store_tile(const GemmParams& p, const f32x4& acc, int64_t m_base,
+                                           int64_t n, float bv, int lane) {
+  if (n >= p.N) return;
+  TO* out = static_cast<TO*>(p.out);
+  const int64_t m0 = m_base + (lane >> 4) * 4;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t m = m0 + e;
+    if (m < p.M) out[m * p.N + n] = from_f32<TO>(acc[e] + bv);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit weights, large M
+// ---------------------------------------------------------------------------
+
+template <typename TA, typename W, typename TO, int BM, int BN>
+__global__ void __launch_bounds__(256) tile_kernel(const GemmParams p) {
+  constexpr int TM = BM / 32;              // 16-row MFMA tiles per wave
+  constexpr int TN = BN / 32;              // 16-col MFMA tiles per wave
+  constexpr int AE = BM * kBK / 256;       // A elements each thread stages per slice
+  constexpr int BE = BN * kBK / 256;
+  static_assert(AE % 8 == 0 && BE % 8 == 0, "stage in 8-element chunks");
+  __shared__ __align__(16) uint16_t As[2][BM][kBK + kPad];
+  __shared__ __align__(16) uint16_t Bs[2][BN][kBK + kPad];
+
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kBM;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kBN;
-  const int wm = (wave >> 1) * 32;
-  const int wn = (wave & 1) * 32;
+  const int64_t tiles_n = (p.N + BN - 1) / BN;
+  const int64_t tiles = tiles_n * ((p.M + BM - 1) / BM);
+  const int64_t tile = xcd_tile(blockIdx.x, tiles);
+  const int64_t m0 = (tile / tiles_n) * BM;
+  const int64_t n0 = (tile % tiles_n) * BN;
+  const int wm = (wave >> 1) * (BM / 2);
+  const int wn = (wave & 1) * (BN / 2);
   const TA* A = static_cast<const TA*>(p.a);
   const W* Wt = static_cast<const W*>(p.w);
 
+  // Staging assignment: thread -> (row, 8-element chunks along k).
+  const int a_row = tid / (kBK / AE);
+  const int a_k = (tid % (kBK / AE)) * AE;
+  const int b_row = tid / (kBK / BE);
+  const int b_k = (tid % (kBK / BE)) * BE;
+  const bool a_ok = m0 + a_row < p.M;
+  const bool b_ok = n0 + b_row < p.N;
+  const TA* a_src = A + (a_ok ? (m0 + a_row) * p.lda : 0);
+  const W* b_src = Wt + (b_ok ? (n0 + b_row) * p.K : 0);
+
+  uint4 ra[AE / 8], rb[BE / 8];
+  auto fetch = [&](int64_t k0) {
+#pragma unroll
+    for (int c = 0; c < AE / 8; ++c) {
+      const int64_t k = k0 + a_k + 8 * c;
+      ra[c] = (a_ok && k < p.K) ? load8<TA, W>(a_src, k) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int c = 0; c < BE / 8; ++c) {
+      const int64_t k = k0 + b_k + 8 * c;
+      rb[c] = (b_ok && k < p.K) ? load8<W, W>(b_src, k) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int c = 0; c < AE / 8; ++c) *reinterpret_cast<uint4*>(&As[buf][a_row][a_k + 8 * c]) = ra[c];
+#pragma unroll
+    for (int c = 0; c < BE / 8; ++c) *reinterpret_cast<uint4*>(&Bs[buf][b_row][b_k + 8 * c]) = rb[c];
+  };
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int64_t slices = (p.K + kBK - 1) / kBK;
+  fetch(0);
+  stage(0);
+  __syncthreads();
+  const int r16 = lane & 15;
+  const int kq = (lane >> 4) * 8;
+  for (int64_t s = 0; s < slices; ++s) {
+    const int cur = static_cast<int>(s & 1);
+    if (s + 1 < slices) fetch((s + 1) * kBK);
+    u16x8 a[TM], b[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      a[i] = *reinterpret_cast<const u16x8*>(&As[cur][wm + i * 16 + r16][kq]);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      b[j] = *reinterpret_cast<const u16x8*>(&Bs[cur][wn + j * 16 + r16][kq]);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = mfma16<W>(a[i], b[j], acc[i][j]);
+    if (s + 1 < slices) stage(cur ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t n = n0 + wn + j * 16 + r16;
+    const float bv = (p.bias && n < p.N) ? load_any_f(p.bias, p.bias_dtype, n) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) store_tile<TO>(p, acc[i][j], m0 + wm + i * 16, n, bv, lane);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit weights, M <= 64 (decode)
+// ---------------------------------------------------------------------------
+
+template <typename TA, typename W, typename TO, int MT>
+__global__ void __launch_bounds__(256) skinny_kernel(const GemmParams p) {
+  __shared__ f32x4 part[4][MT][kWave];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
+  const int r16 = lane & 15;
+  const int kq = (lane >> 4) * 8;
+  const TA* A = static_cast<const TA*>(p.a);
+  const W* Wt = static_cast<const W*>(p.w);
+  const bool n_ok = n0 + r16 < p.N;
+  const W* wrow = Wt + (n_ok ? (n0 + r16) * p.K : 0);
+  const TA* arow[MT];
+  bool m_ok[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int64_t m = i * 16 + r16;
+    m_ok[i] = m < p.M;
+    arow[i] = A + (m_ok[i] ? m * p.lda : 0);
+  }
+  f32x4 acc[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // Wave w takes k-slices w, w+4, ...; two slices per trip keep two loads in flight.
+  for (int64_t k0 = static_cast<int64_t>(wave) * kBK; k0 < p.K; k0 += 8 * kBK) {
+    // K is a multiple of 8, so an 8-element chunk is either wholly inside or past K.
+    const int64_t k1 = k0 + 4 * kBK;
+    const bool in0 = k0 + kq < p.K;
+    const bool in1 = k1 + kq < p.K;
+    const uint4 b0 = (n_ok && in0) ? load8<W, W>(wrow, k0 + kq) : make_uint4(0, 0, 0, 0);
+    const uint4 b1 = (n_ok && in1) ? load8<W, W>(wrow, k1 + kq) : make_uint4(0, 0, 0, 0);
+    uint4 a0[MT], a1[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      a0[i] = (m_ok[i] && in0) ? load8<TA, W>(arow[i], k0 + kq) : make_uint4(0, 0, 0, 0);
+      a1[i] = (m_ok[i] && in1) ? load8<TA, W>(arow[i], k1 + kq) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      acc[i] = mfma16<W>(__builtin_bit_cast(u16x8, a0[i]), __builtin_bit_cast(u16x8, b0), acc[i]);
+      acc[i] = mfma16<W>(__builtin_bit_cast(u16x8, a1[i]), __builtin_bit_cast(u16x8, b1), acc[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < MT; ++i) part[wave][i][lane] = acc[i];
+  __syncthreads();
+  if (wave != 0) return;
+  const int64_t n = n0 + r16;
+  const float bv = (p.bias && n < p.N) ? load_any_f(p.bias, p.bias_dtype, n) : 0.0f;
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const f32x4 s = ((part[0][i][lane] + part[1][i][lane]) + part[2][i][lane]) + part[3][i][lane];
+    store_tile<TO>(p, s, i * 16, n, bv, lane);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 weights (fp32 MFMA, K steps of 4 per instruction)
+// ---------------------------------------------------------------------------
+
+// 64x64 workgroup tile, 2x2 waves of 32x32; 16-element k-slices in LDS.
+template <typename TO>
+__global__ void __launch_bounds__(256) f32_tile_kernel(const GemmParams p) {
+  constexpr int BM = 64, BN = 64, BKF = 16;
+  __shared__ float As[BKF][BM + 4];
+  __shared__ float Bs[BKF][BN + 4];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int64_t tiles_n = (p.N + BN - 1) / BN;
+  const int64_t tiles = tiles_n * ((p.M + BM - 1) / BM);
+  const int64_t tile = xcd_tile(blockIdx.x, tiles);
+  const int64_t m0 = (tile / tiles_n) * BM;
+  const int64_t n0 = (tile % tiles_n) * BN;
+  const int wm = (wave >> 1) * 32;
+  const int wn = (wave & 1) * 32;
+  const float* A = static_cast<const float*>(p.a);
+  const float* Wt = static_cast<const float*>(p.w);
   f32x4 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  const int lrow = tid >> 2;        // 0..63
-  const int lk = (tid & 3) * 8;     // 0,8,16,24
-  for (int64_t k0 = 0; k0 < p.K; k0 += kBK) {
-    {
-      const int64_t m = m0 + lrow;
-      uint4 va = make_uint4(0, 0, 0, 0);
-      if (m < p.M) va = load_a8<TA, W>(A + m * p.lda, k0 + lk, p.K);
-      *reinterpret_cast<uint4*>(&As[lrow][lk]) = va;
-      const int64_t n = n0 + lrow;
-      uint4 vb = make_uint4(0, 0, 0, 0);
-      if (n < p.N) vb = load_a8<W, W>(Wt + n * p.K, k0 + lk, p.K);
-      *reinterpret_cast<uint4*>(&Bs[lrow][lk]) = vb;
+  const int row = tid >> 2;        // 0..63
+  const int kc = (tid & 3) * 4;    // 0,4,8,12
+  const int r16 = lane & 15;
+  const int k4 = lane >> 4;
+  for (int64_t k0 = 0; k0 < p.K; k0 += BKF) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t k = k0 + kc + e;
+      const int64_t m = m0 + row, n = n0 + row;
+      As[kc + e][row] = (m < p.M && k < p.K) ? A[m * p.lda + k] : 0.0f;
+      Bs[kc + e][row] = (n < p.N && k < p.K) ? Wt[n * p.K + k] : 0.0f;
     }
     __syncthreads();
-    const int r16 = lane & 15;
-    const int kq = (lane >> 4) * 8;
-    u16x8 a[2], b[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      a[i] = *reinterpret_cast<const u16x8*>(&As[wm + i * 16 + r16][kq]);
+    for (int kk = 0; kk < BKF; kk += 4) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      b[j] = *reinterpret_cast<const u16x8*>(&Bs[wn + j * 16 + r16][kq]);
+      for (int i = 0; i < 2; ++i) {
+        const float av = As[kk + k4][wm + i * 16 + r16];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = mfma16<W>(a[i], b[j], acc[i][j]);
-    __syncthreads();
-  }
-
-  TO* out = static_cast<TO*>(p.out);
-  const int col16 = lane & 15;
-  const int row4 = (lane >> 4) * 4;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int64_t n = n0 + wn + j * 16 + col16;
-    if (n >= p.N) continue;
-    const float bv = p.bias ? load_any_f(p.bias, p.bias_dtype, n) : 0.0f;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t m = m0 + wm + i * 16 + row4 + e;
-        if (m < p.M) out[m * p.N + n] = from_f32<TO>(acc[i][j][e] + bv);
+        for (int j = 0; j < 2; ++j) {
+          const float bv = Bs[kk + k4][wn + j * 16 + r16];
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[i][j], 0, 0, 0);
+        }
       }
     }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t n = n0 + wn + j * 16 + r16;
+    const float bv = (p.bias && n < p.N) ? load_any_f(p.bias, p.bias_dtype, n) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) store_tile<TO>(p, acc[i][j], m0 + wm + i * 16, n, bv, lane);
   }
 }
 
-template <typename TO>
-__global__ void __launch_bounds__(256) gemm_f32_kernel(const GemmParams p) {
-  __shared__ float As[kBK][kBM + 4];
-  __shared__ float Bs[kBK][kBN + 4];
-  const int tid = threadIdx.x;
-  const int tx = tid & 15;
-  const int ty = tid >> 4;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kBM;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kBN;
-  const float* A = static_cast<const float*>(p.a);
-  const float* Wt = static_cast<const float*>(p.w);
-  float acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
-  for (int64_t k0 = 0; k0 < p.K; k0 += kBK) {
-    for (int idx = tid; idx < kBM * kBK; idx += 256) {
-      const int r = idx / kBK;
-      const int k = idx % kBK;
-      const int64_t m = m0 + r, n = n0 + r, kk = k0 + k;
-      As[k][r] = (m < p.M && kk < p.K) ? A[m * p.lda + kk] : 0.0f;
-      Bs[k][r] = (n < p.N && kk < p.K) ? Wt[n * p.K + kk] : 0.0f;
-    }
-    __syncthreads();
-#pragma unroll 8
-    for (int k = 0; k < kBK; ++k) {
-      float av[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = As[k][ty + 16 * i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = Bs[k][tx + 16 * j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * bv[j];
-    }
-    __syncthreads();
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+template <typename TA, typename W, typename TO>
+hipError_t launch_typed(const GemmParams& p, hipStream_t s) {
+  if (p.M <= kSkinnyM) {
+    const dim3 grid(static_cast<unsigned>((p.N + 15) / 16));
+    const int mt = static_cast<int>((p.M + 15) / 16);
+    if (mt <= 1)
+      hipLaunchKernelGGL((skinny_kernel<TA, W, TO, 1>), grid, dim3(256), 0, s, p);
+    else if (mt == 2)
+      hipLaunchKernelGGL((skinny_kernel<TA, W, TO, 2>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((skinny_kernel<TA, W, TO, 4>), grid, dim3(256), 0, s, p);
+    return launch_status("linear");
   }
-  TO* out = static_cast<TO*>(p.out);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t n = n0 + tx + 16 * j;
-    if (n >= p.N) continue;
-    const float bv = p.bias ? load_any_f(p.bias, p.bias_dtype, n) : 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t m = m0 + ty + 16 * i;
-      if (m < p.M) out[m * p.N + n] = from_f32<TO>(acc[i][j] + bv);
-    }
+  const int64_t big = ((p.M + 127) / 128) * ((p.N + 127) / 128);
+  if (big >= 256) {
+    hipLaunchKernelGGL((tile_kernel<TA, W, TO, 128, 128>), dim3(static_cast<unsigned>(big)),
+                       dim3(256), 0, s, p);
+  } else {
+    const int64_t small = ((p.M + 63) / 64) * ((p.N + 127) / 128);
+    hipLaunchKernelGGL((tile_kernel<TA, W, TO, 64, 128>), dim3(static_cast<unsigned>(small)),
+                       dim3(256), 0, s, p);
   }
+  return launch_status("linear");
 }
 
 template <typename TA, typename W>
-hipError_t launch_mfma_out(const GemmParams& p, int out_dtype, dim3 grid, hipStream_t s) {
-  if (out_dtype == RLM_F32) {
-    hipLaunchKernelGGL((gemm_mfma_kernel<TA, W, float>), grid, dim3(256), 0, s, p);
-  } else if (out_dtype == RLM_BF16) {
-    hipLaunchKernelGGL((gemm_mfma_kernel<TA, W, bf16>), grid, dim3(256), 0, s, p);
-  } else {
-    hipLaunchKernelGGL((gemm_mfma_kernel<TA, W, f16>), grid, dim3(256), 0, s, p);
-  }
-  return launch_status("linear");
+hipError_t launch_out(const GemmParams& p, int out_dtype, hipStream_t s) {
+  if (out_dtype == RLM_F32) return launch_typed<TA, W, float>(p, s);
+  if (out_dtype == RLM_BF16) return launch_typed<TA, W, bf16>(p, s);
+  return launch_typed<TA, W, f16>(p, s);
 }
 
 hipError_t linear_impl(const rlm_tensor* input, const rlm_tensor* weight, const rlm_tensor* bias,
@@ -241,18 +401,17 @@ hipError_t linear_impl(const rlm_tensor* input, const rlm_tensor* weight, const 
   p.bias_dtype = bias ? bias->dtype : RLM_F32;
   p.out = out->data;
   if (M == 0 || N == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>((N + kBN - 1) / kBN),
-                  static_cast<unsigned>((M + kBM - 1) / kBM));
-  RLM_REQUIRE(grid.y <= 0x7fffffffu && grid.x <= 0x7fffffffu, "%s: problem too large", what);
+  RLM_REQUIRE(((M + 63) / 64) * ((N + 63) / 64) <= 0x7fffffff, "%s: problem too large", what);
   if (weight->dtype == RLM_F32) {
     RLM_REQUIRE(input->dtype == RLM_F32, "%s: fp32 weights need fp32 input (got %s)", what,
                 dtype_name(input->dtype));
+    const dim3 grid(static_cast<unsigned>(((M + 63) / 64) * ((N + 63) / 64)));
     if (out->dtype == RLM_F32)
-      hipLaunchKernelGGL((gemm_f32_kernel<float>), grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((f32_tile_kernel<float>), grid, dim3(256), 0, stream, p);
     else if (out->dtype == RLM_BF16)
-      hipLaunchKernelGGL((gemm_f32_kernel<bf16>), grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((f32_tile_kernel<bf16>), grid, dim3(256), 0, stream, p);
     else
-      hipLaunchKernelGGL((gemm_f32_kernel<f16>), grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((f32_tile_kernel<f16>), grid, dim3(256), 0, stream, p);
     return launch_status(what);
   }
   RLM_REQUIRE(K % 8 == 0 && p.lda % 8 == 0,
@@ -264,11 +423,11 @@ hipError_t linear_impl(const rlm_tensor* input, const rlm_tensor* weight, const 
   RLM_REQUIRE(input->dtype == weight->dtype || input->dtype == RLM_F32,
               "%s: input must be fp32 or share the weight dtype", what);
   if (weight->dtype == RLM_BF16) {
-    if (input->dtype == RLM_F32) return launch_mfma_out<float, bf16>(p, out->dtype, grid, stream);
-    return launch_mfma_out<bf16, bf16>(p, out->dtype, grid, stream);
+    if (input->dtype == RLM_F32) return launch_out<float, bf16>(p, out->dtype, stream);
+    return launch_out<bf16, bf16>(p, out->dtype, stream);
   }
-  if (input->dtype == RLM_F32) return launch_mfma_out<float, f16>(p, out->dtype, grid, stream);
-  return launch_mfma_out<f16, f16>(p, out->dtype, grid, stream);
+  if (input->dtype == RLM_F32) return launch_out<float, f16>(p, out->dtype, stream);
+  return launch_out<f16, f16>(p, out->dtype, stream);
 }
 
 }  // namespace

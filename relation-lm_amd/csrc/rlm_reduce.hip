@@ -4,11 +4,19 @@
 //
 // Reference semantics: src/relation_lm/kernels/relation_reduce.py:72-450.
 //
-// hidden_kernel: a workgroup owns 64 consecutive (query, partner) rows of the
-//   flattened [Q*K] row space and 64 hidden columns.  The gathered product
-//   rows a*p (fp32, rounded as the reference does) and the W_m tile are staged
-//   in LDS r-major, 64 r at a time; each thread accumulates a 4x4 fp32 block.
-//   Out-of-range indices read zero rows instead of faulting.
+// Relation hidden, hidden[row, n] = GELU(W_m[n] . (op[a] * op[p]) + X[a,n] + X[p,H+n])
+// for every (query, partner) row, is a GEMM whose A operand is gathered.  A
+// workgroup owns 64 rows x BN hidden columns.  It gathers the operand rows of
+// its rows' anchors and partners, forms the products in fp32 and stages them
+// in LDS together with the W_m tile; the matrix cores do the product term and
+// the epilogue adds the gathered expanded-cache halves and applies erf-GELU.
+//   * 16-bit bf16 caches: a bf16 x bf16 product is exact in fp32 and splits
+//     exactly into hi = bf16(x) and lo = x - hi (lo has at most 8 significant
+//     bits), so two v_mfma_f32_16x16x32_bf16 passes (hi and lo against the
+//     bf16 W_m) give exact products with fp32 accumulation: the numerics of the
+//     reference's fp32 "ieee" dot, at bf16 matrix-core rate.
+//   * fp32 (and fp16) caches: fp32 products, v_mfma_f32_16x16x4f32.
+// Out-of-range indices read zero rows instead of faulting.
 // norm_reduce_kernel: one wavefront per query; each lane owns D/64 columns,
 //   LayerNorm moments are wave64 reductions, the K softmax weights live in
 //   lanes 0..K-1 and are broadcast by shuffles.
@@ -17,9 +25,15 @@
 namespace rlm {
 namespace {
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+
 constexpr int kRows = 64;   // (query, partner) rows per workgroup
-constexpr int kCols = 64;   // hidden columns per workgroup
-constexpr int kRC = 64;     // relation-dim chunk staged in LDS
+constexpr int kRC16 = 128;  // relation-dim chunk staged in LDS, 16-bit path
+constexpr int kRC32 = 64;   // relation-dim chunk staged in LDS, fp32 path
+constexpr int kPad16 = 8;   // 16-bit elements of row padding (conflict-free b128 reads)
+constexpr int kPad32 = 4;
 
 struct HiddenParams {
   int64_t B, Tq, T;   // batch, queries per row, cache rows
@@ -39,152 +53,370 @@ struct HiddenParams {
   int pos_dtype;
   void* expanded_out;     // same buffer as expanded (mutated)
   float* out;             // [rows, H]
+  // Byte sizes of the buffers addressed through range-checked descriptors.
+  uint32_t expanded_bytes, operand_bytes, wm_bytes, out_bytes;
 };
 
-__device__ __forceinline__ float gelu_erf(float x) {
-  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
-}
 
-// Fresh expanded value of row `t` (relation_reduce.py:215-236): half 0 is the
-// anchor half W_a op[t] + b1, half 1 the partner half W_p op[t].  The cache
-// write and every use of row t evaluate this same function, so the stored row
-// is the rounding of exactly the fp32 value the hidden uses.
+// Per-row bookkeeping of a workgroup's 64 (query, partner) rows, in LDS.
+// Offsets are byte offsets into the caches; kNoOffset marks an index outside
+// [0, T) (the row then gathers zeros) or a padding row past the end.
+struct RowTable {
+  int32_t b[kRows];      // batch row
+  int32_t a[kRows];      // anchor index (-1 if out of range)
+  int32_t p[kRows];      // partner index (-1 if out of range)
+  uint32_t op_a[kRows];  // operand row of the anchor (kNoOffset unless both indices are valid)
+  uint32_t op_p[kRows];  // operand row of the partner (same validity)
+  uint32_t x_a[kRows];   // anchor half of the anchor's expanded row
+  uint32_t x_p[kRows];   // partner half of the partner's expanded row
+};
+
 template <typename T>
-__device__ __forceinline__ float fresh_value(const HiddenParams& p, int half, int64_t b,
-                                             int64_t t, int n) {
-  const T* w = static_cast<const T*>(half == 0 ? p.wa : p.wp) + static_cast<int64_t>(n) * p.R;
-  const T* op = static_cast<const T*>(p.operand) + (b * p.T + t) * p.R;
-  float acc = 0.0f;
-  for (int r = 0; r < p.R; ++r) acc += to_f32(w[r]) * to_f32(op[r]);
-  if (half == 0) acc += to_f32(static_cast<const T*>(p.b1)[n]);
-  return acc;
-}
-
-template <typename T, bool UPDATE>
-__global__ void __launch_bounds__(256) hidden_kernel(const HiddenParams p) {
-  __shared__ float prodT[kRC][kRows];     // prodT[r][row]
-  __shared__ float wT[kRC][kCols + 4];    // wT[r][col]
-  __shared__ int64_t row_b[kRows], row_a[kRows], row_p[kRows];
-
+__device__ __forceinline__ void load_rows(const HiddenParams& p, int64_t r0, RowTable& rt) {
   const int tid = threadIdx.x;
-  const int tx = tid & 15;   // column group
-  const int ty = tid >> 4;   // row group
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kRows;
-  const int n0 = blockIdx.x * kCols;
-  const int64_t QK = p.Tq * p.K;
-
   if (tid < kRows) {
     const int64_t row = r0 + tid;
-    int64_t b = 0, a = -1, pp = -1;
+    int32_t b = 0, a = -1, pp = -1;
     if (row < p.rows) {
       const int64_t q = row / p.K;
-      b = q / p.Tq;
-      a = load_any_i(p.anchor, p.index_dtype_a, q);
-      pp = load_any_i(p.partner, p.index_dtype_p, row);
+      b = static_cast<int32_t>(q / p.Tq);
+      const int64_t ai = load_any_i(p.anchor, p.index_dtype_a, q);
+      const int64_t pi = load_any_i(p.partner, p.index_dtype_p, row);
+      a = (ai >= 0 && ai < p.T) ? static_cast<int32_t>(ai) : -1;
+      pp = (pi >= 0 && pi < p.T) ? static_cast<int32_t>(pi) : -1;
     }
-    row_b[tid] = b;
-    row_a[tid] = a;
-    row_p[tid] = pp;
+    const uint32_t base = static_cast<uint32_t>(b) * static_cast<uint32_t>(p.T);
+    const bool ok = a >= 0 && pp >= 0;
+    constexpr uint32_t es = sizeof(T);
+    rt.b[tid] = b;
+    rt.a[tid] = a;
+    rt.p[tid] = pp;
+    rt.op_a[tid] = ok ? (base + a) * p.R * es : kNoOffset;
+    rt.op_p[tid] = ok ? (base + pp) * p.R * es : kNoOffset;
+    rt.x_a[tid] = a >= 0 ? (base + a) * (2 * p.H) * es : kNoOffset;
+    rt.x_p[tid] = pp >= 0 ? ((base + pp) * (2 * p.H) + p.H) * es : kNoOffset;
   }
+}
 
-  int64_t t = -1;
-  if (UPDATE) {
-    t = load_any_i(p.pos, p.pos_dtype, 0);
-    if (t < 0 || t >= p.T) t = -1;  // out-of-range position: nothing to write or reuse
-    // The tile holding row (b, k=0) writes batch b's fresh row for its columns.
-    if (t >= 0) {
-      const int64_t b_lo = (r0 + QK - 1) / QK;
-      int64_t b_hi = (r0 + kRows - 1) / QK;
-      if (b_hi > p.B - 1) b_hi = p.B - 1;
-      const int64_t items = (b_hi - b_lo + 1) * 2 * kCols;
-      for (int64_t idx = tid; idx < items; idx += 256) {
-        const int c = static_cast<int>(idx % kCols);
-        const int half = static_cast<int>((idx / kCols) % 2);
-        const int64_t b = b_lo + idx / (2 * kCols);
-        const int n = n0 + c;
-        if (n >= p.H) continue;
-        T* dst = static_cast<T*>(p.expanded_out) + (b * p.T + t) * (2 * static_cast<int64_t>(p.H)) +
-                 static_cast<int64_t>(half) * p.H + n;
-        *dst = from_f32<T>(fresh_value<T>(p, half, b, t, n));
+// Update form (relation_reduce.py:215-251): the fresh expanded row t of every
+// batch row the tile touches, for the tile's columns: half 0 = W_a op[t] + b1,
+// half 1 = W_p op[t], fp32.  Eight lanes share one dot (16-byte loads, three
+// shuffle steps).  The tile holding row (b, k=0) then stores batch b's row.
+// fresh[(bi * 2 + half) * cols + c] for bi = b - b_first.
+template <typename T>
+__device__ void fresh_rows(const HiddenParams& p, int64_t t, int64_t b_first, int nb, int n0,
+                           int cols, float* fresh) {
+  const int tid = threadIdx.x;
+  const int j = tid & 7;
+  const int group = tid >> 3;
+  const int groups = blockDim.x >> 3;
+  const int items = nb * 2 * cols;
+  const int chunks = p.R / 8;
+  for (int base = 0; base < items; base += groups) {
+    const int item = base + group;
+    const bool live = item < items;
+    const int c = live ? item % cols : 0;
+    const int half = live ? (item / cols) % 2 : 0;
+    const int bi = live ? item / (2 * cols) : 0;
+    const int n = n0 + c;
+    float acc = 0.0f;
+    if (live && n < p.H) {
+      const T* w = static_cast<const T*>(half == 0 ? p.wa : p.wp) + static_cast<int64_t>(n) * p.R;
+      const T* op = static_cast<const T*>(p.operand) + ((b_first + bi) * p.T + t) * p.R;
+      for (int ch = j; ch < chunks; ch += 8) {
+        const float4 w0 = load4(w + 8 * ch), w1 = load4(w + 8 * ch + 4);
+        const float4 o0 = load4(op + 8 * ch), o1 = load4(op + 8 * ch + 4);
+        acc += w0.x * o0.x + w0.y * o0.y + w0.z * o0.z + w0.w * o0.w;
+        acc += w1.x * o1.x + w1.y * o1.y + w1.z * o1.z + w1.w * o1.w;
       }
+    }
+    acc += __shfl_xor(acc, 1, 8);
+    acc += __shfl_xor(acc, 2, 8);
+    acc += __shfl_xor(acc, 4, 8);
+    if (live && j == 0) {
+      if (half == 0 && n < p.H) acc += to_f32(static_cast<const T*>(p.b1)[n]);
+      fresh[item] = acc;
     }
   }
   __syncthreads();
+  const int64_t QK = p.Tq * p.K;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kRows;
+  const int64_t b_lo = (r0 + QK - 1) / QK;
+  int64_t b_hi = (r0 + kRows - 1) / QK;
+  if (b_hi > p.B - 1) b_hi = p.B - 1;
+  for (int item = tid; item < items; item += blockDim.x) {
+    const int c = item % cols;
+    const int half = (item / cols) % 2;
+    const int64_t b = b_first + item / (2 * cols);
+    const int n = n0 + c;
+    if (b < b_lo || b > b_hi || n >= p.H) continue;
+    T* dst = static_cast<T*>(p.expanded_out) + (b * p.T + t) * (2 * static_cast<int64_t>(p.H)) +
+             static_cast<int64_t>(half) * p.H + n;
+    *dst = from_f32<T>(fresh[item]);
+  }
+}
 
-  float acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+// Largest number of batch rows one 64-row tile can touch in the update form.
+__host__ __device__ constexpr int fresh_batches() { return kRows; }
 
-  const T* operand = static_cast<const T*>(p.operand);
-  const T* wm = static_cast<const T*>(p.wm);
-  for (int rc = 0; rc < p.R; rc += kRC) {
-    __syncthreads();
-    // product rows: prodT[r][row] = fp32(op[a][r] * op[p][r])
-    for (int idx = tid; idx < kRows * kRC; idx += 256) {
-      const int row = idx / kRC;
-      const int r = idx % kRC;
-      float v = 0.0f;
-      const int64_t a = row_a[row], pp = row_p[row], b = row_b[row];
-      if (rc + r < p.R && a >= 0 && a < p.T && pp >= 0 && pp < p.T) {
-        const float oa = to_f32(operand[(b * p.T + a) * p.R + rc + r]);
-        const float op = to_f32(operand[(b * p.T + pp) * p.R + rc + r]);
-        v = op * oa;
+// Anchor + partner halves of the expanded cache for the lane's accumulator
+// elements (rows 4*(lane/16)+e of column n), gathered before the matrix-core
+// work so their latency overlaps it.  Row t of the update form is taken from
+// `fresh` instead of the cache row this launch rewrites.
+template <typename T, bool UPDATE>
+__device__ __forceinline__ void gather_bases(const HiddenParams& p, rsrc_t xr, const RowTable& rt,
+                                             int mrow, int n, int c, int64_t t, int64_t b_first,
+                                             const float* fresh, int cols, int lane,
+                                             float (&xs)[4]) {
+  const uint32_t col = (n < p.H ? static_cast<uint32_t>(n) : 0u) * sizeof(T);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int m = mrow + (lane >> 4) * 4 + e;
+    const uint32_t oa = n < p.H ? rt.x_a[m] : kNoOffset;
+    const uint32_t op = n < p.H ? rt.x_p[m] : kNoOffset;
+    float xa = buf_load_elem<T>(xr, oa + col);
+    float xp = buf_load_elem<T>(xr, op + col);
+    if (UPDATE && t >= 0 && n < p.H) {
+      if (rt.a[m] == t) xa = fresh[((rt.b[m] - b_first) * 2 + 0) * cols + c];
+      if (rt.p[m] == t) xp = fresh[((rt.b[m] - b_first) * 2 + 1) * cols + c];
+    }
+    xs[e] = xa + xp;
+  }
+}
+
+// GELU(acc + bases) for the lane's four rows of column n; rows past the end
+// fall outside the output descriptor and are dropped.
+__device__ __forceinline__ void store_hidden(const HiddenParams& p, rsrc_t outr, const f32x4& acc,
+                                             const float (&xs)[4], int64_t r0, int mrow, int n,
+                                             int lane) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t grow = static_cast<uint32_t>(r0 + mrow + (lane >> 4) * 4 + e);
+    const uint32_t off = n < p.H ? (grow * static_cast<uint32_t>(p.H) + n) * 4u : kNoOffset;
+    buf_store_f32(gelu_erf(acc[e] + xs[e]), outr, off);
+  }
+}
+
+// Update-form set-up shared by both kernels: position, the batch range of the
+// tile and the fresh rows (computed, and stored to the cache by the owning tile).
+template <typename T, bool UPDATE>
+__device__ __forceinline__ int64_t update_setup(const HiddenParams& p, int64_t r0, int n0,
+                                                int cols, int64_t& b_first, float* fresh) {
+  b_first = 0;
+  if (!UPDATE) return -1;
+  int64_t t = load_any_i(p.pos, p.pos_dtype, 0);
+  if (t < 0 || t >= p.T) t = -1;  // out-of-range position: nothing to write or reuse
+  const int64_t QK = p.Tq * p.K;
+  b_first = r0 / QK;
+  int64_t b_last = (r0 + kRows - 1) / QK;
+  if (b_last > p.B - 1) b_last = p.B - 1;
+  if (t >= 0) fresh_rows<T>(p, t, b_first, static_cast<int>(b_last - b_first + 1), n0, cols, fresh);
+  return t;
+}
+
+// bf16 caches: exact hi/lo split products on bf16 MFMA.  BN hidden columns
+// per workgroup (64 or 128); waves in 2x2, each 32 rows x BN/2 columns.
+template <bool UPDATE, int BN>
+__global__ void __launch_bounds__(256) hidden_bf16_kernel(const HiddenParams p) {
+  constexpr int TN = BN / 32;
+  constexpr int LD = kRC16 + kPad16;
+  constexpr int kAChunks = kRows * (kRC16 / 8) / 256;   // product chunks staged per thread
+  constexpr int kWChunks = BN * (kRC16 / 8) / 256;      // W_m chunks staged per thread
+  __shared__ __align__(16) uint16_t a_hi[kRows][LD];
+  __shared__ __align__(16) uint16_t a_lo[kRows][LD];
+  __shared__ __align__(16) uint16_t w_t[BN][LD];
+  __shared__ RowTable rt;
+  __shared__ float fresh[UPDATE ? fresh_batches() * 2 * BN : 1];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kRows;
+  const int n0 = blockIdx.x * BN;
+  const rsrc_t xr = make_rsrc(p.expanded, p.expanded_bytes);
+  const rsrc_t opr = make_rsrc(p.operand, p.operand_bytes);
+  const rsrc_t wr_ = make_rsrc(p.wm, p.wm_bytes);
+  const rsrc_t outr = make_rsrc(p.out, p.out_bytes);
+  load_rows<bf16>(p, r0, rt);
+  int64_t b_first;
+  const int64_t t = update_setup<bf16, UPDATE>(p, r0, n0, BN, b_first, fresh);
+  __syncthreads();
+
+  const int wr = (wave >> 1) * 32;
+  const int wc = (wave & 1) * (BN / 2);
+  const int r16 = lane & 15;
+  const int kq = (lane >> 4) * 8;
+  float xs[2][TN][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      gather_bases<bf16, UPDATE>(p, xr, rt, wr + i * 16, n0 + wc + j * 16 + r16,
+                                 wc + j * 16 + r16, t, b_first, fresh, BN, lane, xs[i][j]);
+
+  f32x4 acc[2][TN];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int rc = 0; rc < p.R; rc += kRC16) {
+    if (rc) __syncthreads();
+    // Gather first (every load in flight), then form and stage the products.
+    uint4 va[kAChunks], vp[kAChunks], vw[kWChunks];
+#pragma unroll
+    for (int c = 0; c < kAChunks; ++c) {
+      const int idx = tid + 256 * c;
+      const int row = idx / (kRC16 / 8);
+      const int r = rc + (idx % (kRC16 / 8)) * 8;
+      const bool in = r < p.R;
+      va[c] = buf_load_b128(opr, in ? rt.op_a[row] + 2u * r : kNoOffset);
+      vp[c] = buf_load_b128(opr, in ? rt.op_p[row] + 2u * r : kNoOffset);
+    }
+#pragma unroll
+    for (int c = 0; c < kWChunks; ++c) {
+      const int idx = tid + 256 * c;
+      const int n = n0 + idx / (kRC16 / 8);
+      const int r = rc + (idx % (kRC16 / 8)) * 8;
+      vw[c] = buf_load_b128(wr_, (n < p.H && r < p.R)
+                                      ? 2u * (static_cast<uint32_t>(n) * p.R + r)
+                                      : kNoOffset);
+    }
+#pragma unroll
+    for (int c = 0; c < kAChunks; ++c) {
+      const int idx = tid + 256 * c;
+      const int row = idx / (kRC16 / 8);
+      const int r = (idx % (kRC16 / 8)) * 8;
+      const uint32_t wa[4] = {va[c].x, va[c].y, va[c].z, va[c].w};
+      const uint32_t wp[4] = {vp[c].x, vp[c].y, vp[c].z, vp[c].w};
+      uint32_t h[4], l[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        // Exact fp32 products of the two bf16 pairs in this word.
+        const float x0 = __uint_as_float(wp[q] << 16) * __uint_as_float(wa[q] << 16);
+        const float x1 = __uint_as_float(wp[q] & 0xffff0000u) * __uint_as_float(wa[q] & 0xffff0000u);
+        h[q] = pack_bf16x2(x0, x1);
+        l[q] = pack_bf16x2(x0 - __uint_as_float(h[q] << 16), x1 - __uint_as_float(h[q] & 0xffff0000u));
       }
-      prodT[r][row] = v;
+      *reinterpret_cast<uint4*>(&a_hi[row][r]) = make_uint4(h[0], h[1], h[2], h[3]);
+      *reinterpret_cast<uint4*>(&a_lo[row][r]) = make_uint4(l[0], l[1], l[2], l[3]);
     }
-    // W_m tile: wT[r][col] = W_m[n0+col][rc+r]
-    for (int idx = tid; idx < kCols * kRC; idx += 256) {
-      const int col = idx / kRC;
-      const int r = idx % kRC;
-      const int n = n0 + col;
-      wT[r][col] = (n < p.H && rc + r < p.R) ? to_f32(wm[static_cast<int64_t>(n) * p.R + rc + r])
-                                             : 0.0f;
+#pragma unroll
+    for (int c = 0; c < kWChunks; ++c) {
+      const int idx = tid + 256 * c;
+      *reinterpret_cast<uint4*>(&w_t[idx / (kRC16 / 8)][(idx % (kRC16 / 8)) * 8]) = vw[c];
     }
     __syncthreads();
-    const int rlen = p.R - rc < kRC ? p.R - rc : kRC;
-    for (int r = 0; r < rlen; ++r) {
-      float av[4], wv[4];
+    const int rlen = p.R - rc < kRC16 ? p.R - rc : kRC16;
+    for (int kk = 0; kk < rlen; kk += 32) {
+      u16x8 ah[2], al[2], bw[TN];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = prodT[r][ty + 16 * i];
+      for (int i = 0; i < 2; ++i) {
+        ah[i] = *reinterpret_cast<const u16x8*>(&a_hi[wr + i * 16 + r16][kk + kq]);
+        al[i] = *reinterpret_cast<const u16x8*>(&a_lo[wr + i * 16 + r16][kk + kq]);
+      }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) wv[j] = wT[r][tx + 16 * j];
+      for (int j = 0; j < TN; ++j)
+        bw[j] = *reinterpret_cast<const u16x8*>(&w_t[wc + j * 16 + r16][kk + kq]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * wv[j];
+        for (int j = 0; j < TN; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8, ah[i]), __builtin_bit_cast(bf16x8, bw[j]), acc[i][j], 0,
+              0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8, al[i]), __builtin_bit_cast(bf16x8, bw[j]), acc[i][j], 0,
+              0, 0);
+        }
     }
   }
-  const T* expanded = static_cast<const T*>(p.expanded);
-  const int64_t xrow = 2 * static_cast<int64_t>(p.H);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = ty + 16 * i;
-    const int64_t grow = r0 + row;
-    if (grow >= p.rows) continue;
-    const int64_t b = row_b[row], a = row_a[row], pp = row_p[row];
-    const bool a_ok = a >= 0 && a < p.T;
-    const bool p_ok = pp >= 0 && pp < p.T;
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = tx + 16 * j;
-      const int n = n0 + col;
-      if (n >= p.H) continue;
-      // Row t is being rewritten by this launch: never read it, recompute it.
-      float xa, xp;
-      if (UPDATE && t >= 0 && a == t)
-        xa = fresh_value<T>(p, 0, b, t, n);
-      else
-        xa = a_ok ? to_f32(expanded[(b * p.T + a) * xrow + n]) : 0.0f;
-      if (UPDATE && t >= 0 && pp == t)
-        xp = fresh_value<T>(p, 1, b, t, n);
-      else
-        xp = p_ok ? to_f32(expanded[(b * p.T + pp) * xrow + p.H + n]) : 0.0f;
-      const float h = acc[i][j] + (xa + xp);
-      p.out[grow * p.H + n] = gelu_erf(h);
+    for (int j = 0; j < TN; ++j)
+      store_hidden(p, outr, acc[i][j], xs[i][j], r0, wr + i * 16, n0 + wc + j * 16 + r16, lane);
+}
+
+// fp32 / fp16 caches: fp32 products on v_mfma_f32_16x16x4f32.  64 hidden
+// columns per workgroup; waves in 2x2, each 32 x 32.
+template <typename T, bool UPDATE>
+__global__ void __launch_bounds__(256) hidden_f32_kernel(const HiddenParams p) {
+  constexpr int BN = 64;
+  constexpr int LD = kRC32 + kPad32;
+  constexpr uint32_t es = sizeof(T);
+  __shared__ float a_s[kRows][LD];
+  __shared__ float w_s[BN][LD];
+  __shared__ RowTable rt;
+  __shared__ float fresh[UPDATE ? fresh_batches() * 2 * BN : 1];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kRows;
+  const int n0 = blockIdx.x * BN;
+  const rsrc_t xr = make_rsrc(p.expanded, p.expanded_bytes);
+  const rsrc_t opr = make_rsrc(p.operand, p.operand_bytes);
+  const rsrc_t wr_ = make_rsrc(p.wm, p.wm_bytes);
+  const rsrc_t outr = make_rsrc(p.out, p.out_bytes);
+  load_rows<T>(p, r0, rt);
+  int64_t b_first;
+  const int64_t t = update_setup<T, UPDATE>(p, r0, n0, BN, b_first, fresh);
+  __syncthreads();
+
+  const int wr = (wave >> 1) * 32;
+  const int wc = (wave & 1) * 32;
+  const int r16 = lane & 15;
+  const int k4 = lane >> 4;
+  float xs[2][2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      gather_bases<T, UPDATE>(p, xr, rt, wr + i * 16, n0 + wc + j * 16 + r16, wc + j * 16 + r16,
+                              t, b_first, fresh, BN, lane, xs[i][j]);
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int rc = 0; rc < p.R; rc += kRC32) {
+    if (rc) __syncthreads();
+    for (int idx = tid; idx < kRows * kRC32; idx += 256) {
+      const int row = idx / kRC32;
+      const int r = rc + idx % kRC32;
+      const bool in = r < p.R;
+      const float oa = buf_load_elem<T>(opr, in ? rt.op_a[row] + es * r : kNoOffset);
+      const float op = buf_load_elem<T>(opr, in ? rt.op_p[row] + es * r : kNoOffset);
+      a_s[row][idx % kRC32] = op * oa;
+    }
+    for (int idx = tid; idx < BN * kRC32; idx += 256) {
+      const int n = n0 + idx / kRC32;
+      const int r = rc + idx % kRC32;
+      w_s[idx / kRC32][idx % kRC32] = buf_load_elem<T>(
+          wr_, (n < p.H && r < p.R) ? es * (static_cast<uint32_t>(n) * p.R + r) : kNoOffset);
+    }
+    __syncthreads();
+    const int rlen = p.R - rc < kRC32 ? p.R - rc : kRC32;
+    for (int kk = 0; kk < rlen; kk += 4) {
+      float av[2], bv[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) av[i] = a_s[wr + i * 16 + r16][kk + k4];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bv[j] = w_s[wc + j * 16 + r16][kk + k4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
   }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      store_hidden(p, outr, acc[i][j], xs[i][j], r0, wr + i * 16, n0 + wc + j * 16 + r16, lane);
 }
 
 struct NormParams {
@@ -202,6 +434,119 @@ struct NormParams {
   float* out;           // [Q,D]
 };
 
+// Softmax weight of partner `lane` (lanes 0..K-1; K <= 64) for the query at
+// position t: k_limit = clamp(ceil(log2(t + 2)), 1, K) == clamp(bit_length(t + 1), 1, K),
+// active = rank < k_limit and score > -1e30, p = softmax(where(active, s, -1e4)) * active,
+// renormalised by max(sum, 1e-9) (relation_reduce.py:399-411).
+__device__ __forceinline__ float partner_weight(const NormParams& p, int64_t q, int64_t t,
+                                                int lane) {
+  const int64_t n = t + 1;
+  int k_limit = n > 0 ? 64 - __clzll(static_cast<unsigned long long>(n)) : 0;
+  k_limit = k_limit < 1 ? 1 : (k_limit > p.K ? p.K : k_limit);
+  const float s = lane < p.K ? p.scores[q * p.K + lane] : -INFINITY;
+  const bool active = lane < p.K && lane < k_limit && s > -1.0e30f;
+  const float safe = active ? s : -1.0e4f;
+  const float m = wave_max_f32(lane < p.K ? safe : -INFINITY);
+  const float prob = active ? expf(safe - m) : 0.0f;
+  const float total = wave_sum_f32(prob);
+  return prob / fmaxf(total, 1.0e-9f);
+}
+
+// Four consecutive raw elements as floats.
+__device__ __forceinline__ float4 load_raw4(const float* p) {
+  return *reinterpret_cast<const float4*>(p);
+}
+__device__ __forceinline__ float4 load_raw4(const bf16* p) { return load4(p); }
+__device__ __forceinline__ float4 load_raw4(const f16* p) {
+  const uint2 raw = *reinterpret_cast<const uint2*>(p);
+  const f16* h = reinterpret_cast<const f16*>(&raw);
+  return make_float4(static_cast<float>(h[0]), static_cast<float>(h[1]),
+                     static_cast<float>(h[2]), static_cast<float>(h[3]));
+}
+
+// D % 4 == 0: lane owns column groups g = lane + 64*i (columns 4g..4g+3), so
+// every raw row is read with 16-byte (fp32) or 8-byte (16-bit) coalesced
+// loads.  KB partner rows are loaded before any of them is reduced, which puts
+// the whole query's traffic in flight at once.
+template <typename TR, int G, int KB>
+__global__ void __launch_bounds__(256) norm_reduce_vec_kernel(const NormParams p) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (q >= p.Q) return;
+  const int64_t b = q / p.Tq;
+  const int64_t tq = q - b * p.Tq;
+  const int64_t t = load_any_i(p.pos, p.pos_dtype, b * p.pos_sb + tq * p.pos_sq);
+  const float prob = partner_weight(p, q, t, lane);
+  const int groups = p.D >> 2;
+  const TR* raw = static_cast<const TR*>(p.raw) + q * p.K * static_cast<int64_t>(p.D);
+
+  float4 gam[G], bet[G], ctx[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int g = lane + kWave * i;
+    float4 w4 = make_float4(0.f, 0.f, 0.f, 0.f), b4 = w4;
+    if (g < groups) {
+      w4 = make_float4(load_any_f(p.w, p.w_dtype, 4 * g), load_any_f(p.w, p.w_dtype, 4 * g + 1),
+                       load_any_f(p.w, p.w_dtype, 4 * g + 2), load_any_f(p.w, p.w_dtype, 4 * g + 3));
+      b4 = make_float4(load_any_f(p.bias, p.b_dtype, 4 * g),
+                       load_any_f(p.bias, p.b_dtype, 4 * g + 1),
+                       load_any_f(p.bias, p.b_dtype, 4 * g + 2),
+                       load_any_f(p.bias, p.b_dtype, 4 * g + 3));
+    }
+    gam[i] = w4;
+    bet[i] = b4;
+    ctx[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const float inv_d = 1.0f / static_cast<float>(p.D);
+  for (int k0 = 0; k0 < p.K; k0 += KB) {
+    float4 x[KB][G];
+#pragma unroll
+    for (int kk = 0; kk < KB; ++kk)
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const int g = lane + kWave * i;
+        x[kk][i] = (k0 + kk < p.K && g < groups)
+                       ? load_raw4(raw + static_cast<int64_t>(k0 + kk) * p.D + 4 * g)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+    for (int kk = 0; kk < KB; ++kk) {
+      if (k0 + kk >= p.K) break;
+      const float pk = __shfl(prob, k0 + kk, kWave);
+      if (pk == 0.0f) continue;  // wave-uniform: inactive rows contribute exactly 0
+      float sum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < G; ++i) sum += (x[kk][i].x + x[kk][i].y) + (x[kk][i].z + x[kk][i].w);
+      const float mean = wave_sum_f32(sum) * inv_d;
+      float sq = 0.0f;
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const bool in = lane + kWave * i < groups;
+        float4& v = x[kk][i];
+        v.x = in ? v.x - mean : 0.0f;
+        v.y = in ? v.y - mean : 0.0f;
+        v.z = in ? v.z - mean : 0.0f;
+        v.w = in ? v.w - mean : 0.0f;
+        sq += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+      }
+      const float inv_std = rsqrtf(wave_sum_f32(sq) * inv_d + p.eps);
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        ctx[i].x += (x[kk][i].x * inv_std * gam[i].x + bet[i].x) * pk;
+        ctx[i].y += (x[kk][i].y * inv_std * gam[i].y + bet[i].y) * pk;
+        ctx[i].z += (x[kk][i].z * inv_std * gam[i].z + bet[i].z) * pk;
+        ctx[i].w += (x[kk][i].w * inv_std * gam[i].w + bet[i].w) * pk;
+      }
+    }
+  }
+  float* out = p.out + q * static_cast<int64_t>(p.D);
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int g = lane + kWave * i;
+    if (g < groups) *reinterpret_cast<float4*>(out + 4 * g) = ctx[i];
+  }
+}
+
 template <typename TR, int VPL>
 __global__ void __launch_bounds__(256) norm_reduce_kernel(const NormParams p) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -210,19 +555,7 @@ __global__ void __launch_bounds__(256) norm_reduce_kernel(const NormParams p) {
   const int64_t b = q / p.Tq;
   const int64_t tq = q - b * p.Tq;
   const int64_t t = load_any_i(p.pos, p.pos_dtype, b * p.pos_sb + tq * p.pos_sq);
-  // k_limit = clamp(ceil(log2(t + 2)), 1, K) == clamp(bit_length(t + 1), 1, K)
-  const int64_t n = t + 1;
-  int k_limit = n > 0 ? 64 - __clzll(static_cast<unsigned long long>(n)) : 0;
-  k_limit = k_limit < 1 ? 1 : (k_limit > p.K ? p.K : k_limit);
-
-  // Softmax weights: lane k holds partner k (K <= 64).
-  const float s = lane < p.K ? p.scores[q * p.K + lane] : -INFINITY;
-  const bool active = lane < p.K && lane < k_limit && s > -1.0e30f;
-  const float safe = active ? s : -1.0e4f;
-  const float m = wave_max_f32(lane < p.K ? safe : -INFINITY);
-  float prob = active ? expf(safe - m) : 0.0f;
-  const float total = wave_sum_f32(prob);
-  prob = prob / fmaxf(total, 1.0e-9f);
+  const float prob = partner_weight(p, q, t, lane);
 
   float gam[VPL], bet[VPL], ctx[VPL];
 #pragma unroll
@@ -273,19 +606,33 @@ __global__ void __launch_bounds__(256) norm_reduce_kernel(const NormParams p) {
 
 hipError_t launch_hidden(HiddenParams& p, int dtype, bool update, hipStream_t stream) {
   if (p.rows == 0 || p.H == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>((p.H + kCols - 1) / kCols),
-                  static_cast<unsigned>((p.rows + kRows - 1) / kRows));
-  RLM_REQUIRE(grid.y <= 65535u * 1024u, "too many relation rows");
-#define RLM_HIDDEN_CASE(ID, T)                                                           \
-  if (dtype == ID) {                                                                     \
-    if (update)                                                                          \
-      hipLaunchKernelGGL((hidden_kernel<T, true>), grid, dim3(256), 0, stream, p);       \
-    else                                                                                 \
-      hipLaunchKernelGGL((hidden_kernel<T, false>), grid, dim3(256), 0, stream, p);      \
-    return launch_status("relation_hidden");                                             \
+  const unsigned row_tiles = static_cast<unsigned>((p.rows + kRows - 1) / kRows);
+  RLM_REQUIRE(row_tiles <= 65535u * 1024u, "too many relation rows");
+  if (dtype == RLM_BF16) {
+    // 128-column tiles when there are enough rows to fill the chip, else 64
+    // (always 64 in the update form, whose fresh rows live in LDS too).
+    if (update) {
+      const dim3 grid(static_cast<unsigned>((p.H + 63) / 64), row_tiles);
+      hipLaunchKernelGGL((hidden_bf16_kernel<true, 64>), grid, dim3(256), 0, stream, p);
+    } else if (p.rows >= 4096) {
+      const dim3 grid(static_cast<unsigned>((p.H + 127) / 128), row_tiles);
+      hipLaunchKernelGGL((hidden_bf16_kernel<false, 128>), grid, dim3(256), 0, stream, p);
+    } else {
+      const dim3 grid(static_cast<unsigned>((p.H + 63) / 64), row_tiles);
+      hipLaunchKernelGGL((hidden_bf16_kernel<false, 64>), grid, dim3(256), 0, stream, p);
+    }
+    return launch_status("relation_hidden");
+  }
+  const dim3 grid(static_cast<unsigned>((p.H + 63) / 64), row_tiles);
+#define RLM_HIDDEN_CASE(ID, T)                                                             \
+  if (dtype == ID) {                                                                       \
+    if (update)                                                                            \
+      hipLaunchKernelGGL((hidden_f32_kernel<T, true>), grid, dim3(256), 0, stream, p);     \
+    else                                                                                   \
+      hipLaunchKernelGGL((hidden_f32_kernel<T, false>), grid, dim3(256), 0, stream, p);    \
+    return launch_status("relation_hidden");                                               \
   }
   RLM_HIDDEN_CASE(RLM_F32, float)
-  RLM_HIDDEN_CASE(RLM_BF16, bf16)
   RLM_HIDDEN_CASE(RLM_F16, f16)
 #undef RLM_HIDDEN_CASE
   set_error("relation_hidden: unsupported dtype %s", dtype_name(dtype));
@@ -320,8 +667,17 @@ hipError_t hidden_impl(bool seq, const rlm_tensor* expanded_cache,
   const int64_t Tq = seq ? anchor_index->shape[1] : 1;
   if (seq) RLM_TRY(check_dim(partner_index, "partner_index", 1, Tq));
   const int64_t K = partner_index->shape[qd];
-  RLM_REQUIRE(R >= 1 && R <= 4096 && H <= (1 << 20) && K <= 4096,
-              "relation dim, hidden dim or partner count out of range");
+  RLM_REQUIRE(R >= 8 && R <= 4096 && R % 8 == 0 && H <= (1 << 20) && K <= 4096,
+              "relation dim must be a multiple of 8 in [8, 4096]; hidden dim and partner count "
+              "out of range otherwise");
+  const int64_t es = operand_cache->dtype == RLM_F32 ? 4 : 2;
+  constexpr int64_t kMaxBytes = int64_t(1) << 31;
+  RLM_REQUIRE(B * T * 2 * H * es < kMaxBytes && B * T * R * es < kMaxBytes &&
+                  H * R * es < kMaxBytes,
+              "expanded_cache, operand_cache and product_weight must each be smaller than 2 GiB");
+  RLM_REQUIRE((reinterpret_cast<uintptr_t>(operand_cache->data) & 15u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(product_weight->data) & 15u) == 0,
+              "operand_cache and product_weight must be 16-byte aligned");
   RLM_TRY(check_tensor(out, "out", qd + 2));
   RLM_TRY(check_dtype_is(out, "out", RLM_F32));
   RLM_TRY(check_dim(out, "out", 0, B));
@@ -344,7 +700,31 @@ hipError_t hidden_impl(bool seq, const rlm_tensor* expanded_cache,
   p.index_dtype_p = partner_index->dtype;
   p.wm = product_weight->data;
   p.out = static_cast<float*>(out->data);
+  RLM_REQUIRE(p.rows * H * 4 + 64 * H * 4 < kMaxBytes,
+              "relation hidden output must be smaller than 2 GiB");
+  p.expanded_bytes = static_cast<uint32_t>(B * T * 2 * H * es);
+  p.operand_bytes = static_cast<uint32_t>(B * T * R * es);
+  p.wm_bytes = static_cast<uint32_t>(H * R * es);
+  p.out_bytes = static_cast<uint32_t>(p.rows * H * 4);
   return hipSuccess;
+}
+
+template <int G, int KB>
+hipError_t launch_norm_vec(const NormParams& p, int dtype, hipStream_t stream) {
+  const int waves = 4;
+  const dim3 grid(static_cast<unsigned>((p.Q + waves - 1) / waves));
+#define RLM_NORM_CASE(ID, T)                                                                   \
+  if (dtype == ID) {                                                                           \
+    hipLaunchKernelGGL((norm_reduce_vec_kernel<T, G, KB>), grid, dim3(waves * kWave), 0, stream, \
+                       p);                                                                     \
+    return launch_status("relation_norm_reduce");                                             \
+  }
+  RLM_NORM_CASE(RLM_F32, float)
+  RLM_NORM_CASE(RLM_BF16, bf16)
+  RLM_NORM_CASE(RLM_F16, f16)
+#undef RLM_NORM_CASE
+  set_error("relation_norm_reduce: unsupported raw dtype %s", dtype_name(dtype));
+  return hipErrorInvalidValue;
 }
 
 template <int VPL>
@@ -430,6 +810,14 @@ hipError_t norm_impl(bool seq, const rlm_tensor* raw, const rlm_tensor* partner_
   p.eps = static_cast<float>(norm_eps);
   p.out = static_cast<float*>(out->data);
   if (p.Q == 0) return hipSuccess;
+  if (D % 4 == 0 && (reinterpret_cast<uintptr_t>(raw->data) & 15u) == 0) {
+    const int groups = static_cast<int>((D / 4 + kWave - 1) / kWave);
+    if (groups <= 1) return launch_norm_vec<1, 8>(p, raw->dtype, stream);
+    if (groups <= 2) return launch_norm_vec<2, 8>(p, raw->dtype, stream);
+    if (groups <= 3) return launch_norm_vec<3, 8>(p, raw->dtype, stream);
+    if (groups <= 4) return launch_norm_vec<4, 8>(p, raw->dtype, stream);
+    return launch_norm_vec<8, 2>(p, raw->dtype, stream);
+  }
   const int vpl = static_cast<int>((D + kWave - 1) / kWave);
   if (vpl <= 2) return launch_norm_vpl<2>(p, raw->dtype, stream);
   if (vpl <= 4) return launch_norm_vpl<4>(p, raw->dtype, stream);

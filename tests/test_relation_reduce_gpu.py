@@ -161,6 +161,25 @@ def test_norm_reduce_non_power_of_two_budget(device, batch, k_out, position):
     assert rel_err(host(actual), expected) <= FP32_REL
 
 
+@pytest.mark.parametrize("width", [7, 100, 256, 512, 1000, 2048])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_norm_reduce_widths(device, width, dtype):
+    """Vector (width % 4 == 0) and scalar column layouts, fp32 and bf16 raw rows, K=12."""
+    g = torch.Generator().manual_seed(9000 + width)
+    raw = torch.randn(5, 12, width, generator=g).to(dtype)
+    scores = torch.randn(5, 12, generator=g)
+    scores[1, 3:] = -torch.inf
+    norm_weight = torch.randn(width, generator=g) * 0.05 + 1.0
+    norm_bias = torch.randn(width, generator=g) * 0.01
+    pos = torch.tensor(300, device=device)
+    actual = relation_norm_reduce(raw.to(device), scores.to(device), norm_weight.to(device),
+                                  norm_bias.to(device), pos, 1e-5)
+    torch.cuda.synchronize()
+    expected = ored.relation_norm_reduce(raw.float().numpy(), scores.numpy(), norm_weight.numpy(),
+                                         norm_bias.numpy(), 300, 1e-5)
+    assert rel_err(host(actual), expected) <= FP32_REL
+
+
 def test_hidden_guards_out_of_range_indices(device):
     """Sentinel partner indices (t-LOCAL+1 < 0) read zero rows, never out of bounds."""
     cfg = CONFIGS["cfg1"]
@@ -199,6 +218,9 @@ def test_bf16_decode_reduce(device, batch):
     exp_hidden = ored.relation_hidden_cached(host(expanded), host(operand), host(anchor),
                                              host(partner), host(red["product_weight"]))
     assert abs_err(host(hidden), exp_hidden) <= BF16_ABS
+    # Exact bf16 products (hi/lo split on the matrix cores) with fp32 accumulation:
+    # the hidden agrees with the float64 oracle to fp32 precision, not just bf16's.
+    assert rel_err(host(hidden), exp_hidden) <= FP32_REL
     mutable = expanded.clone()
     mutable[:, 511] = 0
     updated = relation_hidden_cache_update(mutable, operand, anchor, partner,
@@ -211,6 +233,7 @@ def test_bf16_decode_reduce(device, batch):
         host(red["partner_weight"]), host(red["product_weight"]),
         host(red["expanded_bias"][:2304]), 511, cache_dtype="bfloat16")
     assert abs_err(host(updated), exp_updated) <= BF16_ABS
+    assert rel_err(host(updated), exp_updated) <= FP32_REL
     assert abs_err(host(mutable), exp_cache) <= BF16_ABS
     raw = relation_linear(hidden, red["second_weight"], red["second_bias"],
                           out_dtype=torch.float32)
@@ -259,6 +282,7 @@ def test_sequence_chain_cfg2(device):
                                                  ea[rows][:, :96], ep[rows][:, :96],
                                                  host(red["product_weight"]))
     assert abs_err(host(hidden)[rows][:, :96], exp_hidden) <= BF16_ABS
+    assert rel_err(host(hidden)[rows][:, :96], exp_hidden) <= FP32_REL
     exp_raw = ored.linear(host(hidden)[rows][:, :96], host(red["second_weight"]),
                           host(red["second_bias"]))
     assert abs_err(host(raw)[rows][:, :96], exp_raw) <= BF16_ABS
@@ -291,7 +315,9 @@ def test_packed_projection_matches_separate_linears(device, dtype, batch):
     assert tuple(projection.project_dict(memory)) == projection.names
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 512, 576), (8, 4608, 128), (100, 72, 40), (4096, 1024, 128)])
+@pytest.mark.parametrize("m,n,k", [(1, 512, 576), (8, 4608, 128), (100, 72, 40), (4096, 1024, 128),
+                                   (8, 576, 2304), (64, 576, 2304), (65, 200, 96), (8, 24, 40),
+                                   (33, 130, 72), (1000, 300, 520)])
 def test_linear_shapes(device, m, n, k):
     g = torch.Generator().manual_seed(m * 7 + n)
     x = torch.randn(m, k, generator=g)
@@ -344,3 +370,33 @@ def test_graph_replay_matches_eager(device):
         other = step()  # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(other, eager)
+
+
+@pytest.mark.parametrize("m", [8, 300])
+def test_linear_row_strided_input(device, m):
+    """A cache column (cache[:, t], row stride T*R) goes in without a copy."""
+    g = torch.Generator().manual_seed(4242 + m)
+    cache = torch.randn(m, 6, 128, generator=g).bfloat16()
+    w = (torch.randn(256, 128, generator=g) * 128 ** -0.5).bfloat16()
+    bias = torch.randn(256, generator=g) * 0.1
+    column = cache.to(device)[:, 3]
+    assert not column.is_contiguous()
+    got = relation_linear(column, w.to(device), bias.to(device), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    expected = ored.linear(cache[:, 3].float().numpy(), w.float().numpy(), bias.numpy())
+    assert rel_err(host(got), expected) <= FP32_REL
+
+
+def test_linear_second_linear_shape(device):
+    """cfg2's second linear: fp32 hidden x bf16 weight -> fp32, checked on a row sample."""
+    g = torch.Generator().manual_seed(777)
+    hidden = torch.randn(32768, 512, generator=g)
+    w = (torch.randn(512, 512, generator=g) * 512 ** -0.5).bfloat16()
+    bias = (torch.randn(512, generator=g) * 0.01).bfloat16()
+    got = relation_linear(hidden.to(device), w.to(device), bias.to(device),
+                          out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    rows = torch.randperm(32768, generator=g)[:512].sort().values
+    x16 = hidden[rows].bfloat16().float().numpy()
+    expected = ored.linear(x16, w.float().numpy(), bias.float().numpy())
+    assert rel_err(host(got)[rows.numpy()], expected) <= FP32_REL
