@@ -86,7 +86,8 @@ def block_scores(router_query, block_mean, block_std, gamma, bias, batch_of, t, 
     Per head h (relation_select.py:70-96):
         s_h = (sum_d mean*q_h + softplus(gamma_h) * sum_d std*|q_h|) * HD^-0.5
               + bias[h, bucket]
-    combined in head order by pairwise log-sum-exp (:97-103), masked (:104-106).
+    combined by log-sum-exp over heads (:97-103, see logsumexp_heads), masked
+    (:104-106).
     """
     blocks, heads, head_dim = block_mean.shape[1], block_mean.shape[2], block_mean.shape[3]
     rel_buckets = bias.shape[1]
@@ -102,14 +103,34 @@ def block_scores(router_query, block_mean, block_std, gamma, bias, batch_of, t, 
     bias64 = _f64(bias)
     per_head = (content + sp[None, None, :] * uncertainty) * head_scale
     per_head = per_head + np.transpose(bias64[:, bucket], (1, 2, 0))
-    acc = per_head[..., 0]
-    for h in range(1, heads):
-        s = per_head[..., h]
-        mx = np.maximum(acc, s)
-        acc = mx + np.log(np.exp(acc - mx) + np.exp(s - mx))
+    acc = logsumexp_heads(per_head)
     out = acc.astype(np.float32)
     out[~eligible] = NEG_INF32
     return out
+
+
+def logsumexp_heads(per_head: np.ndarray) -> np.ndarray:
+    """log(sum_h exp(s_h)) over the last axis in float64, as m + log(sum_h exp(s_h - m)).
+
+    The reference kernel folds the heads pairwise in head order
+    (relation_select.py:97-103: acc = m + log(exp(acc - m) + exp(s_h - m))); its
+    block router writes the same quantity as one logsumexp (block_router.py:99).
+    Both are the same real number; evaluated in float64 they agree to a few
+    float64 ulps (tests/test_oracle_select.py pins this), far below the one
+    rounding to float32 that every comparison sees.
+    """
+    mx = per_head.max(axis=-1, keepdims=True)
+    return mx[..., 0] + np.log(np.exp(per_head - mx).sum(axis=-1))
+
+
+def logsumexp_heads_pairwise(per_head: np.ndarray) -> np.ndarray:
+    """The reference kernel's pairwise fold in head order (relation_select.py:97-103)."""
+    acc = per_head[..., 0]
+    for h in range(1, per_head.shape[-1]):
+        s = per_head[..., h]
+        mx = np.maximum(acc, s)
+        acc = mx + np.log(np.exp(acc - mx) + np.exp(s - mx))
+    return acc
 
 
 def pick_blocks(scores: np.ndarray, top_blocks: int):

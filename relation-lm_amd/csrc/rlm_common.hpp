@@ -170,13 +170,68 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint64_t o = __shfl_xor(static_cast<unsigned long long>(v), off, kWave);
-    v = v > o ? v : o;
-  }
+// DPP lane exchanges within a row of 16 lanes (no LDS traffic):
+//   quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2),
+//   row_half_mirror (lane i <-> 7 - i within 8), row_mirror (i <-> 15 - i).
+// After the two quad steps every lane of a quad holds the same value, so the
+// mirrors pair each quad (or half row) with its neighbour, which is all a
+// commutative reduction needs.
+constexpr int kDppXor1 = 0xB1;
+constexpr int kDppXor2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint64_t lo = dpp_u32<CTRL>(static_cast<uint32_t>(u));
+  const uint64_t hi = dpp_u32<CTRL>(static_cast<uint32_t>(u >> 32));
+  return __builtin_bit_cast(double, lo | (hi << 32));
+}
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t u) {
+  const uint64_t lo = dpp_u32<CTRL>(static_cast<uint32_t>(u));
+  const uint64_t hi = dpp_u32<CTRL>(static_cast<uint32_t>(u >> 32));
+  return lo | (hi << 32);
+}
+
+// Sum over aligned groups of G consecutive lanes (G a power of two <= 64);
+// every lane of a group ends with the same bits.
+__device__ __forceinline__ double group_sum_f64(double v, int G) {
+  if (G >= 2) v += dpp_f64<kDppXor1>(v);
+  if (G >= 4) v += dpp_f64<kDppXor2>(v);
+  if (G >= 8) v += dpp_f64<kDppHalfMirror>(v);
+  if (G >= 16) v += dpp_f64<kDppMirror>(v);
+  if (G >= 32) v += __shfl_xor(v, 16, kWave);
+  if (G >= 64) v += __shfl_xor(v, 32, kWave);
   return v;
+}
+
+// Maximum over the wave, returned in every lane (rows reduced with DPP, the
+// four row maxima combined through readlane).
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  uint64_t o = dpp_u64<kDppXor1>(v);
+  v = v > o ? v : o;
+  o = dpp_u64<kDppXor2>(v);
+  v = v > o ? v : o;
+  o = dpp_u64<kDppHalfMirror>(v);
+  v = v > o ? v : o;
+  o = dpp_u64<kDppMirror>(v);
+  v = v > o ? v : o;
+  uint64_t best = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(v), 16 * r);
+    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(v >> 32), 16 * r);
+    const uint64_t x = static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+    best = x > best ? x : best;
+  }
+  return best;
 }
 
 __device__ __forceinline__ float wave_sum_f32(float v) {

@@ -4,18 +4,29 @@
 // Reference semantics: src/relation_lm/kernels/relation_select.py:9-308 (packed)
 // and src/relation_lm/kernels/triton_select.py:9-252 (two-op form).
 //
-// Mapping: one wavefront per query (batch row b, position t).  The serial
-// chain of the reference (block scoring -> picks -> exact scores -> argmax
-// passes) stays inside one wave, so every reduction is a 6-step wave64
-// shuffle and the only memory traffic is the query's own gathers.
+// Mapping.  A workgroup holds up to W queries of one batch row, one wavefront
+// per query (W = 8 consecutive positions for the sequence form, 1 for the
+// decode form).  The workgroup first stages, in one round of loads, what its
+// queries share: the block statistics of both streams and the union of their
+// local key windows (rows [t0-L+1, t0+W-1]).  Each wave then runs the
+// reference's chain for its query -- block scores, TOP block picks, exact
+// candidate scores, argmax -- with every reduction inside the wave.
+//
+// Exact scores: a key row is E elements = E/8 16-byte chunks (bf16), so a
+// group of G = E*sizeof/16 lanes scores one candidate row per instruction
+// (8 rows per wave instruction at E = 64 bf16): each lane holds its chunk of
+// the query in float64 registers, multiplies its chunk of the row and the
+// group reduces with a float64 butterfly.  Local-window rows come from LDS,
+// picked remote blocks from L2.
 //
 // Numerics: every dot product is accumulated in float64 from exact products
 // and rounded once to float32; block scores (softplus, per-head terms,
 // pairwise log-sum-exp) are evaluated in float64 and rounded once.  All
 // comparisons use those float32 values.  Ties: anchor -> lowest position,
 // blocks -> lowest block, partners -> lowest candidate lane (local window
-// first, then picked blocks in pick order).  Both are encoded in one 64-bit
-// key so a single wave max-reduction yields the winner.
+// first, then picked blocks in pick order).  Each rule is one 64-bit key
+// (order-preserving score bits above the complemented tie index), so one
+// wave max-reduction yields the winner.
 #include "rlm_common.hpp"
 
 namespace rlm {
@@ -60,245 +71,622 @@ struct SelectParams {
   float* out_anchor_score;
   int32_t* out_partner;
   float* out_partner_score;
-  int lds_per_wave;  // bytes
+  // launch geometry and LDS layout (bytes)
+  int W;            // queries (waves) per workgroup
+  int tiles;        // workgroups per batch row
+  int G;            // lanes per key row (E * sizeof / 16)
+  int H_log2;       // heads is a power of two
+  int BS_log2;      // block size is a power of two
+  int G_log2;
+  int WR;           // rows of each staged local-key window
+  int row_bytes;    // LDS bytes per staged key row (padded by 16)
+  int stage;        // statistics, bias tables and windows staged in LDS (W > 1)
+  int off_stats_a, off_stats_p, off_bias_a, off_bias_p, off_win_a, off_win_p;
+  int off_wave, wave_bytes, lds_total;
+  uint32_t key_bytes;  // byte size of each key cache (range of the buffer descriptors)
 };
 
-// LDS bytes one wave needs (layout mirrored in select_kernel).
-// The float64 head-score region is padded to an even count so the float4
-// query rows that follow it stay 16-byte aligned.
-inline int select_lds_bytes(int NB, int H, int E, int RD, int TOP, int CAP) {
-  const int bytes = 8 * ((NB * H + 1) & ~1) + 4 * (E + RD + NB + 2 * TOP + CAP);
+// Per-wave LDS region: f64 exact query [E] and router query [RD], then f32
+// block scores [NB], picks [TOP] and their validity [TOP], candidate scores [CAP].
+inline int wave_region_bytes(int E, int NB, int RD, int TOP, int CAP) {
+  const int bytes = 8 * (E + RD) + 4 * (NB + 2 * TOP + CAP);
   return (bytes + 15) & ~15;
 }
 
 template <typename TA>
-__device__ __forceinline__ float exact_score(const TA* row, const float* q, int E, double scale) {
-  double acc0 = 0.0, acc1 = 0.0;
-  for (int d = 0; d < E; d += 4) {
-    const float4 k = load4(row + d);
-    const float4 v = *reinterpret_cast<const float4*>(q + d);
-    acc0 += static_cast<double>(k.x) * static_cast<double>(v.x);
-    acc1 += static_cast<double>(k.y) * static_cast<double>(v.y);
-    acc0 += static_cast<double>(k.z) * static_cast<double>(v.z);
-    acc1 += static_cast<double>(k.w) * static_cast<double>(v.w);
+__device__ __forceinline__ void chunk_to_f64(const uint4& v, double* out);
+template <>
+__device__ __forceinline__ void chunk_to_f64<bf16>(const uint4& v, double* out) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = static_cast<double>(__uint_as_float(w[i] << 16));
+    out[2 * i + 1] = static_cast<double>(__uint_as_float(w[i] & 0xffff0000u));
   }
-  return static_cast<float>((acc0 + acc1) * scale);
+}
+template <>
+__device__ __forceinline__ void chunk_to_f64<f16>(const uint4& v, double* out) {
+  const f16* h = reinterpret_cast<const f16*>(&v);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = static_cast<double>(static_cast<float>(h[i]));
+}
+template <>
+__device__ __forceinline__ void chunk_to_f64<float>(const uint4& v, double* out) {
+  out[0] = static_cast<double>(__uint_as_float(v.x));
+  out[1] = static_cast<double>(__uint_as_float(v.y));
+  out[2] = static_cast<double>(__uint_as_float(v.z));
+  out[3] = static_cast<double>(__uint_as_float(v.w));
 }
 
-// Per-head terms then pairwise log-sum-exp in head order, masked by
-// eligibility (relation_select.py:53-106).  Writes blk[NB] (float32).
+// Elements of TA per 16-byte chunk.
+template <typename TA>
+constexpr int kEpc = 16 / static_cast<int>(sizeof(TA));
+
+// Group max over aligned groups of G lanes (G a power of two <= 64).
+__device__ __forceinline__ double group_max_f64(double v, int G) {
+  if (G >= 2) v = fmax(v, dpp_f64<kDppXor1>(v));
+  if (G >= 4) v = fmax(v, dpp_f64<kDppXor2>(v));
+  if (G >= 8) v = fmax(v, dpp_f64<kDppHalfMirror>(v));
+  if (G >= 16) v = fmax(v, dpp_f64<kDppMirror>(v));
+  if (G >= 32) v = fmax(v, __shfl_xor(v, 16, kWave));
+  if (G >= 64) v = fmax(v, __shfl_xor(v, 32, kWave));
+  return v;
+}
+
+struct WaveScratch {
+  double* qx;    // [E]
+  double* qr;    // [RD]
+  float* blk;    // [NB]
+  int* sel;      // [TOP]
+  int* selv;     // [TOP]
+  float* sc;     // [CAP]
+};
+
+struct Query {
+  int64_t b, q, t, local_start;
+  int64_t wbase;  // first position of the staged windows
+};
+
+// Block scores of one stream (relation_select.py:53-106) into ws.blk[NB]
+// (float32, -inf where not eligible).  Lane = (block j, head h) pair, heads of
+// a block in consecutive lanes:
+//   s_h = (sum_d mean*q_h + softplus(gamma_h) * sum_d std*|q_h|) * HD^-0.5 + bias[h, bucket]
+// then log-sum-exp over the block's H lanes, m + log(sum_h exp(s_h - m)), with
+// DPP group reductions.  All in float64, rounded once.  Statistics and bias
+// come from LDS when the workgroup staged them, else from L2.  `sp` is
+// softplus(gamma_h) for this lane's head h = lane mod H.
 template <typename TS>
-__device__ void block_scores(const SelectParams& p, const Stream& s, int64_t b, int64_t t,
-                             int64_t local_start, const float* qr, double* sh, float* blk,
+__device__ void block_scores(const SelectParams& p, const Stream& s, const float* stats,
+                             const float* bias_tab, double sp, const Query& qy, WaveScratch& ws,
                              int lane) {
   const int pairs = p.NB * p.H;
-  const TS* mean = static_cast<const TS*>(s.mean) + b * static_cast<int64_t>(pairs) * p.HD;
-  const TS* stdv = static_cast<const TS*>(s.stdev) + b * static_cast<int64_t>(pairs) * p.HD;
-  for (int pr = lane; pr < pairs; pr += kWave) {
-    const int j = pr / p.H;
-    const int h = pr - j * p.H;
-    const TS* mr = mean + static_cast<int64_t>(pr) * p.HD;
-    const TS* sr = stdv + static_cast<int64_t>(pr) * p.HD;
-    const float* qh = qr + h * p.HD;
+  const int RD = p.H * p.HD;
+  for (int base = 0; base < pairs; base += kWave) {
+    const int pr = base + lane;
+    const bool live = pr < pairs;
+    const int prc = live ? pr : 0;
+    const int j = prc >> p.H_log2;
+    const int h = prc & (p.H - 1);
+    const double* qh = ws.qr + h * p.HD;
     double c = 0.0, u = 0.0;
-    for (int d = 0; d < p.HD; d += 4) {
-      const float4 m = load4(mr + d);
-      const float4 sd = load4(sr + d);
-      const float4 v = *reinterpret_cast<const float4*>(qh + d);
-      c += static_cast<double>(m.x) * v.x;
-      c += static_cast<double>(m.y) * v.y;
-      c += static_cast<double>(m.z) * v.z;
-      c += static_cast<double>(m.w) * v.w;
-      u += static_cast<double>(sd.x) * fabsf(v.x);
-      u += static_cast<double>(sd.y) * fabsf(v.y);
-      u += static_cast<double>(sd.z) * fabsf(v.z);
-      u += static_cast<double>(sd.w) * fabsf(v.w);
+    if (stats != nullptr) {
+      const float* mr = stats + prc * p.HD;
+      const float* sr = stats + p.NB * RD + prc * p.HD;
+      for (int d = 0; d < p.HD; d += 4) {
+        const float4 m = *reinterpret_cast<const float4*>(mr + d);
+        const float4 sd = *reinterpret_cast<const float4*>(sr + d);
+        c += static_cast<double>(m.x) * qh[d] + static_cast<double>(m.y) * qh[d + 1] +
+             static_cast<double>(m.z) * qh[d + 2] + static_cast<double>(m.w) * qh[d + 3];
+        u += static_cast<double>(sd.x) * fabs(qh[d]) + static_cast<double>(sd.y) * fabs(qh[d + 1]) +
+             static_cast<double>(sd.z) * fabs(qh[d + 2]) + static_cast<double>(sd.w) * fabs(qh[d + 3]);
+      }
+    } else {
+      const TS* mr = static_cast<const TS*>(s.mean) + (qy.b * pairs + prc) * p.HD;
+      const TS* sr = static_cast<const TS*>(s.stdev) + (qy.b * pairs + prc) * p.HD;
+      for (int d = 0; d < p.HD; d += 4) {
+        const float4 m = load4(mr + d);
+        const float4 sd = load4(sr + d);
+        c += static_cast<double>(m.x) * qh[d] + static_cast<double>(m.y) * qh[d + 1] +
+             static_cast<double>(m.z) * qh[d + 2] + static_cast<double>(m.w) * qh[d + 3];
+        u += static_cast<double>(sd.x) * fabs(qh[d]) + static_cast<double>(sd.y) * fabs(qh[d + 1]) +
+             static_cast<double>(sd.z) * fabs(qh[d + 2]) + static_cast<double>(sd.w) * fabs(qh[d + 3]);
+      }
     }
-    const double g = load_any_f(s.gamma, s.gamma_dtype, h);
-    const int64_t end = static_cast<int64_t>(j + 1) * p.BS - 1;
-    const int64_t dist = (t > end ? t - end : 0) + 1;
-    int bucket = 63 - __clzll(static_cast<unsigned long long>(dist));
+    const int end = (j + 1) * p.BS - 1;
+    const int dist = (qy.t > end ? static_cast<int>(qy.t - end) : 0) + 1;
+    int bucket = 31 - __clz(dist);
     bucket = bucket < p.RB - 1 ? bucket : p.RB - 1;
-    const double bias = load_any_f(s.bias, s.bias_dtype, static_cast<int64_t>(h) * p.RB + bucket);
+    const double bias = bias_tab != nullptr ? bias_tab[h * p.RB + bucket]
+                                            : load_any_f(s.bias, s.bias_dtype, h * p.RB + bucket);
+    double sv;
     {
 #pragma clang fp contract(off)
-      const double sp = log(1.0 + exp(g));
-      const double uncertainty = sp * u;
-      const double content = c + uncertainty;
-      sh[pr] = content * p.head_scale + bias;
+      const double content = c + sp * u;
+      sv = live ? content * p.head_scale + bias : 0.0;
     }
-  }
-  wave_sync();
-  for (int j = lane; j < p.NB; j += kWave) {
-    double acc = sh[j * p.H];
-    for (int h = 1; h < p.H; ++h) {
-#pragma clang fp contract(off)
-      const double v = sh[j * p.H + h];
-      const double m = fmax(acc, v);
-      acc = m + log(exp(acc - m) + exp(v - m));
+    const double m = group_max_f64(sv, p.H);
+    const double sum = group_sum_f64(exp(sv - m), p.H);
+    if (live && h == 0) {
+      const double lse = m + log(sum);
+      const bool eligible = end <= qy.t && (!p.strict || end < qy.local_start);
+      ws.blk[j] = eligible ? static_cast<float>(lse) : -INFINITY;
     }
-    const int64_t end = static_cast<int64_t>(j + 1) * p.BS - 1;
-    const bool eligible = end <= t && (!p.strict || end < local_start);
-    blk[j] = eligible ? static_cast<float>(acc) : -INFINITY;
   }
   wave_sync();
 }
 
-// TOP sequential argmax picks, ties to the lowest block; a pick is valid iff
-// its value is > -1e30 (relation_select.py:229-242).
-__device__ void pick_blocks(const SelectParams& p, float* blk, int* sel, int* selv, int lane) {
-  for (int r = 0; r < p.TOP; ++r) {
-    uint64_t best = 0;
-    for (int j = lane; j < p.NB; j += kWave) {
-      const uint64_t k = select_key(blk[j], static_cast<uint32_t>(j));
-      best = k > best ? k : best;
-    }
-    const uint64_t win = wave_max_u64(best);
-    const int j = static_cast<int>(key_index(win));
-    if (lane == 0) {
-      sel[r] = j;
-      selv[r] = key_score(win) > -1.0e30f ? 1 : 0;
-    }
-    if ((j & (kWave - 1)) == lane) blk[j] = -INFINITY;
-    wave_sync();
+// The TOP picks of the reference's sequential argmax loop (ties to the lowest
+// block; a pick is valid iff its value is > -1e30, relation_select.py:229-242),
+// found by ranking: block j is pick number rank(j) = #{k : key_k > key_j}.
+// Picks past the last block repeat block 0 as invalid, as the reference's
+// argmax over an all -inf vector does.  NB <= 64: block scores are held one
+// per lane and broadcast with readlane; larger NB reads them from LDS.
+__device__ void pick_blocks(const SelectParams& p, WaveScratch& ws, int lane) {
+  for (int r = lane; r < p.TOP; r += kWave) {
+    ws.sel[r] = 0;
+    ws.selv[r] = 0;
   }
+  wave_sync();
+  if (p.NB <= kWave) {
+    const float mine = lane < p.NB ? ws.blk[lane] : -INFINITY;
+    const uint64_t kj = select_key(mine, static_cast<uint32_t>(lane));
+    int rank = 0;
+    for (int k = 0; k < p.NB; ++k) {
+      const float other = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), k));
+      rank += select_key(other, static_cast<uint32_t>(k)) > kj;
+    }
+    if (lane < p.NB && rank < p.TOP) {
+      ws.sel[rank] = lane;
+      ws.selv[rank] = mine > -1.0e30f ? 1 : 0;
+    }
+  } else {
+    for (int j = lane; j < p.NB; j += kWave) {
+      const uint64_t kj = select_key(ws.blk[j], static_cast<uint32_t>(j));
+      int rank = 0;
+      for (int k = 0; k < p.NB; ++k) rank += select_key(ws.blk[k], static_cast<uint32_t>(k)) > kj;
+      if (rank < p.TOP) {
+        ws.sel[rank] = j;
+        ws.selv[rank] = ws.blk[j] > -1.0e30f ? 1 : 0;
+      }
+    }
+  }
+  wave_sync();
 }
 
 // Candidate lane c: local window first, then TOP*BS remote lanes in pick order
 // (relation_select.py:244-283).
-__device__ __forceinline__ void candidate(const SelectParams& p, int c, int64_t t,
-                                          int64_t local_start, const int* sel, const int* selv,
-                                          int64_t& pos, bool& valid) {
+__device__ __forceinline__ void candidate(const SelectParams& p, int c, const Query& qy,
+                                          const WaveScratch& ws, int64_t& pos, bool& valid) {
   if (c < p.L) {
-    pos = t - p.L + 1 + c;
-    valid = pos >= 0 && pos <= t && pos < p.T;
+    pos = qy.t - p.L + 1 + c;
+    valid = pos >= 0 && pos <= qy.t && pos < p.T;
   } else {
-    const int r = (c - p.L) / p.BS;
-    const int o = c - p.L - r * p.BS;
-    pos = static_cast<int64_t>(sel[r]) * p.BS + o;
-    valid = selv[r] != 0 && pos <= t && pos < local_start && pos < p.T;
+    const int r = (c - p.L) >> p.BS_log2;
+    const int o = (c - p.L) & (p.BS - 1);
+    pos = static_cast<int64_t>(ws.sel[r]) * p.BS + o;
+    valid = ws.selv[r] != 0 && pos <= qy.t && pos < qy.local_start && pos < p.T;
+  }
+}
+
+// Exact scores of every candidate lane into ws.sc (float32; -inf when invalid
+// or equal to `exclude`).  One lane per candidate, NCL candidates per lane per
+// pass: each lane gathers its rows whole (16-byte loads, all in flight before
+// any is used) and accumulates the 64-element dot alone in float64 against
+// the query, which the wave reads from LDS by broadcast -- no cross-lane
+// reduction at all.  Local rows come from the staged LDS window when the
+// query's whole window lies inside it (a per-wave decision); other rows come
+// through range-checked buffer loads whose offset is pushed past the end for
+// invalid rows (they read zero and are masked to -inf).
+template <typename TA, int NCL>
+__device__ void candidate_scores(const SelectParams& p, const Stream& s, const unsigned char* win,
+                                 const Query& qy, int exclude, WaveScratch& ws, int lane) {
+  constexpr int EPC = kEpc<TA>;
+  const rsrc_t keys = make_rsrc(s.keys, p.key_bytes);
+  const uint32_t row0 = static_cast<uint32_t>(qy.b * p.T);
+  const uint32_t row_bytes = static_cast<uint32_t>(p.E) * sizeof(TA);
+  const int t = static_cast<int>(qy.t);
+  const int ls = static_cast<int>(qy.local_start);
+  const int T = static_cast<int>(p.T);
+  const bool lds = win != nullptr && t - p.L + 1 >= qy.wbase && t < qy.wbase + p.WR;
+  const int wb = static_cast<int>(qy.wbase);
+  const int chunks = p.G;  // 16-byte chunks per row
+  for (int c0 = 0; c0 < p.CAP; c0 += kWave * NCL) {
+    int pos[NCL];
+    bool ok[NCL], from_lds[NCL];
+#pragma unroll
+    for (int u = 0; u < NCL; ++u) {
+      const int c = c0 + lane + kWave * u;
+      bool v = c < p.CAP;
+      int ps;
+      if (c < p.L) {
+        ps = t - p.L + 1 + c;
+        v = v && ps >= 0 && ps <= t && ps < T;
+        from_lds[u] = lds;
+      } else {
+        const int r = v ? (c - p.L) >> p.BS_log2 : 0;
+        ps = ws.sel[r] * p.BS + ((c - p.L) & (p.BS - 1));
+        v = v && ws.selv[r] != 0 && ps <= t && ps < ls && ps < T;
+        from_lds[u] = false;
+      }
+      ok[u] = v && ps != exclude;
+      pos[u] = ps;
+    }
+    double acc[NCL];
+#pragma unroll
+    for (int u = 0; u < NCL; ++u) acc[u] = 0.0;
+    // Rows in groups of CG chunks: all loads of a group in flight.
+    constexpr int CG = 4;
+    for (int ch0 = 0; ch0 < chunks; ch0 += CG) {
+      uint4 kc[NCL][CG];
+#pragma unroll
+      for (int u = 0; u < NCL; ++u)
+#pragma unroll
+        for (int cc = 0; cc < CG; ++cc) {
+          const int ch = ch0 + cc;
+          if (ch >= chunks) {
+            kc[u][cc] = make_uint4(0, 0, 0, 0);
+          } else if (from_lds[u]) {
+            const int wr = ok[u] ? pos[u] - wb : 0;
+            kc[u][cc] = *reinterpret_cast<const uint4*>(win + wr * p.row_bytes + 16 * ch);
+          } else {
+            kc[u][cc] = buf_load_b128(
+                keys, ok[u] ? (row0 + static_cast<uint32_t>(pos[u])) * row_bytes + 16u * ch
+                            : kNoOffset);
+          }
+        }
+#pragma unroll
+      for (int cc = 0; cc < CG; ++cc) {
+        const int ch = ch0 + cc;
+        if (ch >= chunks) break;
+        double q[EPC];
+#pragma unroll
+        for (int e = 0; e < EPC; e += 2) {
+          const double2 q2 = *reinterpret_cast<const double2*>(ws.qx + EPC * ch + e);
+          q[e] = q2.x;
+          q[e + 1] = q2.y;
+        }
+#pragma unroll
+        for (int u = 0; u < NCL; ++u) {
+          double k[EPC];
+          chunk_to_f64<TA>(kc[u][cc], k);
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) acc[u] += k[e] * q[e];
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < NCL; ++u) {
+      const int c = c0 + lane + kWave * u;
+      if (c < p.CAP) ws.sc[c] = ok[u] ? static_cast<float>(acc[u] * p.exact_scale) : -INFINITY;
+    }
+  }
+  wave_sync();
+}
+
+// Workgroup staging (W > 1): block statistics (f32), bias tables (f32) and
+// the union of the local key windows of both streams, in one burst of loads
+// (eight 16-byte chunks per thread in flight before any LDS store).
+template <typename TA, typename TS, int MODE>
+__device__ void stage_workgroup(const SelectParams& p, int64_t b, int64_t wbase,
+                                unsigned char* smem) {
+  constexpr int EPC = kEpc<TA>;
+  constexpr bool kUseA = MODE != kPartnerOnly;
+  constexpr bool kUseP = MODE != kAnchorOnly;
+  const int tid = threadIdx.x;
+  const int nt = blockDim.x;
+  const int RD = p.H * p.HD;
+  const int n_stat = p.NB * RD / 4;            // float4 per statistic tensor
+  const int n_stats = 4 * n_stat;              // mean+std of both streams
+  const int n_win = p.WR * p.G;                // 16-byte chunks per window
+  const int total = n_stats + 2 * n_win;
+  // bias tables (tiny): one element per thread
+  for (int i = tid; i < 2 * p.H * p.RB; i += nt) {
+    const int side = i / (p.H * p.RB);
+    const int k = i - side * p.H * p.RB;
+    if ((side == 0 && !kUseA) || (side == 1 && !kUseP)) continue;
+    const Stream& s = side == 0 ? p.as : p.ps;
+    float* dst = reinterpret_cast<float*>(smem + (side == 0 ? p.off_bias_a : p.off_bias_p));
+    dst[k] = load_any_f(s.bias, s.bias_dtype, k);
+  }
+  // Item i < n_stats: statistic float4 (side, mean/std, index) with n_stat a
+  // power of two; else window chunk: row-major over 2*WR rows (side 0 then 1)
+  // of G chunks, G a power of two.  No divisions.
+  const int stat_log2 = 31 - __clz(n_stat);
+  constexpr int UB = 8;
+  for (int i0 = tid; i0 < total; i0 += UB * nt) {
+    uint4 v[UB];
+    int dst[UB];  // LDS byte offset, -1: nothing to store
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+      const int i = i0 + u * nt;
+      v[u] = make_uint4(0, 0, 0, 0);
+      dst[u] = -1;
+      if (i >= total) continue;
+      if (i < n_stats) {
+        const int side = i >> (stat_log2 + 1);
+        const int k = i & (2 * n_stat - 1);
+        if ((side == 0 && !kUseA) || (side == 1 && !kUseP)) continue;
+        const Stream& s = side == 0 ? p.as : p.ps;
+        const bool is_std = k >= n_stat;
+        const TS* src = static_cast<const TS*>(is_std ? s.stdev : s.mean) + b * p.NB * RD;
+        const float4 f = load4(src + 4 * (k & (n_stat - 1)));
+        v[u] = make_uint4(__float_as_uint(f.x), __float_as_uint(f.y), __float_as_uint(f.z),
+                          __float_as_uint(f.w));
+        dst[u] = (side == 0 ? p.off_stats_a : p.off_stats_p) + 16 * k;
+      } else {
+        const int w = i - n_stats;
+        int row = w >> p.G_log2;
+        const int ch = w & (p.G - 1);
+        const int side = row >= p.WR ? 1 : 0;
+        row -= side * p.WR;
+        if ((side == 0 && !kUseA) || (side == 1 && !kUseP)) continue;
+        const int64_t pos = wbase + row;
+        const TA* keys = static_cast<const TA*>(side == 0 ? p.as.keys : p.ps.keys) + b * p.T * p.E;
+        if (pos >= 0 && pos < p.T)
+          v[u] = *reinterpret_cast<const uint4*>(keys + pos * p.E + EPC * ch);
+        dst[u] = (side == 0 ? p.off_win_a : p.off_win_p) + row * p.row_bytes + 16 * ch;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UB; ++u)
+      if (dst[u] >= 0) *reinterpret_cast<uint4*>(smem + dst[u]) = v[u];
   }
 }
 
 template <typename TA, typename TS, int MODE>
-__global__ void __launch_bounds__(256) select_kernel(const SelectParams p) {
+__global__ void __launch_bounds__(512) select_kernel(const SelectParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int waves = blockDim.x / kWave;
-  const int64_t q = static_cast<int64_t>(blockIdx.x) * waves + wave;
-  if (q >= p.B * p.Tq) return;  // whole wave leaves; no workgroup barriers below
-
-  unsigned char* base = smem + wave * p.lds_per_wave;
-  double* sh = reinterpret_cast<double*>(base);
-  float* qx = reinterpret_cast<float*>(sh + ((p.NB * p.H + 1) & ~1));
-  float* qr = qx + p.E;
-  float* blk = qr + p.H * p.HD;
-  int* sel = reinterpret_cast<int*>(blk + p.NB);
-  int* selv = sel + p.TOP;
-  float* sc = reinterpret_cast<float*>(selv + p.TOP);
-
+  constexpr int EPC = kEpc<TA>;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int64_t b = blockIdx.x / p.tiles;
+  const int64_t tq0 = (blockIdx.x - b * p.tiles) * static_cast<int64_t>(p.W);
+  const int64_t tq = tq0 + wave;
   const int RD = p.H * p.HD;
-  const int64_t b = q / p.Tq;
-  const int64_t tq = q - b * p.Tq;
-  const int64_t t = load_any_i(p.pos, p.pos_dtype, b * p.pos_sb + tq * p.pos_sq);
-  const int64_t local_start = t - p.L + 1 > 0 ? t - p.L + 1 : 0;
+  constexpr bool kUseA = MODE != kPartnerOnly;
+  constexpr bool kUseP = MODE != kAnchorOnly;
+
+  // ---- Query-side loads first (independent of everything staged below). ----
+  // Waves past the last query read row tq0's vectors and leave after staging.
+  const int64_t tq_ld = tq < p.Tq ? tq : tq0;
+  const int64_t q_ld = b * p.Tq + tq_ld;
+  const int64_t t_own = load_any_i(p.pos, p.pos_dtype, b * p.pos_sb + tq_ld * p.pos_sq);
+  const int jg = lane & (p.G - 1);
+  const TA* q_exact = static_cast<const TA*>(kUseA ? p.aq : p.pq) +
+                      q_ld * (kUseA ? static_cast<int64_t>(p.E) : p.pq_row);
+  const uint4 q_chunk = *reinterpret_cast<const uint4*>(q_exact + EPC * jg);
+  uint4 pb_chunk = make_uint4(0, 0, 0, 0);
+  if (MODE == kPacked)
+    pb_chunk = *reinterpret_cast<const uint4*>(static_cast<const TA*>(p.pq) + q_ld * p.pq_row +
+                                               EPC * jg);
+  // softplus(gamma_h) = log(1 + exp(gamma_h)) in float64 (relation_select.py:87)
+  // for this lane's head h = lane mod H, both streams, while the loads fly.
+  double sp_a = 0.0, sp_p = 0.0;
+  {
+#pragma clang fp contract(off)
+    const int h = lane & (p.H - 1);
+    if (kUseA) sp_a = log(1.0 + exp(static_cast<double>(load_any_f(p.as.gamma, p.as.gamma_dtype, h))));
+    if (kUseP) sp_p = log(1.0 + exp(static_cast<double>(load_any_f(p.ps.gamma, p.ps.gamma_dtype, h))));
+  }
+  constexpr int kRq = 4;  // router-query elements held per lane (RD <= 256)
+  float rq_a[kRq], rq_p[kRq];
+  {
+    const TA* ra = static_cast<const TA*>(kUseA ? p.arq : p.prq) +
+                   q_ld * (kUseA ? static_cast<int64_t>(RD) : p.prq_row);
+    const TA* rp = static_cast<const TA*>(p.prq) + q_ld * p.prq_row;
+#pragma unroll
+    for (int i = 0; i < kRq; ++i) {
+      const int d = lane + kWave * i;
+      rq_a[i] = d < RD ? to_f32(ra[d]) : 0.0f;
+      rq_p[i] = (MODE == kPacked && d < RD) ? to_f32(rp[d]) : 0.0f;
+    }
+  }
+
+  // ---- Workgroup staging (several queries share statistics and windows). ----
+  const int64_t t_first = p.W > 1 ? load_any_i(p.pos, p.pos_dtype, b * p.pos_sb + tq0 * p.pos_sq)
+                                  : t_own;
+  const int64_t wbase = t_first - p.L + 1;
+  const bool staged = p.stage != 0;
+  if (staged) {
+    stage_workgroup<TA, TS, MODE>(p, b, wbase, smem);
+    __syncthreads();
+  }
+  if (tq >= p.Tq) return;  // no workgroup barriers below
+  const float* stats_a = staged && kUseA ? reinterpret_cast<const float*>(smem + p.off_stats_a) : nullptr;
+  const float* stats_p = staged && kUseP ? reinterpret_cast<const float*>(smem + p.off_stats_p) : nullptr;
+  const float* bias_a = staged && kUseA ? reinterpret_cast<const float*>(smem + p.off_bias_a) : nullptr;
+  const float* bias_p = staged && kUseP ? reinterpret_cast<const float*>(smem + p.off_bias_p) : nullptr;
+  const unsigned char* win_a = staged && kUseA ? smem + p.off_win_a : nullptr;
+  const unsigned char* win_p = staged && kUseP ? smem + p.off_win_p : nullptr;
+
+  unsigned char* base = smem + p.off_wave + wave * p.wave_bytes;
+  WaveScratch ws;
+  ws.qx = reinterpret_cast<double*>(base);
+  ws.qr = ws.qx + p.E;
+  ws.blk = reinterpret_cast<float*>(ws.qr + RD);
+  ws.sel = reinterpret_cast<int*>(ws.blk + p.NB);
+  ws.selv = ws.sel + p.TOP;
+  ws.sc = reinterpret_cast<float*>(ws.selv + p.TOP);
+
+  Query qy;
+  qy.b = b;
+  qy.q = b * p.Tq + tq;
+  qy.t = t_own;
+  qy.local_start = qy.t - p.L + 1 > 0 ? qy.t - p.L + 1 : 0;
+  qy.wbase = wbase;
+  const int j = jg;
+  double qx[EPC];
+  // The exact query chunk of this lane (lanes of one chunk group hold the
+  // same values) into the wave's scratch.
+  auto put_exact = [&]() {
+    if (lane < p.G) {
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) ws.qx[EPC * lane + e] = qx[e];
+    }
+  };
+  // Router query into the wave's scratch (f64); RD > 4*64 reloads the rest.
+  auto put_router = [&](const float* held, const TA* src, int64_t row_stride) {
+#pragma unroll
+    for (int i = 0; i < kRq; ++i) {
+      const int d = lane + kWave * i;
+      if (d < RD) ws.qr[d] = static_cast<double>(held[i]);
+    }
+    for (int d = lane + kWave * kRq; d < RD; d += kWave)
+      ws.qr[d] = static_cast<double>(to_f32(src[qy.q * row_stride + d]));
+  };
 
   int64_t anchor;
-  if (MODE != kPartnerOnly) {
-    const TA* aq = static_cast<const TA*>(p.aq) + q * p.E;
-    const TA* arq = static_cast<const TA*>(p.arq) + q * RD;
-    for (int d = lane; d < p.E; d += kWave) qx[d] = to_f32(aq[d]);
-    for (int d = lane; d < RD; d += kWave) qr[d] = to_f32(arq[d]);
+  if (kUseA) {
+    chunk_to_f64<TA>(q_chunk, qx);
+    put_exact();
+    put_router(rq_a, static_cast<const TA*>(p.arq), RD);
     wave_sync();
-    block_scores<TS>(p, p.as, b, t, local_start, qr, sh, blk, lane);
-    pick_blocks(p, blk, sel, selv, lane);
-    const TA* keys = static_cast<const TA*>(p.as.keys) + b * p.T * p.E;
+    block_scores<TS>(p, p.as, stats_a, bias_a, sp_a, qy, ws, lane);
+    pick_blocks(p, ws, lane);
+    candidate_scores<TA, 3>(p, p.as, win_a, qy, -1, ws, lane);
     uint64_t best = 0;
     float best_score = -INFINITY;
     for (int c = lane; c < p.CAP; c += kWave) {
       int64_t pos;
       bool valid;
-      candidate(p, c, t, local_start, sel, selv, pos, valid);
+      candidate(p, c, qy, ws, pos, valid);
       if (valid) {
-        const float s = exact_score(keys + pos * p.E, qx, p.E, p.exact_scale);
-        const uint64_t k = select_key(s, static_cast<uint32_t>(pos));
+        const float sc = ws.sc[c];
+        const uint64_t k = select_key(sc, static_cast<uint32_t>(pos));
         if (k > best) {
           best = k;
-          best_score = s;
+          best_score = sc;
         }
       }
     }
     const uint64_t win = wave_max_u64(best);
     if (win == 0) {
-      anchor = t - p.L + 1;
+      anchor = qy.t - p.L + 1;
       if (lane == 0) {
-        p.out_anchor[q] = static_cast<int32_t>(anchor);
-        p.out_anchor_score[q] = -INFINITY;
+        p.out_anchor[qy.q] = static_cast<int32_t>(anchor);
+        p.out_anchor_score[qy.q] = -INFINITY;
       }
     } else {
       anchor = key_index(win);
       if (best == win) {
-        p.out_anchor[q] = static_cast<int32_t>(anchor);
-        p.out_anchor_score[q] = best_score;
+        p.out_anchor[qy.q] = static_cast<int32_t>(anchor);
+        p.out_anchor_score[qy.q] = best_score;
       }
     }
     if (MODE == kAnchorOnly) return;
     wave_sync();
   } else {
-    anchor = load_any_i(p.anchor_in, p.anchor_dtype, q);
+    anchor = load_any_i(p.anchor_in, p.anchor_dtype, qy.q);
   }
 
   // Partner queries (relation_select.py:165-193): fp32 sum of the query-side
   // projection and the anchor row of the cached anchor-side projection.
   {
-    const TA* pq = static_cast<const TA*>(p.pq) + q * p.pq_row;
-    const TA* prq = static_cast<const TA*>(p.prq) + q * p.prq_row;
+    const TA* prq = static_cast<const TA*>(p.prq) + qy.q * p.prq_row;
     if (MODE == kPacked) {
       const bool have = anchor >= 0 && anchor < p.T;
       const TA* pc = static_cast<const TA*>(p.pcache) + (b * p.T + (have ? anchor : 0)) * (2 * p.E);
-      for (int d = lane; d < p.E; d += kWave)
-        qx[d] = to_f32(pq[d]) + (have ? to_f32(pc[d]) : 0.0f);
-      for (int d = lane; d < RD; d += kWave)
-        qr[d] = to_f32(prq[d]) + (have ? to_f32(pc[p.E + d]) : 0.0f);
+      double base_q[EPC], cache_q[EPC];
+      chunk_to_f64<TA>(pb_chunk, base_q);
+      const uint4 cc = *reinterpret_cast<const uint4*>(pc + EPC * j);
+      float cr[kRq];
+#pragma unroll
+      for (int i = 0; i < kRq; ++i) {
+        const int d = lane + kWave * i;
+        cr[i] = d < RD ? to_f32(pc[p.E + d]) : 0.0f;
+      }
+      chunk_to_f64<TA>(cc, cache_q);
+#pragma unroll
+      for (int e = 0; e < EPC; ++e)
+        qx[e] = static_cast<double>(static_cast<float>(base_q[e]) +
+                                    (have ? static_cast<float>(cache_q[e]) : 0.0f));
+#pragma unroll
+      for (int i = 0; i < kRq; ++i) {
+        const int d = lane + kWave * i;
+        if (d < RD) ws.qr[d] = static_cast<double>(rq_p[i] + (have ? cr[i] : 0.0f));
+      }
+      for (int d = lane + kWave * kRq; d < RD; d += kWave)
+        ws.qr[d] = static_cast<double>(to_f32(prq[d]) + (have ? to_f32(pc[p.E + d]) : 0.0f));
     } else {
-      for (int d = lane; d < p.E; d += kWave) qx[d] = to_f32(pq[d]);
-      for (int d = lane; d < RD; d += kWave) qr[d] = to_f32(prq[d]);
+      chunk_to_f64<TA>(q_chunk, qx);
+      put_router(rq_a, static_cast<const TA*>(p.prq), p.prq_row);
     }
+    put_exact();
   }
   wave_sync();
-  block_scores<TS>(p, p.ps, b, t, local_start, qr, sh, blk, lane);
-  pick_blocks(p, blk, sel, selv, lane);
+  block_scores<TS>(p, p.ps, stats_p, bias_p, sp_p, qy, ws, lane);
+  pick_blocks(p, ws, lane);
+  candidate_scores<TA, 3>(p, p.ps, win_p, qy, static_cast<int>(anchor), ws, lane);
 
-  const TA* keys = static_cast<const TA*>(p.ps.keys) + b * p.T * p.E;
+  // K argmax passes (relation_select.py:298-308), ties to the lowest lane.
+  // While finite scores remain, this is a stable descending order of the
+  // lanes; once they are exhausted the reference's argmax over an all -inf
+  // vector returns lane 0 for every remaining slot: position t-L+1, -inf.
+  const int nc = (p.CAP + kWave - 1) / kWave;
+  if (nc <= 4 && p.K <= kWave) {
+    // Each lane keeps its (at most four) candidate keys sorted in registers
+    // and pops its head when it wins a pass; lane k collects the k-th winner
+    // and all K slots are written together at the end.
+    uint64_t k4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = lane + kWave * i;
+      k4[i] = c < p.CAP ? select_key(ws.sc[c], static_cast<uint32_t>(c)) : 0;
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int bb = 0; bb < 3 - a; ++bb)
+        if (k4[bb] < k4[bb + 1]) {
+          const uint64_t tmp = k4[bb];
+          k4[bb] = k4[bb + 1];
+          k4[bb + 1] = tmp;
+        }
+    int my_c = -1;  // winning candidate lane of slot `lane` (-1: exhausted)
+    for (int k = 0; k < p.K; ++k) {
+      const uint64_t win = wave_max_u64(k4[0]);
+      if (!(key_score(win) > -INFINITY)) break;  // wave-uniform
+      if (lane == k) my_c = static_cast<int>(key_index(win));
+      if (k4[0] == win) {
+        k4[0] = k4[1];
+        k4[1] = k4[2];
+        k4[2] = k4[3];
+        k4[3] = 0;
+      }
+    }
+    if (lane < p.K) {
+      int64_t pos = qy.t - p.L + 1;
+      float score = -INFINITY;
+      if (my_c >= 0) {
+        bool valid;
+        candidate(p, my_c, qy, ws, pos, valid);
+        score = ws.sc[my_c];
+      }
+      p.out_partner[qy.q * p.K + lane] = static_cast<int32_t>(pos);
+      p.out_partner_score[qy.q * p.K + lane] = score;
+    }
+    return;
+  }
   uint64_t best = 0;
   for (int c = lane; c < p.CAP; c += kWave) {
-    int64_t pos;
-    bool valid;
-    candidate(p, c, t, local_start, sel, selv, pos, valid);
-    valid = valid && pos != anchor;
-    const float s = valid ? exact_score(keys + pos * p.E, qx, p.E, p.exact_scale) : -INFINITY;
-    sc[c] = s;
-    const uint64_t k = select_key(s, static_cast<uint32_t>(c));
+    const uint64_t k = select_key(ws.sc[c], static_cast<uint32_t>(c));
     best = k > best ? k : best;
   }
-  // K argmax passes; picked lanes drop to -inf but stay in the pool, so once
-  // the finite lanes are exhausted every pass lands on lane 0 with -inf
-  // (relation_select.py:298-308).
   for (int k = 0; k < p.K; ++k) {
     const uint64_t win = wave_max_u64(best);
     const int c = static_cast<int>(key_index(win));
     if ((c & (kWave - 1)) == lane) {
       int64_t pos;
       bool valid;
-      candidate(p, c, t, local_start, sel, selv, pos, valid);
+      candidate(p, c, qy, ws, pos, valid);
       const bool exhausted = !(key_score(win) > -INFINITY);
-      p.out_partner[q * p.K + k] = static_cast<int32_t>(pos);
-      p.out_partner_score[q * p.K + k] = exhausted ? -INFINITY : sc[c];
-      sc[c] = -INFINITY;
+      p.out_partner[qy.q * p.K + k] = static_cast<int32_t>(pos);
+      p.out_partner_score[qy.q * p.K + k] = exhausted ? -INFINITY : ws.sc[c];
+      ws.sc[c] = -INFINITY;
       best = 0;
       for (int cc = lane; cc < p.CAP; cc += kWave) {
-        const uint64_t kk = select_key(sc[cc], static_cast<uint32_t>(cc));
+        const uint64_t kk = select_key(ws.sc[cc], static_cast<uint32_t>(cc));
         best = kk > best ? kk : best;
       }
     }
@@ -367,7 +755,8 @@ Stream make_stream(const rlm_tensor* keys, const rlm_tensor* mean, const rlm_ten
 
 // Validates the routing hyper-parameters and fills the derived fields.
 hipError_t finish_params(SelectParams& p, const Geometry& g, int64_t local_window,
-                         int64_t top_blocks, int64_t k_out, int32_t strict_valid) {
+                         int64_t top_blocks, int64_t k_out, int32_t strict_valid,
+                         int act_size) {
   RLM_REQUIRE(local_window >= 1 && local_window <= 4096,
               "local_window must be in [1, 4096], got %lld", (long long)local_window);
   RLM_REQUIRE(top_blocks >= 0 && top_blocks <= 64, "top_blocks must be in [0, 64], got %lld",
@@ -375,9 +764,7 @@ hipError_t finish_params(SelectParams& p, const Geometry& g, int64_t local_windo
   RLM_REQUIRE(k_out >= 0 && k_out <= 1024, "k_out must be in [0, 1024], got %lld",
               (long long)k_out);
   RLM_REQUIRE(g.NB >= 1 && g.BS >= 1, "need at least one block of at least one row");
-  RLM_REQUIRE(g.E % 4 == 0 && g.E <= 1024, "exact dim must be a multiple of 4 and <= 1024");
-  RLM_REQUIRE(g.HD % 4 == 0 && g.H >= 1 && g.H * g.HD <= 1024,
-              "router head dim must be a multiple of 4 and heads*head_dim <= 1024");
+  RLM_REQUIRE(g.H >= 1 && g.H * g.HD <= 1024, "heads*head_dim must be <= 1024");
   RLM_REQUIRE(g.RB >= 1, "relative buckets must be >= 1");
   const int64_t cap = local_window + top_blocks * static_cast<int64_t>(g.BS);
   RLM_REQUIRE(cap <= 8192, "local_window + top_blocks * block_size must be <= 8192");
@@ -397,8 +784,61 @@ hipError_t finish_params(SelectParams& p, const Geometry& g, int64_t local_windo
   p.strict = strict_valid ? 1 : 0;
   p.exact_scale = 1.0 / std::sqrt(static_cast<double>(g.E));
   p.head_scale = 1.0 / std::sqrt(static_cast<double>(g.HD));
-  p.lds_per_wave = select_lds_bytes(p.NB, p.H, p.E, p.H * p.HD, p.TOP, p.CAP);
-  RLM_REQUIRE(p.lds_per_wave <= 65536, "selection working set exceeds 64 KiB of LDS per query");
+  const int elem = act_size;
+  RLM_REQUIRE((g.E * elem) % 16 == 0, "exact dim times element size must be a multiple of 16 bytes");
+  const int G = g.E * elem / 16;
+  RLM_REQUIRE(G <= kWave && (G & (G - 1)) == 0,
+              "exact dim must be a power of two of at most %d elements for this dtype",
+              kWave * 16 / elem);
+  RLM_REQUIRE(g.HD % 4 == 0, "router head dim must be a multiple of 4");
+  RLM_REQUIRE(g.H <= kWave && (g.H & (g.H - 1)) == 0, "router heads must be a power of two <= 64");
+  RLM_REQUIRE((g.BS & (g.BS - 1)) == 0,
+              "block size (cache length / blocks) must be a power of two, got %d", g.BS);
+  p.G = G;
+  p.G_log2 = 31 - __builtin_clz(static_cast<unsigned>(G));
+  p.H_log2 = 31 - __builtin_clz(static_cast<unsigned>(g.H));
+  p.BS_log2 = 31 - __builtin_clz(static_cast<unsigned>(g.BS));
+  p.W = g.Tq > 1 ? 8 : 1;
+  p.tiles = static_cast<int>((g.Tq + p.W - 1) / p.W);
+  p.WR = p.L + p.W - 1;
+  p.row_bytes = g.E * elem + 16;
+  const int RD = g.H * g.HD;
+  const int stats_bytes = 2 * g.NB * RD * 4;  // mean + std, one stream
+  const bool stats_pow2 = ((g.NB * RD / 4) & (g.NB * RD / 4 - 1)) == 0;
+  const int bias_bytes = ((g.H * g.RB * 4) + 15) & ~15;
+  int off = 0;
+  p.stage = p.W > 1 && stats_pow2 ? 1 : 0;
+  p.off_stats_a = p.off_stats_p = p.off_bias_a = p.off_bias_p = p.off_win_a = p.off_win_p = 0;
+  if (p.stage) {
+    p.off_stats_a = off;
+    off += stats_bytes;
+    p.off_stats_p = off;
+    off += stats_bytes;
+    p.off_bias_a = off;
+    off += bias_bytes;
+    p.off_bias_p = off;
+    off += bias_bytes;
+    p.off_win_a = off;
+    off += p.WR * p.row_bytes;
+    p.off_win_p = off;
+    off += p.WR * p.row_bytes;
+  }
+  const int64_t key_bytes = g.B * g.T * g.E * elem;
+  RLM_REQUIRE(key_bytes < (int64_t(1) << 31), "key caches must be smaller than 2 GiB");
+  p.key_bytes = static_cast<uint32_t>(key_bytes);
+  p.off_wave = off;
+  p.wave_bytes = wave_region_bytes(g.E, g.NB, RD, p.TOP, p.CAP);
+  off += p.W * p.wave_bytes;
+  if (p.stage && off > 96 * 1024) {
+    // Too large to share: every wave reads statistics and keys from L2.
+    p.stage = 0;
+    off = 0;
+    p.off_wave = 0;
+    off += p.W * p.wave_bytes;
+  }
+  RLM_REQUIRE(off <= 160 * 1024,
+              "selection working set (%d bytes of LDS) exceeds the 160 KiB of one CU", off);
+  p.lds_total = off;
   return hipSuccess;
 }
 
@@ -407,11 +847,9 @@ hipError_t launch_select(const SelectParams& p, int act_dtype, int stat_dtype,
                          hipStream_t stream) {
   const int64_t queries = p.B * p.Tq;
   if (queries == 0) return hipSuccess;
-  int waves = p.Tq > 1 ? 4 : 1;
-  while (waves > 1 && waves * p.lds_per_wave > 65536) waves >>= 1;
-  const dim3 block(waves * kWave);
-  const dim3 grid(static_cast<unsigned>((queries + waves - 1) / waves));
-  const size_t lds = static_cast<size_t>(waves) * p.lds_per_wave;
+  const dim3 block(p.W * kWave);
+  const dim3 grid(static_cast<unsigned>(p.B * p.tiles));
+  const size_t lds = static_cast<size_t>(p.lds_total);
 #define RLM_SELECT_CASE(TA_ID, TA, TS_ID, TS)                                          \
   if (act_dtype == TA_ID && stat_dtype == TS_ID) {                                     \
     hipLaunchKernelGGL((select_kernel<TA, TS, MODE>), grid, block, lds, stream, p);    \
@@ -542,7 +980,8 @@ hipError_t select_packed_impl(
   RLM_TRY(check_position(position, "position", g, seq, p));
   RLM_TRY(check_outputs(out_anchor, out_anchor_score, "anchor", g, seq, -1));
   RLM_TRY(check_outputs(out_partner, out_partner_score, "partner", g, seq, k_out));
-  hipError_t err = finish_params(p, g, local_window, top_blocks, k_out, strict_valid);
+  hipError_t err = finish_params(p, g, local_window, top_blocks, k_out, strict_valid,
+                                 act == RLM_F32 ? 4 : 2);
   if (err != hipSuccess) return err;
   p.aq = anchor_query->data;
   p.arq = anchor_router_query->data;
@@ -640,7 +1079,8 @@ extern "C" hipError_t rlm_anchor_select(
   SelectParams p{};
   RLM_TRY(check_position(position, "position", g, false, p));
   RLM_TRY(check_outputs(out_index, out_score, "index", g, false, -1));
-  hipError_t err = finish_params(p, g, local_window, top_blocks, 0, strict_valid);
+  hipError_t err = finish_params(p, g, local_window, top_blocks, 0, strict_valid,
+                                 act == RLM_F32 ? 4 : 2);
   if (err != hipSuccess) return err;
   p.aq = anchor_query->data;
   p.arq = router_query->data;
@@ -689,7 +1129,8 @@ extern "C" hipError_t rlm_partner_topk(
   SelectParams p{};
   RLM_TRY(check_position(position, "position", g, false, p));
   RLM_TRY(check_outputs(out_index, out_score, "index", g, false, k_out));
-  hipError_t err = finish_params(p, g, local_window, top_blocks, k_out, strict_valid);
+  hipError_t err = finish_params(p, g, local_window, top_blocks, k_out, strict_valid,
+                                 act == RLM_F32 ? 4 : 2);
   if (err != hipSuccess) return err;
   p.pq = partner_query->data;
   p.pq_row = g.E;

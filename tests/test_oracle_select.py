@@ -88,6 +88,20 @@ def test_block_scores_match_router_logsumexp(strict):
         assert np.array_equal(np.isfinite(got), np.isfinite(expected))
 
 
+def test_one_shot_and_pairwise_head_logsumexp_agree():
+    """The reference kernel's pairwise fold == one-shot logsumexp, to float64 ulps."""
+    rng = np.random.default_rng(17)
+    per_head = rng.standard_normal((20000, 4)) * rng.choice([0.01, 1.0, 30.0], (20000, 1))
+    one = osel.logsumexp_heads(per_head)
+    pair = osel.logsumexp_heads_pairwise(per_head)
+    assert np.max(np.abs(one - pair) / np.maximum(np.abs(pair), 1.0)) < 1e-14
+    # and both round to the same float32 on this sample
+    assert np.array_equal(one.astype(np.float32), pair.astype(np.float32))
+    # exact special cases: equal heads give s + log(H); one dominant head gives s
+    assert osel.logsumexp_heads(np.full((1, 4), 2.5))[0] == 2.5 + np.log(4.0)
+    assert osel.logsumexp_heads(np.array([[800.0, 0.0, 0.0, 0.0]]))[0] == 800.0
+
+
 def test_block_statistics_match_torch():
     rng = np.random.default_rng(5)
     keys = rng.standard_normal((2, 40, 64))
