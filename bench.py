@@ -4,12 +4,16 @@
 Step = one pass of the cfg2 prefill workload (B=8, T=512, d=512, block 32,
 local 64, top 4, K=8, bf16 activations / fp32 scores, relation hidden 512):
     expanded-cache projection -> relation_select (all 4096 queries)
-    -> relation hidden -> second linear -> LayerNorm / softmax / partner sum.
+    -> fused relation reduce (hidden -> second linear -> LayerNorm / softmax /
+       partner sum in one kernel).
 `value` is queries per second with every input resident in HBM.
 
 Also reported:
+  * the same step through the reference's unfused op sequence
+    (relation_hidden_cached -> linear -> relation_norm_reduce);
   * per-kernel average duration (HIP events on the launch stream) and the
-    HBM roofline fraction of the dominant kernel at its operator-contract bytes;
+    roofline fraction of the dominant kernel (HBM bytes at the operator
+    contract, or matrix-core FLOPs for the fused reduce);
   * decode-step latency (cfg3: packed 576->512 projection, cache-row writes,
     select, reduce) at B=1 and B=8, eager and replayed from a HIP graph;
   * the CPU oracle timed on this host's cores on a bounded sample.
@@ -28,6 +32,7 @@ for _p in (ROOT, os.path.join(ROOT, "relation-lm_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def parse_args():
@@ -58,6 +63,20 @@ def algorithmic_bytes(cfg):
         "relation_hidden": b * t * (2 * h + r) * s + h * r * s + q * k * h * 4 + q * (1 + k) * 4,
         "second_linear": q * k * h * 4 + d * h * s + d * s + q * k * d * 4,
         "norm_reduce": q * k * d * 4 + q * k * 4 + 2 * d * s + q * d * 4,
+        "relation_reduce_fused": (b * t * (2 * h + r) * s + h * r * s + d * h * s + d * s
+                                  + q * (1 + k) * 4 + q * k * 4 + 2 * d * s + q * d * 4),
+    }
+
+
+def algorithmic_flops(cfg):
+    """Matrix-core FLOPs per launch at the operator contract (each product counted once)."""
+    q, k = cfg.batch * cfg.context, cfg.k_out
+    r, h, d = cfg.relation_dim, cfg.hidden_dim, cfg.d_model
+    return {
+        "expanded_projection": 2 * q * r * 2 * h,
+        "relation_hidden": 2 * q * k * r * h,
+        "second_linear": 2 * q * k * h * d,
+        "relation_reduce_fused": 2 * q * k * (r * h + h * d),
     }
 
 
@@ -77,6 +96,7 @@ def main() -> int:
         relation_linear,
         relation_norm_reduce,
         relation_norm_reduce_seq,
+        relation_reduce_fused_seq,
     )
     from relation_lm.kernels.relation_select import (
         relation_select_packed,
@@ -118,7 +138,17 @@ def main() -> int:
         return relation_norm_reduce_seq(raw, ps, red["norm_weight"], red["norm_bias"], positions,
                                         1e-5)
 
+    def run_fused(expanded, a, p, ps):
+        return relation_reduce_fused_seq(expanded, operand, a, p, red["product_weight"],
+                                         red["second_weight"], red["second_bias"], ps,
+                                         red["norm_weight"], red["norm_bias"], positions, 1e-5)
+
     def step():
+        expanded = run_expanded()
+        a, s, p, ps = run_select()
+        return run_fused(expanded, a, p, ps)
+
+    def step_unfused():
         expanded = run_expanded()
         a, s, p, ps = run_select()
         hidden = run_hidden(expanded, a, p)
@@ -127,23 +157,30 @@ def main() -> int:
 
     for _ in range(args.warmup):
         step()
+        step_unfused()
     torch.cuda.synchronize()
     if args.only_chain:
         for _ in range(args.steps):
             step()
+            step_unfused()
         torch.cuda.synchronize()
         print(json.dumps({"only_chain": True, "steps": args.steps}), flush=True)
         return 0
 
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(args.steps):
-        step()
-    end.record()
-    torch.cuda.synchronize()
-    ms_per_step = start.elapsed_time(end) / args.steps
+
+    def timed(fn, count):
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(count):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / count
+
+    ms_per_step = timed(step, args.steps)
+    ms_unfused = timed(step_unfused, args.steps)
     queries = cfg.queries
     value = queries / (ms_per_step / 1e3)
 
@@ -155,6 +192,7 @@ def main() -> int:
     kernels = {
         "expanded_projection": run_expanded,
         "relation_select": run_select,
+        "relation_reduce_fused": lambda: run_fused(expanded, a, p, ps),
         "relation_hidden": lambda: run_hidden(expanded, a, p),
         "second_linear": lambda: run_second(hidden),
         "norm_reduce": lambda: run_norm(raw, ps),
@@ -171,12 +209,27 @@ def main() -> int:
         torch.cuda.synchronize()
         per_kernel_us[name] = start.elapsed_time(end) * 1e3 / args.kernel_repeats
     nbytes = algorithmic_bytes(cfg)
-    dominant = max(per_kernel_us, key=per_kernel_us.get)
-    achieved = nbytes[dominant] / (per_kernel_us[dominant] * 1e-6) / 1e9
+    nflops = algorithmic_flops(cfg)
+    headline = ("expanded_projection", "relation_select", "relation_reduce_fused")
+    dominant = max(headline, key=per_kernel_us.get)
+    if dominant == "relation_reduce_fused":
+        achieved = nflops[dominant] / (per_kernel_us[dominant] * 1e-6) / 1e12
+        roof = {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 1),
+                "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                "algorithmic_flops": nflops[dominant]}
+    else:
+        achieved = nbytes[dominant] / (per_kernel_us[dominant] * 1e-6) / 1e9
+        roof = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "algorithmic_bytes": nbytes[dominant]}
+    roof["traffic"] = measured_traffic(dominant)
     trio = ("relation_select", "relation_hidden", "norm_reduce")
     trio_bytes = sum(nbytes[k] for k in trio)
     trio_us = sum(per_kernel_us[k] for k in trio)
-    chain_bytes = sum(nbytes.values())
+    unfused_bytes = sum(nbytes[k] for k in ("expanded_projection", "relation_select",
+                                            "relation_hidden", "second_linear", "norm_reduce"))
+    fused_bytes = sum(nbytes[k] for k in headline)
 
     # Decode step (cfg3) at B=1 and B=8.
     decode = {}
@@ -262,28 +315,39 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) activations/caches, N(0,1/fan_in) weights)",
         "config": {
             "workload": "cfg2 prefill: B=8 T=512 d=512 block32 local64 top4 K=8 hidden512 "
-                        "(expanded projection + select + hidden + linear2 + norm-reduce)",
+                        "(expanded projection + select + fused hidden/linear2/norm-reduce)",
             "batch": cfg.batch, "context": cfg.context, "d_model": cfg.d_model,
             "queries_per_step": queries, "parallelism": "single GPU",
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": dominant,
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "algorithmic_bytes": nbytes[dominant],
-        },
+        "roofline": roof,
         "per_kernel_us": {k: round(v, 2) for k, v in per_kernel_us.items()},
-        "select_hidden_norm_frac": round(trio_bytes / (trio_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-        "chain_frac": round(chain_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "hbm_frac_fused_chain": round(fused_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "unfused_chain": {
+            "ms_per_step": round(ms_unfused, 5),
+            "value": round(queries / (ms_unfused / 1e3), 1),
+            "hbm_frac_chain": round(unfused_bytes / (ms_unfused * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "hbm_frac_select_hidden_norm": round(
+                trio_bytes / (trio_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        },
         "decode_step_us": decode,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
     return 0
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` measured with rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, calibrated against a copy kernel), read from the committed summary
+    profiles/cfg2_traffic.json; None when that kernel was not measured."""
+    path = os.path.join(ROOT, "profiles", "cfg2_traffic.json")
+    try:
+        with open(path) as f:
+            table = json.load(f)
+    except (OSError, ValueError):
+        return None
+    entry = table.get("kernels", {}).get(kernel)
+    return None if entry is None else entry.get("hbm_bytes_per_launch")
 
 
 def cpu_baseline(cfg, sel, red, torch):

@@ -205,6 +205,29 @@ hipError_t rlm_relation_norm_reduce_seq(
     const rlm_tensor* positions, double norm_eps, const rlm_tensor* out,
     hipStream_t stream);
 
+/*
+ * Fused relation reduce, sequence form (no reference counterpart: the
+ * reference runs relation_hidden_cached -> F.linear -> relation_norm_reduce,
+ * src/relation_lm/kernels/relation_reduce.py:149,420 and the call sequence of
+ * benchmarks/benchmark_relation_reduce.py:55-64, with fp32 intermediates).
+ *   ctx[b,q] = sum_k p_k LayerNorm(W2 h_k + b2),
+ *   h_k = GELU(W_m (op[a]*op[p_k]) + X[a,0:H] + X[p_k,H:2H]) rounded to bf16,
+ *   p = the active-K softmax of relation_norm_reduce.
+ *   expanded_cache [B,T,2H], operand_cache [B,T,R], product_weight [H,R],
+ *   second_weight [D,H] (all bf16), second_bias [D], partner_scores f32
+ *   [B,Tq,K], norm_weight/norm_bias [D], anchor_index [B,Tq], partner_index
+ *   [B,Tq,K], positions [Tq] or [B,Tq].  K in {1,2,4,8,16}, R a multiple of 32
+ *   up to 128, H a multiple of 128, D in {256, 384, 512}.
+ * Output: out f32 [B,Tq,D].
+ */
+hipError_t rlm_relation_reduce_fused_seq(
+    const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
+    const rlm_tensor* anchor_index, const rlm_tensor* partner_index,
+    const rlm_tensor* product_weight, const rlm_tensor* second_weight,
+    const rlm_tensor* second_bias, const rlm_tensor* partner_scores,
+    const rlm_tensor* norm_weight, const rlm_tensor* norm_bias, const rlm_tensor* positions,
+    double norm_eps, const rlm_tensor* out, hipStream_t stream);
+
 /* ------------------------------------------------------------------------
  * Dense projections (MFMA)
  * ---------------------------------------------------------------------- */

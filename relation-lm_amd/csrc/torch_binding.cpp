@@ -305,6 +305,37 @@ at::Tensor relation_norm_reduce_seq(const at::Tensor& raw, const at::Tensor& par
   return norm_common(true, raw, partner_scores, norm_weight, norm_bias, positions, norm_eps);
 }
 
+at::Tensor relation_reduce_fused_seq(const at::Tensor& expanded_cache,
+                                     const at::Tensor& operand_cache,
+                                     const at::Tensor& anchor_index,
+                                     const at::Tensor& partner_index,
+                                     const at::Tensor& product_weight,
+                                     const at::Tensor& second_weight,
+                                     const at::Tensor& second_bias,
+                                     const at::Tensor& partner_scores,
+                                     const at::Tensor& norm_weight, const at::Tensor& norm_bias,
+                                     const at::Tensor& positions, double norm_eps) {
+  const char* op = "relation_lm::relation_reduce_fused_seq";
+  c10::DeviceGuard guard(operand_cache.device());
+  hipStream_t stream = device_stream(
+      op, {&operand_cache, &expanded_cache, &anchor_index, &partner_index, &product_weight,
+           &second_weight, &second_bias, &partner_scores, &norm_weight, &norm_bias, &positions});
+  TORCH_CHECK(partner_index.dim() == 3 && second_weight.dim() == 2, op,
+              ": partner_index must be [B,Tq,K] and second_weight [D,H]");
+  at::Tensor out = at::empty({partner_index.size(0), partner_index.size(1), second_weight.size(0)},
+                             f32(operand_cache));
+  rlm_tensor d[12] = {desc(expanded_cache, "expanded_cache"), desc(operand_cache, "operand_cache"),
+                      desc(anchor_index, "anchor_index"), desc(partner_index, "partner_index"),
+                      desc(product_weight, "product_weight"), desc(second_weight, "second_weight"),
+                      desc(second_bias, "second_bias"), desc(partner_scores, "partner_scores"),
+                      desc(norm_weight, "norm_weight"), desc(norm_bias, "norm_bias"),
+                      desc(positions, "positions"), desc(out, "out")};
+  check(rlm_relation_reduce_fused_seq(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7],
+                                      &d[8], &d[9], &d[10], norm_eps, &d[11], stream),
+        op);
+  return out;
+}
+
 at::Tensor linear_common(const char* op, const at::Tensor& input, const at::Tensor& weight,
                          const c10::optional<at::Tensor>& bias, at::ScalarType out_dtype,
                          bool packed) {
@@ -380,6 +411,11 @@ TORCH_LIBRARY(relation_lm, m) {
   m.def(
       "relation_norm_reduce_seq(Tensor raw, Tensor partner_scores, Tensor norm_weight, Tensor "
       "norm_bias, Tensor positions, float norm_eps) -> Tensor");
+  m.def(
+      "relation_reduce_fused_seq(Tensor expanded_cache, Tensor operand_cache, Tensor "
+      "anchor_index, Tensor partner_index, Tensor product_weight, Tensor second_weight, Tensor "
+      "second_bias, Tensor partner_scores, Tensor norm_weight, Tensor norm_bias, Tensor "
+      "positions, float norm_eps) -> Tensor");
   m.def("packed_sparse_cache_projection(Tensor memory, Tensor weight) -> Tensor");
   m.def(
       "relation_linear(Tensor input, Tensor weight, Tensor? bias=None, ScalarType? "
@@ -406,6 +442,7 @@ TORCH_LIBRARY_IMPL(relation_lm, CUDA, m) {
   m.impl("relation_hidden_cache_update", TORCH_FN(relation_hidden_cache_update));
   m.impl("relation_norm_reduce", TORCH_FN(relation_norm_reduce));
   m.impl("relation_norm_reduce_seq", TORCH_FN(relation_norm_reduce_seq));
+  m.impl("relation_reduce_fused_seq", TORCH_FN(relation_reduce_fused_seq));
   m.impl("packed_sparse_cache_projection", TORCH_FN(packed_sparse_cache_projection));
   m.impl("relation_linear", TORCH_FN(relation_linear));
 }

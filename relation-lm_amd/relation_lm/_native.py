@@ -73,6 +73,12 @@ def _register_fakes() -> None:
     torch.library.register_fake("relation_lm::relation_norm_reduce")(fake_norm)
     torch.library.register_fake("relation_lm::relation_norm_reduce_seq")(fake_norm)
 
+    @torch.library.register_fake("relation_lm::relation_reduce_fused_seq")
+    def _(expanded_cache, operand_cache, anchor_index, partner_index, product_weight,
+          second_weight, *rest):
+        return operand_cache.new_empty(tuple(partner_index.shape[:2]) + (second_weight.shape[0],),
+                                       dtype=torch.float32)
+
     @torch.library.register_fake("relation_lm::packed_sparse_cache_projection")
     def _(memory, weight):
         return memory.new_empty(tuple(memory.shape[:-1]) + (weight.shape[0],))

@@ -142,6 +142,33 @@ def relation_norm_reduce_seq(
         raw, partner_scores, norm_weight, norm_bias, positions, float(norm_eps))
 
 
+def relation_reduce_fused_seq(
+    expanded_cache: Tensor,
+    operand_cache: Tensor,
+    anchor_index: Tensor,
+    partner_index: Tensor,
+    product_weight: Tensor,
+    second_weight: Tensor,
+    second_bias: Tensor,
+    partner_scores: Tensor,
+    norm_weight: Tensor,
+    norm_bias: Tensor,
+    positions: Tensor,
+    norm_eps: float,
+) -> Tensor:
+    """Relation hidden -> second linear -> norm-reduce in one kernel -> f32 [B, Tq, D].
+
+    Same result as ``relation_norm_reduce_seq(relation_linear(relation_hidden_cached_seq(...),
+    second_weight, second_bias), ...)`` (the reference's three-call sequence,
+    benchmarks/benchmark_relation_reduce.py:55-64) with bf16 caches and weights: the
+    hidden is rounded to bf16 before the second linear, as the unfused bf16 linear does.
+    """
+    return torch.ops.relation_lm.relation_reduce_fused_seq(
+        expanded_cache, operand_cache, anchor_index, partner_index, product_weight,
+        second_weight, second_bias, partner_scores, norm_weight, norm_bias, positions,
+        float(norm_eps))
+
+
 def relation_linear(input: Tensor, weight: Tensor, bias: Tensor | None = None,
                     out_dtype: torch.dtype | None = None) -> Tensor:
     """``input @ weight.T + bias`` on MFMA (bf16/f16 weights) or fp32 FMA (fp32 weights)."""

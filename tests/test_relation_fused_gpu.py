@@ -1,0 +1,161 @@
+"""GPU parity of the fused relation reduce (hidden -> second linear -> norm-reduce).
+
+The fused op has no reference counterpart; the reference runs the three ops in
+sequence (benchmarks/benchmark_relation_reduce.py:55-64).  It is checked
+  * against the float64 oracle chain with the hidden rounded to bf16 before the
+    second linear (what the bf16 linear of the unfused path sees), and
+  * against this library's own unfused three-op chain on the same inputs.
+Tolerance: bf16 inputs, absolute error <= 2e-2 (north_star).  A 5e-3 bound is
+asserted too so that a dropped or mis-indexed term cannot hide under the loose
+one; what remains is the rare hidden value that lands on the other side of a
+bf16 rounding boundary (different fp32 summation order), worth ~1e-3 at most.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reduce as ored
+from relation_lm.kernels.relation_reduce import (
+    relation_hidden_cached_seq,
+    relation_linear,
+    relation_norm_reduce_seq,
+    relation_reduce_fused_seq,
+)
+from relation_lm.workloads import CONFIGS, RelationConfig, reduce_inputs
+
+pytestmark = pytest.mark.gpu
+
+BF16_ABS = 2e-2
+TIGHT_ABS = 5e-3
+
+
+def host(t):
+    return t.detach().float().cpu().numpy() if t.dtype.is_floating_point else t.cpu().numpy()
+
+
+def abs_err(got, expected):
+    return float(np.abs(np.asarray(got, np.float64) - np.asarray(expected, np.float64)).max())
+
+
+def indices_and_scores(batch, queries, context, k, seed, *, sentinels=True):
+    """Anchor/partner indices over the causal history plus partner scores.
+
+    Query tq sits at position tq (the sequence form of cfg2); partner slots past
+    the available history carry the select op's sentinel (t-LOCAL+1, -inf).
+    """
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.arange(queries)
+    anchor = (torch.rand(batch, queries, generator=g) * (pos + 1)).long()
+    partner = (torch.rand(batch, queries, k, generator=g) * (pos[None, :, None] + 1)).long()
+    scores = torch.randn(batch, queries, k, generator=g)
+    if sentinels:
+        few = pos < k  # fewer than k candidates: trailing slots are sentinels
+        for t in range(min(queries, k)):
+            partner[:, t, t:] = t - 64 + 1
+            scores[:, t, t:] = -torch.inf
+        assert few.any()
+    return anchor.int(), partner.int(), scores, pos
+
+
+def oracle_chain(red, expanded, anchor, partner, scores, positions, rows=slice(None)):
+    """float64 chain on the device's bf16 expanded cache, hidden rounded to bf16."""
+    expanded = host(expanded)
+    hidden = ored.relation_hidden_cached_seq(expanded[rows], host(red["operand_cache"])[rows],
+                                             anchor[rows], partner[rows],
+                                             host(red["product_weight"]))
+    hidden = ored.round_to(hidden, "bfloat16")
+    raw = ored.linear(hidden, host(red["second_weight"]), host(red["second_bias"]))
+    return ored.relation_norm_reduce_seq(raw, scores[rows], host(red["norm_weight"]),
+                                         host(red["norm_bias"]), positions, 1e-5)
+
+
+def run_fused(red, expanded, anchor, partner, scores, positions, device):
+    return relation_reduce_fused_seq(expanded, red["operand_cache"], anchor.to(device),
+                                     partner.to(device), red["product_weight"],
+                                     red["second_weight"], red["second_bias"], scores.to(device),
+                                     red["norm_weight"], red["norm_bias"], positions.to(device),
+                                     1e-5)
+
+
+def run_unfused(red, expanded, anchor, partner, scores, positions, device):
+    hidden = relation_hidden_cached_seq(expanded, red["operand_cache"], anchor.to(device),
+                                        partner.to(device), red["product_weight"])
+    raw = relation_linear(hidden, red["second_weight"], red["second_bias"],
+                          out_dtype=torch.float32)
+    return relation_norm_reduce_seq(raw, scores.to(device), red["norm_weight"],
+                                    red["norm_bias"], positions.to(device), 1e-5)
+
+
+def test_cfg2_fused_matches_unfused_and_oracle(device):
+    cfg = CONFIGS["cfg2"]
+    red = reduce_inputs(cfg, device=device)
+    expanded = relation_linear(red["operand_cache"], red["expanded_weight"], red["expanded_bias"])
+    anchor, partner, scores, pos = indices_and_scores(cfg.batch, cfg.context, cfg.context,
+                                                      cfg.k_out, seed=31)
+    fused = run_fused(red, expanded, anchor, partner, scores, pos, device)
+    unfused = run_unfused(red, expanded, anchor, partner, scores, pos, device)
+    torch.cuda.synchronize()
+    assert fused.shape == (cfg.batch, cfg.context, cfg.d_model)
+    assert torch.isfinite(fused).all()
+    assert abs_err(host(fused), host(unfused)) <= TIGHT_ABS
+    # oracle on batch row 0, the first 96 queries (covers the sentinel slots)
+    rows = slice(0, 1)
+    expected = oracle_chain(red, expanded, host(anchor)[:, :96], host(partner)[:, :96],
+                            host(scores)[:, :96], np.arange(96), rows)
+    got = host(fused)[0:1, :96]
+    assert abs_err(got, expected) <= BF16_ABS
+    assert abs_err(got, expected) <= TIGHT_ABS
+
+
+@pytest.mark.parametrize("k_out", [1, 2, 4, 16])
+@pytest.mark.parametrize("d_model", [256, 384])
+def test_fused_partner_counts_and_widths(device, k_out, d_model):
+    cfg = RelationConfig("fused", 2, 96, d_model, 32, 64, 2, k_out, torch.bfloat16,
+                         relation_dim=64, hidden_dim=256, seed=777 + k_out)
+    red = reduce_inputs(cfg, device=device)
+    expanded = relation_linear(red["operand_cache"], red["expanded_weight"], red["expanded_bias"])
+    anchor, partner, scores, pos = indices_and_scores(2, 96, 96, k_out, seed=5 + k_out)
+    fused = run_fused(red, expanded, anchor, partner, scores, pos, device)
+    unfused = run_unfused(red, expanded, anchor, partner, scores, pos, device)
+    torch.cuda.synchronize()
+    assert abs_err(host(fused), host(unfused)) <= TIGHT_ABS
+    expected = oracle_chain(red, expanded, host(anchor), host(partner), host(scores),
+                            np.arange(96))
+    assert abs_err(host(fused), expected) <= TIGHT_ABS
+
+
+def test_fused_batched_positions_and_ragged_rows(device):
+    """[B,Tq] positions, Tq not a multiple of the workgroup's 16 queries."""
+    cfg = RelationConfig("fused", 3, 80, 512, 16, 32, 2, 8, torch.bfloat16,
+                         relation_dim=128, hidden_dim=384, seed=4321)
+    red = reduce_inputs(cfg, device=device)
+    expanded = relation_linear(red["operand_cache"], red["expanded_weight"], red["expanded_bias"])
+    anchor, partner, scores, _ = indices_and_scores(3, 37, 80, 8, seed=9, sentinels=False)
+    positions = torch.stack([torch.arange(37) + 40, torch.arange(37) + 3, torch.arange(37)])
+    fused = run_fused(red, expanded, anchor, partner, scores, positions, device)
+    unfused = run_unfused(red, expanded, anchor, partner, scores, positions, device)
+    torch.cuda.synchronize()
+    assert fused.shape == (3, 37, 512)
+    assert abs_err(host(fused), host(unfused)) <= TIGHT_ABS
+
+
+def test_fused_rejects_unsupported_shapes(device):
+    cfg = CONFIGS["cfg3"]  # d_model 576 is outside the fused kernel's register budget
+    red = reduce_inputs(RelationConfig(**{**cfg.__dict__, "batch": 1}), device=device)
+    expanded = relation_linear(red["operand_cache"], red["expanded_weight"], red["expanded_bias"])
+    anchor = torch.zeros(1, 4, dtype=torch.int32, device=device)
+    partner = torch.zeros(1, 4, 8, dtype=torch.int32, device=device)
+    scores = torch.zeros(1, 4, 8, device=device)
+    with pytest.raises(RuntimeError, match="d_model"):
+        relation_reduce_fused_seq(expanded, red["operand_cache"], anchor, partner,
+                                  red["product_weight"], red["second_weight"],
+                                  red["second_bias"], scores, red["norm_weight"],
+                                  red["norm_bias"], torch.arange(4, device=device), 1e-5)
+    with pytest.raises(RuntimeError, match="bfloat16"):
+        relation_reduce_fused_seq(expanded.float(), red["operand_cache"].float(), anchor,
+                                  partner, red["product_weight"].float(),
+                                  red["second_weight"].float(), red["second_bias"], scores,
+                                  red["norm_weight"], red["norm_bias"],
+                                  torch.arange(4, device=device), 1e-5)
