@@ -9,24 +9,27 @@
 //
 // Mapping: a workgroup of 8 waves (2 per SIMD) owns 128 consecutive
 // (query, partner) rows, so it holds whole queries (K in {1, 2, 4, 8, 16}).
-//   set-up   the exact hi/lo bf16 split of every row's operand product
-//            (op[anchor] * op[partner], exact in fp32) goes to LDS, and the
-//            row's active-K softmax weight is computed once.
+//   set-up   wave w keeps the exact hi/lo bf16 split of the operand products
+//            (op[anchor] * op[partner], exact in fp32) of rows 16w..16w+15 in
+//            registers; the rows' active-K softmax weights and the b2 / gamma /
+//            beta vectors go to LDS.
 //   phase 1  per 128-column chunk of the hidden dimension, wave w forms
-//            hidden^T[64 cols x 32 rows] = W_m[chunk cols] . P^T on the matrix
-//            cores (A = W_m rows streamed from L2, B = P hi and lo from LDS),
-//            starting from the gathered expanded-cache halves, applies GELU and
-//            rounds to bf16 -- the operand the unfused path's bf16 second
-//            linear sees -- into a double-buffered LDS hidden chunk.  The
-//            transposed product leaves 4 consecutive hidden columns of one row
-//            in a lane, so the gathers are 8-byte loads and the LDS writes
-//            ds_write_b64.
+//            hidden^T[128 cols x its 16 rows] = W_m[chunk] . P^T on the matrix
+//            cores, adds the rows' expanded-cache halves, applies GELU and
+//            rounds to bf16 -- the operand the unfused path's bf16 second linear
+//            sees -- into the LDS hidden chunk.  The W_m chunk and the gathered
+//            expanded-cache halves of the 128 rows reach LDS by LDS-DMA
+//            (buffer_load ... lds), issued while the previous chunk's phase 2
+//            runs.  The transposed product leaves 4 consecutive hidden columns
+//            of one row in a lane, so the LDS writes are ds_write_b64.
 //   phase 2  raw[128 rows x D/8 cols of wave w] += hidden chunk . W2^T; the
-//            hidden fragments come from LDS, W2 fragments from L2, and the raw
-//            accumulators stay in registers for the whole kernel.
+//            hidden fragments come from LDS, W2 fragments from L2 one k-step
+//            ahead, and the raw accumulators stay in registers for the whole
+//            kernel.  Two waves per SIMD let one wave's GELU work overlap the
+//            other's matrix-core work.
 // Epilogue: + b2, LayerNorm per row (moments combined across the 8 waves in
 // LDS), partner weights, sum over the query's rows (in-lane, then the
-// neighbouring 16-lane groups), fp32 store.
+// neighbouring 16-lane groups), fp32 buffer stores.
 #include "rlm_common.hpp"
 
 namespace rlm {
@@ -41,17 +44,27 @@ constexpr int kThreads = kWaves * kWave;
 constexpr int kRows = 128;                 // (query, partner) rows per workgroup
 constexpr int kRowTiles = kRows / 16;
 constexpr int kHC = 128;                   // hidden columns per chunk
-constexpr int kMaxR = 128;                 // relation dim held in LDS
-constexpr int kLd = 136;                   // LDS row stride (bf16): 128 + 8, conflict-free b128 reads
-constexpr int kTileElems = kRows * kLd;    // one [128 x kLd] bf16 LDS tile
-constexpr size_t kLdsBytes =
-    static_cast<size_t>(4 * kTileElems) * 2 + (kRows + 2 * kRows + kWaves * kRows) * 4;
+constexpr int kMaxR = 128;
+constexpr int kMaxD = 512;
+constexpr int kLd = 136;                   // hidden row stride (bf16): conflict-free b128 reads
+// LDS layout (bytes): the W_m chunk, the gathered expanded-cache halves of the
+// chunk ([128 rows][anchor half 256 B | partner half 256 B]), the hidden chunk,
+// fp32 vectors, the rows' expanded-cache byte offsets.
+constexpr int kWmBytes = kHC * kMaxR * 2;
+constexpr int kGatherRowBytes = 2 * kHC * 2;
+constexpr int kOffGather = kWmBytes;
+constexpr int kOffHid = kOffGather + kRows * kGatherRowBytes;
+constexpr int kOffF32 = kOffHid + kRows * kLd * 2;
+constexpr int kF32Words = kRows + 2 * kRows + kWaves * kRows + 3 * kMaxD;
+constexpr int kOffRowOff = kOffF32 + kF32Words * 4;
+constexpr size_t kLdsBytes = static_cast<size_t>(kOffRowOff) + kRows * 2 * 4;
+constexpr int kWaitVm0 = 0x0F70;           // s_waitcnt vmcnt(0), other counters untouched
 
 struct FusedParams {
-  int64_t B, Tq, T;
-  int R, H, D, K;
-  int64_t rows;        // B*Tq*K
-  int64_t queries;     // B*Tq
+  int64_t T;
+  uint32_t Tq, K, k_log2, R, H, D;
+  uint32_t rows;       // B*Tq*K
+  uint32_t queries;    // B*Tq
   const void* expanded;   // [B,T,2H] bf16
   const void* operand;    // [B,T,R] bf16
   const void* anchor;     // [B*Tq]
@@ -78,11 +91,22 @@ __device__ __forceinline__ f32x4 mfma_bf16(const u16x8& a, const u16x8& b, f32x4
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ u16x8 lds_frag(const uint16_t* p) {
+__device__ __forceinline__ u16x8 lds_frag(const unsigned char* p) {
   return *reinterpret_cast<const u16x8*>(p);
 }
 
 __device__ __forceinline__ u16x8 as_frag(uint4 v) { return __builtin_bit_cast(u16x8, v); }
+
+// 16 bytes per lane from global memory straight into LDS: lane i's bytes land
+// at lds_addr + 16*i.  Issued as inline assembly so that the compiler does not
+// follow it with a full vmcnt(0) before the next LDS access; the caller waits
+// (s_waitcnt vmcnt(0) + barrier) before the tile is read.
+__device__ __forceinline__ void lds_dma16(rsrc_t r, uint32_t lds_addr, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
 
 // Row sum over the 16 lanes of a DPP row (every lane gets the same bits).
 __device__ __forceinline__ float row16_sum(float v) {
@@ -93,93 +117,133 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
-// Weight p_k of row `grow` in its query's partner mixture: softmax over the
-// active partners (rank < k_limit, score > -1e30; inactive scores -1e4),
-// renormalised by max(sum, 1e-9) -- relation_reduce.py:399-411.
-__device__ float row_weight(const FusedParams& p, int64_t grow) {
-  if (grow >= p.rows) return 0.0f;
-  const int K = p.K;
-  const int64_t q = grow / K;
-  const int k = static_cast<int>(grow - q * K);
-  const int64_t b = q / p.Tq;
+// Weight p_k of row `grow` (< rows) in its query's partner mixture: softmax
+// over the active partners (rank < k_limit, score > -1e30; inactive scores
+// -1e4), renormalised by max(sum, 1e-9) -- relation_reduce.py:399-411.
+__device__ float row_weight(const FusedParams& p, uint32_t grow) {
+  const uint32_t K = p.K;
+  const uint32_t q = grow >> p.k_log2;
+  const uint32_t k = grow & (K - 1);
+  const uint32_t b = q / p.Tq;
   const int64_t t = load_any_i(p.pos, p.pos_dtype, b * p.pos_sb + (q - b * p.Tq) * p.pos_sq);
   const int64_t n = t + 1;
   int k_limit = n > 0 ? 64 - __clzll(static_cast<unsigned long long>(n)) : 0;  // ceil(log2(t+2))
-  k_limit = k_limit < 1 ? 1 : (k_limit > K ? K : k_limit);
-  const float* sq = p.scores + q * K;
+  k_limit = k_limit < 1 ? 1 : (k_limit > static_cast<int>(K) ? static_cast<int>(K) : k_limit);
+  const float* sq = p.scores + static_cast<size_t>(q) * K;
+  float sc[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) sc[c] = c < static_cast<int>(K) ? sq[c] : -INFINITY;
   float m = -INFINITY;
-  for (int c = 0; c < K; ++c) {
-    const float sc = sq[c];
-    m = fmaxf(m, (c < k_limit && sc > -1.0e30f) ? sc : -1.0e4f);
-  }
+#pragma unroll
+  for (int c = 0; c < 16; ++c)
+    if (c < static_cast<int>(K)) m = fmaxf(m, (c < k_limit && sc[c] > -1.0e30f) ? sc[c] : -1.0e4f);
   float total = 0.0f, mine = 0.0f;
-  for (int c = 0; c < K; ++c) {
-    const float sc = sq[c];
-    const float pc = (c < k_limit && sc > -1.0e30f) ? expf(sc - m) : 0.0f;
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    const float pc = (c < k_limit && sc[c] > -1.0e30f) ? expf(sc[c] - m) : 0.0f;
     total += pc;
-    mine = c == k ? pc : mine;
+    mine = c == static_cast<int>(k) ? pc : mine;
   }
   return mine / fmaxf(total, 1.0e-9f);
-}
-
-struct RowIndex {
-  int32_t b, a, p;  // a / p = -1 when out of range
-};
-
-__device__ __forceinline__ RowIndex row_index(const FusedParams& p, int64_t grow) {
-  RowIndex r{0, -1, -1};
-  if (grow < p.rows) {
-    const int64_t q = grow / p.K;
-    r.b = static_cast<int32_t>(q / p.Tq);
-    const int64_t ai = load_any_i(p.anchor, p.index_dtype_a, q);
-    const int64_t pi = load_any_i(p.partner, p.index_dtype_p, grow);
-    r.a = (ai >= 0 && ai < p.T) ? static_cast<int32_t>(ai) : -1;
-    r.p = (pi >= 0 && pi < p.T) ? static_cast<int32_t>(pi) : -1;
-  }
-  return r;
 }
 
 __device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
 
+// Streams rows [chunk*128, chunk*128+128) of W_m into an LDS tile of 128 rows
+// x R bf16.  16-byte piece q of row n is stored at piece q ^ (n % (R/8)) so
+// that the 16 rows of an MFMA fragment read hit distinct banks.
+template <int KS1>
+__device__ __forceinline__ void dma_wm_chunk(rsrc_t wmr, uint32_t tile, int chunk, int wave,
+                                             int lane) {
+  constexpr int R = KS1 * 32;
+  constexpr int QPR = R / 8;                               // pieces per row
+  constexpr int kInsts = kHC * QPR / (kWaves * kWave);     // DMA instructions per lane
+#pragma unroll
+  for (int i = 0; i < kInsts; ++i) {
+    const int slot = (i * kWaves + wave) * kWave + lane;   // LDS piece written by this lane
+    const int n = slot / QPR;
+    const int src = (slot % QPR) ^ (n % QPR);
+    const uint32_t voff = (static_cast<uint32_t>(chunk * kHC + n) * R + 8 * src) * 2u;
+    lds_dma16(wmr, __builtin_amdgcn_readfirstlane(tile + (i * kWaves + wave) * kWave * 16), voff);
+  }
+}
+
+// Gathered expanded-cache halves of one chunk: LDS row m holds the anchor
+// half's columns [chunk*128, +128) then the partner half's, 16 pieces of 16 B
+// each, piece q stored at q ^ (m % 16).  Lane `lane` of DMA instruction i of
+// wave w writes piece lane % 32 of row 2*(kWaves*i + w) + lane / 32; src[i] is
+// that piece's byte offset for chunk 0 (kNoOffset for a missing row: zeros).
+constexpr int kGatherInsts = kRows * kGatherRowBytes / 16 / kThreads;
+__device__ __forceinline__ void dma_gather_chunk(rsrc_t xr, uint32_t tile,
+                                                 const uint32_t (&src)[kGatherInsts], int chunk,
+                                                 int wave) {
+#pragma unroll
+  for (int i = 0; i < kGatherInsts; ++i)
+    lds_dma16(xr, __builtin_amdgcn_readfirstlane(tile + (i * kWaves + wave) * kWave * 16),
+              src[i] == kNoOffset ? kNoOffset : src[i] + chunk * kHC * 2u);
+}
+
 template <int DT, int KS1>
 __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParams p) {
+  // DT = 16-column tiles of D per wave in phase 2 (D = 128*DT); KS1 = R/32.
   extern __shared__ __align__(16) unsigned char smem[];
-  uint16_t* phi = reinterpret_cast<uint16_t*>(smem);   // [kRows][kLd] products, bf16 high part
-  uint16_t* plo = phi + kTileElems;                     // low part
-  uint16_t* hid0 = plo + kTileElems;                    // two [kRows][kLd] hidden chunks
-  float* wts = reinterpret_cast<float*>(hid0 + 2 * kTileElems);  // [kRows]
-  float* mom = wts + kRows;                             // [2][kRows] mean, rstd
-  float* part = mom + 2 * kRows;                        // [kWaves][kRows]
+  unsigned char* hid = smem + kOffHid;                            // [kRows][kLd] bf16
+  float* wts = reinterpret_cast<float*>(smem + kOffF32);           // [kRows]
+  float* mom = wts + kRows;                                        // [2][kRows] mean, rstd
+  float* part = mom + 2 * kRows;                                   // [kWaves][kRows]
+  float* cst = part + kWaves * kRows;                              // [3][kMaxD] b2, gamma, beta
+  uint32_t* rowoff = reinterpret_cast<uint32_t*>(smem + kOffRowOff);  // [kRows][2]
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
 
+  constexpr int R = KS1 * 32;
+  constexpr int QPR = R / 8;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
   const int r16 = lane & 15;
   const int g = lane >> 4;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kRows;
+  const uint32_t row0 = blockIdx.x * kRows;
+  const uint32_t H = p.H;
   const rsrc_t xr = make_rsrc(p.expanded, p.expanded_bytes);
   const rsrc_t opr = make_rsrc(p.operand, p.operand_bytes);
   const rsrc_t wmr = make_rsrc(p.wm, p.wm_bytes);
   const rsrc_t w2r = make_rsrc(p.w2, p.w2_bytes);
-  const int R = KS1 * 32, H = p.H;
 
-  // ---- Set-up: partner weights and the hi/lo operand products.
-  if (tid < kRows) wts[tid] = row_weight(p, row0 + tid);
+  // ---- Set-up.
+  dma_wm_chunk<KS1>(wmr, lds0, 0, wave, lane);
+  // This lane's phase-1 row: 16*wave + r16.
+  const int lrow = 16 * wave + r16;
+  u16x8 ph[KS1], pl[KS1];
   {
-    constexpr int cpr = KS1 * 4;  // 16-byte chunks per row
-    for (int i = tid; i < kRows * cpr; i += kThreads) {
-      const int r = i / cpr;
-      const int c = i % cpr;
-      const RowIndex ix = row_index(p, row0 + r);
-      const bool ok = ix.a >= 0 && ix.p >= 0;
-      const uint32_t base = static_cast<uint32_t>(ix.b) * static_cast<uint32_t>(p.T);
-      const uint32_t oa = ok ? ((base + ix.a) * R + 8 * c) * 2u : kNoOffset;
-      const uint32_t op = ok ? ((base + ix.p) * R + 8 * c) * 2u : kNoOffset;
-      const uint4 va = buf_load_b128(opr, oa);
-      const uint4 vp = buf_load_b128(opr, op);
-      const uint32_t wa[4] = {va.x, va.y, va.z, va.w};
-      const uint32_t wp[4] = {vp.x, vp.y, vp.z, vp.w};
+    const uint32_t grow = row0 + lrow;
+    int32_t a = -1, pp = -1;
+    uint32_t base = 0;
+    if (grow < p.rows) {
+      const uint32_t q = grow >> p.k_log2;
+      base = (q / p.Tq) * static_cast<uint32_t>(p.T);
+      const int64_t ai = load_any_i(p.anchor, p.index_dtype_a, q);
+      const int64_t pi = load_any_i(p.partner, p.index_dtype_p, grow);
+      a = (ai >= 0 && ai < p.T) ? static_cast<int32_t>(ai) : -1;
+      pp = (pi >= 0 && pi < p.T) ? static_cast<int32_t>(pi) : -1;
+    }
+    if (g == 0) {
+      rowoff[2 * lrow] = a >= 0 ? (base + a) * (4u * H) : kNoOffset;               // anchor, first half
+      rowoff[2 * lrow + 1] = pp >= 0 ? (base + pp) * (4u * H) + 2u * H : kNoOffset;  // partner, second half
+    }
+    const bool ok = a >= 0 && pp >= 0;
+    const uint32_t oa = ok ? (base + a) * (2u * R) + 16u * g : kNoOffset;
+    const uint32_t op = ok ? (base + pp) * (2u * R) + 16u * g : kNoOffset;
+    uint4 va[KS1], vp[KS1];
+#pragma unroll
+    for (int s = 0; s < KS1; ++s) {
+      va[s] = buf_load_b128(opr, ok ? oa + 64u * s : kNoOffset);
+      vp[s] = buf_load_b128(opr, ok ? op + 64u * s : kNoOffset);
+    }
+#pragma unroll
+    for (int s = 0; s < KS1; ++s) {
+      const uint32_t wa[4] = {va[s].x, va[s].y, va[s].z, va[s].w};
+      const uint32_t wp[4] = {vp[s].x, vp[s].y, vp[s].z, vp[s].w};
       uint32_t h[4], l[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -188,37 +252,40 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
         h[k] = pack_bf16x2(x0, x1);
         l[k] = pack_bf16x2(x0 - bf16_lo(h[k]), x1 - bf16_hi(h[k]));
       }
-      *reinterpret_cast<uint4*>(phi + r * kLd + 8 * c) = make_uint4(h[0], h[1], h[2], h[3]);
-      *reinterpret_cast<uint4*>(plo + r * kLd + 8 * c) = make_uint4(l[0], l[1], l[2], l[3]);
+      ph[s] = as_frag(make_uint4(h[0], h[1], h[2], h[3]));
+      pl[s] = as_frag(make_uint4(l[0], l[1], l[2], l[3]));
     }
   }
-
-  // Phase-1 roles: row tiles 2*rg, 2*rg+1 and chunk columns [64*cg, 64*cg+64).
-  const int rg = wave >> 1, cg = wave & 1;
-  uint32_t xa_off[2], xp_off[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const RowIndex ix = row_index(p, row0 + 32 * rg + 16 * i + r16);
-    const uint32_t base = static_cast<uint32_t>(ix.b) * static_cast<uint32_t>(p.T);
-    xa_off[i] = ix.a >= 0 ? (base + ix.a) * (4u * H) : kNoOffset;           // anchor row, first half
-    xp_off[i] = ix.p >= 0 ? (base + ix.p) * (4u * H) + 2u * H : kNoOffset;  // partner row, second half
+  if (tid < kRows) wts[tid] = row0 + tid < p.rows ? row_weight(p, row0 + tid) : 0.0f;
+  for (int i = tid; i < static_cast<int>(p.D); i += kThreads) {
+    cst[i] = load_any_f(p.b2, p.b2_dtype, i);
+    cst[kMaxD + i] = load_any_f(p.gamma, p.gamma_dtype, i);
+    cst[2 * kMaxD + i] = load_any_f(p.beta, p.beta_dtype, i);
   }
-  // W_m fragments (A operand of phase 1): rows chunk*128 + 64cg + 16j + r16, k = 32s + 8g.
-  const uint32_t wm_lane = (static_cast<uint32_t>(64 * cg + r16) * R + 8 * g) * 2u;
-  auto load_wm = [&](u16x8 (&w)[4], int chunk, int s) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      w[j] = as_frag(buf_load_b128(
-          wmr, wm_lane + (static_cast<uint32_t>(chunk * kHC + 16 * j) * R + 32 * s) * 2u));
-  };
-  // W2 fragments (B operand of phase 2): rows dcol0 + 16j + r16, k = chunk*128 + 32s + 8g.
-  const int dcol0 = wave * DT * 16;    // this wave's phase-2 output columns
+
+  // W2 fragments (B operand of phase 2) in groups of JC column tiles: rows
+  // dcol0 + 16(JC*jg + j) + r16, k = chunk*128 + 32s + 8g.
+  constexpr int JC = (DT % 2 == 0) ? DT / 2 : DT;
+  constexpr int NG = DT / JC;
+  const int dcol0 = wave * DT * 16;
   const uint32_t w2_lane = (static_cast<uint32_t>(dcol0 + r16) * H + 8 * g) * 2u;
-  auto load_w2 = [&](u16x8 (&w)[DT], int chunk, int s) {
+  auto load_w2 = [&](u16x8 (&w)[JC], int chunk, int jg, int s) {
 #pragma unroll
-    for (int j = 0; j < DT; ++j)
+    for (int j = 0; j < JC; ++j)
       w[j] = as_frag(buf_load_b128(
-          w2r, w2_lane + (static_cast<uint32_t>(16 * j) * H + chunk * kHC + 32 * s) * 2u));
+          w2r, w2_lane + (16u * (JC * jg + j) * H + chunk * kHC + 32 * s) * 2u));
+  };
+  // Gather DMA sources of this lane (piece lane%32 of row 2*(8i + wave) + lane/32), chunk 0.
+  auto gather_chunk = [&](int chunk) {
+    uint32_t src[kGatherInsts];
+#pragma unroll
+    for (int i = 0; i < kGatherInsts; ++i) {
+      const int m = 2 * (i * kWaves + wave) + lane / 32;
+      const int q = lane & 31;
+      const uint32_t base = rowoff[2 * m + q / 16];
+      src[i] = base == kNoOffset ? kNoOffset : base + 16u * ((q & 15) ^ (m & 15));
+    }
+    dma_gather_chunk(xr, lds0 + kOffGather, src, chunk, wave);
   };
 
   f32x4 raw[kRowTiles][DT];
@@ -227,93 +294,95 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
 #pragma unroll
     for (int j = 0; j < DT; ++j) raw[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+  const unsigned char* my_gat = smem + kOffGather + lrow * kGatherRowBytes;
+  unsigned char* my_hid = hid + lrow * (2 * kLd) + 8 * g;
+
   const int nchunks = H / kHC;
-  u16x8 wa[4];
-  load_wm(wa, 0, 0);
-  __syncthreads();  // products and weights visible
+  __syncthreads();  // row offsets visible
+  gather_chunk(0);
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this lane's W_m and gather pieces of chunk 0 are in LDS
+  __syncthreads();
 
   for (int c = 0; c < nchunks; ++c) {
-    uint16_t* hid = hid0 + (c & 1) * kTileElems;
-    u16x8 b[DT];
-    // ---- Phase 1: hidden^T[chunk cols 64*cg.. x rows 32*rg..] on the matrix cores.
-    {
-      // Expanded-cache halves of this lane's hidden entries (added after the products).
-      uint2 ga[2][4], gp[2][4];
-      const uint32_t col = 2u * static_cast<uint32_t>(c * kHC + 64 * cg + 4 * g);
+    // ---- Phase 1, two halves of 64 columns: hidden^T[cols x 16 rows of this wave].
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+    for (int hh = 0; hh < 2; ++hh) {
+      f32x4 acc[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          ga[i][j] = buf_load_b64(xr, xa_off[i] == kNoOffset ? kNoOffset : xa_off[i] + col + 32u * j);
-          gp[i][j] = buf_load_b64(xr, xp_off[i] == kNoOffset ? kNoOffset : xp_off[i] + col + 32u * j);
-        }
-      f32x4 acc[2][4];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int jj = 0; jj < 4; ++jj) acc[jj] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int s = 0; s < KS1; ++s) {
-        u16x8 wn[4];
-        if (s + 1 < KS1) load_wm(wn, c, s + 1);
-        else load_w2(b, c, 0);
+        // A fragment: W_m tile row 16j + r16, k-piece (4s + g) stored swizzled.
+        const uint32_t frag = r16 * (2u * R) + 16u * ((4 * s + g) ^ (r16 % QPR));
+        u16x8 w[4];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int m = 32 * rg + 16 * i + r16;
-          const u16x8 bh = lds_frag(phi + m * kLd + 32 * s + 8 * g);
-          const u16x8 bl = lds_frag(plo + m * kLd + 32 * s + 8 * g);
+        for (int jj = 0; jj < 4; ++jj) w[jj] = lds_frag(smem + (16 * (4 * hh + jj)) * (2 * R) + frag);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            acc[i][j] = mfma_bf16(wa[j], bh, acc[i][j]);
-            acc[i][j] = mfma_bf16(wa[j], bl, acc[i][j]);
-          }
-        }
-        if (s + 1 < KS1) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) wa[j] = wn[j];
+        for (int jj = 0; jj < 4; ++jj) {
+          acc[jj] = mfma_bf16(w[jj], ph[s], acc[jj]);
+          acc[jj] = mfma_bf16(w[jj], pl[s], acc[jj]);
         }
       }
-      // acc[i][j][e] = hidden[row 32rg+16i+r16][col 64cg+16j+4g+e]
+      // acc[jj][e] = hidden[row lrow][col 16(4hh+jj) + 4g + e]; the row's
+      // expanded-cache values for those columns sit in piece 2j + g/2.
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float h0 = acc[i][j][0] + (bf16_lo(ga[i][j].x) + bf16_lo(gp[i][j].x));
-          const float h1 = acc[i][j][1] + (bf16_hi(ga[i][j].x) + bf16_hi(gp[i][j].x));
-          const float h2 = acc[i][j][2] + (bf16_lo(ga[i][j].y) + bf16_lo(gp[i][j].y));
-          const float h3 = acc[i][j][3] + (bf16_hi(ga[i][j].y) + bf16_hi(gp[i][j].y));
-          const uint32_t lo = pack_bf16x2(gelu_erf(h0), gelu_erf(h1));
-          const uint32_t hi = pack_bf16x2(gelu_erf(h2), gelu_erf(h3));
-          *reinterpret_cast<uint2*>(hid + (32 * rg + 16 * i + r16) * kLd + 64 * cg + 16 * j +
-                                    4 * g) = make_uint2(lo, hi);
-        }
-    }
-    __syncthreads();  // hidden chunk complete; the other buffer is free for chunk c+1
-    // ---- Phase 2: raw[128 x 16*DT] += hidden chunk . W2[cols, chunk]^T.
-#pragma unroll
-    for (int s = 0; s < kHC / 32; ++s) {
-      u16x8 bn[DT];
-      if (s + 1 < kHC / 32) load_w2(bn, c, s + 1);
-      else if (c + 1 < nchunks) load_wm(wa, c + 1, 0);
-      u16x8 a[kRowTiles];
-#pragma unroll
-      for (int i = 0; i < kRowTiles; ++i) a[i] = lds_frag(hid + (16 * i + r16) * kLd + 32 * s + 8 * g);
-#pragma unroll
-      for (int i = 0; i < kRowTiles; ++i)
-#pragma unroll
-        for (int j = 0; j < DT; ++j) raw[i][j] = mfma_bf16(a[i], b[j], raw[i][j]);
-      if (s + 1 < kHC / 32) {
-#pragma unroll
-        for (int j = 0; j < DT; ++j) b[j] = bn[j];
+      for (int jj = 0; jj < 4; ++jj) {
+        const int j = 4 * hh + jj;
+        const int piece = ((2 * j + (g >> 1)) ^ r16) * 16 + 8 * (g & 1);
+        const uint2 ga = *reinterpret_cast<const uint2*>(my_gat + piece);
+        const uint2 gp = *reinterpret_cast<const uint2*>(my_gat + 256 + piece);
+        const float h0 = acc[jj][0] + (bf16_lo(ga.x) + bf16_lo(gp.x));
+        const float h1 = acc[jj][1] + (bf16_hi(ga.x) + bf16_hi(gp.x));
+        const float h2 = acc[jj][2] + (bf16_lo(ga.y) + bf16_lo(gp.y));
+        const float h3 = acc[jj][3] + (bf16_hi(ga.y) + bf16_hi(gp.y));
+        *reinterpret_cast<uint2*>(my_hid + 32 * j) =
+            make_uint2(pack_bf16x2(gelu_erf(h0), gelu_erf(h1)),
+                       pack_bf16x2(gelu_erf(h2), gelu_erf(h3)));
       }
     }
+    u16x8 b[JC];
+    load_w2(b, c, 0, 0);
+    __syncthreads();  // hidden chunk complete; the W_m and gather tiles are free
+    if (c + 1 < nchunks) {
+      dma_wm_chunk<KS1>(wmr, lds0, c + 1, wave, lane);
+      gather_chunk(c + 1);
+    }
+    // ---- Phase 2: raw[128 x 16*DT] += hidden chunk . W2[cols, chunk]^T, JC column
+    // tiles at a time (W2 fragments of the next k-step in flight), row tile by
+    // row tile (the next hidden fragment in flight).
+#pragma unroll
+    for (int jg = 0; jg < NG; ++jg) {
+#pragma unroll
+      for (int s = 0; s < kHC / 32; ++s) {
+        u16x8 bn[JC];
+        if (s + 1 < kHC / 32) load_w2(bn, c, jg, s + 1);
+        else if (jg + 1 < NG) load_w2(bn, c, jg + 1, 0);
+        const unsigned char* arow = hid + r16 * (2 * kLd) + 64 * s + 16 * g;
+        u16x8 a = lds_frag(arow);
+#pragma unroll
+        for (int i = 0; i < kRowTiles; ++i) {
+          u16x8 an;
+          if (i + 1 < kRowTiles) an = lds_frag(arow + (i + 1) * 16 * (2 * kLd));
+#pragma unroll
+          for (int j = 0; j < JC; ++j) raw[i][JC * jg + j] = mfma_bf16(a, b[j], raw[i][JC * jg + j]);
+          if (i + 1 < kRowTiles) a = an;
+        }
+        if (s + 1 < kHC / 32 || jg + 1 < NG) {
+#pragma unroll
+          for (int j = 0; j < JC; ++j) b[j] = bn[j];
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep each k-step's loads next to its products
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this lane's pieces of chunk c+1 are in LDS
+    __syncthreads();  // ... and everyone's; the hidden chunk is free again
   }
 
   // ---- Epilogue.  raw[i][j][e] = row 16i+4g+e, column dcol0+16j+r16.
   const float inv_d = 1.0f / static_cast<float>(p.D);
 #pragma unroll
   for (int j = 0; j < DT; ++j) {
-    const float bias = load_any_f(p.b2, p.b2_dtype, dcol0 + 16 * j + r16);
+    const float bias = cst[dcol0 + 16 * j + r16];
 #pragma unroll
     for (int i = 0; i < kRowTiles; ++i)
 #pragma unroll
@@ -365,50 +434,71 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
     mom[kRows + tid] = rsqrtf(sum * inv_d + p.eps);
   }
   __syncthreads();
-  // LayerNorm, weights, sum over each query's K consecutive rows, store.
-  const int K = p.K;
+  // LayerNorm, weights, sum over each query's K consecutive rows, store:
+  //   out[q] = sum_k w_k (gamma (x_k - mu_k) rs_k + beta)
+  //          = gamma * sum_k (A_k x_k - B_k) + beta * sum_k w_k,
+  // A_k = w_k rs_k, B_k = A_k mu_k, so each raw value costs one FMA.  The store
+  // descriptor covers this workgroup's queries only, so rows past the end of
+  // the last workgroup are dropped by the buffer bounds check.
+  const uint32_t K = p.K, D = p.D;
+  const uint32_t q0 = row0 >> p.k_log2;
+  const uint32_t nq = min(p.queries - q0, static_cast<uint32_t>(kRows) >> p.k_log2);
+  const rsrc_t outr = make_rsrc(p.out + static_cast<size_t>(q0) * D, nq * D * 4u);
+  float gm[DT], bt[DT];
+#pragma unroll
+  for (int j = 0; j < DT; ++j) {
+    gm[j] = cst[kMaxD + dcol0 + 16 * j + r16];
+    bt[j] = cst[2 * kMaxD + dcol0 + 16 * j + r16];
+  }
 #pragma unroll
   for (int i = 0; i < kRowTiles; ++i) {
     const float4 m4 = mean[i];
     const float4 r4 = *reinterpret_cast<const float4*>(mom + kRows + 16 * i + 4 * g);
     const float4 w4 = *reinterpret_cast<const float4*>(wts + 16 * i + 4 * g);
-    const float mu[4] = {m4.x, m4.y, m4.z, m4.w};
-    const float rs[4] = {r4.x, r4.y, r4.z, r4.w};
-    const float wt[4] = {w4.x, w4.y, w4.z, w4.w};
-    const int64_t trow = row0 + 16 * i + 4 * g;  // first row of this lane group
+    const float A[4] = {w4.x * r4.x, w4.y * r4.y, w4.z * r4.z, w4.w * r4.w};
+    const float nB[4] = {-A[0] * m4.x, -A[1] * m4.y, -A[2] * m4.z, -A[3] * m4.w};
+    const uint32_t lrow = 16 * i + 4 * g;  // first local row of this lane group
+    if (K >= 4) {
+      // Rows of one query: K = 4 -> this group, K = 8 -> groups {0,1} / {2,3}, K = 16 -> all.
+      float W = (w4.x + w4.y) + (w4.z + w4.w);
+      if (K >= 8) W += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(W), 0x401F));
+      if (K >= 16) W += __shfl_xor(W, 32, kWave);
+      const bool lead = (lrow & (K - 1)) == 0;
+      const uint32_t obase = (lrow >> p.k_log2) * D + dcol0 + r16;
 #pragma unroll
-    for (int j = 0; j < DT; ++j) {
-      const int n = dcol0 + 16 * j + r16;
-      const float gm = load_any_f(p.gamma, p.gamma_dtype, n);
-      const float bt = load_any_f(p.beta, p.beta_dtype, n);
-      float y[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        y[e] = wt[e] > 0.0f ? ((raw[i][j][e] - mu[e]) * rs[e] * gm + bt) * wt[e] : 0.0f;
-      if (K >= 4) {
-        // Rows of one query: K = 4 -> this group, K = 8 -> groups {0,1} / {2,3}, K = 16 -> all.
-        float v = (y[0] + y[1]) + (y[2] + y[3]);
+      for (int j = 0; j < DT; ++j) {
+        float v = fmaf(raw[i][j][0], A[0], nB[0]) + fmaf(raw[i][j][1], A[1], nB[1]) +
+                  (fmaf(raw[i][j][2], A[2], nB[2]) + fmaf(raw[i][j][3], A[3], nB[3]));
         if (K >= 8) v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
         if (K >= 16) v += __shfl_xor(v, 32, kWave);
-        const int lead = (g * 4 / K) * K / 4;
-        const int64_t q = trow / K;
-        if (g == lead && q < p.queries) p.out[q * p.D + n] = v;
-      } else if (K == 2) {
-        const int64_t q0 = trow / 2;
-        if (q0 < p.queries) p.out[q0 * p.D + n] = y[0] + y[1];
-        if (q0 + 1 < p.queries) p.out[(q0 + 1) * p.D + n] = y[2] + y[3];
-      } else {
+        if (lead) buf_store_f32(fmaf(gm[j], v, bt[j] * W), outr, (obase + 16 * j) * 4u);
+      }
+    } else if (K == 2) {
+      const float W0 = w4.x + w4.y, W1 = w4.z + w4.w;
+      const uint32_t obase = (lrow >> 1) * D + dcol0 + r16;
+#pragma unroll
+      for (int j = 0; j < DT; ++j) {
+        const float v0 = fmaf(raw[i][j][0], A[0], nB[0]) + fmaf(raw[i][j][1], A[1], nB[1]);
+        const float v1 = fmaf(raw[i][j][2], A[2], nB[2]) + fmaf(raw[i][j][3], A[3], nB[3]);
+        buf_store_f32(fmaf(gm[j], v0, bt[j] * W0), outr, (obase + 16 * j) * 4u);
+        buf_store_f32(fmaf(gm[j], v1, bt[j] * W1), outr, (obase + D + 16 * j) * 4u);
+      }
+    } else {
+      const float Wk[4] = {w4.x, w4.y, w4.z, w4.w};
+      const uint32_t obase = lrow * D + dcol0 + r16;
+#pragma unroll
+      for (int j = 0; j < DT; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (trow + e < p.queries) p.out[(trow + e) * p.D + n] = y[e];
-      }
+          buf_store_f32(fmaf(gm[j], fmaf(raw[i][j][e], A[e], nB[e]), bt[j] * Wk[e]), outr,
+                        (obase + e * D + 16 * j) * 4u);
     }
   }
 }
 
 template <int DT, int KS1>
 hipError_t launch_fused(const FusedParams& p, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>((p.rows + kRows - 1) / kRows));
+  const dim3 grid((p.rows + kRows - 1) / kRows);
   static bool attr_set = false;  // the LDS opt-in is a per-process function attribute
   if (!attr_set) {
     const hipError_t e = hipFuncSetAttribute(
@@ -506,18 +596,20 @@ extern "C" hipError_t rlm_relation_reduce_fused_seq(
   constexpr int64_t kMaxBytes = int64_t(1) << 31;
   RLM_REQUIRE(B * T * 2 * H * 2 < kMaxBytes && B * T * R * 2 < kMaxBytes && D * H * 2 < kMaxBytes,
               "caches and weights must each be smaller than 2 GiB");
+  RLM_REQUIRE(B * Tq * K < kMaxBytes && B * Tq * D * 4 < kMaxBytes,
+              "fused relation reduce: B*Tq*K rows and the fp32 output must stay below 2^31");
   for (const rlm_tensor* t : {operand_cache, product_weight, second_weight})
     RLM_REQUIRE((reinterpret_cast<uintptr_t>(t->data) & 15u) == 0,
                 "operand_cache, product_weight and second_weight must be 16-byte aligned");
-  p.B = B;
-  p.Tq = Tq;
+  p.Tq = static_cast<uint32_t>(Tq);
   p.T = T;
-  p.R = static_cast<int>(R);
-  p.H = static_cast<int>(H);
-  p.D = static_cast<int>(D);
-  p.K = static_cast<int>(K);
-  p.rows = B * Tq * K;
-  p.queries = B * Tq;
+  p.R = static_cast<uint32_t>(R);
+  p.H = static_cast<uint32_t>(H);
+  p.D = static_cast<uint32_t>(D);
+  p.K = static_cast<uint32_t>(K);
+  p.k_log2 = static_cast<uint32_t>(__builtin_ctzll(static_cast<unsigned long long>(K)));
+  p.rows = static_cast<uint32_t>(B * Tq * K);
+  p.queries = static_cast<uint32_t>(B * Tq);
   p.expanded = expanded_cache->data;
   p.operand = operand_cache->data;
   p.anchor = anchor_index->data;
