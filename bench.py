@@ -33,6 +33,16 @@ for _p in (ROOT, os.path.join(ROOT, "relation-lm_amd")):
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+CALIBRATION_BYTES = 256 << 20   # plain copy whose counter readings scale FETCH/WRITE_SIZE
+# Kernel-name prefixes (as rocprofv3 reports them) of the timed kernels.
+KERNEL_SYMBOLS = {
+    "expanded_projection": "tile_kernel<rlm::bf16, rlm::bf16, rlm::bf16",
+    "relation_select": "select_kernel<",
+    "relation_reduce_fused": "fused_reduce_kernel<",
+    "relation_hidden": "hidden_bf16_kernel<",
+    "second_linear": "tile_kernel<float, rlm::bf16, float",
+    "norm_reduce": "norm_reduce_vec_kernel<",
+}
 
 
 def parse_args():
@@ -45,6 +55,12 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-chain", action="store_true",
                     help="run only the timed chain (for profiler runs)")
+    ap.add_argument("--profile-kernels", type=int, default=0, metavar="N",
+                    help="run a 256 MiB calibration copy, then each timed kernel N times, and "
+                         "exit (the command profiled by rocprofv3 --kernel-trace / --pmc)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE, "
+                         "WRITE_SIZE) of a --profile-kernels run into profiles/cfg2_traffic.json")
     return ap.parse_args()
 
 
@@ -82,6 +98,8 @@ def algorithmic_flops(cfg):
 
 def main() -> int:
     args = parse_args()
+    if args.summarize_pmc:
+        return summarize_pmc(*args.summarize_pmc)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the routed relation path is batch-separable; "
               f"see DESIGN.md for the sharding plan); got --gpus {args.gpus}", file=sys.stderr)
@@ -159,6 +177,30 @@ def main() -> int:
         step()
         step_unfused()
     torch.cuda.synchronize()
+    expanded = run_expanded()
+    a, s, p, ps = run_select()
+    hidden = run_hidden(expanded, a, p)
+    raw = run_second(hidden)
+    kernels = {
+        "expanded_projection": run_expanded,
+        "relation_select": run_select,
+        "relation_reduce_fused": lambda: run_fused(expanded, a, p, ps),
+        "relation_hidden": lambda: run_hidden(expanded, a, p),
+        "second_linear": lambda: run_second(hidden),
+        "norm_reduce": lambda: run_norm(raw, ps),
+    }
+    if args.profile_kernels:
+        src = torch.empty(CALIBRATION_BYTES // 4, dtype=torch.float32, device=device).normal_()
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        for fn in kernels.values():
+            for _ in range(args.profile_kernels):
+                fn()
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_kernels": args.profile_kernels, "kernels": list(kernels)}),
+              flush=True)
+        return 0
     if args.only_chain:
         for _ in range(args.steps):
             step()
@@ -181,22 +223,22 @@ def main() -> int:
 
     ms_per_step = timed(step, args.steps)
     ms_unfused = timed(step_unfused, args.steps)
+    # The same fixed-shape step replayed from a HIP graph, reported beside it.
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    step_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(step_graph):
+        step()
+    for _ in range(args.warmup):
+        step_graph.replay()
+    ms_graph = timed(step_graph.replay, args.steps)
     queries = cfg.queries
     value = queries / (ms_per_step / 1e3)
 
     # Per-kernel average duration on the launch stream (torch's current stream).
-    expanded = run_expanded()
-    a, s, p, ps = run_select()
-    hidden = run_hidden(expanded, a, p)
-    raw = run_second(hidden)
-    kernels = {
-        "expanded_projection": run_expanded,
-        "relation_select": run_select,
-        "relation_reduce_fused": lambda: run_fused(expanded, a, p, ps),
-        "relation_hidden": lambda: run_hidden(expanded, a, p),
-        "second_linear": lambda: run_second(hidden),
-        "norm_reduce": lambda: run_norm(raw, ps),
-    }
     per_kernel_us = {}
     for name, fn in kernels.items():
         for _ in range(3):
@@ -321,6 +363,8 @@ def main() -> int:
         },
         "roofline": roof,
         "per_kernel_us": {k: round(v, 2) for k, v in per_kernel_us.items()},
+        "graph_replay": {"ms_per_step": round(ms_graph, 5),
+                         "value": round(queries / (ms_graph / 1e3), 1)},
         "hbm_frac_fused_chain": round(fused_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "unfused_chain": {
             "ms_per_step": round(ms_unfused, 5),
@@ -333,6 +377,49 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
+    return 0
+
+
+def summarize_pmc(fetch_csv, write_csv):
+    """Per-launch HBM bytes of each timed kernel from rocprofv3 --pmc FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch), each scaled by what the same counter reads for the
+    plain calibration copy of CALIBRATION_BYTES (which reads and writes that many bytes)."""
+    import csv
+    import statistics
+
+    def per_kernel(path, counter):
+        values = {}
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                if row["Counter_Name"] != counter:
+                    continue
+                values.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+        return values
+
+    out = {"calibration_bytes": CALIBRATION_BYTES, "kernels": {}}
+    scale = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        values = per_kernel(path, counter)
+        copy = [v for name, vs in values.items() if "copyBuffer" in name for v in vs]
+        kib = max(copy)  # the calibration copy is the largest copyBuffer dispatch
+        scale[counter] = CALIBRATION_BYTES / (kib * 1024.0)
+        out[f"{counter.lower()}_copy_kib"] = kib
+        out[f"{counter.lower()}_scale"] = round(scale[counter], 4)
+        for key, prefix in KERNEL_SYMBOLS.items():
+            vs = [v for name, vv in values.items() if prefix in name for v in vv]
+            if vs:
+                entry = out["kernels"].setdefault(key, {})
+                entry[f"{counter.lower()}_kib"] = statistics.median(vs)
+                entry[f"{counter.lower()}_bytes"] = round(
+                    statistics.median(vs) * 1024.0 * scale[counter])
+    for entry in out["kernels"].values():
+        if "fetch_size_bytes" in entry and "write_size_bytes" in entry:
+            entry["hbm_bytes_per_launch"] = entry["fetch_size_bytes"] + entry["write_size_bytes"]
+    path = os.path.join(ROOT, "profiles", "cfg2_traffic.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=2, sort_keys=True)
+        f.write("\n")
+    print(json.dumps(out, sort_keys=True), flush=True)
     return 0
 
 

@@ -15,6 +15,11 @@
 //                 on the matrix cores.  Workgroups are renumbered so that the
 //                 tiles sharing an A row-block run on the same XCD (one L2),
 //                 which keeps A's HBM traffic at one read.
+//   smallk_kernel (M > 64, K in {32, 64, 96, 128})  e.g. the expanded-cache
+//                 projection (K = relation dim).  Each wave owns a 64x64 output
+//                 tile and loads all of its A and W fragments for the whole K
+//                 straight from L2 in MFMA operand layout -- one round trip,
+//                 no LDS staging and no barriers.
 //   skinny_kernel (M <= 64)  decode shapes.  A workgroup owns 16 output columns
 //                 and every row; its four waves split K, each streaming its
 //                 W and A slices straight from global memory in MFMA operand
@@ -214,6 +219,90 @@ __global__ void __launch_bounds__(256) tile_kernel(const GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// 16-bit weights, small K (K = 32*KS, KS <= 4)
+// ---------------------------------------------------------------------------
+
+template <typename TA, typename W, typename TO, int KS>
+__global__ void __launch_bounds__(256) smallk_kernel(const GemmParams p) {
+  constexpr int kLdo = 64 + 16 / static_cast<int>(sizeof(TO));  // staged row stride (elements)
+  __shared__ __align__(16) TO stage[4][64 * kLdo];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t tiles_n = (p.N + 127) / 128;
+  const int64_t tiles = tiles_n * ((p.M + 127) / 128);
+  const int64_t tile = xcd_tile(blockIdx.x, tiles);
+  const int64_t m0 = (tile / tiles_n) * 128 + (wave >> 1) * 64;
+  const int64_t n0 = (tile % tiles_n) * 128 + (wave & 1) * 64;
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  const int kq = g * 8;
+  const TA* A = static_cast<const TA*>(p.a);
+  const W* Wt = static_cast<const W*>(p.w);
+
+  u16x8 a[KS][4], b[KS][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t m = m0 + 16 * i + r16;
+    const int64_t n = n0 + 16 * i + r16;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      a[s][i] = __builtin_bit_cast(
+          u16x8, m < p.M ? load8<TA, W>(A + m * p.lda, 32 * s + kq) : make_uint4(0, 0, 0, 0));
+      b[s][i] = __builtin_bit_cast(
+          u16x8, n < p.N ? load8<W, W>(Wt + n * p.K, 32 * s + kq) : make_uint4(0, 0, 0, 0));
+    }
+  }
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<W>(a[s][i], b[s][j], acc[i][j]);
+
+  float bv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t n = n0 + 16 * j + r16;
+    bv[j] = (p.bias && n < p.N) ? load_any_f(p.bias, p.bias_dtype, n) : 0.0f;
+  }
+  TO* out = static_cast<TO*>(p.out);
+  constexpr int kVec = 16 / static_cast<int>(sizeof(TO));  // elements per 16-byte store
+  const bool full = m0 + 64 <= p.M && n0 + 64 <= p.N && p.N % kVec == 0 &&
+                    (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+  if (!full) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) store_tile<TO>(p, acc[i][j], m0 + 16 * i, n0 + 16 * j + r16, bv[j], lane);
+    return;
+  }
+  // Stage the wave's 64x64 tile in LDS, then write whole 16-byte row pieces.
+  TO* st = stage[wave];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        st[(16 * i + 4 * g + e) * kLdo + 16 * j + r16] = from_f32<TO>(acc[i][j][e] + bv[j]);
+  wave_sync();
+  constexpr int kPieces = 64 * 64 / kVec;
+#pragma unroll
+  for (int t = 0; t < kPieces / kWave; ++t) {
+    const int piece = t * kWave + lane;
+    const int row = piece / (64 / kVec);
+    const int col = (piece % (64 / kVec)) * kVec;
+    *reinterpret_cast<uint4*>(out + (m0 + row) * p.N + n0 + col) =
+        *reinterpret_cast<const uint4*>(st + row * kLdo + col);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 16-bit weights, M <= 64 (decode)
 // ---------------------------------------------------------------------------
 
@@ -355,6 +444,16 @@ hipError_t launch_typed(const GemmParams& p, hipStream_t s) {
     return launch_status("linear");
   }
   const int64_t big = ((p.M + 127) / 128) * ((p.N + 127) / 128);
+  if (p.K <= 128 && p.K % 32 == 0) {
+    const dim3 grid(static_cast<unsigned>(big));
+    switch (p.K / 32) {
+      case 1: hipLaunchKernelGGL((smallk_kernel<TA, W, TO, 1>), grid, dim3(256), 0, s, p); break;
+      case 2: hipLaunchKernelGGL((smallk_kernel<TA, W, TO, 2>), grid, dim3(256), 0, s, p); break;
+      case 3: hipLaunchKernelGGL((smallk_kernel<TA, W, TO, 3>), grid, dim3(256), 0, s, p); break;
+      default: hipLaunchKernelGGL((smallk_kernel<TA, W, TO, 4>), grid, dim3(256), 0, s, p); break;
+    }
+    return launch_status("linear");
+  }
   if (big >= 256) {
     hipLaunchKernelGGL((tile_kernel<TA, W, TO, 128, 128>), dim3(static_cast<unsigned>(big)),
                        dim3(256), 0, s, p);

@@ -434,7 +434,7 @@ __device__ void stage_workgroup(const SelectParams& p, int64_t b, int64_t wbase,
 }
 
 template <typename TA, typename TS, int MODE>
-__global__ void __launch_bounds__(512) select_kernel(const SelectParams p) {
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) select_kernel(const SelectParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int EPC = kEpc<TA>;
   const int tid = threadIdx.x;

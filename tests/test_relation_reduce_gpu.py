@@ -317,7 +317,7 @@ def test_packed_projection_matches_separate_linears(device, dtype, batch):
 
 @pytest.mark.parametrize("m,n,k", [(1, 512, 576), (8, 4608, 128), (100, 72, 40), (4096, 1024, 128),
                                    (8, 576, 2304), (64, 576, 2304), (65, 200, 96), (8, 24, 40),
-                                   (33, 130, 72), (1000, 300, 520)])
+                                   (33, 130, 72), (1000, 300, 520), (129, 40, 32), (300, 136, 64)])
 def test_linear_shapes(device, m, n, k):
     g = torch.Generator().manual_seed(m * 7 + n)
     x = torch.randn(m, k, generator=g)
@@ -334,6 +334,22 @@ def test_linear_shapes(device, m, n, k):
     assert rel_err(host(got16), exp16) <= FP32_REL
     expmix = ored.linear(x16.float().numpy(), w16.float().numpy())
     assert rel_err(host(gotmix), expmix) <= FP32_REL
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 1024, 128), (200, 264, 64), (77, 48, 32)])
+def test_linear_small_k_bf16_out(device, m, n, k):
+    """K <= 128 takes the one-round-trip small-K kernel; bf16 output as the expanded cache."""
+    g = torch.Generator().manual_seed(m + 3 * n + k)
+    x = torch.randn(m, k, generator=g).bfloat16()
+    w = (torch.randn(n, k, generator=g) * k ** -0.5).bfloat16()
+    bias = torch.randn(n, generator=g) * 0.1
+    got = relation_linear(x.to(device), w.to(device), bias.to(device))
+    torch.cuda.synchronize()
+    assert got.dtype == torch.bfloat16 and got.shape == (m, n)
+    expected = ored.linear(x.float().numpy(), w.float().numpy(), bias.numpy())
+    assert abs_err(host(got), expected) <= BF16_ABS
+    assert abs_err(host(got), ored.round_to(expected, "bfloat16")) <= 2 ** -7 * max(
+        1.0, float(np.abs(expected).max()))
 
 
 def test_graph_replay_matches_eager(device):
