@@ -55,7 +55,7 @@ constexpr int kGatherRowBytes = 2 * kHC * 2;
 constexpr int kOffGather = kWmBytes;
 constexpr int kOffHid = kOffGather + kRows * kGatherRowBytes;
 constexpr int kOffF32 = kOffHid + kRows * kLd * 2;
-constexpr int kF32Words = kRows + 2 * kRows + kWaves * kRows + 3 * kMaxD;
+constexpr int kF32Words = kRows + 2 * kRows + 2 * kWaves * kRows + 3 * kMaxD;
 constexpr int kOffRowOff = kOffF32 + kF32Words * 4;
 constexpr size_t kLdsBytes = static_cast<size_t>(kOffRowOff) + kRows * 2 * 4;
 constexpr int kWaitVm0 = 0x0F70;           // s_waitcnt vmcnt(0), other counters untouched
@@ -153,20 +153,24 @@ __device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v 
 // Streams rows [chunk*128, chunk*128+128) of W_m into an LDS tile of 128 rows
 // x R bf16.  16-byte piece q of row n is stored at piece q ^ (n % (R/8)) so
 // that the 16 rows of an MFMA fragment read hit distinct banks.
+// Instruction i of kHC*R/8/kThreads = KS1 per lane.
+template <int KS1>
+__device__ __forceinline__ void dma_wm_one(rsrc_t wmr, uint32_t tile, int chunk, int wave, int lane,
+                                           int i) {
+  constexpr int R = KS1 * 32;
+  constexpr int QPR = R / 8;                               // pieces per row
+  const int slot = (i * kWaves + wave) * kWave + lane;     // LDS piece written by this lane
+  const int n = slot / QPR;
+  const int src = (slot % QPR) ^ (n % QPR);
+  const uint32_t voff = (static_cast<uint32_t>(chunk * kHC + n) * R + 8 * src) * 2u;
+  lds_dma16(wmr, __builtin_amdgcn_readfirstlane(tile + (i * kWaves + wave) * kWave * 16), voff);
+}
 template <int KS1>
 __device__ __forceinline__ void dma_wm_chunk(rsrc_t wmr, uint32_t tile, int chunk, int wave,
                                              int lane) {
-  constexpr int R = KS1 * 32;
-  constexpr int QPR = R / 8;                               // pieces per row
-  constexpr int kInsts = kHC * QPR / (kWaves * kWave);     // DMA instructions per lane
+  static_assert(kHC * KS1 * 4 % kThreads == 0 && kHC * KS1 * 4 / kThreads == KS1, "");
 #pragma unroll
-  for (int i = 0; i < kInsts; ++i) {
-    const int slot = (i * kWaves + wave) * kWave + lane;   // LDS piece written by this lane
-    const int n = slot / QPR;
-    const int src = (slot % QPR) ^ (n % QPR);
-    const uint32_t voff = (static_cast<uint32_t>(chunk * kHC + n) * R + 8 * src) * 2u;
-    lds_dma16(wmr, __builtin_amdgcn_readfirstlane(tile + (i * kWaves + wave) * kWave * 16), voff);
-  }
+  for (int i = 0; i < KS1; ++i) dma_wm_one<KS1>(wmr, tile, chunk, wave, lane, i);
 }
 
 // Gathered expanded-cache halves of one chunk: LDS row m holds the anchor
@@ -191,8 +195,8 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
   unsigned char* hid = smem + kOffHid;                            // [kRows][kLd] bf16
   float* wts = reinterpret_cast<float*>(smem + kOffF32);           // [kRows]
   float* mom = wts + kRows;                                        // [2][kRows] mean, rstd
-  float* part = mom + 2 * kRows;                                   // [kWaves][kRows]
-  float* cst = part + kWaves * kRows;                              // [3][kMaxD] b2, gamma, beta
+  float* part = mom + 2 * kRows;                                   // [2][kWaves][kRows]
+  float* cst = part + 2 * kWaves * kRows;                          // [3][kMaxD] b2, gamma, beta
   uint32_t* rowoff = reinterpret_cast<uint32_t*>(smem + kOffRowOff);  // [kRows][2]
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
 
@@ -276,17 +280,19 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
           w2r, w2_lane + (16u * (JC * jg + j) * H + chunk * kHC + 32 * s) * 2u));
   };
   // Gather DMA sources of this lane (piece lane%32 of row 2*(8i + wave) + lane/32), chunk 0.
+  auto gather_src = [&](int i) {
+    const int m = 2 * (i * kWaves + wave) + lane / 32;
+    const int q = lane & 31;
+    const uint32_t base = rowoff[2 * m + q / 16];
+    return base == kNoOffset ? kNoOffset : base + 16u * ((q & 15) ^ (m & 15));
+  };
   auto gather_chunk = [&](int chunk) {
     uint32_t src[kGatherInsts];
 #pragma unroll
-    for (int i = 0; i < kGatherInsts; ++i) {
-      const int m = 2 * (i * kWaves + wave) + lane / 32;
-      const int q = lane & 31;
-      const uint32_t base = rowoff[2 * m + q / 16];
-      src[i] = base == kNoOffset ? kNoOffset : base + 16u * ((q & 15) ^ (m & 15));
-    }
+    for (int i = 0; i < kGatherInsts; ++i) src[i] = gather_src(i);
     dma_gather_chunk(xr, lds0 + kOffGather, src, chunk, wave);
   };
+
 
   f32x4 raw[kRowTiles][DT];
 #pragma unroll
@@ -388,7 +394,11 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
 #pragma unroll
       for (int e = 0; e < 4; ++e) raw[i][j][e] += bias;
   }
-  // Mean: per-wave partial row sums, combined per row by threads 0..127.
+  // Row moments.  Each wave takes the mean and centred sum of squares of its
+  // 16*DT columns of every row (DPP sums over the 16 lanes of a column tile
+  // row); threads 0..127 merge the 8 waves' pairs (Chan, Golub and LeVeque's
+  // pairwise update, equal counts) -- one barrier round, no E[x^2]-mu^2.
+  constexpr float kInvCols = 1.0f / (16.0f * DT);
 #pragma unroll
   for (int i = 0; i < kRowTiles; ++i)
 #pragma unroll
@@ -396,50 +406,47 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
       float sum = 0.0f;
 #pragma unroll
       for (int j = 0; j < DT; ++j) sum += raw[i][j][e];
-      sum = row16_sum(sum);
-      if (r16 == 0) part[wave * kRows + 16 * i + 4 * g + e] = sum;
+      const float mu = row16_sum(sum) * kInvCols;
+      float sq = 0.0f;
+#pragma unroll
+      for (int j = 0; j < DT; ++j) {
+        const float d = raw[i][j][e] - mu;
+        sq = fmaf(d, d, sq);
+      }
+      sq = row16_sum(sq);
+      if (r16 == 0) {
+        part[wave * kRows + 16 * i + 4 * g + e] = mu;
+        part[(kWaves + wave) * kRows + 16 * i + 4 * g + e] = sq;
+      }
     }
   __syncthreads();
   if (tid < kRows) {
-    float sum = 0.0f;
+    float mw[kWaves], mu = 0.0f, m2 = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) sum += part[w * kRows + tid];
-    mom[tid] = sum * inv_d;
+    for (int w = 0; w < kWaves; ++w) {
+      mw[w] = part[w * kRows + tid];
+      mu += mw[w];
+      m2 += part[(kWaves + w) * kRows + tid];
+    }
+    mu *= 1.0f / kWaves;
+    float spread = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) spread = fmaf(mw[w] - mu, mw[w] - mu, spread);
+    mom[tid] = mu;
+    mom[kRows + tid] = rsqrtf(fmaf(spread, 16.0f * DT, m2) * inv_d + p.eps);
   }
   __syncthreads();
   float4 mean[kRowTiles];
 #pragma unroll
   for (int i = 0; i < kRowTiles; ++i) mean[i] = *reinterpret_cast<const float4*>(mom + 16 * i + 4 * g);
-  // Biased variance from the centred values.
-#pragma unroll
-  for (int i = 0; i < kRowTiles; ++i) {
-    const float mu[4] = {mean[i].x, mean[i].y, mean[i].z, mean[i].w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float sum = 0.0f;
-#pragma unroll
-      for (int j = 0; j < DT; ++j) {
-        const float d = raw[i][j][e] - mu[e];
-        sum += d * d;
-      }
-      sum = row16_sum(sum);
-      if (r16 == 0) part[wave * kRows + 16 * i + 4 * g + e] = sum;
-    }
-  }
-  __syncthreads();
-  if (tid < kRows) {
-    float sum = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) sum += part[w * kRows + tid];
-    mom[kRows + tid] = rsqrtf(sum * inv_d + p.eps);
-  }
-  __syncthreads();
   // LayerNorm, weights, sum over each query's K consecutive rows, store:
   //   out[q] = sum_k w_k (gamma (x_k - mu_k) rs_k + beta)
   //          = gamma * sum_k (A_k x_k - B_k) + beta * sum_k w_k,
-  // A_k = w_k rs_k, B_k = A_k mu_k, so each raw value costs one FMA.  The store
-  // descriptor covers this workgroup's queries only, so rows past the end of
-  // the last workgroup are dropped by the buffer bounds check.
+  // A_k = w_k rs_k, B_k = A_k mu_k, so each raw value costs one FMA.  Rows of
+  // one query: K <= 4 -> inside a lane group, K = 8 -> groups {0,1} / {2,3}
+  // (v_permlane16_swap), K = 16 -> all four (and v_permlane32_swap).  The
+  // store descriptor covers this workgroup's queries only, so rows past the end
+  // of the last workgroup are dropped by the buffer bounds check.
   const uint32_t K = p.K, D = p.D;
   const uint32_t q0 = row0 >> p.k_log2;
   const uint32_t nq = min(p.queries - q0, static_cast<uint32_t>(kRows) >> p.k_log2);
@@ -450,48 +457,83 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
     gm[j] = cst[kMaxD + dcol0 + 16 * j + r16];
     bt[j] = cst[2 * kMaxD + dcol0 + 16 * j + r16];
   }
+  auto cross16 = [](float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  };
+  auto cross32 = [](float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  };
+  if (K >= 4) {
+    float v[kRowTiles][DT], W[kRowTiles];
 #pragma unroll
-  for (int i = 0; i < kRowTiles; ++i) {
-    const float4 m4 = mean[i];
-    const float4 r4 = *reinterpret_cast<const float4*>(mom + kRows + 16 * i + 4 * g);
-    const float4 w4 = *reinterpret_cast<const float4*>(wts + 16 * i + 4 * g);
-    const float A[4] = {w4.x * r4.x, w4.y * r4.y, w4.z * r4.z, w4.w * r4.w};
-    const float nB[4] = {-A[0] * m4.x, -A[1] * m4.y, -A[2] * m4.z, -A[3] * m4.w};
-    const uint32_t lrow = 16 * i + 4 * g;  // first local row of this lane group
-    if (K >= 4) {
-      // Rows of one query: K = 4 -> this group, K = 8 -> groups {0,1} / {2,3}, K = 16 -> all.
-      float W = (w4.x + w4.y) + (w4.z + w4.w);
-      if (K >= 8) W += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(W), 0x401F));
-      if (K >= 16) W += __shfl_xor(W, 32, kWave);
-      const bool lead = (lrow & (K - 1)) == 0;
-      const uint32_t obase = (lrow >> p.k_log2) * D + dcol0 + r16;
-#pragma unroll
-      for (int j = 0; j < DT; ++j) {
-        float v = fmaf(raw[i][j][0], A[0], nB[0]) + fmaf(raw[i][j][1], A[1], nB[1]) +
-                  (fmaf(raw[i][j][2], A[2], nB[2]) + fmaf(raw[i][j][3], A[3], nB[3]));
-        if (K >= 8) v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
-        if (K >= 16) v += __shfl_xor(v, 32, kWave);
-        if (lead) buf_store_f32(fmaf(gm[j], v, bt[j] * W), outr, (obase + 16 * j) * 4u);
-      }
-    } else if (K == 2) {
-      const float W0 = w4.x + w4.y, W1 = w4.z + w4.w;
-      const uint32_t obase = (lrow >> 1) * D + dcol0 + r16;
-#pragma unroll
-      for (int j = 0; j < DT; ++j) {
-        const float v0 = fmaf(raw[i][j][0], A[0], nB[0]) + fmaf(raw[i][j][1], A[1], nB[1]);
-        const float v1 = fmaf(raw[i][j][2], A[2], nB[2]) + fmaf(raw[i][j][3], A[3], nB[3]);
-        buf_store_f32(fmaf(gm[j], v0, bt[j] * W0), outr, (obase + 16 * j) * 4u);
-        buf_store_f32(fmaf(gm[j], v1, bt[j] * W1), outr, (obase + D + 16 * j) * 4u);
-      }
-    } else {
-      const float Wk[4] = {w4.x, w4.y, w4.z, w4.w};
-      const uint32_t obase = lrow * D + dcol0 + r16;
+    for (int i = 0; i < kRowTiles; ++i) {
+      const float4 m4 = mean[i];
+      const float4 r4 = *reinterpret_cast<const float4*>(mom + kRows + 16 * i + 4 * g);
+      const float4 w4 = *reinterpret_cast<const float4*>(wts + 16 * i + 4 * g);
+      const float A[4] = {w4.x * r4.x, w4.y * r4.y, w4.z * r4.z, w4.w * r4.w};
+      const float nB[4] = {-A[0] * m4.x, -A[1] * m4.y, -A[2] * m4.z, -A[3] * m4.w};
+      W[i] = (w4.x + w4.y) + (w4.z + w4.w);
 #pragma unroll
       for (int j = 0; j < DT; ++j)
+        v[i][j] = (fmaf(raw[i][j][0], A[0], nB[0]) + fmaf(raw[i][j][1], A[1], nB[1])) +
+                  (fmaf(raw[i][j][2], A[2], nB[2]) + fmaf(raw[i][j][3], A[3], nB[3]));
+    }
+    if (K >= 8) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          buf_store_f32(fmaf(gm[j], fmaf(raw[i][j][e], A[e], nB[e]), bt[j] * Wk[e]), outr,
-                        (obase + e * D + 16 * j) * 4u);
+      for (int i = 0; i < kRowTiles; ++i) {
+        W[i] = cross16(W[i]);
+#pragma unroll
+        for (int j = 0; j < DT; ++j) v[i][j] = cross16(v[i][j]);
+      }
+    }
+    if (K >= 16) {
+#pragma unroll
+      for (int i = 0; i < kRowTiles; ++i) {
+        W[i] = cross32(W[i]);
+#pragma unroll
+        for (int j = 0; j < DT; ++j) v[i][j] = cross32(v[i][j]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kRowTiles; ++i) {
+      const uint32_t lrow = 16 * i + 4 * g;  // first local row of this lane group
+      if ((lrow & (K - 1)) != 0) continue;
+      const uint32_t obase = (lrow >> p.k_log2) * D + dcol0 + r16;
+#pragma unroll
+      for (int j = 0; j < DT; ++j)
+        buf_store_f32(fmaf(gm[j], v[i][j], bt[j] * W[i]), outr, (obase + 16 * j) * 4u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kRowTiles; ++i) {
+      const float4 m4 = mean[i];
+      const float4 r4 = *reinterpret_cast<const float4*>(mom + kRows + 16 * i + 4 * g);
+      const float4 w4 = *reinterpret_cast<const float4*>(wts + 16 * i + 4 * g);
+      const float A[4] = {w4.x * r4.x, w4.y * r4.y, w4.z * r4.z, w4.w * r4.w};
+      const float nB[4] = {-A[0] * m4.x, -A[1] * m4.y, -A[2] * m4.z, -A[3] * m4.w};
+      const uint32_t lrow = 16 * i + 4 * g;
+      if (K == 2) {
+        const float W0 = w4.x + w4.y, W1 = w4.z + w4.w;
+        const uint32_t obase = (lrow >> 1) * D + dcol0 + r16;
+#pragma unroll
+        for (int j = 0; j < DT; ++j) {
+          const float v0 = fmaf(raw[i][j][0], A[0], nB[0]) + fmaf(raw[i][j][1], A[1], nB[1]);
+          const float v1 = fmaf(raw[i][j][2], A[2], nB[2]) + fmaf(raw[i][j][3], A[3], nB[3]);
+          buf_store_f32(fmaf(gm[j], v0, bt[j] * W0), outr, (obase + 16 * j) * 4u);
+          buf_store_f32(fmaf(gm[j], v1, bt[j] * W1), outr, (obase + D + 16 * j) * 4u);
+        }
+      } else {
+        const float Wk[4] = {w4.x, w4.y, w4.z, w4.w};
+        const uint32_t obase = lrow * D + dcol0 + r16;
+#pragma unroll
+        for (int j = 0; j < DT; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            buf_store_f32(fmaf(gm[j], fmaf(raw[i][j][e], A[e], nB[e]), bt[j] * Wk[e]), outr,
+                          (obase + e * D + 16 * j) * 4u);
+      }
     }
   }
 }
