@@ -12,21 +12,22 @@
 // reference's chain for its query -- block scores, TOP block picks, exact
 // candidate scores, argmax -- with every reduction inside the wave.
 //
-// Exact scores: a key row is E elements = E/8 16-byte chunks (bf16), so a
-// group of G = E*sizeof/16 lanes scores one candidate row per instruction
-// (8 rows per wave instruction at E = 64 bf16): each lane holds its chunk of
-// the query in float64 registers, multiplies its chunk of the row and the
-// group reduces with a float64 butterfly.  Local-window rows come from LDS,
-// picked remote blocks from L2.
+// Exact scores: one lane per candidate (3 candidates per lane per pass at
+// CAP = 192): the lane streams its candidate's key row in 16-byte chunks --
+// local-window rows from the staged LDS window, picked remote blocks from L2
+// through a buffer descriptor (out-of-range rows read as zero) -- and
+// accumulates the dot with the query, held in float64 registers, in float64.
 //
 // Numerics: every dot product is accumulated in float64 from exact products
-// and rounded once to float32; block scores (softplus, per-head terms,
-// pairwise log-sum-exp) are evaluated in float64 and rounded once.  All
-// comparisons use those float32 values.  Ties: anchor -> lowest position,
-// blocks -> lowest block, partners -> lowest candidate lane (local window
-// first, then picked blocks in pick order).  Each rule is one 64-bit key
-// (order-preserving score bits above the complemented tie index), so one
-// wave max-reduction yields the winner.
+// and rounded once to float32; block scores (softplus, per-head terms, the
+// log-sum-exp over heads, m + log(sum_h exp(s_h - m))) are evaluated in
+// float64 and rounded once.  The reference combines heads pairwise in float32
+// (relation_select.py:97-103); in float64 the one-shot and pairwise forms
+// agree far below a float32 ulp.  All comparisons use those float32 values.
+// Ties: anchor -> lowest position, blocks -> lowest block, partners -> lowest
+// candidate lane (local window first, then picked blocks in pick order).
+// Each rule is one 64-bit key (order-preserving score bits above the
+// complemented tie index), so one wave max-reduction yields the winner.
 #include "rlm_common.hpp"
 
 namespace rlm {
