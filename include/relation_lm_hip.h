@@ -216,8 +216,8 @@ hipError_t rlm_relation_norm_reduce_seq(
  *   expanded_cache [B,T,2H], operand_cache [B,T,R], product_weight [H,R],
  *   second_weight [D,H] (all bf16), second_bias [D], partner_scores f32
  *   [B,Tq,K], norm_weight/norm_bias [D], anchor_index [B,Tq], partner_index
- *   [B,Tq,K], positions [Tq] or [B,Tq].  K in {1,2,4,8,16}, R a multiple of 32
- *   up to 128, H a multiple of 128, D in {256, 384, 512}.
+ *   [B,Tq,K], positions [Tq] or [B,Tq].  K in {1,2,4,8,16}, R in {32,64,128},
+ *   H a multiple of 128, D in {128, 256, 384, 512}.
  * Output: out f32 [B,Tq,D].
  */
 hipError_t rlm_relation_reduce_fused_seq(
@@ -227,6 +227,30 @@ hipError_t rlm_relation_reduce_fused_seq(
     const rlm_tensor* second_bias, const rlm_tensor* partner_scores,
     const rlm_tensor* norm_weight, const rlm_tensor* norm_bias, const rlm_tensor* positions,
     double norm_eps, const rlm_tensor* out, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Router cache (decode producer of the selection's block statistics)
+ * ---------------------------------------------------------------------- */
+
+/*
+ * Replaces relation_lm::router_cache_update
+ *   (src/relation_lm/kernels/router_cache.py:181-241; kernel :9-178).
+ *   anchor_raw / partner_raw [B,D] rows (any row stride, unit column stride),
+ *   raw and conv caches [B,T,D], anchor/partner mean and std [B,NB,...] with D
+ *   values per block, conv weights [D,3], position 0-d int32/int64 (device).
+ *   Writes raw/conv cache row `position`, the statistics of block
+ *   position / block_size and out f32 [B,2,D] (the two streams' conv rows).
+ *   A position outside [0,T) writes zeros to out and leaves the caches alone.
+ */
+hipError_t rlm_router_cache_update(
+    const rlm_tensor* anchor_raw, const rlm_tensor* partner_raw,
+    const rlm_tensor* anchor_raw_cache, const rlm_tensor* partner_raw_cache,
+    const rlm_tensor* anchor_conv_cache, const rlm_tensor* partner_conv_cache,
+    const rlm_tensor* anchor_mean, const rlm_tensor* anchor_std,
+    const rlm_tensor* partner_mean, const rlm_tensor* partner_std,
+    const rlm_tensor* anchor_conv_weight, const rlm_tensor* partner_conv_weight,
+    const rlm_tensor* position, int64_t block_size, const rlm_tensor* out,
+    hipStream_t stream);
 
 /* ------------------------------------------------------------------------
  * Dense projections (MFMA)

@@ -1,0 +1,246 @@
+// Router cache update for gfx950: one decode token of both router streams --
+// the depthwise causal conv (kernel 3) from the two previous raw rows, the
+// raw/conv cache writes at the token's position, and the mean / biased std of
+// the block that holds the token.
+//
+// Reference semantics: src/relation_lm/kernels/router_cache.py:9-197 (the
+// decode-time form of DistilledBlockRouter._causal_conv / block_statistics,
+// block_router.py:50-68).
+//
+// Mapping: one wavefront per (batch row, stream); a lane owns one router
+// column (columns beyond 64 loop).  The whole update is a handful of
+// dependent loads, so the kernel is latency-bound: the block's BS conv rows
+// are loaded in one batch, before the conv of the current row is known, and
+// the current row's value is taken from registers rather than re-read after
+// its own store (the reference substitutes it the same way, :113-117).
+//
+// Numerics follow the reference's fp32 evaluation order: conv = raw*w2, then
+// + (prev1*w1), then + (prev2*w0), each product rounded before its add; the
+// block mean is the fp32 sum of the BS rows divided by BS and the variance the
+// mean squared deviation from it.
+//
+// A position outside [0, T) writes zeros to `out` and touches no cache (the
+// reference reads and writes out of bounds there); a block index past the
+// statistics' block count updates no statistics; block rows past the cache
+// end count as zero.
+#include "rlm_common.hpp"
+
+namespace rlm {
+namespace {
+
+struct RouterParams {
+  int B, T, D, NB, BS;
+  const void* raw[2];        // [B, D] rows, stride raw_stride
+  int64_t raw_stride[2];
+  int raw_dtype[2];
+  void* raw_cache[2];        // [B, T, D]
+  void* conv_cache[2];       // [B, T, D]
+  int raw_cache_dtype[2], conv_cache_dtype[2];
+  void* mean[2];             // [B, NB, D]
+  void* stdev[2];
+  int mean_dtype[2], std_dtype[2];
+  const void* weight[2];     // [D, 3]
+  int weight_dtype[2];
+  const void* pos;
+  int pos_dtype;
+  float* out;                // [B, 2, D]
+};
+
+__device__ __forceinline__ void store_any_f(void* p, int dtype, int64_t i, float v) {
+  switch (dtype) {
+    case RLM_BF16: static_cast<bf16*>(p)[i] = f32_to_bf16(v); break;
+    case RLM_F16: static_cast<f16*>(p)[i] = static_cast<f16>(v); break;
+    default: static_cast<float*>(p)[i] = v; break;
+  }
+}
+
+constexpr int kRowBatch = 8;  // block rows loaded per batch of independent loads
+
+__global__ void __launch_bounds__(kWave) router_cache_kernel(const RouterParams p) {
+  const int b = blockIdx.x;
+  const int side = blockIdx.y;  // 0 anchor stream, 1 partner stream
+  const int lane = threadIdx.x;
+  const int64_t t = load_any_i(p.pos, p.pos_dtype, 0);
+  float* out = p.out + (static_cast<int64_t>(b) * 2 + side) * p.D;
+  if (t < 0 || t >= p.T) {
+    for (int c = lane; c < p.D; c += kWave) out[c] = 0.0f;
+    return;
+  }
+  const int64_t row_t = static_cast<int64_t>(b) * p.T + t;
+  const int64_t j = t / p.BS;
+  const int64_t first = j * p.BS;
+  for (int c = lane; c < p.D; c += kWave) {
+    // Independent loads first: this token's raw value, the two previous raw
+    // rows, the conv weights and the block's conv rows.
+    const float x = load_any_f(p.raw[side], p.raw_dtype[side], b * p.raw_stride[side] + c);
+    const float p1 = t >= 1 ? load_any_f(p.raw_cache[side], p.raw_cache_dtype[side],
+                                         (row_t - 1) * p.D + c)
+                            : 0.0f;
+    const float p2 = t >= 2 ? load_any_f(p.raw_cache[side], p.raw_cache_dtype[side],
+                                         (row_t - 2) * p.D + c)
+                            : 0.0f;
+    const float w0 = load_any_f(p.weight[side], p.weight_dtype[side], 3 * c);
+    const float w1 = load_any_f(p.weight[side], p.weight_dtype[side], 3 * c + 1);
+    const float w2 = load_any_f(p.weight[side], p.weight_dtype[side], 3 * c + 2);
+    float conv;
+    {
+#pragma clang fp contract(off)
+      conv = x * w2;
+      if (t >= 1) conv = conv + p1 * w1;
+      if (t >= 2) conv = conv + p2 * w0;
+    }
+    store_any_f(p.raw_cache[side], p.raw_cache_dtype[side], row_t * p.D + c, x);
+    store_any_f(p.conv_cache[side], p.conv_cache_dtype[side], row_t * p.D + c, conv);
+    out[c] = conv;
+    if (j >= p.NB) continue;
+    // Block statistics over all BS rows; the token's own row from registers.
+    float sum = 0.0f;
+    float rows[kRowBatch];
+    for (int r0 = 0; r0 < p.BS; r0 += kRowBatch) {
+#pragma unroll
+      for (int u = 0; u < kRowBatch; ++u) {
+        const int64_t idx = first + r0 + u;
+        rows[u] = (r0 + u < p.BS && idx < p.T && idx != t)
+                      ? load_any_f(p.conv_cache[side], p.conv_cache_dtype[side],
+                                   (static_cast<int64_t>(b) * p.T + idx) * p.D + c)
+                      : 0.0f;
+        if (idx == t) rows[u] = conv;
+      }
+#pragma unroll
+      for (int u = 0; u < kRowBatch; ++u)
+        if (r0 + u < p.BS) sum += rows[u];
+    }
+    const float mean = sum / static_cast<float>(p.BS);
+    float sq = 0.0f;
+    for (int r0 = 0; r0 < p.BS; r0 += kRowBatch) {
+#pragma unroll
+      for (int u = 0; u < kRowBatch; ++u) {
+        const int64_t idx = first + r0 + u;
+        float v = (r0 + u < p.BS && idx < p.T && idx != t)
+                      ? load_any_f(p.conv_cache[side], p.conv_cache_dtype[side],
+                                   (static_cast<int64_t>(b) * p.T + idx) * p.D + c)
+                      : 0.0f;
+        if (idx == t) v = conv;
+        if (r0 + u < p.BS) {
+          const float d = v - mean;
+          sq += d * d;
+        }
+      }
+    }
+    const int64_t s = (static_cast<int64_t>(b) * p.NB + j) * p.D + c;
+    store_any_f(p.mean[side], p.mean_dtype[side], s, mean);
+    store_any_f(p.stdev[side], p.std_dtype[side], s, sqrtf(sq / static_cast<float>(p.BS)));
+  }
+}
+
+// Statistics tensors are [B, NB, ...] with D values per block, contiguous.
+bool check_stats(const rlm_tensor* t, const char* name, int64_t B, int64_t D, int64_t* nb) {
+  if (t == nullptr || t->ndim < 2) {
+    set_error("%s: expected a [B, blocks, ...] tensor", name);
+    return false;
+  }
+  if (!check_tensor(t, name, t->ndim) || !check_dtype_float(t, name)) return false;
+  int64_t per_block = 1;
+  for (int i = 2; i < t->ndim; ++i) per_block *= t->shape[i];
+  if (t->shape[0] != B || per_block != D) {
+    set_error("%s: expected [B=%lld, blocks, ...] with %lld values per block", name,
+              (long long)B, (long long)D);
+    return false;
+  }
+  *nb = t->shape[1];
+  return true;
+}
+
+}  // namespace
+}  // namespace rlm
+
+using namespace rlm;
+
+extern "C" hipError_t rlm_router_cache_update(
+    const rlm_tensor* anchor_raw, const rlm_tensor* partner_raw,
+    const rlm_tensor* anchor_raw_cache, const rlm_tensor* partner_raw_cache,
+    const rlm_tensor* anchor_conv_cache, const rlm_tensor* partner_conv_cache,
+    const rlm_tensor* anchor_mean, const rlm_tensor* anchor_std,
+    const rlm_tensor* partner_mean, const rlm_tensor* partner_std,
+    const rlm_tensor* anchor_conv_weight, const rlm_tensor* partner_conv_weight,
+    const rlm_tensor* position, int64_t block_size, const rlm_tensor* out, hipStream_t stream) {
+  clear_error();
+  RLM_TRY(check_rows(anchor_raw, "anchor_raw"));
+  RLM_TRY(check_rows(partner_raw, "partner_raw"));
+  RLM_TRY(check_dtype_float(anchor_raw, "anchor_raw"));
+  RLM_TRY(check_dtype_float(partner_raw, "partner_raw"));
+  const int64_t B = anchor_raw->shape[0], D = anchor_raw->shape[1];
+  RLM_TRY(check_dim(partner_raw, "partner_raw", 0, B));
+  RLM_TRY(check_dim(partner_raw, "partner_raw", 1, D));
+  const rlm_tensor* caches[4] = {anchor_raw_cache, partner_raw_cache, anchor_conv_cache,
+                                 partner_conv_cache};
+  const char* cache_names[4] = {"anchor_raw_cache", "partner_raw_cache", "anchor_conv_cache",
+                                "partner_conv_cache"};
+  for (int i = 0; i < 4; ++i) {
+    RLM_TRY(check_tensor(caches[i], cache_names[i], 3));
+    RLM_TRY(check_dtype_float(caches[i], cache_names[i]));
+    RLM_TRY(check_dim(caches[i], cache_names[i], 0, B));
+    RLM_TRY(check_dim(caches[i], cache_names[i], 1, anchor_raw_cache->shape[1]));
+    RLM_TRY(check_dim(caches[i], cache_names[i], 2, D));
+  }
+  const int64_t T = anchor_raw_cache->shape[1];
+  int64_t nb[4];
+  RLM_TRY(check_stats(anchor_mean, "anchor_mean", B, D, &nb[0]));
+  RLM_TRY(check_stats(anchor_std, "anchor_std", B, D, &nb[1]));
+  RLM_TRY(check_stats(partner_mean, "partner_mean", B, D, &nb[2]));
+  RLM_TRY(check_stats(partner_std, "partner_std", B, D, &nb[3]));
+  RLM_REQUIRE(nb[1] == nb[0] && nb[2] == nb[0] && nb[3] == nb[0],
+              "router statistics must all have the same number of blocks");
+  for (const rlm_tensor* w : {anchor_conv_weight, partner_conv_weight}) {
+    const char* name = w == anchor_conv_weight ? "anchor_conv_weight" : "partner_conv_weight";
+    RLM_TRY(check_tensor(w, name, 2));
+    RLM_TRY(check_dtype_float(w, name));
+    RLM_TRY(check_dim(w, name, 0, D));
+    RLM_TRY(check_dim(w, name, 1, 3));
+  }
+  RLM_REQUIRE(position != nullptr && position->ndim == 0 && is_index_dtype(position->dtype) &&
+                  position->data != nullptr,
+              "position: expected a 0-d int32/int64 device tensor");
+  RLM_REQUIRE(block_size > 0 && block_size <= (int64_t(1) << 20),
+              "block_size must be positive, got %lld", (long long)block_size);
+  RLM_TRY(check_tensor(out, "out", 3));
+  RLM_TRY(check_dtype_is(out, "out", RLM_F32));
+  RLM_TRY(check_dim(out, "out", 0, B));
+  RLM_TRY(check_dim(out, "out", 1, 2));
+  RLM_TRY(check_dim(out, "out", 2, D));
+  RLM_REQUIRE(B < (int64_t(1) << 31) && T < (int64_t(1) << 31) && D < (int64_t(1) << 31) &&
+                  nb[0] < (int64_t(1) << 31),
+              "router cache dimensions must be below 2^31");
+  if (B == 0 || D == 0) return hipSuccess;
+  RouterParams p{};
+  p.B = static_cast<int>(B);
+  p.T = static_cast<int>(T);
+  p.D = static_cast<int>(D);
+  p.NB = static_cast<int>(nb[0]);
+  p.BS = static_cast<int>(block_size);
+  const rlm_tensor* raws[2] = {anchor_raw, partner_raw};
+  const rlm_tensor* means[2] = {anchor_mean, partner_mean};
+  const rlm_tensor* stds[2] = {anchor_std, partner_std};
+  const rlm_tensor* weights[2] = {anchor_conv_weight, partner_conv_weight};
+  for (int s = 0; s < 2; ++s) {
+    p.raw[s] = raws[s]->data;
+    p.raw_stride[s] = B > 1 ? raws[s]->stride[0] : D;
+    p.raw_dtype[s] = raws[s]->dtype;
+    p.raw_cache[s] = caches[s]->data;
+    p.raw_cache_dtype[s] = caches[s]->dtype;
+    p.conv_cache[s] = caches[2 + s]->data;
+    p.conv_cache_dtype[s] = caches[2 + s]->dtype;
+    p.mean[s] = means[s]->data;
+    p.mean_dtype[s] = means[s]->dtype;
+    p.stdev[s] = stds[s]->data;
+    p.std_dtype[s] = stds[s]->dtype;
+    p.weight[s] = weights[s]->data;
+    p.weight_dtype[s] = weights[s]->dtype;
+  }
+  p.pos = position->data;
+  p.pos_dtype = position->dtype;
+  p.out = static_cast<float*>(out->data);
+  hipLaunchKernelGGL(router_cache_kernel, dim3(static_cast<unsigned>(B), 2), dim3(kWave), 0,
+                     stream, p);
+  return launch_status("router_cache_update");
+}

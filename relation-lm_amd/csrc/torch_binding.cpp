@@ -7,7 +7,9 @@
 //   relation_lm::relation_hidden_cached      (relation_reduce.py:149)
 //   relation_lm::relation_hidden_cache_update(relation_reduce.py:312)
 //   relation_lm::relation_norm_reduce        (relation_reduce.py:420)
-// plus the sequence forms, the packed sparse-cache projection and the linear.
+//   relation_lm::router_cache_update         (router_cache.py:181)
+// plus the sequence forms, the fused reduce, the packed sparse-cache
+// projection and the linear.
 // Only a CUDA-key (ROCm device) implementation exists: CPU tensors raise.
 // Outputs are allocated with the caching allocator on the input device and
 // every kernel is enqueued on the current HIP stream, so the ops compose
@@ -378,6 +380,42 @@ at::Tensor relation_linear(const at::Tensor& input, const at::Tensor& weight,
                        out_dtype.value_or(input.scalar_type()), false);
 }
 
+at::Tensor router_cache_update(const at::Tensor& anchor_raw, const at::Tensor& partner_raw,
+                               at::Tensor& anchor_raw_cache, at::Tensor& partner_raw_cache,
+                               at::Tensor& anchor_conv_cache, at::Tensor& partner_conv_cache,
+                               at::Tensor& anchor_mean, at::Tensor& anchor_std,
+                               at::Tensor& partner_mean, at::Tensor& partner_std,
+                               const at::Tensor& anchor_conv_weight,
+                               const at::Tensor& partner_conv_weight, const at::Tensor& position,
+                               int64_t block_size) {
+  const char* op = "relation_lm::router_cache_update";
+  c10::DeviceGuard guard(anchor_raw.device());
+  hipStream_t stream = device_stream(
+      op, {&anchor_raw, &partner_raw, &anchor_raw_cache, &partner_raw_cache, &anchor_conv_cache,
+           &partner_conv_cache, &anchor_mean, &anchor_std, &partner_mean, &partner_std,
+           &anchor_conv_weight, &partner_conv_weight, &position});
+  TORCH_CHECK(anchor_raw.dim() == 2, op, ": anchor_raw must be [B,D]");
+  at::Tensor out = at::empty({anchor_raw.size(0), 2, anchor_raw.size(1)}, f32(anchor_raw));
+  rlm_tensor d[14] = {desc(anchor_raw, "anchor_raw"),
+                      desc(partner_raw, "partner_raw"),
+                      desc(anchor_raw_cache, "anchor_raw_cache"),
+                      desc(partner_raw_cache, "partner_raw_cache"),
+                      desc(anchor_conv_cache, "anchor_conv_cache"),
+                      desc(partner_conv_cache, "partner_conv_cache"),
+                      desc(anchor_mean, "anchor_mean"),
+                      desc(anchor_std, "anchor_std"),
+                      desc(partner_mean, "partner_mean"),
+                      desc(partner_std, "partner_std"),
+                      desc(anchor_conv_weight, "anchor_conv_weight"),
+                      desc(partner_conv_weight, "partner_conv_weight"),
+                      desc(position, "position"),
+                      desc(out, "out")};
+  check(rlm_router_cache_update(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7], &d[8],
+                                &d[9], &d[10], &d[11], &d[12], block_size, &d[13], stream),
+        op);
+  return out;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(relation_lm, m) {
@@ -416,6 +454,12 @@ TORCH_LIBRARY(relation_lm, m) {
       "anchor_index, Tensor partner_index, Tensor product_weight, Tensor second_weight, Tensor "
       "second_bias, Tensor partner_scores, Tensor norm_weight, Tensor norm_bias, Tensor "
       "positions, float norm_eps) -> Tensor");
+  m.def(
+      "router_cache_update(Tensor anchor_raw, Tensor partner_raw, Tensor(a!) anchor_raw_cache, "
+      "Tensor(b!) partner_raw_cache, Tensor(c!) anchor_conv_cache, Tensor(d!) partner_conv_cache, "
+      "Tensor(e!) anchor_mean, Tensor(f!) anchor_std, Tensor(g!) partner_mean, Tensor(h!) "
+      "partner_std, Tensor anchor_conv_weight, Tensor partner_conv_weight, Tensor position, int "
+      "block_size) -> Tensor");
   m.def("packed_sparse_cache_projection(Tensor memory, Tensor weight) -> Tensor");
   m.def(
       "relation_linear(Tensor input, Tensor weight, Tensor? bias=None, ScalarType? "
@@ -443,6 +487,7 @@ TORCH_LIBRARY_IMPL(relation_lm, CUDA, m) {
   m.impl("relation_norm_reduce", TORCH_FN(relation_norm_reduce));
   m.impl("relation_norm_reduce_seq", TORCH_FN(relation_norm_reduce_seq));
   m.impl("relation_reduce_fused_seq", TORCH_FN(relation_reduce_fused_seq));
+  m.impl("router_cache_update", TORCH_FN(router_cache_update));
   m.impl("packed_sparse_cache_projection", TORCH_FN(packed_sparse_cache_projection));
   m.impl("relation_linear", TORCH_FN(relation_linear));
 }

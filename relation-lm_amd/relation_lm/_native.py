@@ -73,6 +73,11 @@ def _register_fakes() -> None:
     torch.library.register_fake("relation_lm::relation_norm_reduce")(fake_norm)
     torch.library.register_fake("relation_lm::relation_norm_reduce_seq")(fake_norm)
 
+    @torch.library.register_fake("relation_lm::router_cache_update")
+    def _(anchor_raw, *rest):
+        return anchor_raw.new_empty((anchor_raw.shape[0], 2, anchor_raw.shape[1]),
+                                    dtype=torch.float32)
+
     @torch.library.register_fake("relation_lm::relation_reduce_fused_seq")
     def _(expanded_cache, operand_cache, anchor_index, partner_index, product_weight,
           second_weight, *rest):
