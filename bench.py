@@ -14,8 +14,9 @@ Also reported:
   * per-kernel average duration (HIP events on the launch stream) and the
     roofline fraction of the dominant kernel (HBM bytes at the operator
     contract, or matrix-core FLOPs for the fused reduce);
-  * decode-step latency (cfg3: packed 576->512 projection, cache-row writes,
-    select, reduce) at B=1 and B=8, eager and replayed from a HIP graph;
+  * decode-step latency (cfg3: packed 576->512 projection, router cache update,
+    cache-row writes, select, reduce) at B=1 and B=8, eager and replayed from a
+    HIP graph;
   * the CPU oracle timed on this host's cores on a bounded sample.
 """
 from __future__ import annotations
@@ -56,6 +57,8 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-chain", action="store_true",
                     help="run only the timed chain (for profiler runs)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="time only the cfg3 decode step (B=1 and B=8) and exit")
     ap.add_argument("--profile-kernels", type=int, default=0, metavar="N",
                     help="run a 256 MiB calibration copy, then each timed kernel N times, and "
                          "exit (the command profiled by rocprofv3 --kernel-trace / --pmc)")
@@ -122,17 +125,101 @@ def main() -> int:
         relation_select_packed_seq,
     )
     from relation_lm.inference import pack_sparse_cache_projection_weights
+    from relation_lm.kernels.router_cache import router_cache_update
     from relation_lm.workloads import (
         CONFIGS,
         RelationConfig,
         packed_projection_inputs,
         reduce_inputs,
+        router_cache_inputs,
         select_args,
         selection_inputs,
     )
 
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+
+    def run_decode():
+        """Decode-step latency (cfg3) at B=1 and B=8, eager and from a HIP graph."""
+        decode = {}
+        for batch in (1, 8):
+            dcfg = RelationConfig(**{**CONFIGS["cfg3"].__dict__, "batch": batch})
+            dsel = selection_inputs(dcfg, queries=1, device=device)
+            dred = reduce_inputs(dcfg, device=device)
+            dexp = relation_linear(dred["operand_cache"], dred["expanded_weight"],
+                                   dred["expanded_bias"])
+            memory, weights = packed_projection_inputs(dcfg, device=device)
+            projection = pack_sparse_cache_projection_weights(weights)
+            rc = router_cache_inputs(dcfg, device=device)
+            dargs = select_args(dsel, dcfg)
+            t = dcfg.context - 1
+            position = dsel["position"]
+
+            def decode_step(dsel=dsel, dred=dred, dexp=dexp, memory=memory, projection=projection,
+                            dargs=dargs, t=t, position=position, batch=batch, rc=rc, dcfg=dcfg):
+                parts = projection.project(memory)
+                router_cache_update(parts[4], parts[5], rc["anchor_raw_cache"],
+                                    rc["partner_raw_cache"], rc["anchor_conv_cache"],
+                                    rc["partner_conv_cache"], dsel["anchor_block_mean"],
+                                    dsel["anchor_block_std"], dsel["partner_block_mean"],
+                                    dsel["partner_block_std"], rc["anchor_conv_weight"],
+                                    rc["partner_conv_weight"], position, dcfg.block_size)
+                dsel["anchor_keys"][:, t] = parts[0]
+                dsel["partner_keys"][:, t] = parts[1]
+                dred["operand_cache"][:, t] = parts[2]
+                dsel["partner_anchor_cache"][:, t] = parts[3]
+                a_, s_, p_, ps_ = relation_select_packed(*dargs)
+                if batch == 1:
+                    hid = relation_hidden_cache_update(
+                        dexp, dred["operand_cache"], a_, p_, dred["anchor_weight"],
+                        dred["partner_weight"], dred["product_weight"], dred["first_bias"], position)
+                else:
+                    row = relation_linear(dred["operand_cache"][:, t], dred["expanded_weight"],
+                                          dred["expanded_bias"])
+                    dexp[:, t] = row
+                    hid = relation_hidden_cached(dexp, dred["operand_cache"], a_, p_,
+                                                 dred["product_weight"])
+                raw_ = relation_linear(hid, dred["second_weight"], dred["second_bias"],
+                                       out_dtype=torch.float32)
+                return relation_norm_reduce(raw_, ps_, dred["norm_weight"], dred["norm_bias"],
+                                            position, 1e-5)
+
+            for _ in range(20):
+                decode_step()
+            torch.cuda.synchronize()
+            start.record()
+            for _ in range(args.decode_steps):
+                decode_step()
+            end.record()
+            torch.cuda.synchronize()
+            eager_us = start.elapsed_time(end) * 1e3 / args.decode_steps
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                decode_step()
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                decode_step()
+            for _ in range(10):
+                graph.replay()
+            torch.cuda.synchronize()
+            start.record()
+            for _ in range(args.decode_steps):
+                graph.replay()
+            end.record()
+            torch.cuda.synchronize()
+            graph_us = start.elapsed_time(end) * 1e3 / args.decode_steps
+            decode[f"B{batch}"] = {"eager_us": round(eager_us, 2), "graph_us": round(graph_us, 2)}
+
+        return decode
+
+    if args.decode_only:
+        print(json.dumps({"decode_step_us": run_decode()}), flush=True)
+        return 0
+
     cfg = CONFIGS["cfg2"]
     sel = selection_inputs(cfg, device=device)
     red = reduce_inputs(cfg, device=device)
@@ -210,9 +297,6 @@ def main() -> int:
         print(json.dumps({"only_chain": True, "steps": args.steps}), flush=True)
         return 0
 
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-
     def timed(fn, count):
         torch.cuda.synchronize()
         start.record()
@@ -274,70 +358,7 @@ def main() -> int:
                                             "relation_hidden", "second_linear", "norm_reduce"))
     fused_bytes = sum(nbytes[k] for k in headline)
 
-    # Decode step (cfg3) at B=1 and B=8.
-    decode = {}
-    for batch in (1, 8):
-        dcfg = RelationConfig(**{**CONFIGS["cfg3"].__dict__, "batch": batch})
-        dsel = selection_inputs(dcfg, queries=1, device=device)
-        dred = reduce_inputs(dcfg, device=device)
-        dexp = relation_linear(dred["operand_cache"], dred["expanded_weight"],
-                               dred["expanded_bias"])
-        memory, weights = packed_projection_inputs(dcfg, device=device)
-        projection = pack_sparse_cache_projection_weights(weights)
-        dargs = select_args(dsel, dcfg)
-        t = dcfg.context - 1
-        position = dsel["position"]
-
-        def decode_step(dsel=dsel, dred=dred, dexp=dexp, memory=memory, projection=projection,
-                        dargs=dargs, t=t, position=position, batch=batch):
-            parts = projection.project(memory)
-            dsel["anchor_keys"][:, t] = parts[0]
-            dsel["partner_keys"][:, t] = parts[1]
-            dred["operand_cache"][:, t] = parts[2]
-            dsel["partner_anchor_cache"][:, t] = parts[3]
-            a_, s_, p_, ps_ = relation_select_packed(*dargs)
-            if batch == 1:
-                hid = relation_hidden_cache_update(
-                    dexp, dred["operand_cache"], a_, p_, dred["anchor_weight"],
-                    dred["partner_weight"], dred["product_weight"], dred["first_bias"], position)
-            else:
-                row = relation_linear(dred["operand_cache"][:, t], dred["expanded_weight"],
-                                      dred["expanded_bias"])
-                dexp[:, t] = row
-                hid = relation_hidden_cached(dexp, dred["operand_cache"], a_, p_,
-                                             dred["product_weight"])
-            raw_ = relation_linear(hid, dred["second_weight"], dred["second_bias"],
-                                   out_dtype=torch.float32)
-            return relation_norm_reduce(raw_, ps_, dred["norm_weight"], dred["norm_bias"],
-                                        position, 1e-5)
-
-        for _ in range(20):
-            decode_step()
-        torch.cuda.synchronize()
-        start.record()
-        for _ in range(args.decode_steps):
-            decode_step()
-        end.record()
-        torch.cuda.synchronize()
-        eager_us = start.elapsed_time(end) * 1e3 / args.decode_steps
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            decode_step()
-        torch.cuda.current_stream().wait_stream(side)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            decode_step()
-        for _ in range(10):
-            graph.replay()
-        torch.cuda.synchronize()
-        start.record()
-        for _ in range(args.decode_steps):
-            graph.replay()
-        end.record()
-        torch.cuda.synchronize()
-        graph_us = start.elapsed_time(end) * 1e3 / args.decode_steps
-        decode[f"B{batch}"] = {"eager_us": round(eager_us, 2), "graph_us": round(graph_us, 2)}
+    decode = run_decode()
 
     cpu = None
     if not args.no_cpu_baseline:

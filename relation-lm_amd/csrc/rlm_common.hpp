@@ -237,16 +237,42 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return best;
 }
 
-__device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+// Sum over the 16 lanes of a DPP row; every lane of the row gets the same bits
+// (each step adds a pair in both orders, and float addition commutes).
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __uint_as_float(dpp_u32<kDppXor1>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<kDppXor2>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<kDppHalfMirror>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<kDppMirror>(__float_as_uint(v)));
   return v;
 }
 
+// Sum of the neighbouring 16-lane rows (0,1) and (2,3), then of the two
+// 32-lane halves: v_permlane16/32_swap exchange whole rows in VALU.
+__device__ __forceinline__ float swap16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float swap32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Wave64 sum / max with DPP row steps and two row swaps (no LDS round trips);
+// every lane gets the same bits.
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  return swap32_sum(swap16_sum(row16_sum(v)));
+}
+
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
+  v = fmaxf(v, __uint_as_float(dpp_u32<kDppXor1>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<kDppXor2>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<kDppHalfMirror>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<kDppMirror>(__float_as_uint(v))));
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // Order-preserving map float -> uint32 (+0.0 and -0.0 map to the same key,

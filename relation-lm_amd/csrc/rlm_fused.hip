@@ -112,15 +112,6 @@ __device__ __forceinline__ void lds_dma16(rsrc_t r, uint32_t lds_addr, uint32_t 
                : "memory");
 }
 
-// Row sum over the 16 lanes of a DPP row (every lane gets the same bits).
-__device__ __forceinline__ float row16_sum(float v) {
-  v += __uint_as_float(dpp_u32<kDppXor1>(__float_as_uint(v)));
-  v += __uint_as_float(dpp_u32<kDppXor2>(__float_as_uint(v)));
-  v += __uint_as_float(dpp_u32<kDppHalfMirror>(__float_as_uint(v)));
-  v += __uint_as_float(dpp_u32<kDppMirror>(__float_as_uint(v)));
-  return v;
-}
-
 // Weight p_k of row `grow` (< rows) in its query's partner mixture: softmax
 // over the active partners (rank < k_limit, score > -1e30; inactive scores
 // -1e4), renormalised by max(sum, 1e-9) -- relation_reduce.py:399-411.
@@ -461,14 +452,8 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
     gm[j] = cst[kMaxD + dcol0 + 16 * j + r16];
     bt[j] = cst[2 * kMaxD + dcol0 + 16 * j + r16];
   }
-  auto cross16 = [](float v) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  };
-  auto cross32 = [](float v) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  };
+  auto cross16 = [](float v) { return swap16_sum(v); };
+  auto cross32 = [](float v) { return swap32_sum(v); };
   if (K >= 4) {
     float v[kRowTiles][DT], W[kRowTiles];
 #pragma unroll

@@ -20,10 +20,11 @@
 //                 tile and loads all of its A and W fragments for the whole K
 //                 straight from L2 in MFMA operand layout -- one round trip,
 //                 no LDS staging and no barriers.
-//   skinny_kernel (M <= 64)  decode shapes.  A workgroup owns 16 output columns
-//                 and every row; its four waves split K, each streaming its
-//                 W and A slices straight from global memory in MFMA operand
-//                 layout, and the partial sums meet once in LDS.
+//   skinny_kernel (M <= 64)  decode shapes.  A workgroup owns one 16x16 output
+//                 tile; its eight waves split K, each issuing the W and A
+//                 fragment loads of up to six 32-wide slices at once straight
+//                 from global memory in MFMA operand layout, and the partial
+//                 tiles meet once in LDS.
 //
 // fp32 weights: f32_tile_kernel, 64x64 tiles on v_mfma_f32_16x16x4f32 (fp32
 // operands, fp32 accumulation), so fp32 mode never passes through reduced
@@ -306,61 +307,55 @@ __global__ void __launch_bounds__(256) smallk_kernel(const GemmParams p) {
 // 16-bit weights, M <= 64 (decode)
 // ---------------------------------------------------------------------------
 
-template <typename TA, typename W, typename TO, int MT>
-__global__ void __launch_bounds__(256) skinny_kernel(const GemmParams p) {
-  __shared__ f32x4 part[4][MT][kWave];
+constexpr int kSkinnyWaves = 8;
+constexpr int kSkinnyBatch = 6;  // k-slices whose loads a wave issues together
+
+// One 16x16 output tile per workgroup (grid: N/16 x M/16).  The 8 waves split
+// K into 32-wide slices (wave w takes slices w, w+8, ...); each wave issues
+// the A and W fragment loads of up to kSkinnyBatch slices at once, so a wave
+// pays about one memory round trip per batch, and the 8 partial tiles are
+// summed in LDS in a fixed order.
+template <typename TA, typename W, typename TO>
+__global__ void __launch_bounds__(kSkinnyWaves * kWave) skinny_kernel(const GemmParams p) {
+  __shared__ f32x4 part[kSkinnyWaves][kWave];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 16;
   const int r16 = lane & 15;
   const int kq = (lane >> 4) * 8;
   const TA* A = static_cast<const TA*>(p.a);
   const W* Wt = static_cast<const W*>(p.w);
   const bool n_ok = n0 + r16 < p.N;
+  const bool m_ok = m0 + r16 < p.M;
   const W* wrow = Wt + (n_ok ? (n0 + r16) * p.K : 0);
-  const TA* arow[MT];
-  bool m_ok[MT];
+  const TA* arow = A + (m_ok ? (m0 + r16) * p.lda : 0);
+  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int64_t slices = (p.K + kBK - 1) / kBK;
+  for (int64_t s0 = wave; s0 < slices; s0 += kSkinnyWaves * kSkinnyBatch) {
+    uint4 a[kSkinnyBatch], b[kSkinnyBatch];
 #pragma unroll
-  for (int i = 0; i < MT; ++i) {
-    const int64_t m = i * 16 + r16;
-    m_ok[i] = m < p.M;
-    arow[i] = A + (m_ok[i] ? m * p.lda : 0);
-  }
-  f32x4 acc[MT];
-#pragma unroll
-  for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  // Wave w takes k-slices w, w+4, ...; two slices per trip keep two loads in flight.
-  for (int64_t k0 = static_cast<int64_t>(wave) * kBK; k0 < p.K; k0 += 8 * kBK) {
-    // K is a multiple of 8, so an 8-element chunk is either wholly inside or past K.
-    const int64_t k1 = k0 + 4 * kBK;
-    const bool in0 = k0 + kq < p.K;
-    const bool in1 = k1 + kq < p.K;
-    const uint4 b0 = (n_ok && in0) ? load8<W, W>(wrow, k0 + kq) : make_uint4(0, 0, 0, 0);
-    const uint4 b1 = (n_ok && in1) ? load8<W, W>(wrow, k1 + kq) : make_uint4(0, 0, 0, 0);
-    uint4 a0[MT], a1[MT];
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      a0[i] = (m_ok[i] && in0) ? load8<TA, W>(arow[i], k0 + kq) : make_uint4(0, 0, 0, 0);
-      a1[i] = (m_ok[i] && in1) ? load8<TA, W>(arow[i], k1 + kq) : make_uint4(0, 0, 0, 0);
+    for (int u = 0; u < kSkinnyBatch; ++u) {
+      // K is a multiple of 8, so an 8-element chunk is either wholly inside or past K.
+      const int64_t k = (s0 + u * kSkinnyWaves) * kBK + kq;
+      const bool in = k < p.K;
+      b[u] = (n_ok && in) ? load8<W, W>(wrow, k) : make_uint4(0, 0, 0, 0);
+      a[u] = (m_ok && in) ? load8<TA, W>(arow, k) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      acc[i] = mfma16<W>(__builtin_bit_cast(u16x8, a0[i]), __builtin_bit_cast(u16x8, b0), acc[i]);
-      acc[i] = mfma16<W>(__builtin_bit_cast(u16x8, a1[i]), __builtin_bit_cast(u16x8, b1), acc[i]);
-    }
+    for (int u = 0; u < kSkinnyBatch; ++u)
+      acc = mfma16<W>(__builtin_bit_cast(u16x8, a[u]), __builtin_bit_cast(u16x8, b[u]), acc);
   }
-#pragma unroll
-  for (int i = 0; i < MT; ++i) part[wave][i][lane] = acc[i];
+  part[wave][lane] = acc;
   __syncthreads();
   if (wave != 0) return;
+  f32x4 sum = part[0][lane];
+#pragma unroll
+  for (int w = 1; w < kSkinnyWaves; ++w) sum += part[w][lane];
   const int64_t n = n0 + r16;
   const float bv = (p.bias && n < p.N) ? load_any_f(p.bias, p.bias_dtype, n) : 0.0f;
-#pragma unroll
-  for (int i = 0; i < MT; ++i) {
-    const f32x4 s = ((part[0][i][lane] + part[1][i][lane]) + part[2][i][lane]) + part[3][i][lane];
-    store_tile<TO>(p, s, i * 16, n, bv, lane);
-  }
+  store_tile<TO>(p, sum, m0, n, bv, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -433,14 +428,8 @@ __global__ void __launch_bounds__(256) f32_tile_kernel(const GemmParams p) {
 template <typename TA, typename W, typename TO>
 hipError_t launch_typed(const GemmParams& p, hipStream_t s) {
   if (p.M <= kSkinnyM) {
-    const dim3 grid(static_cast<unsigned>((p.N + 15) / 16));
-    const int mt = static_cast<int>((p.M + 15) / 16);
-    if (mt <= 1)
-      hipLaunchKernelGGL((skinny_kernel<TA, W, TO, 1>), grid, dim3(256), 0, s, p);
-    else if (mt == 2)
-      hipLaunchKernelGGL((skinny_kernel<TA, W, TO, 2>), grid, dim3(256), 0, s, p);
-    else
-      hipLaunchKernelGGL((skinny_kernel<TA, W, TO, 4>), grid, dim3(256), 0, s, p);
+    const dim3 grid(static_cast<unsigned>((p.N + 15) / 16), static_cast<unsigned>((p.M + 15) / 16));
+    hipLaunchKernelGGL((skinny_kernel<TA, W, TO>), grid, dim3(kSkinnyWaves * kWave), 0, s, p);
     return launch_status("linear");
   }
   const int64_t big = ((p.M + 127) / 128) * ((p.N + 127) / 128);

@@ -512,7 +512,7 @@ __global__ void __launch_bounds__(256) norm_reduce_vec_kernel(const NormParams p
 #pragma unroll
     for (int kk = 0; kk < KB; ++kk) {
       if (k0 + kk >= p.K) break;
-      const float pk = __shfl(prob, k0 + kk, kWave);
+      const float pk = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(prob), k0 + kk));
       if (pk == 0.0f) continue;  // wave-uniform: inactive rows contribute exactly 0
       float sum = 0.0f;
 #pragma unroll
@@ -568,7 +568,7 @@ __global__ void __launch_bounds__(256) norm_reduce_kernel(const NormParams p) {
   const float inv_d = 1.0f / static_cast<float>(p.D);
   const TR* raw = static_cast<const TR*>(p.raw) + q * p.K * static_cast<int64_t>(p.D);
   for (int k = 0; k < p.K; ++k) {
-    const float pk = __shfl(prob, k, kWave);
+    const float pk = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(prob), k));
     if (pk == 0.0f) continue;  // wave-uniform: inactive rows contribute exactly 0
     const TR* row = raw + static_cast<int64_t>(k) * p.D;
     float x[VPL];

@@ -8,11 +8,12 @@
 // block_router.py:50-68).
 //
 // Mapping: one wavefront per (batch row, stream); a lane owns one router
-// column (columns beyond 64 loop).  The whole update is a handful of
-// dependent loads, so the kernel is latency-bound: the block's BS conv rows
-// are loaded in one batch, before the conv of the current row is known, and
-// the current row's value is taken from registers rather than re-read after
-// its own store (the reference substitutes it the same way, :113-117).
+// column (columns beyond 64 loop).  The update is latency-bound, so the fast
+// form (one state dtype, block size 8/16/32/64) issues every load of a lane in
+// one batch and keeps the block's conv rows in registers for both moments; a
+// general form covers mixed dtypes and other block sizes.  The current row's
+// value is taken from registers rather than re-read after its own store (the
+// reference substitutes it the same way, :113-117).
 //
 // Numerics follow the reference's fp32 evaluation order: conv = raw*w2, then
 // + (prev1*w1), then + (prev2*w0), each product rounded before its add; the
@@ -54,9 +55,17 @@ __device__ __forceinline__ void store_any_f(void* p, int dtype, int64_t i, float
   }
 }
 
-constexpr int kRowBatch = 8;  // block rows loaded per batch of independent loads
+template <typename T>
+__device__ __forceinline__ void store_elem(void* p, int64_t i, float v) {
+  static_cast<T*>(p)[i] = from_f32<T>(v);
+}
 
-__global__ void __launch_bounds__(kWave) router_cache_kernel(const RouterParams p) {
+// Fast form: raw rows of type TR; raw/conv caches, statistics and conv weights
+// all of type TC; block size BS known at compile time.  Every load of a lane
+// -- this token's raw value, the two previous raw rows, the weights and the
+// block's BS conv rows -- is issued before any is used.
+template <int BS, typename TR, typename TC>
+__global__ void __launch_bounds__(kWave) router_cache_fast_kernel(const RouterParams p) {
   const int b = blockIdx.x;
   const int side = blockIdx.y;  // 0 anchor stream, 1 partner stream
   const int lane = threadIdx.x;
@@ -67,11 +76,78 @@ __global__ void __launch_bounds__(kWave) router_cache_kernel(const RouterParams 
     return;
   }
   const int64_t row_t = static_cast<int64_t>(b) * p.T + t;
-  const int64_t j = t / p.BS;
-  const int64_t first = j * p.BS;
+  const int64_t j = t / BS;
+  const int64_t first = j * BS;
+  const bool stats = j < p.NB;
+  const TR* raw = static_cast<const TR*>(p.raw[side]) + b * p.raw_stride[side];
+  const TC* raw_cache = static_cast<const TC*>(p.raw_cache[side]);
+  const TC* weight = static_cast<const TC*>(p.weight[side]);
+  // This batch row's conv cache: rows past its end are out of range (read 0).
+  const uint32_t row_bytes = static_cast<uint32_t>(p.D) * sizeof(TC);
+  const rsrc_t conv_rsrc = make_rsrc(
+      static_cast<const unsigned char*>(p.conv_cache[side]) + static_cast<int64_t>(b) * p.T * row_bytes,
+      static_cast<uint32_t>(p.T) * row_bytes);
+  const int64_t prev1 = t >= 1 ? row_t - 1 : row_t;  // clamped: the value is unused at t = 0
+  const int64_t prev2 = t >= 2 ? row_t - 2 : row_t;
   for (int c = lane; c < p.D; c += kWave) {
-    // Independent loads first: this token's raw value, the two previous raw
-    // rows, the conv weights and the block's conv rows.
+    const float x = to_f32(raw[c]);
+    const float p1 = to_f32(raw_cache[prev1 * p.D + c]);
+    const float p2 = to_f32(raw_cache[prev2 * p.D + c]);
+    const float w0 = to_f32(weight[3 * c]);
+    const float w1 = to_f32(weight[3 * c + 1]);
+    const float w2 = to_f32(weight[3 * c + 2]);
+    const uint32_t base = static_cast<uint32_t>(first) * row_bytes + c * sizeof(TC);
+    float rows[BS];
+#pragma unroll
+    for (int r = 0; r < BS; ++r) rows[r] = buf_load_elem<TC>(conv_rsrc, base + r * row_bytes);
+    float conv;
+    {
+#pragma clang fp contract(off)
+      conv = x * w2;
+      if (t >= 1) conv = conv + p1 * w1;
+      if (t >= 2) conv = conv + p2 * w0;
+    }
+    store_elem<TC>(p.raw_cache[side], row_t * p.D + c, x);
+    store_elem<TC>(p.conv_cache[side], row_t * p.D + c, conv);
+    out[c] = conv;
+    if (!stats) continue;
+    // Block statistics over all BS rows; the token's own row from registers.
+    const int own = static_cast<int>(t - first);
+    float sum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < BS; ++r) {
+      rows[r] = r == own ? conv : rows[r];
+      sum += rows[r];
+    }
+    const float mean = sum / static_cast<float>(BS);
+    float sq = 0.0f;
+#pragma unroll
+    for (int r = 0; r < BS; ++r) {
+      const float d = rows[r] - mean;
+      sq += d * d;
+    }
+    const int64_t s = (static_cast<int64_t>(b) * p.NB + j) * p.D + c;
+    store_elem<TC>(p.mean[side], s, mean);
+    store_elem<TC>(p.stdev[side], s, sqrtf(sq / static_cast<float>(BS)));
+  }
+}
+
+// General form: any float dtype per tensor, any block size.
+__global__ void __launch_bounds__(kWave) router_cache_kernel(const RouterParams p) {
+  const int b = blockIdx.x;
+  const int side = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int64_t t = load_any_i(p.pos, p.pos_dtype, 0);
+  float* out = p.out + (static_cast<int64_t>(b) * 2 + side) * p.D;
+  if (t < 0 || t >= p.T) {
+    for (int c = lane; c < p.D; c += kWave) out[c] = 0.0f;
+    return;
+  }
+  const int BS = p.BS;
+  const int64_t row_t = static_cast<int64_t>(b) * p.T + t;
+  const int64_t j = t / BS;
+  const int64_t first = j * BS;
+  for (int c = lane; c < p.D; c += kWave) {
     const float x = load_any_f(p.raw[side], p.raw_dtype[side], b * p.raw_stride[side] + c);
     const float p1 = t >= 1 ? load_any_f(p.raw_cache[side], p.raw_cache_dtype[side],
                                          (row_t - 1) * p.D + c)
@@ -93,43 +169,24 @@ __global__ void __launch_bounds__(kWave) router_cache_kernel(const RouterParams 
     store_any_f(p.conv_cache[side], p.conv_cache_dtype[side], row_t * p.D + c, conv);
     out[c] = conv;
     if (j >= p.NB) continue;
-    // Block statistics over all BS rows; the token's own row from registers.
+    auto block_row = [&](int r) {
+      const int64_t idx = first + r;
+      if (idx == t) return conv;
+      return idx < p.T ? load_any_f(p.conv_cache[side], p.conv_cache_dtype[side],
+                                    (static_cast<int64_t>(b) * p.T + idx) * p.D + c)
+                       : 0.0f;
+    };
     float sum = 0.0f;
-    float rows[kRowBatch];
-    for (int r0 = 0; r0 < p.BS; r0 += kRowBatch) {
-#pragma unroll
-      for (int u = 0; u < kRowBatch; ++u) {
-        const int64_t idx = first + r0 + u;
-        rows[u] = (r0 + u < p.BS && idx < p.T && idx != t)
-                      ? load_any_f(p.conv_cache[side], p.conv_cache_dtype[side],
-                                   (static_cast<int64_t>(b) * p.T + idx) * p.D + c)
-                      : 0.0f;
-        if (idx == t) rows[u] = conv;
-      }
-#pragma unroll
-      for (int u = 0; u < kRowBatch; ++u)
-        if (r0 + u < p.BS) sum += rows[u];
-    }
-    const float mean = sum / static_cast<float>(p.BS);
+    for (int r = 0; r < BS; ++r) sum += block_row(r);
+    const float mean = sum / static_cast<float>(BS);
     float sq = 0.0f;
-    for (int r0 = 0; r0 < p.BS; r0 += kRowBatch) {
-#pragma unroll
-      for (int u = 0; u < kRowBatch; ++u) {
-        const int64_t idx = first + r0 + u;
-        float v = (r0 + u < p.BS && idx < p.T && idx != t)
-                      ? load_any_f(p.conv_cache[side], p.conv_cache_dtype[side],
-                                   (static_cast<int64_t>(b) * p.T + idx) * p.D + c)
-                      : 0.0f;
-        if (idx == t) v = conv;
-        if (r0 + u < p.BS) {
-          const float d = v - mean;
-          sq += d * d;
-        }
-      }
+    for (int r = 0; r < BS; ++r) {
+      const float d = block_row(r) - mean;
+      sq += d * d;
     }
     const int64_t s = (static_cast<int64_t>(b) * p.NB + j) * p.D + c;
     store_any_f(p.mean[side], p.mean_dtype[side], s, mean);
-    store_any_f(p.stdev[side], p.std_dtype[side], s, sqrtf(sq / static_cast<float>(p.BS)));
+    store_any_f(p.stdev[side], p.std_dtype[side], s, sqrtf(sq / static_cast<float>(BS)));
   }
 }
 
@@ -149,6 +206,27 @@ bool check_stats(const rlm_tensor* t, const char* name, int64_t B, int64_t D, in
   }
   *nb = t->shape[1];
   return true;
+}
+
+template <typename TR, typename TC>
+hipError_t launch_fast(const RouterParams& p, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(p.B), 2);
+  switch (p.BS) {
+    case 8: hipLaunchKernelGGL((router_cache_fast_kernel<8, TR, TC>), grid, dim3(kWave), 0, stream, p); break;
+    case 16: hipLaunchKernelGGL((router_cache_fast_kernel<16, TR, TC>), grid, dim3(kWave), 0, stream, p); break;
+    case 32: hipLaunchKernelGGL((router_cache_fast_kernel<32, TR, TC>), grid, dim3(kWave), 0, stream, p); break;
+    default: hipLaunchKernelGGL((router_cache_fast_kernel<64, TR, TC>), grid, dim3(kWave), 0, stream, p); break;
+  }
+  return launch_status("router_cache_update");
+}
+
+template <typename TC>
+hipError_t launch_fast_tc(const RouterParams& p, hipStream_t stream) {
+  switch (p.raw_dtype[0]) {
+    case RLM_BF16: return launch_fast<bf16, TC>(p, stream);
+    case RLM_F16: return launch_fast<f16, TC>(p, stream);
+    default: return launch_fast<float, TC>(p, stream);
+  }
 }
 
 }  // namespace
@@ -240,6 +318,21 @@ extern "C" hipError_t rlm_router_cache_update(
   p.pos = position->data;
   p.pos_dtype = position->dtype;
   p.out = static_cast<float*>(out->data);
+  const int64_t conv_row_block = T * D * (anchor_conv_cache->dtype == RLM_F32 ? 4 : 2);
+  RLM_REQUIRE(conv_row_block + block_size * D * 4 < (int64_t(1) << 31),
+              "a batch row of the conv caches must be smaller than 2 GiB");
+  // One state dtype (fp32 or bf16) for caches, statistics and weights, one raw
+  // dtype, and a block size of 8/16/32/64 take the fast kernel.
+  const int tc = anchor_conv_cache->dtype;
+  bool uniform = tc == RLM_F32 || tc == RLM_BF16;
+  for (const rlm_tensor* x : {partner_raw_cache, anchor_raw_cache, partner_conv_cache,
+                              anchor_mean, anchor_std, partner_mean, partner_std,
+                              anchor_conv_weight, partner_conv_weight})
+    uniform = uniform && x->dtype == tc;
+  uniform = uniform && partner_raw->dtype == anchor_raw->dtype;
+  const bool fast_bs = block_size == 8 || block_size == 16 || block_size == 32 || block_size == 64;
+  if (uniform && fast_bs)
+    return tc == RLM_BF16 ? launch_fast_tc<bf16>(p, stream) : launch_fast_tc<float>(p, stream);
   hipLaunchKernelGGL(router_cache_kernel, dim3(static_cast<unsigned>(B), 2), dim3(kWave), 0,
                      stream, p);
   return launch_status("router_cache_update");

@@ -117,6 +117,21 @@ def selection_inputs(cfg: RelationConfig, *, queries: int | None = None,
     return {k: v.to(device) for k, v in out.items()}
 
 
+def router_cache_inputs(cfg: RelationConfig, *, device: torch.device | str = "cpu",
+                        seed: int | None = None) -> dict:
+    """Decode-time router state of both streams for router_cache_update: raw and
+    conv caches [B,T,RD] (fp32, N(0,1)) and depthwise conv weights [RD,3]
+    (N(0,1) * 0.1, the scale of the reference's test)."""
+    g = _gen((cfg.seed if seed is None else seed) + 7919)
+    b, t, rd = cfg.batch, cfg.context, cfg.heads * cfg.head_dim
+    out = {}
+    for side in ("anchor", "partner"):
+        out[f"{side}_raw_cache"] = _randn(g, b, t, rd)
+        out[f"{side}_conv_cache"] = _randn(g, b, t, rd)
+        out[f"{side}_conv_weight"] = _randn(g, rd, 3, scale=0.1)
+    return {k: v.to(device) for k, v in out.items()}
+
+
 SELECT_ORDER = ("anchor_query", "anchor_keys", "anchor_router_query", "anchor_block_mean",
                 "anchor_block_std", "anchor_gamma", "anchor_bias", "partner_base",
                 "partner_anchor_cache", "partner_keys", "partner_block_mean",
