@@ -141,24 +141,25 @@ __device__ __forceinline__ float buf_load_elem<f16>(rsrc_t r, uint32_t off) {
 // Elementwise math
 // ---------------------------------------------------------------------------
 
-// erf(x) by Abramowitz & Stegun, Handbook of Mathematical Functions, 7.1.26:
-// 1 - (a1 t + ... + a5 t^5) exp(-x^2), t = 1/(1 + p|x|), odd extension;
-// |error| <= 1.5e-7 for all x.
-__device__ __forceinline__ float erf_as7126(float x) {
-  const float ax = fabsf(x);
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, ax, 1.0f));
-  float y = fmaf(1.061405429f, t, -1.453152027f);
-  y = fmaf(y, t, 1.421413741f);
-  y = fmaf(y, t, -0.284496736f);
-  y = fmaf(y, t, 0.254829592f);
-  y *= t;
-  const float r = fmaf(-y, __expf(-ax * ax), 1.0f);
-  return copysignf(r, x);
-}
-
-// Exact (erf) GELU, x * Phi(x) (relation_reduce.py:139).
+// Exact (erf) GELU, x * Phi(x) (relation_reduce.py:139), with erf by
+// Abramowitz & Stegun, Handbook of Mathematical Functions, 7.1.26
+// (1 - erf(z) = t (a1 + a2 t + ... + a5 t^4) exp(-z^2), t = 1/(1 + p z), z >= 0,
+// |error| <= 1.5e-7), constants folded: for a = |x|,
+//   h = Phi(-a) = 0.5 * (1 - erf(a/sqrt2)) = t * poly(t) * exp(-x^2/2),
+//   t = 1/(1 + p a/sqrt2), poly with the A&S coefficients halved,
+// and GELU(x) = x h for x < 0, x - x h for x >= 0.  Forming x h directly keeps
+// the relative accuracy of the negative tail (no 1 + erf cancellation).
+// 12 VALU operations plus one v_rcp and one v_exp.
 __device__ __forceinline__ float gelu_erf(float x) {
-  return 0.5f * x * (1.0f + erf_as7126(x * 0.70710678118654752440f));
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f * 0.70710678118654752440f, fabsf(x), 1.0f));
+  float y = fmaf(0.5f * 1.061405429f, t, 0.5f * -1.453152027f);
+  y = fmaf(y, t, 0.5f * 1.421413741f);
+  y = fmaf(y, t, 0.5f * -0.284496736f);
+  y = fmaf(y, t, 0.5f * 0.254829592f);
+  y *= t;
+  const float e = __builtin_amdgcn_exp2f(x * (x * (-0.5f * 1.44269504088896340736f)));
+  const float xh = x * (y * e);
+  return x < 0.0f ? xh : x - xh;
 }
 
 // ---------------------------------------------------------------------------

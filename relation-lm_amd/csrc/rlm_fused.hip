@@ -296,6 +296,11 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
     for (int j = 0; j < DT; ++j) raw[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   const unsigned char* my_gat = smem + kOffGather + lrow * kGatherRowBytes;
+  // Constant A operand [I16 | I16]: lane (r16, g) holds row r16, k = 8g..8g+7,
+  // 1.0 (bf16 0x3F80) where k % 16 == r16.
+  u16x8 ident;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) ident[k] = (8 * (g & 1) + k == r16) ? 0x3F80 : 0;
   unsigned char* my_hid = hid + lrow * (2 * kLd) + 8 * g;
 
   const int nchunks = H / kHC;
@@ -309,8 +314,17 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       f32x4 acc[4];
+      // The row's expanded-cache values enter on the matrix cores: B operand
+      // rows k < 16 are the anchor half's columns 16j + k, rows k >= 16 the
+      // partner half's columns 16j + k - 16 (piece 2j + g%2 of half g/2, one
+      // 16-byte read), against the constant A = [I | I].  The products by 1.0
+      // are exact.
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) acc[jj] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int jj = 0; jj < 4; ++jj) {
+        const int j = 4 * hh + jj;
+        const u16x8 gv = lds_frag(my_gat + 256 * (g >> 1) + ((2 * j + (g & 1)) ^ r16) * 16);
+        acc[jj] = mfma_bf16(ident, gv, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+      }
 #pragma unroll
       for (int s = 0; s < KS1; ++s) {
         // A fragment: W_m tile row 16j + r16, k-piece (4s + g) stored swizzled.
@@ -324,21 +338,13 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
           acc[jj] = mfma_bf16(w[jj], pl[s], acc[jj]);
         }
       }
-      // acc[jj][e] = hidden[row lrow][col 16(4hh+jj) + 4g + e]; the row's
-      // expanded-cache values for those columns sit in piece 2j + g/2.
+      // acc[jj][e] = hidden[row lrow][col 16(4hh+jj) + 4g + e].
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const int j = 4 * hh + jj;
-        const int piece = ((2 * j + (g >> 1)) ^ r16) * 16 + 8 * (g & 1);
-        const uint2 ga = *reinterpret_cast<const uint2*>(my_gat + piece);
-        const uint2 gp = *reinterpret_cast<const uint2*>(my_gat + 256 + piece);
-        const float h0 = acc[jj][0] + (bf16_lo(ga.x) + bf16_lo(gp.x));
-        const float h1 = acc[jj][1] + (bf16_hi(ga.x) + bf16_hi(gp.x));
-        const float h2 = acc[jj][2] + (bf16_lo(ga.y) + bf16_lo(gp.y));
-        const float h3 = acc[jj][3] + (bf16_hi(ga.y) + bf16_hi(gp.y));
-        *reinterpret_cast<uint2*>(my_hid + 32 * j) =
-            make_uint2(pack_bf16x2(gelu_erf(h0), gelu_erf(h1)),
-                       pack_bf16x2(gelu_erf(h2), gelu_erf(h3)));
+        const f32x4 h = acc[jj];
+        *reinterpret_cast<uint2*>(my_hid + 32 * (4 * hh + jj)) =
+            make_uint2(pack_bf16x2(gelu_erf(h[0]), gelu_erf(h[1])),
+                       pack_bf16x2(gelu_erf(h[2]), gelu_erf(h[3])));
       }
     }
     u16x8 b[JC];
