@@ -107,6 +107,38 @@ hipError_t rlm_relation_select_packed_seq(
     const rlm_tensor* out_partner_score, hipStream_t stream);
 
 /*
+ * Routed multi-anchor selection: no reference kernel.  The reference has only
+ * the dense form, MultiAnchorRelationBlock._select_distinct_anchors and
+ * forward's partner selection (src/relation_lm/models/multi_relation_blocks.py:69-147);
+ * this op restricts its candidates to the routed set of the packed selection.
+ *   anchor_query [B,Tq,S,E], anchor_keys [B,T,S,E], anchor_router_query [B,Tq,RD],
+ *   anchor_block_mean/std [B,NB,H,HD], anchor_gamma [H], anchor_bias [H,RB],
+ *   partner_base [B,Tq,S,E+RD], partner_anchor_cache [B,T,S,E+RD],
+ *   partner_keys [B,T,S,E], partner_block_mean/std [B,NB,H,HD] (shared by the
+ *   slots), partner_gamma [H], partner_bias [H,RB], positions [Tq] or [B,Tq].
+ *   1 <= S <= 8, local_window >= S.
+ * Slot s is active iff s <= t; active slots take distinct anchors (argmax over
+ * the untaken candidates, slot order), inactive slots report anchor 0 and
+ * score -inf.  Each active slot's partners exclude every active anchor of the
+ * query; entries past the available candidates (and every entry of an
+ * inactive slot) hold position t-local_window+1 and score -inf.
+ * Outputs: out_anchor int32 [B,Tq,S], out_anchor_score f32 [B,Tq,S],
+ *          out_partner int32 [B,Tq,S,K], out_partner_score f32 [B,Tq,S,K].
+ */
+hipError_t rlm_multi_relation_select_seq(
+    const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
+    const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
+    const rlm_tensor* anchor_block_std, const rlm_tensor* anchor_gamma,
+    const rlm_tensor* anchor_bias, const rlm_tensor* partner_base,
+    const rlm_tensor* partner_anchor_cache, const rlm_tensor* partner_keys,
+    const rlm_tensor* partner_block_mean, const rlm_tensor* partner_block_std,
+    const rlm_tensor* partner_gamma, const rlm_tensor* partner_bias,
+    const rlm_tensor* positions, int64_t local_window, int64_t top_blocks,
+    int64_t k_out, int32_t strict_valid, const rlm_tensor* out_anchor,
+    const rlm_tensor* out_anchor_score, const rlm_tensor* out_partner,
+    const rlm_tensor* out_partner_score, hipStream_t stream);
+
+/*
  * Replaces relationlex::anchor_select
  *   (src/relation_lm/kernels/triton_select.py:255-295).
  *   anchor_query [B,E], anchor_keys [B,T,E], router_query [B,RD],

@@ -86,3 +86,41 @@ def distinct_anchors(scores: torch.Tensor, anchors: int):
                             torch.zeros_like(index))
         selected.append(index)
     return torch.stack(selected, dim=-1), active
+
+
+def multi_anchor_selection(anchor_query, anchor_keys, partner_base, partner_anchor_cache,
+                           partner_keys, k: int):
+    """MultiAnchorRelationBlock selection over full score matrices
+    (multi_relation_blocks.py:69-147).
+
+    Tensors [B,T,S,*] (S anchor slots), queries at positions 0..T-1.  Per slot:
+    causal anchor scores, distinct anchors by iterative argmax (:69-99), the
+    split partner query partner_base[s] + partner_anchor_cache[anchor, s] (the
+    anchor vector of an inactive slot is zero, :98), partner scores with every
+    active anchor and every inactive slot masked (:133-142), top-k (:144).
+    Returns (anchor [B,T,S], anchor_score [B,T,S], active [T,S],
+    partner [B,T,S,k], partner_score [B,T,S,k]).
+    """
+    batch, length, slots, exact_dim = anchor_query.shape
+    scores = torch.stack([causal_scores(anchor_query[:, :, s], anchor_keys[:, :, s])
+                          for s in range(slots)], dim=1)  # [B,S,T,T]
+    index, active = distinct_anchors(scores, slots)
+    anchor_score = scores.permute(0, 2, 1, 3).gather(-1, index[..., None])[..., 0]
+    anchor_active = active[None].expand(batch, -1, -1)
+    anchor_score = anchor_score.masked_fill(~anchor_active, -torch.inf)
+    one_hot = torch.nn.functional.one_hot(index, num_classes=length).bool()
+    all_anchor = (one_hot & anchor_active[..., None]).any(dim=-2)  # [B,T,T]
+    rows = torch.arange(batch)[:, None]
+    cache = partner_anchor_cache.to(torch.float32)
+    partner, partner_score = [], []
+    for s in range(slots):
+        contribution = cache[rows, index[:, :, s], s] * anchor_active[:, :, s, None]
+        query = partner_base[:, :, s].to(torch.float32)[..., :exact_dim] + contribution[..., :exact_dim]
+        ps = causal_scores(query, partner_keys[:, :, s])
+        ps = ps.masked_fill(all_anchor, -torch.inf)
+        ps = ps.masked_fill(~anchor_active[:, :, s, None], -torch.inf)
+        top, idx = ps.topk(k, dim=-1)
+        partner.append(idx)
+        partner_score.append(top)
+    return (index, anchor_score, active, torch.stack(partner, dim=2),
+            torch.stack(partner_score, dim=2))

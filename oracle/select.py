@@ -335,3 +335,141 @@ def partner_topk(partner_query, partner_keys, router_query, block_mean, block_st
                          block_std, gamma, bias, batch_of, t,
                          np.asarray(anchor_index, dtype=np.int64), int(local_window),
                          int(top_blocks), int(k_out), bool(strict_valid))
+
+
+# ---------------------------------------------------------------------------
+# Routed multi-anchor selection (no reference kernel; dense semantics at
+# src/relation_lm/models/multi_relation_blocks.py:69-147)
+# ---------------------------------------------------------------------------
+
+def _topk_lanes(score: np.ndarray, pos: np.ndarray, k_out: int):
+    """Stable descending top-k over candidate lanes; exhausted slots repeat
+    lane 0 with score -inf (the convention of _partner_core)."""
+    order = np.argsort(-score, axis=1, kind="stable")
+    available = (score > NEG_INF32).sum(axis=1)
+    rows = np.arange(score.shape[0])[:, None]
+    slot = np.arange(k_out)[None, :]
+    lanes = np.zeros((score.shape[0], k_out), dtype=np.int64)
+    take = min(k_out, order.shape[1])
+    lanes[:, :take] = order[:, :take]
+    lanes = np.where(slot < available[:, None], lanes, 0)
+    out_pos = pos[rows, lanes]
+    out_score = np.where(slot < available[:, None], score[rows, lanes], NEG_INF32)
+    return out_pos, out_score
+
+
+def _routed_lanes(router_query, mean, std, gamma, bias, batch_of, t, local_window,
+                  top_blocks, strict_valid, max_t):
+    """Candidate lanes [local | picked blocks in pick order] and their validity."""
+    blocks = mean.shape[1]
+    block_size = max_t // blocks
+    scores = block_scores(router_query, mean, std, gamma, bias, batch_of, t,
+                          block_size=block_size, local_window=local_window,
+                          strict_valid=strict_valid)
+    selected, sel_valid = pick_blocks(scores, top_blocks)
+    _, _, local_start = block_geometry(t, blocks, block_size, local_window, strict_valid,
+                                       bias.shape[1])
+    lpos, lvalid = _local_lanes(t, local_window, max_t)
+    rpos, rvalid = _remote_lanes(selected, sel_valid, t, local_start, block_size, max_t)
+    return np.concatenate([lpos, rpos], axis=1), np.concatenate([lvalid, rvalid], axis=1)
+
+
+def _multi_flat(aq, ak, arq, amean, astd, agamma, abias, pbase, pcache, pk, pmean, pstd,
+                pgamma, pbias, batch_of, t, local_window, top_blocks, k_out, strict_valid):
+    """S anchor slots per query over one routed anchor candidate set, then per
+    slot a routed partner set that excludes every active anchor.
+
+    Follows MultiAnchorRelationBlock (multi_relation_blocks.py):
+      * slot s is active iff s <= t (:84); inactive slots report anchor 0 (:94)
+        and no partners (:140-142);
+      * slot s takes the argmax of its own anchor score over the candidates not
+        already taken by slots < s (:86-95), ties to the lowest position;
+      * slot s's partner query is the split form of partner_query[s](cat(query,
+        anchor)) (:116-124): partner_base[s] + partner_anchor_cache[anchor, s]
+        in float32, exact half and router half;
+      * every active anchor of the query is excluded from every slot's
+        partners (:133-139); top-k as the single-anchor partner pass.
+    Routing replaces the dense causal candidate set by [local window | TOP
+    picked blocks]: the anchor picks come from the anchor router, shared by all
+    slots; each slot's partner picks come from its own router query against the
+    shared partner block statistics.
+    """
+    n = len(t)
+    slots = ak.shape[2]
+    max_t, exact_dim = ak.shape[1], ak.shape[3]
+    scale = 1.0 / math.sqrt(exact_dim)
+    anchor = np.zeros((n, slots), np.int32)
+    anchor_score = np.full((n, slots), NEG_INF32, np.float32)
+    partner = np.zeros((n, slots, k_out), np.int32)
+    partner_score = np.full((n, slots, k_out), NEG_INF32, np.float32)
+    for lo in range(0, n, _CHUNK):
+        sl = slice(lo, min(n, lo + _CHUNK))
+        b, tt = batch_of[sl], t[sl]
+        m = len(tt)
+        active = np.arange(slots)[None, :] <= tt[:, None]  # [m, S]
+        pos, valid = _routed_lanes(arq[sl], amean, astd, agamma, abias, b, tt, local_window,
+                                   top_blocks, strict_valid, max_t)
+        taken = np.zeros((m, 0), np.int64)
+        chosen = np.zeros((m, slots), np.int64)
+        for s in range(slots):
+            v = valid & ~(pos[:, :, None] == taken[:, None, :]).any(axis=2)
+            sc = exact_scores(ak[:, :, s], b, pos, v, aq[sl, s], scale)
+            best = sc.max(axis=1)
+            tie = (sc == best[:, None]) & (sc > NEG_INF32)
+            big = np.iinfo(np.int64).max
+            a = np.where(tie, pos, big).min(axis=1)
+            ok = active[:, s] & (best > NEG_INF32)
+            chosen[:, s] = np.where(ok, a, 0)
+            anchor_score[sl, s] = np.where(ok, best, NEG_INF32)
+            taken = np.concatenate([taken, np.where(ok, a, -1)[:, None]], axis=1)
+        anchor[sl] = chosen.astype(np.int32)
+        lane0 = tt - local_window + 1
+        for s in range(slots):
+            have = active[:, s]
+            contribution = _f32(pcache)[b, chosen[:, s], s]
+            contribution = np.where(have[:, None], contribution, np.float32(0))
+            base = _f32(pbase[sl, s])
+            pq = base[:, :exact_dim] + contribution[:, :exact_dim]
+            prq = base[:, exact_dim:] + contribution[:, exact_dim:]
+            ppos, pvalid = _routed_lanes(prq, pmean, pstd, pgamma, pbias, b, tt, local_window,
+                                         top_blocks, strict_valid, max_t)
+            pvalid &= ~(ppos[:, :, None] == taken[:, None, :]).any(axis=2)
+            pvalid &= have[:, None]
+            sc = exact_scores(pk[:, :, s], b, ppos, pvalid, pq, scale)
+            out_pos, out_score = _topk_lanes(sc, ppos, k_out)
+            out_pos = np.where(have[:, None], out_pos, lane0[:, None])
+            partner[sl, s] = out_pos.astype(np.int32)
+            partner_score[sl, s] = out_score
+    return anchor, anchor_score, partner, partner_score
+
+
+def multi_relation_select_seq(anchor_query, anchor_keys, anchor_router_query, anchor_block_mean,
+                              anchor_block_std, anchor_gamma, anchor_bias, partner_base,
+                              partner_anchor_cache, partner_keys, partner_block_mean,
+                              partner_block_std, partner_gamma, partner_bias, positions,
+                              local_window, top_blocks, k_out, strict_valid):
+    """Sequence form of the routed multi-anchor selection.
+
+    anchor_query [B,Tq,S,E], anchor_keys [B,T,S,E], anchor_router_query [B,Tq,RD],
+    partner_base [B,Tq,S,E+RD], partner_anchor_cache [B,T,S,E+RD],
+    partner_keys [B,T,S,E]; statistics, gamma and bias as the single-anchor op;
+    positions [Tq] or [B,Tq].  Returns anchor int32 [B,Tq,S], anchor_score f32
+    [B,Tq,S], partner int32 [B,Tq,S,K], partner_score f32 [B,Tq,S,K].
+    """
+    batch, queries, slots = anchor_query.shape[0], anchor_query.shape[1], anchor_query.shape[2]
+    batch_of, t = _flatten_queries(batch, queries, positions)
+
+    def flat(x):
+        x = np.asarray(x)
+        return x.reshape((batch * queries,) + x.shape[2:])
+
+    a, s, p, ps = _multi_flat(flat(anchor_query), np.asarray(anchor_keys),
+                              flat(anchor_router_query), anchor_block_mean, anchor_block_std,
+                              anchor_gamma, anchor_bias, flat(partner_base),
+                              np.asarray(partner_anchor_cache), np.asarray(partner_keys),
+                              partner_block_mean, partner_block_std, partner_gamma, partner_bias,
+                              batch_of, t, int(local_window), int(top_blocks), int(k_out),
+                              bool(strict_valid))
+    k = int(k_out)
+    return (a.reshape(batch, queries, slots), s.reshape(batch, queries, slots),
+            p.reshape(batch, queries, slots, k), ps.reshape(batch, queries, slots, k))

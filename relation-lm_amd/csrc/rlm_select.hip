@@ -695,6 +695,296 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
 }
 
 // ---------------------------------------------------------------------------
+// Routed multi-anchor selection (semantics: multi_relation_blocks.py:69-147)
+// ---------------------------------------------------------------------------
+//
+// S anchor slots per query.  The anchor router picks one candidate set per
+// query (local window + TOP blocks); slot s takes the argmax of its own exact
+// score over the candidates not taken by slots < s (distinct anchors,
+// :86-95), and is active only when s <= t (:84).  Each active slot then forms
+// its partner query (partner_base[s] + partner_anchor_cache[anchor_s, s], the
+// split form of partner_query[s](cat(query, anchor)), :116-124), routes its
+// own partner candidate set against the shared partner block statistics and
+// takes the top-k exact scores with every active anchor of the query excluded
+// (:133-139).  One wave per query, slots in order; keys are [B,T,S,E] rows, so
+// slot s's vector of position p sits at byte (p*S + s)*E*elem.
+
+constexpr int kMaxSlots = 8;
+
+struct MultiParams {
+  int S;                   // anchor slots per query
+  uint32_t key_pos_bytes;  // bytes between positions of a key cache (S*E*elem)
+  uint32_t slot_bytes;     // bytes of one slot's exact vector (E*elem)
+  int64_t qrow;            // elements per (query, slot) row of partner_base and of the cache (E+RD)
+};
+
+// Exact scores of every candidate lane of one slot into ws.sc (float32; -inf
+// when invalid or taken by an excluded position).  As candidate_scores, with
+// strided key rows and no staged windows: rows come through range-checked
+// buffer loads from L2.
+template <typename TA, int NCL>
+__device__ void slot_candidate_scores(const SelectParams& p, const void* keys_ptr,
+                                      uint32_t pos_bytes, uint32_t col_bytes, const Query& qy,
+                                      const int (&excl)[kMaxSlots], int nex, WaveScratch& ws,
+                                      int lane) {
+  constexpr int EPC = kEpc<TA>;
+  const rsrc_t keys = make_rsrc(keys_ptr, p.key_bytes);
+  const uint32_t row0 = static_cast<uint32_t>(qy.b * p.T);
+  const int t = static_cast<int>(qy.t);
+  const int ls = static_cast<int>(qy.local_start);
+  const int T = static_cast<int>(p.T);
+  const int chunks = p.G;
+  for (int c0 = 0; c0 < p.CAP; c0 += kWave * NCL) {
+    uint32_t off[NCL];
+    bool ok[NCL];
+#pragma unroll
+    for (int u = 0; u < NCL; ++u) {
+      const int c = c0 + lane + kWave * u;
+      bool v = c < p.CAP;
+      int ps;
+      if (c < p.L) {
+        ps = t - p.L + 1 + c;
+        v = v && ps >= 0 && ps <= t && ps < T;
+      } else {
+        const int r = v ? (c - p.L) >> p.BS_log2 : 0;
+        ps = ws.sel[r] * p.BS + ((c - p.L) & (p.BS - 1));
+        v = v && ws.selv[r] != 0 && ps <= t && ps < ls && ps < T;
+      }
+      bool taken = false;
+#pragma unroll
+      for (int x = 0; x < kMaxSlots; ++x) taken = taken || (x < nex && ps == excl[x]);
+      ok[u] = v && !taken;
+      off[u] = ok[u] ? (row0 + static_cast<uint32_t>(ps)) * pos_bytes + col_bytes : 0u;
+    }
+    double acc[NCL];
+#pragma unroll
+    for (int u = 0; u < NCL; ++u) acc[u] = 0.0;
+    constexpr int CG = 4;
+    for (int ch0 = 0; ch0 < chunks; ch0 += CG) {
+      uint4 kc[NCL][CG];
+#pragma unroll
+      for (int u = 0; u < NCL; ++u)
+#pragma unroll
+        for (int cc = 0; cc < CG; ++cc) {
+          const int ch = ch0 + cc;
+          kc[u][cc] = ch < chunks ? buf_load_b128(keys, ok[u] ? off[u] + 16u * ch : kNoOffset)
+                                  : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+      for (int cc = 0; cc < CG; ++cc) {
+        const int ch = ch0 + cc;
+        if (ch >= chunks) break;
+        double q[EPC];
+#pragma unroll
+        for (int e = 0; e < EPC; e += 2) {
+          const double2 q2 = *reinterpret_cast<const double2*>(ws.qx + EPC * ch + e);
+          q[e] = q2.x;
+          q[e + 1] = q2.y;
+        }
+#pragma unroll
+        for (int u = 0; u < NCL; ++u) {
+          double k[EPC];
+          chunk_to_f64<TA>(kc[u][cc], k);
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) acc[u] += k[e] * q[e];
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < NCL; ++u) {
+      const int c = c0 + lane + kWave * u;
+      if (c < p.CAP) ws.sc[c] = ok[u] ? static_cast<float>(acc[u] * p.exact_scale) : -INFINITY;
+    }
+  }
+  wave_sync();
+}
+
+// K argmax passes over ws.sc (ties to the lowest lane); exhausted slots repeat
+// lane 0 with -inf, as the single-anchor partner pass.  Writes K entries.
+__device__ void topk_lanes_out(const SelectParams& p, const Query& qy, WaveScratch& ws, int lane,
+                               int32_t* out_idx, float* out_score) {
+  uint64_t best = 0;
+  for (int c = lane; c < p.CAP; c += kWave) {
+    const uint64_t k = select_key(ws.sc[c], static_cast<uint32_t>(c));
+    best = k > best ? k : best;
+  }
+  for (int k = 0; k < p.K; ++k) {
+    const uint64_t win = wave_max_u64(best);
+    const int c = static_cast<int>(key_index(win));
+    if ((c & (kWave - 1)) == lane) {
+      int64_t pos;
+      bool valid;
+      candidate(p, c, qy, ws, pos, valid);
+      const bool exhausted = !(key_score(win) > -INFINITY);
+      out_idx[k] = static_cast<int32_t>(exhausted ? qy.t - p.L + 1 : pos);
+      out_score[k] = exhausted ? -INFINITY : ws.sc[c];
+      ws.sc[c] = -INFINITY;
+      best = 0;
+      for (int cc = lane; cc < p.CAP; cc += kWave) {
+        const uint64_t kk = select_key(ws.sc[cc], static_cast<uint32_t>(cc));
+        best = kk > best ? kk : best;
+      }
+    }
+  }
+  wave_sync();
+}
+
+template <typename TA, typename TS>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
+multi_select_kernel(const SelectParams p, const MultiParams m) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int EPC = kEpc<TA>;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int64_t b = blockIdx.x / p.tiles;
+  const int64_t tq0 = (blockIdx.x - b * p.tiles) * static_cast<int64_t>(p.W);
+  const int64_t tq = tq0 + wave;
+  const int RD = p.H * p.HD;
+
+  // Partner statistics and bias tables are read by every slot of every query
+  // of the workgroup: staged once.  Anchor statistics are read once per query,
+  // from L2.
+  if (p.stage) {
+    stage_workgroup<TA, TS, kPartnerOnly>(p, b, 0, smem);
+    __syncthreads();
+  }
+  if (tq >= p.Tq) return;  // no workgroup barriers below
+  const float* stats_p = p.stage ? reinterpret_cast<const float*>(smem + p.off_stats_p) : nullptr;
+  const float* bias_p = p.stage ? reinterpret_cast<const float*>(smem + p.off_bias_p) : nullptr;
+
+  unsigned char* base = smem + p.off_wave + wave * p.wave_bytes;
+  WaveScratch ws;
+  ws.qx = reinterpret_cast<double*>(base);
+  ws.qr = ws.qx + p.E;
+  ws.blk = reinterpret_cast<float*>(ws.qr + RD);
+  ws.sel = reinterpret_cast<int*>(ws.blk + p.NB);
+  ws.selv = ws.sel + p.TOP;
+  ws.sc = reinterpret_cast<float*>(ws.selv + p.TOP);
+
+  Query qy;
+  qy.b = b;
+  qy.q = b * p.Tq + tq;
+  qy.t = load_any_i(p.pos, p.pos_dtype, b * p.pos_sb + tq * p.pos_sq);
+  qy.local_start = qy.t - p.L + 1 > 0 ? qy.t - p.L + 1 : 0;
+  qy.wbase = 0;
+  double sp_a, sp_p;
+  {
+#pragma clang fp contract(off)
+    const int h = lane & (p.H - 1);
+    sp_a = log(1.0 + exp(static_cast<double>(load_any_f(p.as.gamma, p.as.gamma_dtype, h))));
+    sp_p = log(1.0 + exp(static_cast<double>(load_any_f(p.ps.gamma, p.ps.gamma_dtype, h))));
+  }
+
+  // ---- Anchors: one routed candidate set, S distinct argmaxes.
+  {
+    const TA* arq = static_cast<const TA*>(p.arq) + qy.q * RD;
+    for (int d = lane; d < RD; d += kWave) ws.qr[d] = static_cast<double>(to_f32(arq[d]));
+    wave_sync();
+    block_scores<TS>(p, p.as, nullptr, nullptr, sp_a, qy, ws, lane);
+    pick_blocks(p, ws, lane);
+  }
+  int taken[kMaxSlots];
+#pragma unroll
+  for (int x = 0; x < kMaxSlots; ++x) taken[x] = -1;
+  int active = 0;
+  for (int s = 0; s < m.S; ++s) {
+    const int64_t o = qy.q * m.S + s;
+    if (s > qy.t) {  // inactive slot: anchor 0, no partners
+      if (lane == 0) {
+        p.out_anchor[o] = 0;
+        p.out_anchor_score[o] = -INFINITY;
+      }
+      continue;
+    }
+    if (lane < p.G) {
+      const TA* aq = static_cast<const TA*>(p.aq) + o * p.E;
+      double qx[EPC];
+      chunk_to_f64<TA>(*reinterpret_cast<const uint4*>(aq + EPC * lane), qx);
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) ws.qx[EPC * lane + e] = qx[e];
+    }
+    wave_sync();
+    slot_candidate_scores<TA, 3>(p, p.as.keys, m.key_pos_bytes, m.slot_bytes * s, qy, taken,
+                                 active, ws, lane);
+    uint64_t best = 0;
+    float best_score = -INFINITY;
+    for (int c = lane; c < p.CAP; c += kWave) {
+      int64_t pos;
+      bool valid;
+      candidate(p, c, qy, ws, pos, valid);
+      const float sc = ws.sc[c];
+      if (valid && sc > -INFINITY) {
+        const uint64_t k = select_key(sc, static_cast<uint32_t>(pos));
+        if (k > best) {
+          best = k;
+          best_score = sc;
+        }
+      }
+    }
+    const uint64_t win = wave_max_u64(best);
+    // With local_window >= S an active slot always has an untaken candidate
+    // (the window holds min(t+1, L) >= s+1 positions); the host checks that.
+    const int anchor = win == 0 ? 0 : static_cast<int>(key_index(win));
+    if (win == 0) {
+      if (lane == 0) {
+        p.out_anchor[o] = 0;
+        p.out_anchor_score[o] = -INFINITY;
+      }
+    } else if (best == win) {
+      p.out_anchor[o] = anchor;
+      p.out_anchor_score[o] = best_score;
+    }
+    if (win != 0) {
+#pragma unroll
+      for (int x = 0; x < kMaxSlots; ++x)
+        if (x == active) taken[x] = anchor;
+      ++active;
+    }
+    wave_sync();
+  }
+
+  // ---- Partners of each active slot.
+  for (int s = 0; s < m.S; ++s) {
+    const int64_t o = qy.q * m.S + s;
+    int32_t* out_idx = p.out_partner + o * p.K;
+    float* out_score = p.out_partner_score + o * p.K;
+    if (s >= active) {  // inactive (or anchorless) slot: every entry exhausted
+      for (int k = lane; k < p.K; k += kWave) {
+        out_idx[k] = static_cast<int32_t>(qy.t - p.L + 1);
+        out_score[k] = -INFINITY;
+      }
+      continue;
+    }
+    int anchor = taken[0];
+#pragma unroll
+    for (int x = 1; x < kMaxSlots; ++x)
+      if (x == s) anchor = taken[x];
+    // Partner query: float32 sum of the query-side row and the anchor's cached
+    // row, exact half then router half.
+    const TA* pb = static_cast<const TA*>(p.pq) + o * m.qrow;
+    const TA* pc = static_cast<const TA*>(p.pcache) + ((b * p.T + anchor) * m.S + s) * m.qrow;
+    if (lane < p.G) {
+      double bq[EPC], cq[EPC];
+      chunk_to_f64<TA>(*reinterpret_cast<const uint4*>(pb + EPC * lane), bq);
+      chunk_to_f64<TA>(*reinterpret_cast<const uint4*>(pc + EPC * lane), cq);
+#pragma unroll
+      for (int e = 0; e < EPC; ++e)
+        ws.qx[EPC * lane + e] = static_cast<double>(static_cast<float>(bq[e]) +
+                                                    static_cast<float>(cq[e]));
+    }
+    for (int d = lane; d < RD; d += kWave)
+      ws.qr[d] = static_cast<double>(to_f32(pb[p.E + d]) + to_f32(pc[p.E + d]));
+    wave_sync();
+    block_scores<TS>(p, p.ps, stats_p, bias_p, sp_p, qy, ws, lane);
+    pick_blocks(p, ws, lane);
+    slot_candidate_scores<TA, 3>(p, p.ps.keys, m.key_pos_bytes, m.slot_bytes * s, qy, taken,
+                                 active, ws, lane);
+    topk_lanes_out(p, qy, ws, lane, out_idx, out_score);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 
@@ -703,15 +993,10 @@ struct Geometry {
   int NB, BS, E, H, HD, RB;
 };
 
-bool check_stream(const rlm_tensor* keys, const rlm_tensor* mean, const rlm_tensor* stdv,
-                  const rlm_tensor* gamma, const rlm_tensor* bias, const char* side,
-                  const Geometry& g, int act_dtype, int stat_dtype) {
+bool check_router_side(const rlm_tensor* mean, const rlm_tensor* stdv, const rlm_tensor* gamma,
+                       const rlm_tensor* bias, const char* side, const Geometry& g,
+                       int stat_dtype) {
   char name[96];
-  snprintf(name, sizeof(name), "%s_keys", side);
-  if (!check_tensor(keys, name, 3) || !check_dim(keys, name, 0, g.B) ||
-      !check_dim(keys, name, 1, g.T) || !check_dim(keys, name, 2, g.E) ||
-      !check_dtype_is(keys, name, act_dtype))
-    return false;
   snprintf(name, sizeof(name), "%s_block_mean", side);
   if (!check_tensor(mean, name, 4) || !check_dim(mean, name, 0, g.B) ||
       !check_dim(mean, name, 1, g.NB) || !check_dim(mean, name, 2, g.H) ||
@@ -731,6 +1016,18 @@ bool check_stream(const rlm_tensor* keys, const rlm_tensor* mean, const rlm_tens
       !check_dim(bias, name, 1, g.RB) || !check_dtype_float(bias, name))
     return false;
   return true;
+}
+
+bool check_stream(const rlm_tensor* keys, const rlm_tensor* mean, const rlm_tensor* stdv,
+                  const rlm_tensor* gamma, const rlm_tensor* bias, const char* side,
+                  const Geometry& g, int act_dtype, int stat_dtype) {
+  char name[96];
+  snprintf(name, sizeof(name), "%s_keys", side);
+  if (!check_tensor(keys, name, 3) || !check_dim(keys, name, 0, g.B) ||
+      !check_dim(keys, name, 1, g.T) || !check_dim(keys, name, 2, g.E) ||
+      !check_dtype_is(keys, name, act_dtype))
+    return false;
+  return check_router_side(mean, stdv, gamma, bias, side, g, stat_dtype);
 }
 
 bool aligned16(const rlm_tensor* t, const char* name) {
@@ -1002,6 +1299,147 @@ hipError_t select_packed_impl(
   return launch_select<kPacked>(p, act, stat, stream);
 }
 
+bool check_slot_rows(const rlm_tensor* t, const char* name, int64_t d0, int64_t d1, int64_t S,
+                     int64_t width, int act) {
+  return check_tensor(t, name, 4) && check_dim(t, name, 0, d0) && check_dim(t, name, 1, d1) &&
+         check_dim(t, name, 2, S) && check_dim(t, name, 3, width) && check_dtype_is(t, name, act);
+}
+
+hipError_t multi_select_impl(
+    const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
+    const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
+    const rlm_tensor* anchor_block_std, const rlm_tensor* anchor_gamma,
+    const rlm_tensor* anchor_bias, const rlm_tensor* partner_base,
+    const rlm_tensor* partner_anchor_cache, const rlm_tensor* partner_keys,
+    const rlm_tensor* partner_block_mean, const rlm_tensor* partner_block_std,
+    const rlm_tensor* partner_gamma, const rlm_tensor* partner_bias, const rlm_tensor* positions,
+    int64_t local_window, int64_t top_blocks, int64_t k_out, int32_t strict_valid,
+    const rlm_tensor* out_anchor, const rlm_tensor* out_anchor_score,
+    const rlm_tensor* out_partner, const rlm_tensor* out_partner_score, hipStream_t stream) {
+  clear_error();
+  RLM_TRY(check_tensor(anchor_query, "anchor_query", 4));
+  RLM_TRY(check_dtype_float(anchor_query, "anchor_query"));
+  RLM_TRY(check_tensor(anchor_keys, "anchor_keys", 4));
+  RLM_TRY(check_tensor(anchor_block_mean, "anchor_block_mean", 4));
+  RLM_TRY(check_tensor(anchor_bias, "anchor_bias", 2));
+  Geometry g;
+  g.B = anchor_query->shape[0];
+  g.Tq = anchor_query->shape[1];
+  const int64_t S = anchor_query->shape[2];
+  g.E = static_cast<int>(anchor_query->shape[3]);
+  g.T = anchor_keys->shape[1];
+  g.NB = static_cast<int>(anchor_block_mean->shape[1]);
+  g.H = static_cast<int>(anchor_block_mean->shape[2]);
+  g.HD = static_cast<int>(anchor_block_mean->shape[3]);
+  g.RB = static_cast<int>(anchor_bias->shape[1]);
+  RLM_REQUIRE(S >= 1 && S <= kMaxSlots, "anchor slots must be in [1, %d], got %lld", kMaxSlots,
+              (long long)S);
+  RLM_REQUIRE(local_window >= S,
+              "local_window (%lld) must be >= anchor slots (%lld): every active slot needs a "
+              "distinct local candidate",
+              (long long)local_window, (long long)S);
+  RLM_REQUIRE(g.NB >= 1 && g.T >= g.NB, "need 1 <= blocks <= cache length");
+  g.BS = static_cast<int>(g.T / g.NB);
+  const int act = anchor_query->dtype;
+  const int stat = anchor_block_mean->dtype;
+  const int elem = act == RLM_F32 ? 4 : 2;
+  const int RD = g.H * g.HD;
+  RLM_TRY(check_slot_rows(anchor_keys, "anchor_keys", g.B, g.T, S, g.E, act));
+  RLM_TRY(check_slot_rows(partner_keys, "partner_keys", g.B, g.T, S, g.E, act));
+  RLM_TRY(check_slot_rows(partner_base, "partner_base", g.B, g.Tq, S, g.E + RD, act));
+  RLM_TRY(check_slot_rows(partner_anchor_cache, "partner_anchor_cache", g.B, g.T, S, g.E + RD,
+                          act));
+  RLM_TRY(check_router_side(anchor_block_mean, anchor_block_std, anchor_gamma, anchor_bias,
+                            "anchor", g, stat));
+  RLM_TRY(check_router_side(partner_block_mean, partner_block_std, partner_gamma, partner_bias,
+                            "partner", g, stat));
+  RLM_TRY(check_tensor(anchor_router_query, "anchor_router_query", 3));
+  RLM_TRY(check_dtype_is(anchor_router_query, "anchor_router_query", act));
+  RLM_TRY(check_dim(anchor_router_query, "anchor_router_query", 0, g.B));
+  RLM_TRY(check_dim(anchor_router_query, "anchor_router_query", 1, g.Tq));
+  RLM_TRY(check_dim(anchor_router_query, "anchor_router_query", 2, RD));
+  RLM_REQUIRE(((g.E + RD) * elem) % 16 == 0,
+              "partner_base rows (exact dim + router dim) must be a multiple of 16 bytes");
+  for (const rlm_tensor* t : {anchor_query, anchor_keys, anchor_router_query, anchor_block_mean,
+                              anchor_block_std, partner_base, partner_anchor_cache, partner_keys,
+                              partner_block_mean, partner_block_std})
+    RLM_TRY(aligned16(t, "multi-anchor selection inputs"));
+  SelectParams p{};
+  RLM_TRY(check_position(positions, "positions", g, true, p));
+  {
+    const rlm_tensor* outs[2] = {out_anchor, out_anchor_score};
+    const int types[2] = {RLM_I32, RLM_F32};
+    const char* names[2] = {"out_anchor", "out_anchor_score"};
+    for (int i = 0; i < 2; ++i) {
+      RLM_TRY(check_tensor(outs[i], names[i], 3));
+      RLM_TRY(check_dtype_is(outs[i], names[i], types[i]));
+      RLM_TRY(check_dim(outs[i], names[i], 0, g.B));
+      RLM_TRY(check_dim(outs[i], names[i], 1, g.Tq));
+      RLM_TRY(check_dim(outs[i], names[i], 2, S));
+    }
+  }
+  RLM_TRY(check_slot_rows(out_partner, "out_partner", g.B, g.Tq, S, k_out, RLM_I32));
+  RLM_TRY(check_slot_rows(out_partner_score, "out_partner_score", g.B, g.Tq, S, k_out, RLM_F32));
+  hipError_t err = finish_params(p, g, local_window, top_blocks, k_out, strict_valid, elem);
+  if (err != hipSuccess) return err;
+  // LDS: partner statistics and bias table (when the statistic count is a
+  // power of two), then the per-wave regions.  No key windows.
+  p.WR = 0;
+  const int stats_bytes = 2 * g.NB * RD * 4;
+  const bool stats_pow2 = ((g.NB * RD / 4) & (g.NB * RD / 4 - 1)) == 0 && g.NB * RD >= 4;
+  const int bias_bytes = ((g.H * g.RB * 4) + 15) & ~15;
+  p.off_stats_a = p.off_bias_a = p.off_win_a = p.off_win_p = 0;
+  p.off_stats_p = p.off_bias_p = 0;
+  int off = 0;
+  p.stage = p.W > 1 && stats_pow2 && stats_bytes + bias_bytes + p.W * p.wave_bytes <= 80 * 1024;
+  if (p.stage) {
+    p.off_stats_p = 0;
+    p.off_bias_p = stats_bytes;
+    off = stats_bytes + bias_bytes;
+  }
+  p.off_wave = off;
+  off += p.W * p.wave_bytes;
+  RLM_REQUIRE(off <= 160 * 1024,
+              "selection working set (%d bytes of LDS) exceeds the 160 KiB of one CU", off);
+  p.lds_total = off;
+  const int64_t key_bytes = g.B * g.T * S * g.E * elem;
+  RLM_REQUIRE(key_bytes < (int64_t(1) << 31), "key caches must be smaller than 2 GiB");
+  p.key_bytes = static_cast<uint32_t>(key_bytes);
+  p.aq = anchor_query->data;
+  p.arq = anchor_router_query->data;
+  p.as = make_stream(anchor_keys, anchor_block_mean, anchor_block_std, anchor_gamma, anchor_bias);
+  p.pq = partner_base->data;
+  p.pcache = partner_anchor_cache->data;
+  p.ps = make_stream(partner_keys, partner_block_mean, partner_block_std, partner_gamma,
+                     partner_bias);
+  p.out_anchor = static_cast<int32_t*>(out_anchor->data);
+  p.out_anchor_score = static_cast<float*>(out_anchor_score->data);
+  p.out_partner = static_cast<int32_t*>(out_partner->data);
+  p.out_partner_score = static_cast<float*>(out_partner_score->data);
+  MultiParams m;
+  m.S = static_cast<int>(S);
+  m.slot_bytes = static_cast<uint32_t>(g.E * elem);
+  m.key_pos_bytes = static_cast<uint32_t>(S * g.E * elem);
+  m.qrow = g.E + RD;
+  const int64_t queries = g.B * g.Tq;
+  if (queries == 0) return hipSuccess;
+  const dim3 block(p.W * kWave);
+  const dim3 grid(static_cast<unsigned>(g.B * p.tiles));
+  const size_t lds = static_cast<size_t>(p.lds_total);
+#define RLM_MULTI_CASE(TA_ID, TA, TS_ID, TS)                                           \
+  if (act == TA_ID && stat == TS_ID) {                                                 \
+    hipLaunchKernelGGL((multi_select_kernel<TA, TS>), grid, block, lds, stream, p, m); \
+    return launch_status("multi_relation_select");                                     \
+  }
+  RLM_MULTI_CASE(RLM_F32, float, RLM_F32, float)
+  RLM_MULTI_CASE(RLM_BF16, bf16, RLM_F32, float)
+  RLM_MULTI_CASE(RLM_BF16, bf16, RLM_BF16, bf16)
+#undef RLM_MULTI_CASE
+  set_error("multi_relation_select: unsupported dtype combination (activations %s, stats %s)",
+            dtype_name(act), dtype_name(stat));
+  return hipErrorInvalidValue;
+}
+
 }  // namespace
 }  // namespace rlm
 
@@ -1144,4 +1582,23 @@ extern "C" hipError_t rlm_partner_topk(
   p.out_partner = static_cast<int32_t*>(out_index->data);
   p.out_partner_score = static_cast<float*>(out_score->data);
   return launch_select<kPartnerOnly>(p, act, stat, stream);
+}
+
+extern "C" hipError_t rlm_multi_relation_select_seq(
+    const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
+    const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
+    const rlm_tensor* anchor_block_std, const rlm_tensor* anchor_gamma,
+    const rlm_tensor* anchor_bias, const rlm_tensor* partner_base,
+    const rlm_tensor* partner_anchor_cache, const rlm_tensor* partner_keys,
+    const rlm_tensor* partner_block_mean, const rlm_tensor* partner_block_std,
+    const rlm_tensor* partner_gamma, const rlm_tensor* partner_bias, const rlm_tensor* positions,
+    int64_t local_window, int64_t top_blocks, int64_t k_out, int32_t strict_valid,
+    const rlm_tensor* out_anchor, const rlm_tensor* out_anchor_score,
+    const rlm_tensor* out_partner, const rlm_tensor* out_partner_score, hipStream_t stream) {
+  return multi_select_impl(anchor_query, anchor_keys, anchor_router_query, anchor_block_mean,
+                           anchor_block_std, anchor_gamma, anchor_bias, partner_base,
+                           partner_anchor_cache, partner_keys, partner_block_mean,
+                           partner_block_std, partner_gamma, partner_bias, positions,
+                           local_window, top_blocks, k_out, strict_valid, out_anchor,
+                           out_anchor_score, out_partner, out_partner_score, stream);
 }

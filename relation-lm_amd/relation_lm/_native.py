@@ -46,6 +46,15 @@ def _register_fakes() -> None:
     torch.library.register_fake("relation_lm::relation_select_packed")(fake_select)
     torch.library.register_fake("relation_lm::relation_select_packed_seq")(fake_select)
 
+    @torch.library.register_fake("relation_lm::multi_relation_select_seq")
+    def _(anchor_query, *rest):
+        k_out = rest[-2]
+        qshape = tuple(anchor_query.shape[:3])
+        return (anchor_query.new_empty(qshape, dtype=torch.int32),
+                anchor_query.new_empty(qshape, dtype=torch.float32),
+                anchor_query.new_empty(qshape + (k_out,), dtype=torch.int32),
+                anchor_query.new_empty(qshape + (k_out,), dtype=torch.float32))
+
     @torch.library.register_fake("relationlex::anchor_select")
     def _(anchor_query, *rest):
         b = anchor_query.shape[0]

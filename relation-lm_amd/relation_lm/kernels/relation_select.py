@@ -77,3 +77,42 @@ def relation_select_packed_seq(
         anchor_gamma, anchor_bias, partner_base, partner_anchor_cache, partner_keys,
         partner_block_mean, partner_block_std, partner_gamma, partner_bias, positions,
         local_window, top_blocks, k_out, strict_valid)
+
+
+def multi_relation_select_seq(
+    anchor_query: Tensor,
+    anchor_keys: Tensor,
+    anchor_router_query: Tensor,
+    anchor_block_mean: Tensor,
+    anchor_block_std: Tensor,
+    anchor_gamma: Tensor,
+    anchor_bias: Tensor,
+    partner_base: Tensor,
+    partner_anchor_cache: Tensor,
+    partner_keys: Tensor,
+    partner_block_mean: Tensor,
+    partner_block_std: Tensor,
+    partner_gamma: Tensor,
+    partner_bias: Tensor,
+    positions: Tensor,
+    local_window: int,
+    top_blocks: int,
+    k_out: int,
+    strict_valid: bool,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Routed multi-anchor selection (no reference kernel; the dense semantics are
+    MultiAnchorRelationBlock's, multi_relation_blocks.py:69-147).
+
+    anchor_query [B,Tq,S,E], anchor_keys [B,T,S,E], anchor_router_query [B,Tq,RD],
+    partner_base [B,Tq,S,E+RD], partner_anchor_cache [B,T,S,E+RD],
+    partner_keys [B,T,S,E]; block statistics, gamma and bias as the single-anchor
+    op (the partner statistics are shared by the S slots); positions [Tq] or [B,Tq].
+    Slot s is active iff s <= t.  Returns (anchor int32 [B,Tq,S], anchor_score f32
+    [B,Tq,S], partner int32 [B,Tq,S,K], partner_score f32 [B,Tq,S,K]); the partner
+    mask of the dense block is isfinite(partner_score).
+    """
+    return torch.ops.relation_lm.multi_relation_select_seq(
+        anchor_query, anchor_keys, anchor_router_query, anchor_block_mean, anchor_block_std,
+        anchor_gamma, anchor_bias, partner_base, partner_anchor_cache, partner_keys,
+        partner_block_mean, partner_block_std, partner_gamma, partner_bias, positions,
+        local_window, top_blocks, k_out, strict_valid)

@@ -8,6 +8,9 @@ Shapes follow the benchmark configurations of the routed relation path:
   cfg3  decode at t=511 against a 512-row cache, block 32, local 64, top 4,
         K=8, packed 576->512 bf16 projection, R=128 H=2304 D=576, B in {1, 8}
   cfg4  B=8  T=2048 d=512, K=8, hidden 1024 (reduce in isolation)
+  cfg5  B=4  T=4096 d=768, block 64 (64 blocks), local 128, top 8, 4 anchor
+        slots x K=6 partners, bf16 (routed multi-anchor selection, one layer
+        of the 4-layer stack)
 
 Every tensor is drawn on the CPU from one ``torch.Generator`` in a fixed order
 and then copied to the device, so a CPU checker sees the same bits as the GPU.
@@ -115,6 +118,78 @@ def selection_inputs(cfg: RelationConfig, *, queries: int | None = None,
     else:
         out["position"] = torch.tensor(t - 1, dtype=torch.int64)
     return {k: v.to(device) for k, v in out.items()}
+
+
+@dataclass(frozen=True)
+class MultiAnchorConfig:
+    name: str
+    batch: int
+    context: int
+    d_model: int
+    block_size: int
+    local_window: int
+    top_blocks: int
+    slots: int
+    k_out: int
+    dtype: torch.dtype
+    layers: int = 1
+    exact_dim: int = 64
+    heads: int = 4
+    head_dim: int = 16
+    rel_buckets: int = 16
+    strict_valid: bool = False
+    seed: int = 20261205
+
+    @property
+    def blocks(self) -> int:
+        return self.context // self.block_size
+
+    @property
+    def queries(self) -> int:
+        return self.batch * self.context
+
+
+MULTI_CONFIGS = {
+    "cfg5": MultiAnchorConfig("cfg5", 4, 4096, 768, 64, 128, 8, 4, 6, torch.bfloat16, layers=4),
+}
+
+
+def multi_selection_inputs(cfg: MultiAnchorConfig, *, positions=None,
+                           device: torch.device | str = "cpu", seed: int | None = None) -> dict:
+    """Inputs of multi_relation_select_seq: per-slot exact queries/keys
+    [B,*,S,E], per-slot partner rows [B,*,S,E+RD], one anchor router query per
+    query and block statistics of seeded router keys.  ``positions`` (default:
+    every cache position) sets the queries."""
+    g = _gen(cfg.seed if seed is None else seed)
+    b, t, e, s = cfg.batch, cfg.context, cfg.exact_dim, cfg.slots
+    rd = cfg.heads * cfg.head_dim
+    pos = torch.arange(t, dtype=torch.int64) if positions is None else torch.as_tensor(
+        positions, dtype=torch.int64)
+    q = pos.shape[-1]
+    act = cfg.dtype
+    out = {
+        "anchor_query": _randn(g, b, q, s, e, dtype=act),
+        "anchor_keys": _randn(g, b, t, s, e, dtype=act),
+        "anchor_router_query": _randn(g, b, q, rd, dtype=act),
+        "partner_base": _randn(g, b, q, s, e + rd, dtype=act),
+        "partner_anchor_cache": _randn(g, b, t, s, e + rd, dtype=act),
+        "partner_keys": _randn(g, b, t, s, e, dtype=act),
+    }
+    for side in ("anchor", "partner"):
+        router_keys = _randn(g, b, t, rd, dtype=act)
+        mean, std = block_statistics(router_keys, cfg.block_size, cfg.heads, cfg.head_dim)
+        out[f"{side}_block_mean"] = mean
+        out[f"{side}_block_std"] = std
+        out[f"{side}_gamma"] = _randn(g, cfg.heads)
+        out[f"{side}_bias"] = _randn(g, cfg.heads, cfg.rel_buckets)
+    out["positions"] = pos
+    return {k: v.to(device) for k, v in out.items()}
+
+
+def multi_select_args(inputs: dict, cfg: MultiAnchorConfig) -> tuple:
+    """Positional arguments of multi_relation_select_seq."""
+    return tuple(inputs[k] for k in SELECT_ORDER) + (
+        inputs["positions"], cfg.local_window, cfg.top_blocks, cfg.k_out, cfg.strict_valid)
 
 
 def router_cache_inputs(cfg: RelationConfig, *, device: torch.device | str = "cpu",

@@ -202,3 +202,74 @@ def test_fake_kernels_give_shapes():
                                        torch.empty(b, t, 6, dtype=torch.int32),
                                        torch.empty(32, 8))
         assert h.shape == (b, t, 6, 32) and h.dtype == torch.float32
+
+
+def _multi_args(b=2, t=64, e=64, nb=4, s=3, k=4, tq=8, **override):
+    d = {
+        "anchor_query": tensor([b, tq, s, e]), "anchor_keys": tensor([b, t, s, e]),
+        "anchor_router_query": tensor([b, tq, e]), "anchor_block_mean": tensor([b, nb, 4, e // 4]),
+        "anchor_block_std": tensor([b, nb, 4, e // 4]), "anchor_gamma": tensor([4]),
+        "anchor_bias": tensor([4, 16]), "partner_base": tensor([b, tq, s, 2 * e]),
+        "partner_anchor_cache": tensor([b, t, s, 2 * e]), "partner_keys": tensor([b, t, s, e]),
+        "partner_block_mean": tensor([b, nb, 4, e // 4]),
+        "partner_block_std": tensor([b, nb, 4, e // 4]), "partner_gamma": tensor([4]),
+        "partner_bias": tensor([4, 16]), "positions": tensor([tq], RLM_I64),
+        "out_anchor": tensor([b, tq, s], RLM_I32), "out_anchor_score": tensor([b, tq, s]),
+        "out_partner": tensor([b, tq, s, k], RLM_I32), "out_partner_score": tensor([b, tq, s, k]),
+    }
+    d.update(override)
+    return d
+
+
+def _call_multi(lib, d, local=16, top=2, k=4, strict=0):
+    names = ["anchor_query", "anchor_keys", "anchor_router_query", "anchor_block_mean",
+             "anchor_block_std", "anchor_gamma", "anchor_bias", "partner_base",
+             "partner_anchor_cache", "partner_keys", "partner_block_mean", "partner_block_std",
+             "partner_gamma", "partner_bias", "positions"]
+    outs = ["out_anchor", "out_anchor_score", "out_partner", "out_partner_score"]
+    args = [ctypes.byref(d[n]) for n in names] + [ctypes.c_int64(local), ctypes.c_int64(top),
+                                                    ctypes.c_int64(k), ctypes.c_int32(strict)]
+    args += [ctypes.byref(d[n]) for n in outs] + [ctypes.c_void_p(0)]
+    return lib.rlm_multi_relation_select_seq(*args), lib.rlm_last_error().decode()
+
+
+@pytest.mark.parametrize("override,needle", [
+    ({"anchor_keys": tensor([2, 64, 2, 64])}, "anchor_keys"),
+    ({"partner_keys": tensor([2, 64, 3, 64], RLM_BF16)}, "partner_keys"),
+    ({"partner_base": tensor([2, 8, 3, 64])}, "partner_base"),
+    ({"partner_anchor_cache": tensor([2, 64, 3, 64])}, "partner_anchor_cache"),
+    ({"anchor_router_query": tensor([2, 8, 32])}, "anchor_router_query"),
+    ({"positions": tensor([7], RLM_I64)}, "positions"),
+    ({"out_partner": tensor([2, 8, 3, 5], RLM_I32)}, "out_partner"),
+    ({"out_anchor": tensor([2, 8, 2], RLM_I32)}, "out_anchor"),
+    ({"partner_block_mean": tensor([2, 4, 4, 8])}, "partner_block_mean"),
+])
+def test_multi_select_rejects_malformed_arguments(lib, override, needle):
+    status, message = _call_multi(lib, _multi_args(**override))
+    assert status == HIP_ERROR_INVALID_VALUE
+    assert needle in message
+
+
+def test_multi_select_rejects_bad_slot_counts(lib):
+    status, message = _call_multi(lib, _multi_args(), local=2)
+    assert status == HIP_ERROR_INVALID_VALUE and "local_window" in message
+    d = _multi_args(s=9, **{})
+    status, message = _call_multi(lib, d)
+    assert status == HIP_ERROR_INVALID_VALUE and "slots" in message
+
+
+def test_multi_select_fake_shapes():
+    import torch
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from relation_lm.kernels.relation_select import multi_relation_select_seq
+
+    with FakeTensorMode():
+        b, t, s, e = 2, 64, 4, 64
+        args = [torch.empty(b, t, s, e), torch.empty(b, t, s, e), torch.empty(b, t, e),
+                torch.empty(b, 4, 4, 16), torch.empty(b, 4, 4, 16), torch.empty(4),
+                torch.empty(4, 16), torch.empty(b, t, s, 2 * e), torch.empty(b, t, s, 2 * e),
+                torch.empty(b, t, s, e), torch.empty(b, 4, 4, 16), torch.empty(b, 4, 4, 16),
+                torch.empty(4), torch.empty(4, 16), torch.empty(t, dtype=torch.long)]
+        a, sc, p, ps = multi_relation_select_seq(*args, 16, 2, 6, False)
+        assert a.shape == (b, t, s) and p.shape == (b, t, s, 6) and ps.dtype == torch.float32
