@@ -17,6 +17,8 @@ Also reported:
   * decode-step latency (cfg3: packed 576->512 projection, router cache update,
     cache-row writes, select, reduce) at B=1 and B=8, eager and replayed from a
     HIP graph;
+  * routed multi-anchor selection at cfg5 (B=4, T=4096, 4 anchor slots x K=6,
+    block 64, local 128, top 8): one layer's selection over all 16384 queries;
   * the CPU oracle timed on this host's cores on a bounded sample.
 """
 from __future__ import annotations
@@ -39,11 +41,12 @@ CPU_SAMPLE_SECONDS = 10.0       # bounded CPU-oracle sample (whole passes of the
 # Kernel-name prefixes (as rocprofv3 reports them) of the timed kernels.
 KERNEL_SYMBOLS = {
     "expanded_projection": "smallk_kernel<rlm::bf16, rlm::bf16, rlm::bf16",
-    "relation_select": "select_kernel<",
+    "relation_select": "::select_kernel<",
     "relation_reduce_fused": "fused_reduce_kernel<",
     "relation_hidden": "hidden_bf16_kernel<",
     "second_linear": "tile_kernel<float, rlm::bf16, float",
     "norm_reduce": "norm_reduce_vec_kernel<",
+    "multi_anchor_select": "multi_select_kernel<",
 }
 
 
@@ -59,6 +62,8 @@ def parse_args():
                     help="run only the timed chain (for profiler runs)")
     ap.add_argument("--decode-only", action="store_true",
                     help="time only the cfg3 decode step (B=1 and B=8) and exit")
+    ap.add_argument("--multi-only", action="store_true",
+                    help="time only the cfg5 routed multi-anchor selection and exit")
     ap.add_argument("--profile-kernels", type=int, default=0, metavar="N",
                     help="run a 256 MiB calibration copy, then each timed kernel N times, and "
                          "exit (the command profiled by rocprofv3 --kernel-trace / --pmc)")
@@ -86,6 +91,26 @@ def algorithmic_bytes(cfg):
         "relation_reduce_fused": (b * t * (2 * h + r) * s + h * r * s + d * h * s + d * s
                                   + q * (1 + k) * 4 + q * k * 4 + 2 * d * s + q * d * 4),
     }
+
+
+def multi_select_bytes(cfg):
+    """Operator-contract bytes of one multi-anchor selection launch: query-side
+    rows, every key/cache row once, block statistics, outputs."""
+    b, t, e, s_, k = cfg.batch, cfg.context, cfg.exact_dim, cfg.slots, cfg.k_out
+    rd = cfg.heads * cfg.head_dim
+    q = b * t
+    a = 2  # bf16 activations
+    query_side = q * (s_ * e + rd + s_ * (e + rd)) * a
+    memory_side = b * t * s_ * (e + e + (e + rd)) * a + 2 * 2 * b * cfg.blocks * rd * 4
+    outputs = q * s_ * (4 + 4) + q * s_ * k * (4 + 4)
+    return query_side + memory_side + outputs
+
+
+def multi_select_gathered_bytes(cfg):
+    """Key bytes the candidate passes read (each slot's vector of every candidate,
+    anchor and partner side): what the kernel streams from L2 per launch."""
+    cap = cfg.local_window + cfg.top_blocks * cfg.block_size
+    return cfg.batch * cfg.context * 2 * cfg.slots * cap * cfg.exact_dim * 2
 
 
 def algorithmic_flops(cfg):
@@ -121,6 +146,7 @@ def main() -> int:
         relation_reduce_fused_seq,
     )
     from relation_lm.kernels.relation_select import (
+        multi_relation_select_seq,
         relation_select_packed,
         relation_select_packed_seq,
     )
@@ -128,7 +154,10 @@ def main() -> int:
     from relation_lm.kernels.router_cache import router_cache_update
     from relation_lm.workloads import (
         CONFIGS,
+        MULTI_CONFIGS,
         RelationConfig,
+        multi_select_args,
+        multi_selection_inputs,
         packed_projection_inputs,
         reduce_inputs,
         router_cache_inputs,
@@ -215,6 +244,38 @@ def main() -> int:
             decode[f"B{batch}"] = {"eager_us": round(eager_us, 2), "graph_us": round(graph_us, 2)}
 
         return decode
+
+    def run_multi(repeats=20):
+        """cfg5 routed multi-anchor selection: one layer's selection, every query."""
+        mcfg = MULTI_CONFIGS["cfg5"]
+        minp = multi_selection_inputs(mcfg, device=device)
+        margs = multi_select_args(minp, mcfg)
+        for _ in range(3):
+            multi_relation_select_seq(*margs)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(repeats):
+            multi_relation_select_seq(*margs)
+        end.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(end) * 1e3 / repeats
+        nbytes = multi_select_bytes(mcfg)
+        gathered = multi_select_gathered_bytes(mcfg)
+        return {
+            "workload": "cfg5 one layer: B=4 T=4096 4 anchor slots x K=6, block 64, local 128, "
+                        "top 8, bf16, every position a query",
+            "us": round(us, 1),
+            "queries_per_s": round(mcfg.queries / (us * 1e-6), 1),
+            "stack_select_us": round(us * mcfg.layers, 1),
+            "algorithmic_bytes": nbytes,
+            "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "gathered_key_bytes": gathered,
+            "gathered_GBps": round(gathered / (us * 1e-6) / 1e9, 1),
+        }
+
+    if args.multi_only:
+        print(json.dumps({"multi_anchor_select": run_multi()}), flush=True)
+        return 0
 
     if args.decode_only:
         print(json.dumps({"decode_step_us": run_decode()}), flush=True)
@@ -359,6 +420,7 @@ def main() -> int:
     fused_bytes = sum(nbytes[k] for k in headline)
 
     decode = run_decode()
+    multi = run_multi()
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -396,6 +458,7 @@ def main() -> int:
                 trio_bytes / (trio_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         },
         "decode_step_us": decode,
+        "multi_anchor_select": multi,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
