@@ -285,6 +285,65 @@ hipError_t rlm_router_cache_update(
     hipStream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Ring-buffer caches: contexts beyond the cache length
+ *
+ * No reference counterpart: the reference's roadmap item "persistent
+ * ring-buffer state and contexts beyond 512" (README.md:150,
+ * docs/roadmap.md:8).  Each entry point takes exactly the arguments of its
+ * linear form above; positions stay absolute (inputs and outputs) and may
+ * exceed the cache length T, a power of two.  Position p lives in cache row
+ * p mod T; block statistics slot j holds the newest absolute block
+ * jb <= t / BS with jb = j mod NB (NB * BS == T).  The resident positions at
+ * t are [t-T+1, t]; only whole resident blocks are eligible for routing, and
+ * block picks tie to the lowest absolute block.  For t < T each entry point
+ * equals its linear form.
+ * ---------------------------------------------------------------------- */
+
+/* Ring form of rlm_relation_select_packed (decode form). */
+hipError_t rlm_relation_select_packed_ring(
+    const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
+    const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
+    const rlm_tensor* anchor_block_std, const rlm_tensor* anchor_gamma,
+    const rlm_tensor* anchor_bias, const rlm_tensor* partner_base,
+    const rlm_tensor* partner_anchor_cache, const rlm_tensor* partner_keys,
+    const rlm_tensor* partner_block_mean, const rlm_tensor* partner_block_std,
+    const rlm_tensor* partner_gamma, const rlm_tensor* partner_bias,
+    const rlm_tensor* position, int64_t local_window, int64_t top_blocks,
+    int64_t k_out, int32_t strict_valid, const rlm_tensor* out_anchor,
+    const rlm_tensor* out_anchor_score, const rlm_tensor* out_partner,
+    const rlm_tensor* out_partner_score, hipStream_t stream);
+
+/* Ring form of rlm_relation_hidden_cached: indices are absolute positions
+ * (any value >= 0 reads row index mod T). */
+hipError_t rlm_relation_hidden_cached_ring(
+    const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
+    const rlm_tensor* anchor_index, const rlm_tensor* partner_index,
+    const rlm_tensor* product_weight, const rlm_tensor* out, hipStream_t stream);
+
+/* Ring form of rlm_relation_hidden_cache_update: the fresh row of position t
+ * is written to row t mod T and substituted wherever an index equals t. */
+hipError_t rlm_relation_hidden_cache_update_ring(
+    const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
+    const rlm_tensor* anchor_index, const rlm_tensor* partner_index,
+    const rlm_tensor* anchor_weight, const rlm_tensor* partner_weight,
+    const rlm_tensor* product_weight, const rlm_tensor* first_bias,
+    const rlm_tensor* position, const rlm_tensor* out, hipStream_t stream);
+
+/* Ring form of rlm_router_cache_update: raw/conv rows at t mod T (the conv
+ * reads rows t-1, t-2 mod T), statistics of block t/BS in slot (t/BS) mod NB;
+ * rows of that block past t count as zero (they still hold positions from T
+ * earlier). */
+hipError_t rlm_router_cache_update_ring(
+    const rlm_tensor* anchor_raw, const rlm_tensor* partner_raw,
+    const rlm_tensor* anchor_raw_cache, const rlm_tensor* partner_raw_cache,
+    const rlm_tensor* anchor_conv_cache, const rlm_tensor* partner_conv_cache,
+    const rlm_tensor* anchor_mean, const rlm_tensor* anchor_std,
+    const rlm_tensor* partner_mean, const rlm_tensor* partner_std,
+    const rlm_tensor* anchor_conv_weight, const rlm_tensor* partner_conv_weight,
+    const rlm_tensor* position, int64_t block_size, const rlm_tensor* out,
+    hipStream_t stream);
+
+/* ------------------------------------------------------------------------
  * Dense projections (MFMA)
  * ---------------------------------------------------------------------- */
 

@@ -227,3 +227,41 @@ def relation_norm_reduce_seq(raw, partner_scores, norm_weight, norm_bias, positi
 def packed_sparse_cache_projection(memory, weight) -> np.ndarray:
     """memory @ W^T in float64 (inference/packed_cache.py:56)."""
     return linear(memory, weight)
+
+
+def relation_hidden_cached_ring(expanded_cache, operand_cache, anchor_index, partner_index,
+                                product_weight) -> np.ndarray:
+    """relation_hidden_cached with absolute indices over ring caches of C rows
+    (no reference op): index p reads row p mod C."""
+    cap = np.shape(expanded_cache)[1]
+    return relation_hidden_cached(expanded_cache, operand_cache, np.mod(anchor_index, cap),
+                                  np.mod(partner_index, cap), product_weight)
+
+
+def relation_hidden_cache_update_ring(expanded_cache, operand_cache, anchor_index,
+                                      partner_index, anchor_weight, partner_weight,
+                                      product_weight, first_bias, position,
+                                      cache_dtype=np.float32):
+    """relation_hidden_cache_update over ring caches of C rows (no reference op).
+
+    Position t's expanded row is computed from operand row t mod C, stored to
+    row t mod C (rounded to the cache dtype) and used unrounded wherever an
+    index equals t; an index p in the resident range [t-C+1, t] reads row
+    p mod C; any other index reads zeros (an older one would alias the row
+    being rewritten).  Returns (hidden f32 [B,K,H], updated cache float64).
+    """
+    cap = np.shape(expanded_cache)[1]
+    t = int(position)
+
+    def resident_row(index):
+        index = np.asarray(index, dtype=np.int64)
+        ok = (index >= 0) & (index <= t) & (index > t - cap)
+        return np.where(ok, np.mod(index, cap), -1)
+
+    a, p = resident_row(anchor_index), resident_row(partner_index)
+    if t < 0:
+        return (relation_hidden_cached(expanded_cache, operand_cache, a, p, product_weight),
+                _f64(expanded_cache).copy())
+    return relation_hidden_cache_update(expanded_cache, operand_cache, a, p, anchor_weight,
+                                        partner_weight, product_weight, first_bias, t % cap,
+                                        cache_dtype)

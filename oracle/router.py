@@ -148,3 +148,52 @@ def router_cache_update(anchor_raw, partner_raw, anchor_raw_cache, partner_raw_c
             out_bufs[f"{side}_std"].reshape(b, nb, -1)[:, j] = std
             assert out_bufs[f"{side}_mean"].shape == shape
     return output, out_bufs
+
+
+def router_cache_update_ring(anchor_raw, partner_raw, anchor_raw_cache, partner_raw_cache,
+                             anchor_conv_cache, partner_conv_cache, anchor_mean, anchor_std,
+                             partner_mean, partner_std, anchor_conv_weight, partner_conv_weight,
+                             position: int, block_size: int):
+    """router_cache_update over ring-buffer caches of C rows (no reference op).
+
+    Position p lives in row p mod C; block j's statistics in slot j mod NB
+    (NB * block_size == C).  The conv reads rows t-1 and t-2 mod C; the block
+    statistics use the block's rows up to t and count the rows past t as zero
+    (those ring rows still hold positions from C earlier).  t < 0 changes
+    nothing and returns zeros.  Same return convention as router_cache_update.
+    """
+    raw = {"anchor": _f64(anchor_raw), "partner": _f64(partner_raw)}
+    bufs = {"anchor_raw_cache": anchor_raw_cache, "partner_raw_cache": partner_raw_cache,
+            "anchor_conv_cache": anchor_conv_cache, "partner_conv_cache": partner_conv_cache,
+            "anchor_mean": anchor_mean, "anchor_std": anchor_std,
+            "partner_mean": partner_mean, "partner_std": partner_std}
+    out_bufs = {k: np.array(v, copy=True) for k, v in bufs.items()}
+    weights = {"anchor": _f64(anchor_conv_weight), "partner": _f64(partner_conv_weight)}
+    b, cap, d = np.shape(anchor_raw_cache)
+    output = np.zeros((b, 2, d), dtype=np.float64)
+    t = int(position)
+    if t < 0:
+        return output, out_bufs
+    nb = np.shape(anchor_mean)[1]
+    assert nb * block_size == cap, "ring caches hold whole blocks"
+    j = t // block_size
+    for side_index, side in enumerate(("anchor", "partner")):
+        cache = _f64(bufs[f"{side}_raw_cache"])
+        w = weights[side]
+        conv = raw[side] * w[:, 2]
+        if t >= 1:
+            conv = conv + cache[:, (t - 1) % cap] * w[:, 1]
+        if t >= 2:
+            conv = conv + cache[:, (t - 2) % cap] * w[:, 0]
+        output[:, side_index] = conv
+        out_bufs[f"{side}_raw_cache"][:, t % cap] = raw[side]
+        out_bufs[f"{side}_conv_cache"][:, t % cap] = conv
+        rows = np.zeros((b, block_size, d), dtype=np.float64)
+        first = j * block_size
+        for p in range(first, t + 1):
+            rows[:, p - first] = _f64(out_bufs[f"{side}_conv_cache"])[:, p % cap]
+        mean = rows.mean(axis=1)
+        std = np.sqrt(((rows - mean[:, None]) ** 2).mean(axis=1))
+        out_bufs[f"{side}_mean"].reshape(b, nb, -1)[:, j % nb] = mean
+        out_bufs[f"{side}_std"].reshape(b, nb, -1)[:, j % nb] = std
+    return output, out_bufs

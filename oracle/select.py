@@ -473,3 +473,143 @@ def multi_relation_select_seq(anchor_query, anchor_keys, anchor_router_query, an
     k = int(k_out)
     return (a.reshape(batch, queries, slots), s.reshape(batch, queries, slots),
             p.reshape(batch, queries, slots, k), ps.reshape(batch, queries, slots, k))
+
+
+# ---------------------------------------------------------------------------
+# Ring-buffer caches (no reference kernel; the reference's roadmap item
+# "persistent ring-buffer state and contexts beyond 512", README.md:150)
+# ---------------------------------------------------------------------------
+#
+# A cache of C rows (C = cache length, a power of two) holds the last C
+# positions: position p lives in row p mod C, and block-statistics slot j holds
+# the newest absolute block jb <= t // BS with jb = j (mod NB), NB = C / BS.
+# Positions stay absolute in every input and output.  At position t the
+# resident positions are [t-C+1, t]; every block jb in [t//BS - NB + 1, t//BS]
+# lies inside that range, so a block is eligible exactly when the linear rule
+# holds for its absolute index jb (complete, strict-mode local rule) and
+# jb >= 0.  Picks rank by score, ties to the lowest absolute block.
+
+def ring_blocks(t: np.ndarray, blocks: int, block_size: int) -> np.ndarray:
+    """Absolute block index held by each statistics slot, [Q, NB] (negative: never written)."""
+    cur = np.asarray(t, dtype=np.int64) // block_size
+    slot = np.arange(blocks, dtype=np.int64)
+    return cur[:, None] - np.mod(cur[:, None] - slot[None, :], blocks)
+
+
+def ring_block_scores(router_query, block_mean, block_std, gamma, bias, batch_of, t, *,
+                      block_size: int, local_window: int, strict_valid: bool):
+    """Block scores per statistics slot (formula of block_scores) with the
+    eligibility and distance bucket of the slot's absolute block.
+    Returns (scores float32 [Q, NB], absolute block [Q, NB])."""
+    blocks, heads, head_dim = block_mean.shape[1], block_mean.shape[2], block_mean.shape[3]
+    rel_buckets = bias.shape[1]
+    t = np.asarray(t, dtype=np.int64)
+    jb = ring_blocks(t, blocks, block_size)
+    end = (jb + 1) * block_size - 1
+    local_start = np.maximum(t - local_window + 1, 0)
+    eligible = (jb >= 0) & (end <= t[:, None])
+    if strict_valid:
+        eligible &= end < local_start[:, None]
+    distance = np.maximum(t[:, None] - end, 0)
+    bucket = np.minimum(floor_log2(distance + 1), rel_buckets - 1)
+    q = _f64(router_query).reshape(-1, heads, head_dim)
+    mean = _f64(block_mean)[batch_of]
+    std = _f64(block_std)[batch_of]
+    content = np.einsum("qjhd,qhd->qjh", mean, q)
+    uncertainty = np.einsum("qjhd,qhd->qjh", std, np.abs(q))
+    sp = softplus_kernel_form(gamma)
+    bias64 = _f64(bias)
+    per_head = (content + sp[None, None, :] * uncertainty) * (1.0 / math.sqrt(head_dim))
+    per_head = per_head + np.transpose(bias64[:, bucket], (1, 2, 0))
+    out = logsumexp_heads(per_head).astype(np.float32)
+    out[~eligible] = NEG_INF32
+    return out, jb
+
+
+def ring_pick_blocks(scores: np.ndarray, jb: np.ndarray, top_blocks: int):
+    """TOP picks by descending score, ties to the lowest absolute block; returns
+    absolute blocks (selected [Q,TOP]) and validity (value > -1e30)."""
+    n, blocks = scores.shape
+    # stable sort on (-score, absolute block): argsort by block first, then a
+    # stable sort by score keeps the lower block first among equal scores
+    by_block = np.argsort(jb, axis=1, kind="stable")
+    s_sorted = np.take_along_axis(scores, by_block, axis=1)
+    order = np.take_along_axis(by_block, np.argsort(-s_sorted, axis=1, kind="stable"), axis=1)
+    take = order[:, :top_blocks]
+    selected = np.take_along_axis(jb, take, axis=1)
+    valid = np.take_along_axis(scores, take, axis=1) > -1.0e30
+    if top_blocks > blocks:
+        pad = top_blocks - blocks
+        selected = np.concatenate([selected, np.zeros((n, pad), np.int64)], axis=1)
+        valid = np.concatenate([valid, np.zeros((n, pad), bool)], axis=1)
+    return selected, valid
+
+
+def ring_exact_scores(keys, batch_of, pos, valid, query, scale: float) -> np.ndarray:
+    """exact_scores with position p read from cache row p mod C."""
+    rows = np.mod(np.where(valid, pos, 0), keys.shape[1])
+    return exact_scores(keys, batch_of, rows, valid, query, scale)
+
+
+def _ring_lanes(router_query, mean, std, gamma, bias, batch_of, t, local_window, top_blocks,
+                strict_valid, capacity):
+    blocks = mean.shape[1]
+    block_size = capacity // blocks
+    scores, jb = ring_block_scores(router_query, mean, std, gamma, bias, batch_of, t,
+                                   block_size=block_size, local_window=local_window,
+                                   strict_valid=strict_valid)
+    selected, sel_valid = ring_pick_blocks(scores, jb, top_blocks)
+    local_start = np.maximum(t - local_window + 1, 0)
+    lpos = t[:, None] - local_window + 1 + np.arange(local_window, dtype=np.int64)[None, :]
+    lvalid = (lpos >= 0) & (lpos <= t[:, None])
+    offsets = np.arange(block_size, dtype=np.int64)
+    rpos = (selected[:, :, None] * block_size + offsets[None, None, :]).reshape(len(t), -1)
+    rvalid = (np.repeat(sel_valid, block_size, axis=1) & (rpos >= 0) & (rpos <= t[:, None])
+              & (rpos < local_start[:, None]))
+    return np.concatenate([lpos, rpos], axis=1), np.concatenate([lvalid, rvalid], axis=1)
+
+
+def relation_select_packed_ring(anchor_query, anchor_keys, anchor_router_query,
+                                anchor_block_mean, anchor_block_std, anchor_gamma, anchor_bias,
+                                partner_base, partner_anchor_cache, partner_keys,
+                                partner_block_mean, partner_block_std, partner_gamma,
+                                partner_bias, position, local_window, top_blocks, k_out,
+                                strict_valid):
+    """Decode-form packed selection over ring-buffer caches of C rows (any t >= 0).
+
+    The chain of relation_select_packed (anchor top-1 ties to the lowest
+    position, factorized partner query from the anchor's cache row, partner
+    top-k with the anchor excluded, exhausted slots at lane 0 with -inf) with
+    rows addressed mod C and slots mapped to absolute blocks as above.
+    """
+    batch = anchor_query.shape[0]
+    batch_of, t = _flatten_queries(batch, 1, position)
+    capacity, exact_dim = anchor_keys.shape[1], anchor_keys.shape[2]
+    scale = 1.0 / math.sqrt(exact_dim)
+    local_window, top_blocks, k_out = int(local_window), int(top_blocks), int(k_out)
+    strict_valid = bool(strict_valid)
+    pos, valid = _ring_lanes(anchor_router_query, anchor_block_mean, anchor_block_std,
+                             anchor_gamma, anchor_bias, batch_of, t, local_window, top_blocks,
+                             strict_valid, capacity)
+    score = ring_exact_scores(anchor_keys, batch_of, pos, valid, anchor_query, scale)
+    best = score.max(axis=1)
+    tie = score == best[:, None]
+    found = valid.any(axis=1)
+    anchor = np.where(tie & valid, pos, np.iinfo(np.int64).max).min(axis=1)
+    anchor = np.where(found, anchor, t - local_window + 1)
+    anchor_score = np.where(found, best, NEG_INF32).astype(np.float32)
+    have = found & (anchor >= 0)
+    contribution = _f32(partner_anchor_cache)[batch_of, np.mod(np.where(have, anchor, 0),
+                                                                 capacity)]
+    contribution = np.where(have[:, None], contribution, np.float32(0))
+    base = _f32(partner_base)
+    pq = base[:, :exact_dim] + contribution[:, :exact_dim]
+    prq = base[:, exact_dim:] + contribution[:, exact_dim:]
+    ppos, pvalid = _ring_lanes(prq, partner_block_mean, partner_block_std, partner_gamma,
+                               partner_bias, batch_of, t, local_window, top_blocks, strict_valid,
+                               capacity)
+    pvalid &= ppos != anchor[:, None]
+    pscore = ring_exact_scores(partner_keys, batch_of, ppos, pvalid, pq, scale)
+    out_pos, out_score = _topk_lanes(pscore, ppos, k_out)
+    return (anchor.astype(np.int32), anchor_score, out_pos.astype(np.int32),
+            out_score.astype(np.float32))

@@ -51,6 +51,7 @@ struct HiddenParams {
   const void* b1;
   const void* pos;
   int pos_dtype;
+  int ring;               // ring-buffer caches: position p in row p mod T
   void* expanded_out;     // same buffer as expanded (mutated)
   float* out;             // [rows, H]
   // Byte sizes of the buffers addressed through range-checked descriptors.
@@ -82,19 +83,33 @@ __device__ __forceinline__ void load_rows(const HiddenParams& p, int64_t r0, Row
       b = static_cast<int32_t>(q / p.Tq);
       const int64_t ai = load_any_i(p.anchor, p.index_dtype_a, q);
       const int64_t pi = load_any_i(p.partner, p.index_dtype_p, row);
-      a = (ai >= 0 && ai < p.T) ? static_cast<int32_t>(ai) : -1;
-      pp = (pi >= 0 && pi < p.T) ? static_cast<int32_t>(pi) : -1;
+      // Valid index range [lo, hi).  Ring caches (row p mod T): any position
+      // below 2^31, and in the update form only the resident [t-T+1, t] --
+      // an older index would alias the row this launch rewrites.
+      int64_t lo = 0, hi = p.T;
+      if (p.ring) {
+        hi = int64_t(1) << 31;
+        if (p.pos != nullptr) {
+          const int64_t t = load_any_i(p.pos, p.pos_dtype, 0);
+          lo = t - p.T + 1 > 0 ? t - p.T + 1 : 0;
+          hi = t + 1 < hi ? t + 1 : hi;
+        }
+      }
+      a = (ai >= lo && ai < hi) ? static_cast<int32_t>(ai) : -1;
+      pp = (pi >= lo && pi < hi) ? static_cast<int32_t>(pi) : -1;
     }
     const uint32_t base = static_cast<uint32_t>(b) * static_cast<uint32_t>(p.T);
+    const uint32_t mask = p.ring ? static_cast<uint32_t>(p.T - 1) : 0xffffffffu;
+    const uint32_t ra = static_cast<uint32_t>(a) & mask, rp = static_cast<uint32_t>(pp) & mask;
     const bool ok = a >= 0 && pp >= 0;
     constexpr uint32_t es = sizeof(T);
     rt.b[tid] = b;
     rt.a[tid] = a;
     rt.p[tid] = pp;
-    rt.op_a[tid] = ok ? (base + a) * p.R * es : kNoOffset;
-    rt.op_p[tid] = ok ? (base + pp) * p.R * es : kNoOffset;
-    rt.x_a[tid] = a >= 0 ? (base + a) * (2 * p.H) * es : kNoOffset;
-    rt.x_p[tid] = pp >= 0 ? ((base + pp) * (2 * p.H) + p.H) * es : kNoOffset;
+    rt.op_a[tid] = ok ? (base + ra) * p.R * es : kNoOffset;
+    rt.op_p[tid] = ok ? (base + rp) * p.R * es : kNoOffset;
+    rt.x_a[tid] = a >= 0 ? (base + ra) * (2 * p.H) * es : kNoOffset;
+    rt.x_p[tid] = pp >= 0 ? ((base + rp) * (2 * p.H) + p.H) * es : kNoOffset;
   }
 }
 
@@ -122,7 +137,8 @@ __device__ void fresh_rows(const HiddenParams& p, int64_t t, int64_t b_first, in
     float acc = 0.0f;
     if (live && n < p.H) {
       const T* w = static_cast<const T*>(half == 0 ? p.wa : p.wp) + static_cast<int64_t>(n) * p.R;
-      const T* op = static_cast<const T*>(p.operand) + ((b_first + bi) * p.T + t) * p.R;
+      const int64_t row = p.ring ? (t & (p.T - 1)) : t;
+      const T* op = static_cast<const T*>(p.operand) + ((b_first + bi) * p.T + row) * p.R;
       for (int ch = j; ch < chunks; ch += 8) {
         const float4 w0 = load4(w + 8 * ch), w1 = load4(w + 8 * ch + 4);
         const float4 o0 = load4(op + 8 * ch), o1 = load4(op + 8 * ch + 4);
@@ -150,7 +166,8 @@ __device__ void fresh_rows(const HiddenParams& p, int64_t t, int64_t b_first, in
     const int64_t b = b_first + item / (2 * cols);
     const int n = n0 + c;
     if (b < b_lo || b > b_hi || n >= p.H) continue;
-    T* dst = static_cast<T*>(p.expanded_out) + (b * p.T + t) * (2 * static_cast<int64_t>(p.H)) +
+    const int64_t row = p.ring ? (t & (p.T - 1)) : t;
+    T* dst = static_cast<T*>(p.expanded_out) + (b * p.T + row) * (2 * static_cast<int64_t>(p.H)) +
              static_cast<int64_t>(half) * p.H + n;
     *dst = from_f32<T>(fresh[item]);
   }
@@ -205,7 +222,8 @@ __device__ __forceinline__ int64_t update_setup(const HiddenParams& p, int64_t r
   b_first = 0;
   if (!UPDATE) return -1;
   int64_t t = load_any_i(p.pos, p.pos_dtype, 0);
-  if (t < 0 || t >= p.T) t = -1;  // out-of-range position: nothing to write or reuse
+  // Out-of-range position: nothing to write or reuse (ring caches: t < 0 only).
+  if (t < 0 || (!p.ring && t >= p.T) || t >= (int64_t(1) << 31)) t = -1;
   const int64_t QK = p.Tq * p.K;
   b_first = r0 / QK;
   int64_t b_last = (r0 + kRows - 1) / QK;
@@ -861,8 +879,17 @@ extern "C" hipError_t rlm_relation_hidden_cached_seq(const rlm_tensor* expanded_
   return launch_hidden(p, operand_cache->dtype, false, stream);
 }
 
-extern "C" hipError_t rlm_relation_hidden_cache_update(
-    const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
+namespace rlm {
+namespace {
+
+hipError_t require_ring(const HiddenParams& p) {
+  RLM_REQUIRE(p.T > 0 && (p.T & (p.T - 1)) == 0,
+              "ring-buffer caches need a power-of-two cache length, got %lld", (long long)p.T);
+  return hipSuccess;
+}
+
+hipError_t hidden_update_impl(
+    bool ring, const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
     const rlm_tensor* anchor_index, const rlm_tensor* partner_index,
     const rlm_tensor* anchor_weight, const rlm_tensor* partner_weight,
     const rlm_tensor* product_weight, const rlm_tensor* first_bias, const rlm_tensor* position,
@@ -872,6 +899,11 @@ extern "C" hipError_t rlm_relation_hidden_cache_update(
   hipError_t err = hidden_impl(false, expanded_cache, operand_cache, anchor_index, partner_index,
                                product_weight, out, p);
   if (err != hipSuccess) return err;
+  if (ring) {
+    err = require_ring(p);
+    if (err != hipSuccess) return err;
+    p.ring = 1;
+  }
   RLM_TRY(check_tensor(anchor_weight, "anchor_weight", 2));
   RLM_TRY(check_tensor(partner_weight, "partner_weight", 2));
   RLM_TRY(check_tensor(first_bias, "first_bias", 1));
@@ -892,6 +924,48 @@ extern "C" hipError_t rlm_relation_hidden_cache_update(
   p.pos = position->data;
   p.pos_dtype = position->dtype;
   return launch_hidden(p, operand_cache->dtype, true, stream);
+}
+
+}  // namespace
+}  // namespace rlm
+
+extern "C" hipError_t rlm_relation_hidden_cache_update(
+    const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
+    const rlm_tensor* anchor_index, const rlm_tensor* partner_index,
+    const rlm_tensor* anchor_weight, const rlm_tensor* partner_weight,
+    const rlm_tensor* product_weight, const rlm_tensor* first_bias, const rlm_tensor* position,
+    const rlm_tensor* out, hipStream_t stream) {
+  return hidden_update_impl(false, expanded_cache, operand_cache, anchor_index, partner_index,
+                            anchor_weight, partner_weight, product_weight, first_bias, position,
+                            out, stream);
+}
+
+extern "C" hipError_t rlm_relation_hidden_cache_update_ring(
+    const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
+    const rlm_tensor* anchor_index, const rlm_tensor* partner_index,
+    const rlm_tensor* anchor_weight, const rlm_tensor* partner_weight,
+    const rlm_tensor* product_weight, const rlm_tensor* first_bias, const rlm_tensor* position,
+    const rlm_tensor* out, hipStream_t stream) {
+  return hidden_update_impl(true, expanded_cache, operand_cache, anchor_index, partner_index,
+                            anchor_weight, partner_weight, product_weight, first_bias, position,
+                            out, stream);
+}
+
+extern "C" hipError_t rlm_relation_hidden_cached_ring(const rlm_tensor* expanded_cache,
+                                                      const rlm_tensor* operand_cache,
+                                                      const rlm_tensor* anchor_index,
+                                                      const rlm_tensor* partner_index,
+                                                      const rlm_tensor* product_weight,
+                                                      const rlm_tensor* out, hipStream_t stream) {
+  clear_error();
+  HiddenParams p{};
+  hipError_t err = hidden_impl(false, expanded_cache, operand_cache, anchor_index, partner_index,
+                               product_weight, out, p);
+  if (err != hipSuccess) return err;
+  err = require_ring(p);
+  if (err != hipSuccess) return err;
+  p.ring = 1;
+  return launch_hidden(p, operand_cache->dtype, false, stream);
 }
 
 extern "C" hipError_t rlm_relation_norm_reduce(const rlm_tensor* raw,

@@ -24,6 +24,12 @@
 // reference reads and writes out of bounds there); a block index past the
 // statistics' block count updates no statistics; block rows past the cache
 // end count as zero.
+//
+// Ring-buffer form (contexts beyond the cache length T, a power of two): any
+// position t >= 0 is accepted; position p lives in cache row p mod T and block
+// j's statistics in slot j mod NB (NB * BS == T).  Rows of the token's block
+// past t still hold positions from T earlier, so they count as zero -- the
+// value a fresh cache gives them in the linear form.
 #include "rlm_common.hpp"
 
 namespace rlm {
@@ -44,6 +50,7 @@ struct RouterParams {
   int weight_dtype[2];
   const void* pos;
   int pos_dtype;
+  int ring;                  // ring-buffer caches
   float* out;                // [B, 2, D]
 };
 
@@ -71,14 +78,16 @@ __global__ void __launch_bounds__(kWave) router_cache_fast_kernel(const RouterPa
   const int lane = threadIdx.x;
   const int64_t t = load_any_i(p.pos, p.pos_dtype, 0);
   float* out = p.out + (static_cast<int64_t>(b) * 2 + side) * p.D;
-  if (t < 0 || t >= p.T) {
+  if (t < 0 || (!p.ring && t >= p.T)) {
     for (int c = lane; c < p.D; c += kWave) out[c] = 0.0f;
     return;
   }
-  const int64_t row_t = static_cast<int64_t>(b) * p.T + t;
+  const int64_t mask = p.T - 1;  // ring row mask
+  const int64_t row_t = static_cast<int64_t>(b) * p.T + (p.ring ? (t & mask) : t);
   const int64_t j = t / BS;
-  const int64_t first = j * BS;
-  const bool stats = j < p.NB;
+  const int64_t slot = p.ring ? (j & (p.NB - 1)) : j;
+  const int64_t first = p.ring ? ((j * BS) & mask) : j * BS;  // the block's first cache row
+  const bool stats = slot < p.NB;
   const TR* raw = static_cast<const TR*>(p.raw[side]) + b * p.raw_stride[side];
   const TC* raw_cache = static_cast<const TC*>(p.raw_cache[side]);
   const TC* weight = static_cast<const TC*>(p.weight[side]);
@@ -87,8 +96,10 @@ __global__ void __launch_bounds__(kWave) router_cache_fast_kernel(const RouterPa
   const rsrc_t conv_rsrc = make_rsrc(
       static_cast<const unsigned char*>(p.conv_cache[side]) + static_cast<int64_t>(b) * p.T * row_bytes,
       static_cast<uint32_t>(p.T) * row_bytes);
-  const int64_t prev1 = t >= 1 ? row_t - 1 : row_t;  // clamped: the value is unused at t = 0
-  const int64_t prev2 = t >= 2 ? row_t - 2 : row_t;
+  // Previous rows, clamped where unused (t < 1, t < 2).
+  const int64_t row0 = static_cast<int64_t>(b) * p.T;
+  const int64_t prev1 = t >= 1 ? (p.ring ? row0 + ((t - 1) & mask) : row_t - 1) : row_t;
+  const int64_t prev2 = t >= 2 ? (p.ring ? row0 + ((t - 2) & mask) : row_t - 2) : row_t;
   for (int c = lane; c < p.D; c += kWave) {
     const float x = to_f32(raw[c]);
     const float p1 = to_f32(raw_cache[prev1 * p.D + c]);
@@ -111,12 +122,13 @@ __global__ void __launch_bounds__(kWave) router_cache_fast_kernel(const RouterPa
     store_elem<TC>(p.conv_cache[side], row_t * p.D + c, conv);
     out[c] = conv;
     if (!stats) continue;
-    // Block statistics over all BS rows; the token's own row from registers.
-    const int own = static_cast<int>(t - first);
+    // Block statistics over all BS rows; the token's own row from registers
+    // (ring form: rows past it count as zero).
+    const int own = static_cast<int>(t - j * BS);
     float sum = 0.0f;
 #pragma unroll
     for (int r = 0; r < BS; ++r) {
-      rows[r] = r == own ? conv : rows[r];
+      rows[r] = r == own ? conv : ((p.ring && r > own) ? 0.0f : rows[r]);
       sum += rows[r];
     }
     const float mean = sum / static_cast<float>(BS);
@@ -126,7 +138,7 @@ __global__ void __launch_bounds__(kWave) router_cache_fast_kernel(const RouterPa
       const float d = rows[r] - mean;
       sq += d * d;
     }
-    const int64_t s = (static_cast<int64_t>(b) * p.NB + j) * p.D + c;
+    const int64_t s = (static_cast<int64_t>(b) * p.NB + slot) * p.D + c;
     store_elem<TC>(p.mean[side], s, mean);
     store_elem<TC>(p.stdev[side], s, sqrtf(sq / static_cast<float>(BS)));
   }
@@ -139,21 +151,25 @@ __global__ void __launch_bounds__(kWave) router_cache_kernel(const RouterParams 
   const int lane = threadIdx.x;
   const int64_t t = load_any_i(p.pos, p.pos_dtype, 0);
   float* out = p.out + (static_cast<int64_t>(b) * 2 + side) * p.D;
-  if (t < 0 || t >= p.T) {
+  if (t < 0 || (!p.ring && t >= p.T)) {
     for (int c = lane; c < p.D; c += kWave) out[c] = 0.0f;
     return;
   }
   const int BS = p.BS;
-  const int64_t row_t = static_cast<int64_t>(b) * p.T + t;
+  const int64_t mask = p.T - 1;
+  const int64_t row0 = static_cast<int64_t>(b) * p.T;
+  auto row_of = [&](int64_t pos) { return row0 + (p.ring ? (pos & mask) : pos); };
+  const int64_t row_t = row_of(t);
   const int64_t j = t / BS;
+  const int64_t slot = p.ring ? (j & (p.NB - 1)) : j;
   const int64_t first = j * BS;
   for (int c = lane; c < p.D; c += kWave) {
     const float x = load_any_f(p.raw[side], p.raw_dtype[side], b * p.raw_stride[side] + c);
     const float p1 = t >= 1 ? load_any_f(p.raw_cache[side], p.raw_cache_dtype[side],
-                                         (row_t - 1) * p.D + c)
+                                         row_of(t - 1) * p.D + c)
                             : 0.0f;
     const float p2 = t >= 2 ? load_any_f(p.raw_cache[side], p.raw_cache_dtype[side],
-                                         (row_t - 2) * p.D + c)
+                                         row_of(t - 2) * p.D + c)
                             : 0.0f;
     const float w0 = load_any_f(p.weight[side], p.weight_dtype[side], 3 * c);
     const float w1 = load_any_f(p.weight[side], p.weight_dtype[side], 3 * c + 1);
@@ -168,10 +184,13 @@ __global__ void __launch_bounds__(kWave) router_cache_kernel(const RouterParams 
     store_any_f(p.raw_cache[side], p.raw_cache_dtype[side], row_t * p.D + c, x);
     store_any_f(p.conv_cache[side], p.conv_cache_dtype[side], row_t * p.D + c, conv);
     out[c] = conv;
-    if (j >= p.NB) continue;
+    if (slot >= p.NB) continue;
     auto block_row = [&](int r) {
       const int64_t idx = first + r;
       if (idx == t) return conv;
+      if (p.ring) return idx < t ? load_any_f(p.conv_cache[side], p.conv_cache_dtype[side],
+                                              row_of(idx) * p.D + c)
+                                 : 0.0f;
       return idx < p.T ? load_any_f(p.conv_cache[side], p.conv_cache_dtype[side],
                                     (static_cast<int64_t>(b) * p.T + idx) * p.D + c)
                        : 0.0f;
@@ -184,7 +203,7 @@ __global__ void __launch_bounds__(kWave) router_cache_kernel(const RouterParams 
       const float d = block_row(r) - mean;
       sq += d * d;
     }
-    const int64_t s = (static_cast<int64_t>(b) * p.NB + j) * p.D + c;
+    const int64_t s = (static_cast<int64_t>(b) * p.NB + slot) * p.D + c;
     store_any_f(p.mean[side], p.mean_dtype[side], s, mean);
     store_any_f(p.stdev[side], p.std_dtype[side], s, sqrtf(sq / static_cast<float>(BS)));
   }
@@ -229,13 +248,8 @@ hipError_t launch_fast_tc(const RouterParams& p, hipStream_t stream) {
   }
 }
 
-}  // namespace
-}  // namespace rlm
-
-using namespace rlm;
-
-extern "C" hipError_t rlm_router_cache_update(
-    const rlm_tensor* anchor_raw, const rlm_tensor* partner_raw,
+hipError_t router_update_impl(
+    bool ring, const rlm_tensor* anchor_raw, const rlm_tensor* partner_raw,
     const rlm_tensor* anchor_raw_cache, const rlm_tensor* partner_raw_cache,
     const rlm_tensor* anchor_conv_cache, const rlm_tensor* partner_conv_cache,
     const rlm_tensor* anchor_mean, const rlm_tensor* anchor_std,
@@ -289,8 +303,14 @@ extern "C" hipError_t rlm_router_cache_update(
   RLM_REQUIRE(B < (int64_t(1) << 31) && T < (int64_t(1) << 31) && D < (int64_t(1) << 31) &&
                   nb[0] < (int64_t(1) << 31),
               "router cache dimensions must be below 2^31");
+  if (ring)
+    RLM_REQUIRE(T > 0 && (T & (T - 1)) == 0 && nb[0] * block_size == T,
+                "ring-buffer caches need a power-of-two cache length equal to blocks * "
+                "block_size (cache length %lld, %lld blocks of %lld)",
+                (long long)T, (long long)nb[0], (long long)block_size);
   if (B == 0 || D == 0) return hipSuccess;
   RouterParams p{};
+  p.ring = ring ? 1 : 0;
   p.B = static_cast<int>(B);
   p.T = static_cast<int>(T);
   p.D = static_cast<int>(D);
@@ -336,4 +356,37 @@ extern "C" hipError_t rlm_router_cache_update(
   hipLaunchKernelGGL(router_cache_kernel, dim3(static_cast<unsigned>(B), 2), dim3(kWave), 0,
                      stream, p);
   return launch_status("router_cache_update");
+}
+
+}  // namespace
+}  // namespace rlm
+
+using namespace rlm;
+
+extern "C" hipError_t rlm_router_cache_update(
+    const rlm_tensor* anchor_raw, const rlm_tensor* partner_raw,
+    const rlm_tensor* anchor_raw_cache, const rlm_tensor* partner_raw_cache,
+    const rlm_tensor* anchor_conv_cache, const rlm_tensor* partner_conv_cache,
+    const rlm_tensor* anchor_mean, const rlm_tensor* anchor_std,
+    const rlm_tensor* partner_mean, const rlm_tensor* partner_std,
+    const rlm_tensor* anchor_conv_weight, const rlm_tensor* partner_conv_weight,
+    const rlm_tensor* position, int64_t block_size, const rlm_tensor* out, hipStream_t stream) {
+  return router_update_impl(false, anchor_raw, partner_raw, anchor_raw_cache, partner_raw_cache,
+                            anchor_conv_cache, partner_conv_cache, anchor_mean, anchor_std,
+                            partner_mean, partner_std, anchor_conv_weight, partner_conv_weight,
+                            position, block_size, out, stream);
+}
+
+extern "C" hipError_t rlm_router_cache_update_ring(
+    const rlm_tensor* anchor_raw, const rlm_tensor* partner_raw,
+    const rlm_tensor* anchor_raw_cache, const rlm_tensor* partner_raw_cache,
+    const rlm_tensor* anchor_conv_cache, const rlm_tensor* partner_conv_cache,
+    const rlm_tensor* anchor_mean, const rlm_tensor* anchor_std,
+    const rlm_tensor* partner_mean, const rlm_tensor* partner_std,
+    const rlm_tensor* anchor_conv_weight, const rlm_tensor* partner_conv_weight,
+    const rlm_tensor* position, int64_t block_size, const rlm_tensor* out, hipStream_t stream) {
+  return router_update_impl(true, anchor_raw, partner_raw, anchor_raw_cache, partner_raw_cache,
+                            anchor_conv_cache, partner_conv_cache, anchor_mean, anchor_std,
+                            partner_mean, partner_std, anchor_conv_weight, partner_conv_weight,
+                            position, block_size, out, stream);
 }

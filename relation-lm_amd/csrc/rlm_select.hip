@@ -148,6 +148,16 @@ struct Query {
   int64_t wbase;  // first position of the staged windows
 };
 
+// Ring-buffer caches of T rows: position p lives in row p mod T, and
+// statistics slot j holds the newest absolute block jb <= t/BS with
+// jb = j (mod NB) -- negative when no such block has been written.  Every
+// block from t/BS - NB + 1 on is wholly resident, so eligibility and distance
+// follow the linear rules on jb.
+__device__ __forceinline__ int ring_block(const SelectParams& p, const Query& qy, int j) {
+  const int cur = static_cast<int>(qy.t >> p.BS_log2);
+  return cur - ((cur - j) & (p.NB - 1));
+}
+
 // Block scores of one stream (relation_select.py:53-106) into ws.blk[NB]
 // (float32, -inf where not eligible).  Lane = (block j, head h) pair, heads of
 // a block in consecutive lanes:
@@ -156,7 +166,7 @@ struct Query {
 // DPP group reductions.  All in float64, rounded once.  Statistics and bias
 // come from LDS when the workgroup staged them, else from L2.  `sp` is
 // softplus(gamma_h) for this lane's head h = lane mod H.
-template <typename TS>
+template <typename TS, bool RING = false>
 __device__ void block_scores(const SelectParams& p, const Stream& s, const float* stats,
                              const float* bias_tab, double sp, const Query& qy, WaveScratch& ws,
                              int lane) {
@@ -193,7 +203,8 @@ __device__ void block_scores(const SelectParams& p, const Stream& s, const float
              static_cast<double>(sd.z) * fabs(qh[d + 2]) + static_cast<double>(sd.w) * fabs(qh[d + 3]);
       }
     }
-    const int end = (j + 1) * p.BS - 1;
+    const int jb = RING ? ring_block(p, qy, j) : j;  // absolute block held by slot j
+    const int end = (jb + 1) * p.BS - 1;
     const int dist = (qy.t > end ? static_cast<int>(qy.t - end) : 0) + 1;
     int bucket = 31 - __clz(dist);
     bucket = bucket < p.RB - 1 ? bucket : p.RB - 1;
@@ -209,7 +220,7 @@ __device__ void block_scores(const SelectParams& p, const Stream& s, const float
     const double sum = group_sum_f64(exp(sv - m), p.H);
     if (live && h == 0) {
       const double lse = m + log(sum);
-      const bool eligible = end <= qy.t && (!p.strict || end < qy.local_start);
+      const bool eligible = jb >= 0 && end <= qy.t && (!p.strict || end < qy.local_start);
       ws.blk[j] = eligible ? static_cast<float>(lse) : -INFINITY;
     }
   }
@@ -222,31 +233,37 @@ __device__ void block_scores(const SelectParams& p, const Stream& s, const float
 // Picks past the last block repeat block 0 as invalid, as the reference's
 // argmax over an all -inf vector does.  NB <= 64: block scores are held one
 // per lane and broadcast with readlane; larger NB reads them from LDS.
-__device__ void pick_blocks(const SelectParams& p, WaveScratch& ws, int lane) {
+template <bool RING = false>
+__device__ void pick_blocks(const SelectParams& p, const Query& qy, WaveScratch& ws, int lane) {
   for (int r = lane; r < p.TOP; r += kWave) {
     ws.sel[r] = 0;
     ws.selv[r] = 0;
   }
   wave_sync();
   if (p.NB <= kWave) {
+    // Ties rank by block id: the slot, or for ring caches the absolute block.
     const float mine = lane < p.NB ? ws.blk[lane] : -INFINITY;
-    const uint64_t kj = select_key(mine, static_cast<uint32_t>(lane));
+    const int id = RING ? ring_block(p, qy, lane) : lane;
+    const uint64_t kj = select_key(mine, static_cast<uint32_t>(id));
     int rank = 0;
     for (int k = 0; k < p.NB; ++k) {
       const float other = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), k));
-      rank += select_key(other, static_cast<uint32_t>(k)) > kj;
+      const int other_id = RING ? ring_block(p, qy, k) : k;
+      rank += select_key(other, static_cast<uint32_t>(other_id)) > kj;
     }
     if (lane < p.NB && rank < p.TOP) {
-      ws.sel[rank] = lane;
+      ws.sel[rank] = id;
       ws.selv[rank] = mine > -1.0e30f ? 1 : 0;
     }
   } else {
     for (int j = lane; j < p.NB; j += kWave) {
-      const uint64_t kj = select_key(ws.blk[j], static_cast<uint32_t>(j));
+      const int id = RING ? ring_block(p, qy, j) : j;
+      const uint64_t kj = select_key(ws.blk[j], static_cast<uint32_t>(id));
       int rank = 0;
-      for (int k = 0; k < p.NB; ++k) rank += select_key(ws.blk[k], static_cast<uint32_t>(k)) > kj;
+      for (int k = 0; k < p.NB; ++k)
+        rank += select_key(ws.blk[k], static_cast<uint32_t>(RING ? ring_block(p, qy, k) : k)) > kj;
       if (rank < p.TOP) {
-        ws.sel[rank] = j;
+        ws.sel[rank] = id;
         ws.selv[rank] = ws.blk[j] > -1.0e30f ? 1 : 0;
       }
     }
@@ -256,16 +273,19 @@ __device__ void pick_blocks(const SelectParams& p, WaveScratch& ws, int lane) {
 
 // Candidate lane c: local window first, then TOP*BS remote lanes in pick order
 // (relation_select.py:244-283).
+// Ring caches hold every position of [t-T+1, t], so the cache-end test drops
+// (a valid pick is an eligible, hence non-negative, absolute block).
+template <bool RING = false>
 __device__ __forceinline__ void candidate(const SelectParams& p, int c, const Query& qy,
                                           const WaveScratch& ws, int64_t& pos, bool& valid) {
   if (c < p.L) {
     pos = qy.t - p.L + 1 + c;
-    valid = pos >= 0 && pos <= qy.t && pos < p.T;
+    valid = pos >= 0 && pos <= qy.t && (RING || pos < p.T);
   } else {
     const int r = (c - p.L) >> p.BS_log2;
     const int o = (c - p.L) & (p.BS - 1);
     pos = static_cast<int64_t>(ws.sel[r]) * p.BS + o;
-    valid = ws.selv[r] != 0 && pos <= qy.t && pos < qy.local_start && pos < p.T;
+    valid = ws.selv[r] != 0 && pos <= qy.t && pos < qy.local_start && (RING || pos < p.T);
   }
 }
 
@@ -278,7 +298,7 @@ __device__ __forceinline__ void candidate(const SelectParams& p, int c, const Qu
 // query's whole window lies inside it (a per-wave decision); other rows come
 // through range-checked buffer loads whose offset is pushed past the end for
 // invalid rows (they read zero and are masked to -inf).
-template <typename TA, int NCL>
+template <typename TA, int NCL, bool RING = false>
 __device__ void candidate_scores(const SelectParams& p, const Stream& s, const unsigned char* win,
                                  const Query& qy, int exclude, WaveScratch& ws, int lane) {
   constexpr int EPC = kEpc<TA>;
@@ -301,16 +321,16 @@ __device__ void candidate_scores(const SelectParams& p, const Stream& s, const u
       int ps;
       if (c < p.L) {
         ps = t - p.L + 1 + c;
-        v = v && ps >= 0 && ps <= t && ps < T;
+        v = v && ps >= 0 && ps <= t && (RING || ps < T);
         from_lds[u] = lds;
       } else {
         const int r = v ? (c - p.L) >> p.BS_log2 : 0;
         ps = ws.sel[r] * p.BS + ((c - p.L) & (p.BS - 1));
-        v = v && ws.selv[r] != 0 && ps <= t && ps < ls && ps < T;
+        v = v && ws.selv[r] != 0 && ps <= t && ps < ls && (RING || ps < T);
         from_lds[u] = false;
       }
       ok[u] = v && ps != exclude;
-      pos[u] = ps;
+      pos[u] = RING ? (ps & (T - 1)) : ps;  // ring: the cache row (staged windows are linear only)
     }
     double acc[NCL];
 #pragma unroll
@@ -434,7 +454,8 @@ __device__ void stage_workgroup(const SelectParams& p, int64_t b, int64_t wbase,
   }
 }
 
-template <typename TA, typename TS, int MODE>
+// RING: ring-buffer caches (decode form only, no staged windows).
+template <typename TA, typename TS, int MODE, bool RING = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) select_kernel(const SelectParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int EPC = kEpc<TA>;
@@ -543,15 +564,15 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
     put_exact();
     put_router(rq_a, static_cast<const TA*>(p.arq), RD);
     wave_sync();
-    block_scores<TS>(p, p.as, stats_a, bias_a, sp_a, qy, ws, lane);
-    pick_blocks(p, ws, lane);
-    candidate_scores<TA, 3>(p, p.as, win_a, qy, -1, ws, lane);
+    block_scores<TS, RING>(p, p.as, stats_a, bias_a, sp_a, qy, ws, lane);
+    pick_blocks<RING>(p, qy, ws, lane);
+    candidate_scores<TA, 3, RING>(p, p.as, win_a, qy, -1, ws, lane);
     uint64_t best = 0;
     float best_score = -INFINITY;
     for (int c = lane; c < p.CAP; c += kWave) {
       int64_t pos;
       bool valid;
-      candidate(p, c, qy, ws, pos, valid);
+      candidate<RING>(p, c, qy, ws, pos, valid);
       if (valid) {
         const float sc = ws.sc[c];
         const uint64_t k = select_key(sc, static_cast<uint32_t>(pos));
@@ -586,8 +607,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
   {
     const TA* prq = static_cast<const TA*>(p.prq) + qy.q * p.prq_row;
     if (MODE == kPacked) {
-      const bool have = anchor >= 0 && anchor < p.T;
-      const TA* pc = static_cast<const TA*>(p.pcache) + (b * p.T + (have ? anchor : 0)) * (2 * p.E);
+      const bool have = anchor >= 0 && (RING || anchor < p.T);
+      const int64_t arow = RING ? (anchor & (p.T - 1)) : anchor;
+      const TA* pc = static_cast<const TA*>(p.pcache) + (b * p.T + (have ? arow : 0)) * (2 * p.E);
       double base_q[EPC], cache_q[EPC];
       chunk_to_f64<TA>(pb_chunk, base_q);
       const uint4 cc = *reinterpret_cast<const uint4*>(pc + EPC * j);
@@ -616,9 +638,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
     put_exact();
   }
   wave_sync();
-  block_scores<TS>(p, p.ps, stats_p, bias_p, sp_p, qy, ws, lane);
-  pick_blocks(p, ws, lane);
-  candidate_scores<TA, 3>(p, p.ps, win_p, qy, static_cast<int>(anchor), ws, lane);
+  block_scores<TS, RING>(p, p.ps, stats_p, bias_p, sp_p, qy, ws, lane);
+  pick_blocks<RING>(p, qy, ws, lane);
+  candidate_scores<TA, 3, RING>(p, p.ps, win_p, qy, static_cast<int>(anchor), ws, lane);
 
   // K argmax passes (relation_select.py:298-308), ties to the lowest lane.
   // While finite scores remain, this is a stable descending order of the
@@ -661,7 +683,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
       float score = -INFINITY;
       if (my_c >= 0) {
         bool valid;
-        candidate(p, my_c, qy, ws, pos, valid);
+        candidate<RING>(p, my_c, qy, ws, pos, valid);
         score = ws.sc[my_c];
       }
       p.out_partner[qy.q * p.K + lane] = static_cast<int32_t>(pos);
@@ -680,7 +702,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
     if ((c & (kWave - 1)) == lane) {
       int64_t pos;
       bool valid;
-      candidate(p, c, qy, ws, pos, valid);
+      candidate<RING>(p, c, qy, ws, pos, valid);
       const bool exhausted = !(key_score(win) > -INFINITY);
       p.out_partner[qy.q * p.K + k] = static_cast<int32_t>(pos);
       p.out_partner_score[qy.q * p.K + k] = exhausted ? -INFINITY : ws.sc[c];
@@ -882,7 +904,7 @@ multi_select_kernel(const SelectParams p, const MultiParams m) {
     for (int d = lane; d < RD; d += kWave) ws.qr[d] = static_cast<double>(to_f32(arq[d]));
     wave_sync();
     block_scores<TS>(p, p.as, nullptr, nullptr, sp_a, qy, ws, lane);
-    pick_blocks(p, ws, lane);
+    pick_blocks(p, qy, ws, lane);
   }
   int taken[kMaxSlots];
 #pragma unroll
@@ -977,7 +999,7 @@ multi_select_kernel(const SelectParams p, const MultiParams m) {
       ws.qr[d] = static_cast<double>(to_f32(pb[p.E + d]) + to_f32(pc[p.E + d]));
     wave_sync();
     block_scores<TS>(p, p.ps, stats_p, bias_p, sp_p, qy, ws, lane);
-    pick_blocks(p, ws, lane);
+    pick_blocks(p, qy, ws, lane);
     slot_candidate_scores<TA, 3>(p, p.ps.keys, m.key_pos_bytes, m.slot_bytes * s, qy, taken,
                                  active, ws, lane);
     topk_lanes_out(p, qy, ws, lane, out_idx, out_score);
@@ -1140,7 +1162,7 @@ hipError_t finish_params(SelectParams& p, const Geometry& g, int64_t local_windo
   return hipSuccess;
 }
 
-template <int MODE>
+template <int MODE, bool RING = false>
 hipError_t launch_select(const SelectParams& p, int act_dtype, int stat_dtype,
                          hipStream_t stream) {
   const int64_t queries = p.B * p.Tq;
@@ -1150,7 +1172,7 @@ hipError_t launch_select(const SelectParams& p, int act_dtype, int stat_dtype,
   const size_t lds = static_cast<size_t>(p.lds_total);
 #define RLM_SELECT_CASE(TA_ID, TA, TS_ID, TS)                                          \
   if (act_dtype == TA_ID && stat_dtype == TS_ID) {                                     \
-    hipLaunchKernelGGL((select_kernel<TA, TS, MODE>), grid, block, lds, stream, p);    \
+    hipLaunchKernelGGL((select_kernel<TA, TS, MODE, RING>), grid, block, lds, stream, p); \
     return launch_status("relation_select");                                           \
   }
   RLM_SELECT_CASE(RLM_F32, float, RLM_F32, float)
@@ -1214,7 +1236,7 @@ bool check_outputs(const rlm_tensor* idx, const rlm_tensor* score, const char* w
 }
 
 hipError_t select_packed_impl(
-    bool seq, const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
+    bool seq, bool ring, const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
     const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
     const rlm_tensor* anchor_block_std, const rlm_tensor* anchor_gamma,
     const rlm_tensor* anchor_bias, const rlm_tensor* partner_base,
@@ -1296,6 +1318,14 @@ hipError_t select_packed_impl(
   p.out_anchor_score = static_cast<float*>(out_anchor_score->data);
   p.out_partner = static_cast<int32_t*>(out_partner->data);
   p.out_partner_score = static_cast<float*>(out_partner_score->data);
+  if (ring) {
+    RLM_REQUIRE(!seq, "ring-buffer caches are supported by the decode form only");
+    RLM_REQUIRE((g.T & (g.T - 1)) == 0 && static_cast<int64_t>(g.NB) * g.BS == g.T,
+                "ring-buffer caches need a power-of-two cache length split into whole blocks "
+                "(cache length %lld, %d blocks)",
+                (long long)g.T, g.NB);
+    return launch_select<kPacked, true>(p, act, stat, stream);
+  }
   return launch_select<kPacked>(p, act, stat, stream);
 }
 
@@ -1456,7 +1486,7 @@ extern "C" hipError_t rlm_relation_select_packed(
     int64_t local_window, int64_t top_blocks, int64_t k_out, int32_t strict_valid,
     const rlm_tensor* out_anchor, const rlm_tensor* out_anchor_score,
     const rlm_tensor* out_partner, const rlm_tensor* out_partner_score, hipStream_t stream) {
-  return select_packed_impl(false, anchor_query, anchor_keys, anchor_router_query,
+  return select_packed_impl(false, false, anchor_query, anchor_keys, anchor_router_query,
                             anchor_block_mean, anchor_block_std, anchor_gamma, anchor_bias,
                             partner_base, partner_anchor_cache, partner_keys, partner_block_mean,
                             partner_block_std, partner_gamma, partner_bias, position,
@@ -1475,10 +1505,29 @@ extern "C" hipError_t rlm_relation_select_packed_seq(
     int64_t local_window, int64_t top_blocks, int64_t k_out, int32_t strict_valid,
     const rlm_tensor* out_anchor, const rlm_tensor* out_anchor_score,
     const rlm_tensor* out_partner, const rlm_tensor* out_partner_score, hipStream_t stream) {
-  return select_packed_impl(true, anchor_query, anchor_keys, anchor_router_query,
+  return select_packed_impl(true, false, anchor_query, anchor_keys, anchor_router_query,
                             anchor_block_mean, anchor_block_std, anchor_gamma, anchor_bias,
                             partner_base, partner_anchor_cache, partner_keys, partner_block_mean,
                             partner_block_std, partner_gamma, partner_bias, positions,
+                            local_window, top_blocks, k_out, strict_valid, out_anchor,
+                            out_anchor_score, out_partner, out_partner_score, stream);
+}
+
+extern "C" hipError_t rlm_relation_select_packed_ring(
+    const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
+    const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
+    const rlm_tensor* anchor_block_std, const rlm_tensor* anchor_gamma,
+    const rlm_tensor* anchor_bias, const rlm_tensor* partner_base,
+    const rlm_tensor* partner_anchor_cache, const rlm_tensor* partner_keys,
+    const rlm_tensor* partner_block_mean, const rlm_tensor* partner_block_std,
+    const rlm_tensor* partner_gamma, const rlm_tensor* partner_bias, const rlm_tensor* position,
+    int64_t local_window, int64_t top_blocks, int64_t k_out, int32_t strict_valid,
+    const rlm_tensor* out_anchor, const rlm_tensor* out_anchor_score,
+    const rlm_tensor* out_partner, const rlm_tensor* out_partner_score, hipStream_t stream) {
+  return select_packed_impl(false, true, anchor_query, anchor_keys, anchor_router_query,
+                            anchor_block_mean, anchor_block_std, anchor_gamma, anchor_bias,
+                            partner_base, partner_anchor_cache, partner_keys, partner_block_mean,
+                            partner_block_std, partner_gamma, partner_bias, position,
                             local_window, top_blocks, k_out, strict_valid, out_anchor,
                             out_anchor_score, out_partner, out_partner_score, stream);
 }

@@ -82,9 +82,11 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> select_packed_common(
     const at::Tensor& partner_anchor_cache, const at::Tensor& partner_keys,
     const at::Tensor& partner_block_mean, const at::Tensor& partner_block_std,
     const at::Tensor& partner_gamma, const at::Tensor& partner_bias, const at::Tensor& position,
-    int64_t local_window, int64_t top_blocks, int64_t k_out, bool strict_valid) {
-  const char* op = seq ? "relation_lm::relation_select_packed_seq"
-                       : "relation_lm::relation_select_packed";
+    int64_t local_window, int64_t top_blocks, int64_t k_out, bool strict_valid,
+    bool ring = false) {
+  const char* op = ring  ? "relation_lm::relation_select_packed_ring"
+                   : seq ? "relation_lm::relation_select_packed_seq"
+                         : "relation_lm::relation_select_packed";
   c10::DeviceGuard guard(anchor_query.device());
   hipStream_t stream = device_stream(
       op, {&anchor_query, &anchor_keys, &anchor_router_query, &anchor_block_mean,
@@ -113,7 +115,8 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> select_packed_common(
       desc(partner_bias, "partner_bias"), desc(position, "position"),
       desc(out_anchor, "out_anchor"), desc(out_anchor_score, "out_anchor_score"),
       desc(out_partner, "out_partner"), desc(out_partner_score, "out_partner_score")};
-  auto fn = seq ? rlm_relation_select_packed_seq : rlm_relation_select_packed;
+  auto fn = ring ? rlm_relation_select_packed_ring
+                 : seq ? rlm_relation_select_packed_seq : rlm_relation_select_packed;
   check(fn(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7], &d[8], &d[9], &d[10], &d[11],
            &d[12], &d[13], &d[14], local_window, top_blocks, k_out, strict_valid ? 1 : 0, &d[15],
            &d[16], &d[17], &d[18], stream),
@@ -135,6 +138,23 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> relation_select_packe
                               partner_base, partner_anchor_cache, partner_keys,
                               partner_block_mean, partner_block_std, partner_gamma, partner_bias,
                               position, local_window, top_blocks, k_out, strict_valid);
+}
+
+// Ring-buffer caches (no reference op): position p in cache row p mod T.
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> relation_select_packed_ring(
+    const at::Tensor& anchor_query, const at::Tensor& anchor_keys,
+    const at::Tensor& anchor_router_query, const at::Tensor& anchor_block_mean,
+    const at::Tensor& anchor_block_std, const at::Tensor& anchor_gamma,
+    const at::Tensor& anchor_bias, const at::Tensor& partner_base,
+    const at::Tensor& partner_anchor_cache, const at::Tensor& partner_keys,
+    const at::Tensor& partner_block_mean, const at::Tensor& partner_block_std,
+    const at::Tensor& partner_gamma, const at::Tensor& partner_bias, const at::Tensor& position,
+    int64_t local_window, int64_t top_blocks, int64_t k_out, bool strict_valid) {
+  return select_packed_common(false, anchor_query, anchor_keys, anchor_router_query,
+                              anchor_block_mean, anchor_block_std, anchor_gamma, anchor_bias,
+                              partner_base, partner_anchor_cache, partner_keys,
+                              partner_block_mean, partner_block_std, partner_gamma, partner_bias,
+                              position, local_window, top_blocks, k_out, strict_valid, true);
 }
 
 std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> relation_select_packed_seq(
@@ -252,9 +272,11 @@ std::tuple<at::Tensor, at::Tensor> partner_topk(
 
 at::Tensor hidden_common(bool seq, const at::Tensor& expanded_cache,
                          const at::Tensor& operand_cache, const at::Tensor& anchor_index,
-                         const at::Tensor& partner_index, const at::Tensor& product_weight) {
-  const char* op = seq ? "relation_lm::relation_hidden_cached_seq"
-                       : "relation_lm::relation_hidden_cached";
+                         const at::Tensor& partner_index, const at::Tensor& product_weight,
+                         bool ring = false) {
+  const char* op = ring  ? "relation_lm::relation_hidden_cached_ring"
+                   : seq ? "relation_lm::relation_hidden_cached_seq"
+                         : "relation_lm::relation_hidden_cached";
   c10::DeviceGuard guard(operand_cache.device());
   hipStream_t stream = device_stream(
       op, {&operand_cache, &expanded_cache, &anchor_index, &partner_index, &product_weight});
@@ -267,7 +289,8 @@ at::Tensor hidden_common(bool seq, const at::Tensor& expanded_cache,
   rlm_tensor d[6] = {desc(expanded_cache, "expanded_cache"), desc(operand_cache, "operand_cache"),
                      desc(anchor_index, "anchor_index"),     desc(partner_index, "partner_index"),
                      desc(product_weight, "product_weight"), desc(out, "out")};
-  auto fn = seq ? rlm_relation_hidden_cached_seq : rlm_relation_hidden_cached;
+  auto fn = ring ? rlm_relation_hidden_cached_ring
+                 : seq ? rlm_relation_hidden_cached_seq : rlm_relation_hidden_cached;
   check(fn(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], stream), op);
   return out;
 }
@@ -281,6 +304,15 @@ at::Tensor relation_hidden_cached(const at::Tensor& expanded_cache,
                        product_weight);
 }
 
+at::Tensor relation_hidden_cached_ring(const at::Tensor& expanded_cache,
+                                       const at::Tensor& operand_cache,
+                                       const at::Tensor& anchor_index,
+                                       const at::Tensor& partner_index,
+                                       const at::Tensor& product_weight) {
+  return hidden_common(false, expanded_cache, operand_cache, anchor_index, partner_index,
+                       product_weight, true);
+}
+
 at::Tensor relation_hidden_cached_seq(const at::Tensor& expanded_cache,
                                       const at::Tensor& operand_cache,
                                       const at::Tensor& anchor_index,
@@ -290,16 +322,14 @@ at::Tensor relation_hidden_cached_seq(const at::Tensor& expanded_cache,
                        product_weight);
 }
 
-at::Tensor relation_hidden_cache_update(at::Tensor& expanded_cache,
-                                        const at::Tensor& operand_cache,
-                                        const at::Tensor& anchor_index,
-                                        const at::Tensor& partner_index,
-                                        const at::Tensor& anchor_weight,
-                                        const at::Tensor& partner_weight,
-                                        const at::Tensor& product_weight,
-                                        const at::Tensor& first_bias,
-                                        const at::Tensor& position) {
-  const char* op = "relation_lm::relation_hidden_cache_update";
+at::Tensor hidden_update_common(bool ring, at::Tensor& expanded_cache,
+                                const at::Tensor& operand_cache, const at::Tensor& anchor_index,
+                                const at::Tensor& partner_index, const at::Tensor& anchor_weight,
+                                const at::Tensor& partner_weight,
+                                const at::Tensor& product_weight, const at::Tensor& first_bias,
+                                const at::Tensor& position) {
+  const char* op = ring ? "relation_lm::relation_hidden_cache_update_ring"
+                        : "relation_lm::relation_hidden_cache_update";
   c10::DeviceGuard guard(operand_cache.device());
   hipStream_t stream = device_stream(
       op, {&operand_cache, &expanded_cache, &anchor_index, &partner_index, &anchor_weight,
@@ -314,10 +344,37 @@ at::Tensor relation_hidden_cache_update(at::Tensor& expanded_cache,
                       desc(anchor_weight, "anchor_weight"),   desc(partner_weight, "partner_weight"),
                       desc(product_weight, "product_weight"), desc(first_bias, "first_bias"),
                       desc(position, "position"),             desc(out, "out")};
-  check(rlm_relation_hidden_cache_update(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7],
-                                         &d[8], &d[9], stream),
-        op);
+  auto fn = ring ? rlm_relation_hidden_cache_update_ring : rlm_relation_hidden_cache_update;
+  check(fn(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7], &d[8], &d[9], stream), op);
   return out;
+}
+
+at::Tensor relation_hidden_cache_update(at::Tensor& expanded_cache,
+                                        const at::Tensor& operand_cache,
+                                        const at::Tensor& anchor_index,
+                                        const at::Tensor& partner_index,
+                                        const at::Tensor& anchor_weight,
+                                        const at::Tensor& partner_weight,
+                                        const at::Tensor& product_weight,
+                                        const at::Tensor& first_bias,
+                                        const at::Tensor& position) {
+  return hidden_update_common(false, expanded_cache, operand_cache, anchor_index, partner_index,
+                              anchor_weight, partner_weight, product_weight, first_bias,
+                              position);
+}
+
+at::Tensor relation_hidden_cache_update_ring(at::Tensor& expanded_cache,
+                                             const at::Tensor& operand_cache,
+                                             const at::Tensor& anchor_index,
+                                             const at::Tensor& partner_index,
+                                             const at::Tensor& anchor_weight,
+                                             const at::Tensor& partner_weight,
+                                             const at::Tensor& product_weight,
+                                             const at::Tensor& first_bias,
+                                             const at::Tensor& position) {
+  return hidden_update_common(true, expanded_cache, operand_cache, anchor_index, partner_index,
+                              anchor_weight, partner_weight, product_weight, first_bias,
+                              position);
 }
 
 at::Tensor norm_common(bool seq, const at::Tensor& raw, const at::Tensor& partner_scores,
@@ -426,15 +483,16 @@ at::Tensor relation_linear(const at::Tensor& input, const at::Tensor& weight,
                        out_dtype.value_or(input.scalar_type()), false);
 }
 
-at::Tensor router_cache_update(const at::Tensor& anchor_raw, const at::Tensor& partner_raw,
-                               at::Tensor& anchor_raw_cache, at::Tensor& partner_raw_cache,
-                               at::Tensor& anchor_conv_cache, at::Tensor& partner_conv_cache,
-                               at::Tensor& anchor_mean, at::Tensor& anchor_std,
-                               at::Tensor& partner_mean, at::Tensor& partner_std,
-                               const at::Tensor& anchor_conv_weight,
-                               const at::Tensor& partner_conv_weight, const at::Tensor& position,
-                               int64_t block_size) {
-  const char* op = "relation_lm::router_cache_update";
+at::Tensor router_common(bool ring, const at::Tensor& anchor_raw, const at::Tensor& partner_raw,
+                         at::Tensor& anchor_raw_cache, at::Tensor& partner_raw_cache,
+                         at::Tensor& anchor_conv_cache, at::Tensor& partner_conv_cache,
+                         at::Tensor& anchor_mean, at::Tensor& anchor_std,
+                         at::Tensor& partner_mean, at::Tensor& partner_std,
+                         const at::Tensor& anchor_conv_weight,
+                         const at::Tensor& partner_conv_weight, const at::Tensor& position,
+                         int64_t block_size) {
+  const char* op = ring ? "relation_lm::router_cache_update_ring"
+                        : "relation_lm::router_cache_update";
   c10::DeviceGuard guard(anchor_raw.device());
   hipStream_t stream = device_stream(
       op, {&anchor_raw, &partner_raw, &anchor_raw_cache, &partner_raw_cache, &anchor_conv_cache,
@@ -456,11 +514,29 @@ at::Tensor router_cache_update(const at::Tensor& anchor_raw, const at::Tensor& p
                       desc(partner_conv_weight, "partner_conv_weight"),
                       desc(position, "position"),
                       desc(out, "out")};
-  check(rlm_router_cache_update(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7], &d[8],
-                                &d[9], &d[10], &d[11], &d[12], block_size, &d[13], stream),
+  auto fn = ring ? rlm_router_cache_update_ring : rlm_router_cache_update;
+  check(fn(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7], &d[8], &d[9], &d[10], &d[11],
+           &d[12], block_size, &d[13], stream),
         op);
   return out;
 }
+
+#define RLM_ROUTER_ARGS                                                                        \
+  const at::Tensor &anchor_raw, const at::Tensor &partner_raw, at::Tensor &anchor_raw_cache,  \
+      at::Tensor &partner_raw_cache, at::Tensor &anchor_conv_cache,                           \
+      at::Tensor &partner_conv_cache, at::Tensor &anchor_mean, at::Tensor &anchor_std,        \
+      at::Tensor &partner_mean, at::Tensor &partner_std,                                      \
+      const at::Tensor &anchor_conv_weight, const at::Tensor &partner_conv_weight,            \
+      const at::Tensor &position, int64_t block_size
+#define RLM_ROUTER_PASS                                                                       \
+  anchor_raw, partner_raw, anchor_raw_cache, partner_raw_cache, anchor_conv_cache,            \
+      partner_conv_cache, anchor_mean, anchor_std, partner_mean, partner_std,                 \
+      anchor_conv_weight, partner_conv_weight, position, block_size
+
+at::Tensor router_cache_update(RLM_ROUTER_ARGS) { return router_common(false, RLM_ROUTER_PASS); }
+at::Tensor router_cache_update_ring(RLM_ROUTER_ARGS) { return router_common(true, RLM_ROUTER_PASS); }
+#undef RLM_ROUTER_ARGS
+#undef RLM_ROUTER_PASS
 
 }  // namespace
 
@@ -513,6 +589,27 @@ TORCH_LIBRARY(relation_lm, m) {
       "Tensor(e!) anchor_mean, Tensor(f!) anchor_std, Tensor(g!) partner_mean, Tensor(h!) "
       "partner_std, Tensor anchor_conv_weight, Tensor partner_conv_weight, Tensor position, int "
       "block_size) -> Tensor");
+  // Ring-buffer forms (no reference op): the schemas of the linear ops.
+  m.def(
+      "relation_select_packed_ring(Tensor anchor_query, Tensor anchor_keys, Tensor "
+      "anchor_router_query, Tensor anchor_block_mean, Tensor anchor_block_std, Tensor "
+      "anchor_gamma, Tensor anchor_bias, Tensor partner_base, Tensor partner_anchor_cache, "
+      "Tensor partner_keys, Tensor partner_block_mean, Tensor partner_block_std, Tensor "
+      "partner_gamma, Tensor partner_bias, Tensor position, SymInt local_window, SymInt "
+      "top_blocks, SymInt k_out, bool strict_valid) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def(
+      "relation_hidden_cached_ring(Tensor expanded_cache, Tensor operand_cache, Tensor "
+      "anchor_index, Tensor partner_index, Tensor product_weight) -> Tensor");
+  m.def(
+      "relation_hidden_cache_update_ring(Tensor(a!) expanded_cache, Tensor operand_cache, Tensor "
+      "anchor_index, Tensor partner_index, Tensor anchor_weight, Tensor partner_weight, Tensor "
+      "product_weight, Tensor first_bias, Tensor position) -> Tensor");
+  m.def(
+      "router_cache_update_ring(Tensor anchor_raw, Tensor partner_raw, Tensor(a!) "
+      "anchor_raw_cache, Tensor(b!) partner_raw_cache, Tensor(c!) anchor_conv_cache, Tensor(d!) "
+      "partner_conv_cache, Tensor(e!) anchor_mean, Tensor(f!) anchor_std, Tensor(g!) "
+      "partner_mean, Tensor(h!) partner_std, Tensor anchor_conv_weight, Tensor "
+      "partner_conv_weight, Tensor position, int block_size) -> Tensor");
   m.def("packed_sparse_cache_projection(Tensor memory, Tensor weight) -> Tensor");
   m.def(
       "relation_linear(Tensor input, Tensor weight, Tensor? bias=None, ScalarType? "
@@ -542,6 +639,10 @@ TORCH_LIBRARY_IMPL(relation_lm, CUDA, m) {
   m.impl("relation_norm_reduce_seq", TORCH_FN(relation_norm_reduce_seq));
   m.impl("relation_reduce_fused_seq", TORCH_FN(relation_reduce_fused_seq));
   m.impl("router_cache_update", TORCH_FN(router_cache_update));
+  m.impl("relation_select_packed_ring", TORCH_FN(relation_select_packed_ring));
+  m.impl("relation_hidden_cached_ring", TORCH_FN(relation_hidden_cached_ring));
+  m.impl("relation_hidden_cache_update_ring", TORCH_FN(relation_hidden_cache_update_ring));
+  m.impl("router_cache_update_ring", TORCH_FN(router_cache_update_ring));
   m.impl("packed_sparse_cache_projection", TORCH_FN(packed_sparse_cache_projection));
   m.impl("relation_linear", TORCH_FN(relation_linear));
 }

@@ -45,6 +45,7 @@ def _register_fakes() -> None:
 
     torch.library.register_fake("relation_lm::relation_select_packed")(fake_select)
     torch.library.register_fake("relation_lm::relation_select_packed_seq")(fake_select)
+    torch.library.register_fake("relation_lm::relation_select_packed_ring")(fake_select)
 
     @torch.library.register_fake("relation_lm::multi_relation_select_seq")
     def _(anchor_query, *rest):
@@ -75,6 +76,8 @@ def _register_fakes() -> None:
     torch.library.register_fake("relation_lm::relation_hidden_cached")(fake_hidden)
     torch.library.register_fake("relation_lm::relation_hidden_cached_seq")(fake_hidden)
     torch.library.register_fake("relation_lm::relation_hidden_cache_update")(fake_hidden)
+    torch.library.register_fake("relation_lm::relation_hidden_cached_ring")(fake_hidden)
+    torch.library.register_fake("relation_lm::relation_hidden_cache_update_ring")(fake_hidden)
 
     def fake_norm(raw, *rest):
         return raw.new_empty(tuple(raw.shape[:-2]) + (raw.shape[-1],), dtype=torch.float32)
@@ -82,10 +85,12 @@ def _register_fakes() -> None:
     torch.library.register_fake("relation_lm::relation_norm_reduce")(fake_norm)
     torch.library.register_fake("relation_lm::relation_norm_reduce_seq")(fake_norm)
 
-    @torch.library.register_fake("relation_lm::router_cache_update")
-    def _(anchor_raw, *rest):
+    def fake_router(anchor_raw, *rest):
         return anchor_raw.new_empty((anchor_raw.shape[0], 2, anchor_raw.shape[1]),
                                     dtype=torch.float32)
+
+    torch.library.register_fake("relation_lm::router_cache_update")(fake_router)
+    torch.library.register_fake("relation_lm::router_cache_update_ring")(fake_router)
 
     @torch.library.register_fake("relation_lm::relation_reduce_fused_seq")
     def _(expanded_cache, operand_cache, anchor_index, partner_index, product_weight,
