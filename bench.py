@@ -16,7 +16,7 @@ Also reported:
     contract, or matrix-core FLOPs for the fused reduce);
   * decode-step latency (cfg3: packed 576->512 projection, router cache update,
     cache-row writes, select, reduce) at B=1 and B=8, eager and replayed from a
-    HIP graph;
+    HIP graph; the same step at position 4095 over 512-row ring-buffer caches;
   * routed multi-anchor selection at cfg5 (B=4, T=4096, 4 anchor slots x K=6,
     block 64, local 128, top 8): one layer's selection over all 16384 queries;
   * the CPU oracle timed on this host's cores on a bounded sample.
@@ -37,6 +37,7 @@ for _p in (ROOT, os.path.join(ROOT, "relation-lm_amd")):
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 CALIBRATION_BYTES = 256 << 20
+RING_POSITION = 4095            # decode position of the ring-buffer step (512-row caches)
 CPU_SAMPLE_SECONDS = 10.0       # bounded CPU-oracle sample (whole passes of the cfg2 chain)   # plain copy whose counter readings scale FETCH/WRITE_SIZE
 # Kernel-name prefixes (as rocprofv3 reports them) of the timed kernels.
 KERNEL_SYMBOLS = {
@@ -151,6 +152,12 @@ def main() -> int:
         relation_select_packed_seq,
     )
     from relation_lm.inference import pack_sparse_cache_projection_weights
+    from relation_lm.kernels.ring import (
+        relation_hidden_cache_update_ring,
+        relation_hidden_cached_ring,
+        relation_select_packed_ring,
+        router_cache_update_ring,
+    )
     from relation_lm.kernels.router_cache import router_cache_update
     from relation_lm.workloads import (
         CONFIGS,
@@ -170,8 +177,16 @@ def main() -> int:
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
 
-    def run_decode():
-        """Decode-step latency (cfg3) at B=1 and B=8, eager and from a HIP graph."""
+    def run_decode(ring_position=None):
+        """Decode-step latency (cfg3) at B=1 and B=8, eager and from a HIP graph.
+
+        ring_position: decode at that absolute position over ring-buffer caches of
+        the cfg3 length (the *_ring ops; rows written at position mod length)."""
+        ring = ring_position is not None
+        select_op = relation_select_packed_ring if ring else relation_select_packed
+        router_op = router_cache_update_ring if ring else router_cache_update
+        update_op = relation_hidden_cache_update_ring if ring else relation_hidden_cache_update
+        cached_op = relation_hidden_cached_ring if ring else relation_hidden_cached
         decode = {}
         for batch in (1, 8):
             dcfg = RelationConfig(**{**CONFIGS["cfg3"].__dict__, "batch": batch})
@@ -182,14 +197,16 @@ def main() -> int:
             memory, weights = packed_projection_inputs(dcfg, device=device)
             projection = pack_sparse_cache_projection_weights(weights)
             rc = router_cache_inputs(dcfg, device=device)
+            if ring:
+                dsel["position"] = torch.tensor(ring_position, dtype=torch.int64, device=device)
             dargs = select_args(dsel, dcfg)
-            t = dcfg.context - 1
+            t = (ring_position if ring else dcfg.context - 1) % dcfg.context  # cache row
             position = dsel["position"]
 
             def decode_step(dsel=dsel, dred=dred, dexp=dexp, memory=memory, projection=projection,
                             dargs=dargs, t=t, position=position, batch=batch, rc=rc, dcfg=dcfg):
                 parts = projection.project(memory)
-                router_cache_update(parts[4], parts[5], rc["anchor_raw_cache"],
+                router_op(parts[4], parts[5], rc["anchor_raw_cache"],
                                     rc["partner_raw_cache"], rc["anchor_conv_cache"],
                                     rc["partner_conv_cache"], dsel["anchor_block_mean"],
                                     dsel["anchor_block_std"], dsel["partner_block_mean"],
@@ -199,17 +216,16 @@ def main() -> int:
                 dsel["partner_keys"][:, t] = parts[1]
                 dred["operand_cache"][:, t] = parts[2]
                 dsel["partner_anchor_cache"][:, t] = parts[3]
-                a_, s_, p_, ps_ = relation_select_packed(*dargs)
+                a_, s_, p_, ps_ = select_op(*dargs)
                 if batch == 1:
-                    hid = relation_hidden_cache_update(
+                    hid = update_op(
                         dexp, dred["operand_cache"], a_, p_, dred["anchor_weight"],
                         dred["partner_weight"], dred["product_weight"], dred["first_bias"], position)
                 else:
                     row = relation_linear(dred["operand_cache"][:, t], dred["expanded_weight"],
                                           dred["expanded_bias"])
                     dexp[:, t] = row
-                    hid = relation_hidden_cached(dexp, dred["operand_cache"], a_, p_,
-                                                 dred["product_weight"])
+                    hid = cached_op(dexp, dred["operand_cache"], a_, p_, dred["product_weight"])
                 raw_ = relation_linear(hid, dred["second_weight"], dred["second_bias"],
                                        out_dtype=torch.float32)
                 return relation_norm_reduce(raw_, ps_, dred["norm_weight"], dred["norm_bias"],
@@ -278,7 +294,8 @@ def main() -> int:
         return 0
 
     if args.decode_only:
-        print(json.dumps({"decode_step_us": run_decode()}), flush=True)
+        print(json.dumps({"decode_step_us": run_decode(),
+                          "ring_decode_step_us": run_decode(RING_POSITION)}), flush=True)
         return 0
 
     cfg = CONFIGS["cfg2"]
@@ -420,6 +437,7 @@ def main() -> int:
     fused_bytes = sum(nbytes[k] for k in headline)
 
     decode = run_decode()
+    ring_decode = run_decode(RING_POSITION)
     multi = run_multi()
 
     cpu = None
@@ -458,6 +476,7 @@ def main() -> int:
                 trio_bytes / (trio_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         },
         "decode_step_us": decode,
+        "ring_decode_step_us": {"position": RING_POSITION, "cache_rows": 512, **ring_decode},
         "multi_anchor_select": multi,
         "cpu_baseline": cpu,
     }
