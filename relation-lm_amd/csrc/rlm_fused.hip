@@ -170,16 +170,18 @@ __device__ __forceinline__ void dma_wm_chunk(rsrc_t wmr, uint32_t tile, int chun
 
 // Gathered expanded-cache halves of one chunk: LDS row m holds the anchor
 // half's columns [chunk*128, +128) then the partner half's, 16 pieces of 16 B
-// each, piece q stored at q ^ (m % 16).  Lane `lane` of DMA instruction i of
-// wave w writes piece lane % 32 of row 2*(kWaves*i + w) + lane / 32; src[i] is
-// that piece's byte offset for chunk 0 (kNoOffset for a missing row: zeros).
+// each, piece q stored at q ^ (m % 16).  Each wave gathers its own 16 rows
+// (the rows its phase 1 reads): lane `lane` of DMA instruction i of wave w
+// writes piece lane % 32 of row 16w + 2i + lane / 32; src[i] is that piece's
+// byte offset for chunk 0 (kNoOffset for a missing row: zeros).
 constexpr int kGatherInsts = kRows * kGatherRowBytes / 16 / kThreads;
+static_assert(kGatherInsts * 2 * kWaves == kRows, "each wave gathers its own rows");
 __device__ __forceinline__ void dma_gather_chunk(rsrc_t xr, uint32_t tile,
                                                  const uint32_t (&src)[kGatherInsts], int chunk,
                                                  int wave) {
 #pragma unroll
   for (int i = 0; i < kGatherInsts; ++i)
-    lds_dma16(xr, __builtin_amdgcn_readfirstlane(tile + (i * kWaves + wave) * kWave * 16),
+    lds_dma16(xr, __builtin_amdgcn_readfirstlane(tile + (wave * kGatherInsts + i) * kWave * 16),
               src[i] == kNoOffset ? kNoOffset : src[i] + chunk * kHC * 2u);
 }
 
@@ -209,11 +211,27 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
   const rsrc_t wmr = make_rsrc(p.wm, p.wm_bytes);
   const rsrc_t w2r = make_rsrc(p.w2, p.w2_bytes);
 
-  // ---- Set-up.
+  // ---- Set-up: two dependent round trips.  (1) this lane's row indices
+  // (beside the W_m DMA of chunk 0); (2) the wave's gather DMA of chunk 0, the
+  // operand rows, the row-weight inputs and b2 / gamma / beta, all in flight
+  // together.
   dma_wm_chunk<KS1>(wmr, lds0, 0, wave, lane);
   // This lane's phase-1 row: 16*wave + r16.
   const int lrow = 16 * wave + r16;
   u16x8 ph[KS1], pl[KS1];
+  // Gather DMA sources of this lane (piece lane%32 of row 16*wave + 2i + lane/32), chunk 0.
+  auto gather_src = [&](int i) {
+    const int m = 16 * wave + 2 * i + lane / 32;
+    const int q = lane & 31;
+    const uint32_t base = rowoff[2 * m + q / 16];
+    return base == kNoOffset ? kNoOffset : base + 16u * ((q & 15) ^ (m & 15));
+  };
+  auto gather_chunk = [&](int chunk) {
+    uint32_t src[kGatherInsts];
+#pragma unroll
+    for (int i = 0; i < kGatherInsts; ++i) src[i] = gather_src(i);
+    dma_gather_chunk(xr, lds0 + kOffGather, src, chunk, wave);
+  };
   {
     const uint32_t grow = row0 + lrow;
     int32_t a = -1, pp = -1;
@@ -230,6 +248,8 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
       rowoff[2 * lrow] = a >= 0 ? (base + a) * (4u * H) : kNoOffset;               // anchor, first half
       rowoff[2 * lrow + 1] = pp >= 0 ? (base + pp) * (4u * H) + 2u * H : kNoOffset;  // partner, second half
     }
+    wave_sync();  // the wave's row offsets are in LDS (it reads only its own rows)
+    gather_chunk(0);
     const bool ok = a >= 0 && pp >= 0;
     const uint32_t oa = ok ? (base + a) * (2u * R) + 16u * g : kNoOffset;
     const uint32_t op = ok ? (base + pp) * (2u * R) + 16u * g : kNoOffset;
@@ -238,6 +258,12 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
     for (int s = 0; s < KS1; ++s) {
       va[s] = buf_load_b128(opr, ok ? oa + 64u * s : kNoOffset);
       vp[s] = buf_load_b128(opr, ok ? op + 64u * s : kNoOffset);
+    }
+    if (tid < kRows) wts[tid] = row0 + tid < p.rows ? row_weight(p, row0 + tid) : 0.0f;
+    for (int i = tid; i < static_cast<int>(p.D); i += kThreads) {
+      cst[i] = load_any_f(p.b2, p.b2_dtype, i);
+      cst[kMaxD + i] = load_any_f(p.gamma, p.gamma_dtype, i);
+      cst[2 * kMaxD + i] = load_any_f(p.beta, p.beta_dtype, i);
     }
 #pragma unroll
     for (int s = 0; s < KS1; ++s) {
@@ -255,12 +281,6 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
       pl[s] = as_frag(make_uint4(l[0], l[1], l[2], l[3]));
     }
   }
-  if (tid < kRows) wts[tid] = row0 + tid < p.rows ? row_weight(p, row0 + tid) : 0.0f;
-  for (int i = tid; i < static_cast<int>(p.D); i += kThreads) {
-    cst[i] = load_any_f(p.b2, p.b2_dtype, i);
-    cst[kMaxD + i] = load_any_f(p.gamma, p.gamma_dtype, i);
-    cst[2 * kMaxD + i] = load_any_f(p.beta, p.beta_dtype, i);
-  }
 
   // W2 fragments (B operand of phase 2) in groups of JC column tiles: rows
   // dcol0 + 16(JC*jg + j) + r16, k = chunk*128 + 32s + 8g.
@@ -274,20 +294,6 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
       w[j] = as_frag(buf_load_b128(
           w2r, w2_lane + (16u * (JC * jg + j) * H + chunk * kHC + 32 * s) * 2u));
   };
-  // Gather DMA sources of this lane (piece lane%32 of row 2*(8i + wave) + lane/32), chunk 0.
-  auto gather_src = [&](int i) {
-    const int m = 2 * (i * kWaves + wave) + lane / 32;
-    const int q = lane & 31;
-    const uint32_t base = rowoff[2 * m + q / 16];
-    return base == kNoOffset ? kNoOffset : base + 16u * ((q & 15) ^ (m & 15));
-  };
-  auto gather_chunk = [&](int chunk) {
-    uint32_t src[kGatherInsts];
-#pragma unroll
-    for (int i = 0; i < kGatherInsts; ++i) src[i] = gather_src(i);
-    dma_gather_chunk(xr, lds0 + kOffGather, src, chunk, wave);
-  };
-
 
   f32x4 raw[kRowTiles][DT];
 #pragma unroll
@@ -304,8 +310,6 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
   unsigned char* my_hid = hid + lrow * (2 * kLd) + 8 * g;
 
   const int nchunks = H / kHC;
-  __syncthreads();  // row offsets visible
-  gather_chunk(0);
   __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this lane's W_m and gather pieces of chunk 0 are in LDS
   __syncthreads();
 
