@@ -205,17 +205,16 @@ def main() -> int:
 
             def decode_step(dsel=dsel, dred=dred, dexp=dexp, memory=memory, projection=projection,
                             dargs=dargs, t=t, position=position, batch=batch, rc=rc, dcfg=dcfg):
-                parts = projection.project(memory)
-                router_op(parts[4], parts[5], rc["anchor_raw_cache"],
-                                    rc["partner_raw_cache"], rc["anchor_conv_cache"],
-                                    rc["partner_conv_cache"], dsel["anchor_block_mean"],
-                                    dsel["anchor_block_std"], dsel["partner_block_mean"],
-                                    dsel["partner_block_std"], rc["anchor_conv_weight"],
-                                    rc["partner_conv_weight"], position, dcfg.block_size)
-                dsel["anchor_keys"][:, t] = parts[0]
-                dsel["partner_keys"][:, t] = parts[1]
-                dred["operand_cache"][:, t] = parts[2]
-                dsel["partner_anchor_cache"][:, t] = parts[3]
+                # projection + the token's key / operand / partner-anchor cache rows
+                parts = projection.project_into(memory, dsel["anchor_keys"], dsel["partner_keys"],
+                                                dred["operand_cache"],
+                                                dsel["partner_anchor_cache"], position, ring=ring)
+                router_op(parts[4], parts[5], rc["anchor_raw_cache"], rc["partner_raw_cache"],
+                          rc["anchor_conv_cache"], rc["partner_conv_cache"],
+                          dsel["anchor_block_mean"], dsel["anchor_block_std"],
+                          dsel["partner_block_mean"], dsel["partner_block_std"],
+                          rc["anchor_conv_weight"], rc["partner_conv_weight"], position,
+                          dcfg.block_size)
                 a_, s_, p_, ps_ = select_op(*dargs)
                 if batch == 1:
                     hid = update_op(

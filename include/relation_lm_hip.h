@@ -358,6 +358,24 @@ hipError_t rlm_packed_sparse_cache_projection(
     hipStream_t stream);
 
 /*
+ * rlm_packed_sparse_cache_projection plus the decode-time cache writes, in one
+ * kernel: no reference counterpart (the reference projects with F.linear and
+ * leaves the cache writes to the caller, packed_cache.py:52-57).  Output
+ * columns of the first four segments (anchor_key, partner_key, operand,
+ * partner_anchor: SPARSE_CACHE_NAMES order, widths taken from the caches) are
+ * also written to row `position` of anchor_keys [B,T,E], partner_keys [B,T,E],
+ * operand_cache [B,T,R] and partner_anchor_cache [B,T,2E] (row position mod T
+ * when `ring` is set; T a power of two).  B <= 64, 16-bit weights; caches in
+ * the output dtype.  `out` [B,Dout] receives every column (the router segments
+ * feed rlm_router_cache_update).
+ */
+hipError_t rlm_packed_projection_to_caches(
+    const rlm_tensor* memory, const rlm_tensor* weight, const rlm_tensor* out,
+    const rlm_tensor* anchor_keys, const rlm_tensor* partner_keys,
+    const rlm_tensor* operand_cache, const rlm_tensor* partner_anchor_cache,
+    const rlm_tensor* position, int32_t ring, hipStream_t stream);
+
+/*
  * out = input @ weight^T (+ bias), the library GEMM behind the expanded-cache
  * projection (tests/test_relation_reduce_gpu.py:64-68 in the reference) and
  * the relation MLP's second linear (benchmarks/benchmark_relation_reduce.py:63).

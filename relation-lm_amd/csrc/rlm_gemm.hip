@@ -43,6 +43,8 @@ constexpr int kBK = 32;   // k-slice of the 16-bit path
 constexpr int kPad = 8;   // 16-bit elements of padding per LDS row (conflict-free b128 reads)
 constexpr int kSkinnyM = 64;
 
+constexpr int kMaxSegments = 4;
+
 struct GemmParams {
   int64_t M, N, K;
   int64_t lda;  // input row stride in elements (>= K)
@@ -51,6 +53,16 @@ struct GemmParams {
   const void* bias;
   int bias_dtype;
   void* out;
+  // Optional cache-row scatter (decode projection, skinny kernel only): output
+  // columns [seg_lo[s], seg_hi[s]) of row m also go to row `position` of cache
+  // s ([M, seg_rows[s], seg_hi[s] - seg_lo[s]], the output dtype); ring caches
+  // take row position mod seg_rows[s] (a power of two).
+  int nseg;
+  int64_t seg_lo[kMaxSegments], seg_hi[kMaxSegments], seg_rows[kMaxSegments];
+  void* seg_dst[kMaxSegments];
+  const void* pos;
+  int pos_dtype;
+  int ring;
 };
 
 // 16-bit bit pattern of v in the MFMA input type W (bf16 or f16).
@@ -120,6 +132,31 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const f32x4& acc
   for (int e = 0; e < 4; ++e) {
     const int64_t m = m0 + e;
     if (m < p.M) out[m * p.N + n] = from_f32<TO>(acc[e] + bv);
+  }
+}
+
+// The cache-row scatter of one 16x16 accumulator (see GemmParams): column n's
+// four rows also go to their caches' row `position`.  A position outside the
+// cache (linear caches: t >= rows; any: t < 0) writes nothing.
+template <typename TO>
+__device__ __forceinline__ void scatter_tile(const GemmParams& p, const f32x4& acc,
+                                             int64_t m_base, int64_t n, float bv, int lane) {
+  if (p.nseg == 0 || n >= p.N) return;
+  const int64_t t = load_any_i(p.pos, p.pos_dtype, 0);
+  const int64_t m0 = m_base + (lane >> 4) * 4;
+#pragma unroll
+  for (int s = 0; s < kMaxSegments; ++s) {
+    if (s >= p.nseg || n < p.seg_lo[s] || n >= p.seg_hi[s]) continue;
+    const int64_t rows = p.seg_rows[s];
+    if (t < 0 || (!p.ring && t >= rows)) continue;
+    const int64_t row = p.ring ? (t & (rows - 1)) : t;
+    const int64_t width = p.seg_hi[s] - p.seg_lo[s];
+    TO* dst = static_cast<TO*>(p.seg_dst[s]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t m = m0 + e;
+      if (m < p.M) dst[(m * rows + row) * width + (n - p.seg_lo[s])] = from_f32<TO>(acc[e] + bv);
+    }
   }
 }
 
@@ -356,6 +393,7 @@ __global__ void __launch_bounds__(kSkinnyWaves * kWave) skinny_kernel(const Gemm
   const int64_t n = n0 + r16;
   const float bv = (p.bias && n < p.N) ? load_any_f(p.bias, p.bias_dtype, n) : 0.0f;
   store_tile<TO>(p, sum, m0, n, bv, lane);
+  scatter_tile<TO>(p, sum, m0, n, bv, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -462,7 +500,8 @@ hipError_t launch_out(const GemmParams& p, int out_dtype, hipStream_t s) {
 }
 
 hipError_t linear_impl(const rlm_tensor* input, const rlm_tensor* weight, const rlm_tensor* bias,
-                       const rlm_tensor* out, hipStream_t stream, const char* what) {
+                       const rlm_tensor* out, hipStream_t stream, const char* what,
+                       const GemmParams* scatter = nullptr) {
   RLM_TRY(check_rows(input, "input"));
   RLM_TRY(check_tensor(weight, "weight", 2));
   RLM_TRY(check_tensor(out, "out", 2));
@@ -488,6 +527,21 @@ hipError_t linear_impl(const rlm_tensor* input, const rlm_tensor* weight, const 
   p.bias = bias ? bias->data : nullptr;
   p.bias_dtype = bias ? bias->dtype : RLM_F32;
   p.out = out->data;
+  if (scatter != nullptr) {
+    RLM_REQUIRE(M <= kSkinnyM && weight->dtype != RLM_F32,
+                "%s: the cache-row scatter takes at most %d rows and 16-bit weights", what,
+                kSkinnyM);
+    p.nseg = scatter->nseg;
+    for (int s = 0; s < kMaxSegments; ++s) {
+      p.seg_lo[s] = scatter->seg_lo[s];
+      p.seg_hi[s] = scatter->seg_hi[s];
+      p.seg_rows[s] = scatter->seg_rows[s];
+      p.seg_dst[s] = scatter->seg_dst[s];
+    }
+    p.pos = scatter->pos;
+    p.pos_dtype = scatter->pos_dtype;
+    p.ring = scatter->ring;
+  }
   if (M == 0 || N == 0) return hipSuccess;
   RLM_REQUIRE(((M + 63) / 64) * ((N + 63) / 64) <= 0x7fffffff, "%s: problem too large", what);
   if (weight->dtype == RLM_F32) {
@@ -538,4 +592,50 @@ extern "C" hipError_t rlm_packed_sparse_cache_projection(const rlm_tensor* memor
   RLM_REQUIRE(memory != nullptr && out != nullptr && memory->dtype == out->dtype,
               "packed_sparse_cache_projection: output dtype must equal the memory dtype");
   return linear_impl(memory, weight, nullptr, out, stream, "packed_sparse_cache_projection");
+}
+
+extern "C" hipError_t rlm_packed_projection_to_caches(
+    const rlm_tensor* memory, const rlm_tensor* weight, const rlm_tensor* out,
+    const rlm_tensor* anchor_keys, const rlm_tensor* partner_keys,
+    const rlm_tensor* operand_cache, const rlm_tensor* partner_anchor_cache,
+    const rlm_tensor* position, int32_t ring, hipStream_t stream) {
+  clear_error();
+  const char* what = "packed_projection_to_caches";
+  RLM_REQUIRE(memory != nullptr && out != nullptr && memory->dtype == out->dtype,
+              "%s: output dtype must equal the memory dtype", what);
+  RLM_TRY(check_tensor(out, "out", 2));
+  const int64_t M = out->shape[0], N = out->shape[1];
+  const rlm_tensor* caches[kMaxSegments] = {anchor_keys, partner_keys, operand_cache,
+                                            partner_anchor_cache};
+  const char* names[kMaxSegments] = {"anchor_keys", "partner_keys", "operand_cache",
+                                     "partner_anchor_cache"};
+  GemmParams sc{};
+  sc.nseg = kMaxSegments;
+  int64_t lo = 0;
+  for (int s = 0; s < kMaxSegments; ++s) {
+    RLM_TRY(check_tensor(caches[s], names[s], 3));
+    RLM_TRY(check_dtype_is(caches[s], names[s], out->dtype));
+    RLM_TRY(check_dim(caches[s], names[s], 0, M));
+    const int64_t rows = caches[s]->shape[1], width = caches[s]->shape[2];
+    RLM_REQUIRE(rows >= 1, "%s: empty cache", names[s]);
+    if (ring)
+      RLM_REQUIRE((rows & (rows - 1)) == 0,
+                  "%s: ring-buffer caches need a power-of-two length, got %lld", names[s],
+                  (long long)rows);
+    sc.seg_lo[s] = lo;
+    sc.seg_hi[s] = lo + width;
+    sc.seg_rows[s] = rows;
+    sc.seg_dst[s] = caches[s]->data;
+    lo += width;
+  }
+  RLM_REQUIRE(lo <= N,
+              "%s: the four cache widths (%lld in total) exceed the projection width %lld", what,
+              (long long)lo, (long long)N);
+  RLM_REQUIRE(position != nullptr && position->ndim == 0 && is_index_dtype(position->dtype) &&
+                  position->data != nullptr,
+              "position: expected a 0-d int32/int64 device tensor");
+  sc.pos = position->data;
+  sc.pos_dtype = position->dtype;
+  sc.ring = ring ? 1 : 0;
+  return linear_impl(memory, weight, nullptr, out, stream, what, &sc);
 }

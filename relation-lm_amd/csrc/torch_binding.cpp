@@ -538,6 +538,29 @@ at::Tensor router_cache_update_ring(RLM_ROUTER_ARGS) { return router_common(true
 #undef RLM_ROUTER_ARGS
 #undef RLM_ROUTER_PASS
 
+// Packed projection plus the token's cache-row writes (no reference op).
+at::Tensor packed_projection_to_caches(const at::Tensor& memory, const at::Tensor& weight,
+                                       at::Tensor& anchor_keys, at::Tensor& partner_keys,
+                                       at::Tensor& operand_cache, at::Tensor& partner_anchor_cache,
+                                       const at::Tensor& position, bool ring) {
+  const char* op = "relation_lm::packed_projection_to_caches";
+  c10::DeviceGuard guard(memory.device());
+  hipStream_t stream = device_stream(op, {&memory, &weight, &anchor_keys, &partner_keys,
+                                          &operand_cache, &partner_anchor_cache, &position});
+  TORCH_CHECK(memory.dim() == 2, op, ": memory must be [B, Din]");
+  TORCH_CHECK(weight.dim() == 2, op, ": weight must be [Dout, Din]");
+  at::Tensor out = at::empty({memory.size(0), weight.size(0)}, memory.options());
+  rlm_tensor d[8] = {desc(memory, "memory"),       desc(weight, "weight"),
+                     desc(out, "out"),             desc(anchor_keys, "anchor_keys"),
+                     desc(partner_keys, "partner_keys"), desc(operand_cache, "operand_cache"),
+                     desc(partner_anchor_cache, "partner_anchor_cache"),
+                     desc(position, "position")};
+  check(rlm_packed_projection_to_caches(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7],
+                                        ring ? 1 : 0, stream),
+        op);
+  return out;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(relation_lm, m) {
@@ -612,6 +635,10 @@ TORCH_LIBRARY(relation_lm, m) {
       "partner_conv_weight, Tensor position, int block_size) -> Tensor");
   m.def("packed_sparse_cache_projection(Tensor memory, Tensor weight) -> Tensor");
   m.def(
+      "packed_projection_to_caches(Tensor memory, Tensor weight, Tensor(a!) anchor_keys, "
+      "Tensor(b!) partner_keys, Tensor(c!) operand_cache, Tensor(d!) partner_anchor_cache, "
+      "Tensor position, bool ring=False) -> Tensor");
+  m.def(
       "relation_linear(Tensor input, Tensor weight, Tensor? bias=None, ScalarType? "
       "out_dtype=None) -> Tensor");
 }
@@ -644,6 +671,7 @@ TORCH_LIBRARY_IMPL(relation_lm, CUDA, m) {
   m.impl("relation_hidden_cache_update_ring", TORCH_FN(relation_hidden_cache_update_ring));
   m.impl("router_cache_update_ring", TORCH_FN(router_cache_update_ring));
   m.impl("packed_sparse_cache_projection", TORCH_FN(packed_sparse_cache_projection));
+  m.impl("packed_projection_to_caches", TORCH_FN(packed_projection_to_caches));
   m.impl("relation_linear", TORCH_FN(relation_linear));
 }
 

@@ -98,6 +98,10 @@ def _register_fakes() -> None:
         return operand_cache.new_empty(tuple(partner_index.shape[:2]) + (second_weight.shape[0],),
                                        dtype=torch.float32)
 
+    @torch.library.register_fake("relation_lm::packed_projection_to_caches")
+    def _(memory, weight, *rest):
+        return memory.new_empty((memory.shape[0], weight.shape[0]))
+
     @torch.library.register_fake("relation_lm::packed_sparse_cache_projection")
     def _(memory, weight):
         return memory.new_empty(tuple(memory.shape[:-1]) + (weight.shape[0],))

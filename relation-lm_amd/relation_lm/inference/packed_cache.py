@@ -60,6 +60,27 @@ class PackedSparseCacheProjection:
         packed = torch.ops.relation_lm.packed_sparse_cache_projection(memory, self.weight)
         return packed.split(self.split_sizes, dim=-1)
 
+    def project_into(self, memory: Tensor, anchor_keys: Tensor, partner_keys: Tensor,
+                     operand_cache: Tensor, partner_anchor_cache: Tensor, position: Tensor,
+                     *, ring: bool = False) -> tuple[Tensor, ...]:
+        """``project`` plus the decode-time cache writes in one kernel (no reference
+        counterpart).
+
+        The first four segments (anchor_key, partner_key, operand, partner_anchor)
+        are also written to row ``position`` of the four caches ``[B, T, width]``
+        (row ``position % T`` when ``ring``; T a power of two), as
+        ``cache[:, position] = segment`` would.  ``memory`` is ``[B, input_width]``
+        with B <= 64.  Returns the same views as ``project``.
+        """
+        if memory.size(-1) != self.input_width:
+            raise ValueError("memory width does not match packed projection input")
+        caches = (anchor_keys, partner_keys, operand_cache, partner_anchor_cache)
+        if tuple(int(c.size(-1)) for c in caches) != tuple(self.split_sizes[:4]):
+            raise ValueError("cache widths must equal the first four split sizes")
+        packed = torch.ops.relation_lm.packed_projection_to_caches(
+            memory, self.weight, *caches, position, ring)
+        return packed.split(self.split_sizes, dim=-1)
+
     def project_dict(self, memory: Tensor) -> dict[str, Tensor]:
         """Project ``memory`` and return a name-to-tensor mapping."""
         return dict(zip(self.names, self.project(memory), strict=True))

@@ -315,6 +315,46 @@ def test_packed_projection_matches_separate_linears(device, dtype, batch):
     assert tuple(projection.project_dict(memory)) == projection.names
 
 
+@pytest.mark.parametrize("batch", [1, 8])
+@pytest.mark.parametrize("position,ring", [(0, False), (300, False), (511, False), (512, False),
+                                           (-1, False), (300, True), (1000, True), (4095, True)])
+def test_projection_to_caches(device, batch, position, ring):
+    """project_into == project + cache[:, row] = segment (row = position, or position % T)."""
+    cfg = CONFIGS["cfg3"]
+    memory, weights = packed_projection_inputs(cfg, device=device)
+    memory = memory[:batch].contiguous()
+    projection = pack_sparse_cache_projection_weights(weights)
+    g = torch.Generator().manual_seed(31 + position)
+    caches = [torch.randn(batch, 512, w, generator=g).to(torch.bfloat16).to(device)
+              for w in (64, 64, 128, 128)]
+    expected = [c.clone() for c in caches]
+    pos = torch.tensor(position, device=device)
+    got = projection.project_into(memory, *caches, pos, ring=ring)
+    ref = projection.project(memory)
+    torch.cuda.synchronize()
+    row = position % 512 if ring else position
+    if 0 <= position and (ring or position < 512):
+        for c, seg in zip(expected, ref[:4]):
+            c[:, row] = seg
+    for gp, rp in zip(got, ref):
+        assert torch.equal(gp, rp)
+    for c, e in zip(caches, expected):
+        assert torch.equal(c, e)
+
+
+def test_projection_to_caches_rejects_mismatched_widths(device):
+    cfg = CONFIGS["cfg3"]
+    memory, weights = packed_projection_inputs(cfg, device=device)
+    projection = pack_sparse_cache_projection_weights(weights)
+    caches = [torch.zeros(cfg.batch, 512, w, dtype=torch.bfloat16, device=device)
+              for w in (64, 64, 128, 64)]
+    with pytest.raises(ValueError, match="cache widths"):
+        projection.project_into(memory, *caches, torch.tensor(3, device=device))
+    caches[3] = torch.zeros(cfg.batch, 500, 128, dtype=torch.bfloat16, device=device)
+    with pytest.raises(RuntimeError, match="power-of-two"):
+        projection.project_into(memory, *caches, torch.tensor(3, device=device), ring=True)
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 512, 576), (8, 4608, 128), (100, 72, 40), (4096, 1024, 128),
                                    (8, 576, 2304), (64, 576, 2304), (65, 200, 96), (8, 24, 40),
                                    (33, 130, 72), (1000, 300, 520), (129, 40, 32), (300, 136, 64)])
