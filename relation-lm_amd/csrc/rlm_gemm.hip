@@ -345,7 +345,7 @@ __global__ void __launch_bounds__(256) smallk_kernel(const GemmParams p) {
 // ---------------------------------------------------------------------------
 
 constexpr int kSkinnyWaves = 8;
-constexpr int kSkinnyBatch = 6;  // k-slices whose loads a wave issues together
+constexpr int kSkinnyBatch = 9;  // k-slices whose loads a wave issues together (K = 2304: one round trip)
 
 // One 16x16 output tile per workgroup (grid: N/16 x M/16).  The 8 waves split
 // K into 32-wide slices (wave w takes slices w, w+8, ...); each wave issues

@@ -456,12 +456,15 @@ struct NormParams {
 // position t: k_limit = clamp(ceil(log2(t + 2)), 1, K) == clamp(bit_length(t + 1), 1, K),
 // active = rank < k_limit and score > -1e30, p = softmax(where(active, s, -1e4)) * active,
 // renormalised by max(sum, 1e-9) (relation_reduce.py:399-411).
-__device__ __forceinline__ float partner_weight(const NormParams& p, int64_t q, int64_t t,
+__device__ __forceinline__ float partner_score(const NormParams& p, int64_t q, int lane) {
+  return lane < p.K ? p.scores[q * p.K + lane] : -INFINITY;
+}
+// s: this lane's partner score (partner_score), loaded by the caller.
+__device__ __forceinline__ float partner_weight(const NormParams& p, float s, int64_t t,
                                                 int lane) {
   const int64_t n = t + 1;
   int k_limit = n > 0 ? 64 - __clzll(static_cast<unsigned long long>(n)) : 0;
   k_limit = k_limit < 1 ? 1 : (k_limit > p.K ? p.K : k_limit);
-  const float s = lane < p.K ? p.scores[q * p.K + lane] : -INFINITY;
   const bool active = lane < p.K && lane < k_limit && s > -1.0e30f;
   const float safe = active ? s : -1.0e4f;
   const float m = wave_max_f32(lane < p.K ? safe : -INFINITY);
@@ -493,8 +496,10 @@ __global__ void __launch_bounds__(256) norm_reduce_vec_kernel(const NormParams p
   if (q >= p.Q) return;
   const int64_t b = q / p.Tq;
   const int64_t tq = q - b * p.Tq;
+  // Every load of the query is issued before any is used: position, scores,
+  // gamma / beta, and the first KB partner rows (one memory round trip).
   const int64_t t = load_any_i(p.pos, p.pos_dtype, b * p.pos_sb + tq * p.pos_sq);
-  const float prob = partner_weight(p, q, t, lane);
+  const float score = partner_score(p, q, lane);
   const int groups = p.D >> 2;
   const TR* raw = static_cast<const TR*>(p.raw) + q * p.K * static_cast<int64_t>(p.D);
 
@@ -516,6 +521,7 @@ __global__ void __launch_bounds__(256) norm_reduce_vec_kernel(const NormParams p
     ctx[i] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   const float inv_d = 1.0f / static_cast<float>(p.D);
+  float prob = 0.0f;
   for (int k0 = 0; k0 < p.K; k0 += KB) {
     float4 x[KB][G];
 #pragma unroll
@@ -527,6 +533,7 @@ __global__ void __launch_bounds__(256) norm_reduce_vec_kernel(const NormParams p
                        ? load_raw4(raw + static_cast<int64_t>(k0 + kk) * p.D + 4 * g)
                        : make_float4(0.f, 0.f, 0.f, 0.f);
       }
+    if (k0 == 0) prob = partner_weight(p, score, t, lane);
 #pragma unroll
     for (int kk = 0; kk < KB; ++kk) {
       if (k0 + kk >= p.K) break;
@@ -573,7 +580,7 @@ __global__ void __launch_bounds__(256) norm_reduce_kernel(const NormParams p) {
   const int64_t b = q / p.Tq;
   const int64_t tq = q - b * p.Tq;
   const int64_t t = load_any_i(p.pos, p.pos_dtype, b * p.pos_sb + tq * p.pos_sq);
-  const float prob = partner_weight(p, q, t, lane);
+  const float prob = partner_weight(p, partner_score(p, q, lane), t, lane);
 
   float gam[VPL], bet[VPL], ctx[VPL];
 #pragma unroll
