@@ -9,27 +9,32 @@
 //
 // Mapping: a workgroup of 8 waves (2 per SIMD) owns 128 consecutive
 // (query, partner) rows, so it holds whole queries (K in {1, 2, 4, 8, 16}).
+// Inside the workgroup the rows are kept in "slot" order (slot_row below),
+// chosen so that phase 2 leaves each query's partners in as few lanes as
+// possible.
 //   set-up   wave w keeps the exact hi/lo bf16 split of the operand products
-//            (op[anchor] * op[partner], exact in fp32) of rows 16w..16w+15 in
+//            (op[anchor] * op[partner], exact in fp32) of slots 16w..16w+15 in
 //            registers; the rows' active-K softmax weights and the b2 / gamma /
-//            beta vectors go to LDS.
+//            beta vectors go to LDS.  All loads that do not depend on the row
+//            indices are issued in one round, branch-free.
 //   phase 1  per 128-column chunk of the hidden dimension, wave w forms
-//            hidden^T[128 cols x its 16 rows] = W_m[chunk] . P^T on the matrix
-//            cores, adds the rows' expanded-cache halves, applies GELU and
-//            rounds to bf16 -- the operand the unfused path's bf16 second linear
-//            sees -- into the LDS hidden chunk.  The W_m chunk and the gathered
-//            expanded-cache halves of the 128 rows reach LDS by LDS-DMA
-//            (buffer_load ... lds), issued while the previous chunk's phase 2
-//            runs.  The transposed product leaves 4 consecutive hidden columns
-//            of one row in a lane, so the LDS writes are ds_write_b64.
-//   phase 2  raw[128 rows x D/8 cols of wave w] += hidden chunk . W2^T; the
-//            hidden fragments come from LDS, W2 fragments from L2 one k-step
-//            ahead, and the raw accumulators stay in registers for the whole
-//            kernel.  Two waves per SIMD let one wave's GELU work overlap the
-//            other's matrix-core work.
-// Epilogue: + b2, LayerNorm per row (moments combined across the 8 waves in
-// LDS), partner weights, sum over the query's rows (in-lane, then the
-// neighbouring 16-lane groups), fp32 buffer stores.
+//            hidden^T[128 cols x its 16 slots] = W_m[chunk] . P^T on the matrix
+//            cores (16x16x32), adds the rows' expanded-cache halves (one more
+//            MFMA against a constant [I|I]), applies GELU and rounds to bf16 --
+//            the operand the unfused path's bf16 second linear sees -- into the
+//            LDS hidden chunk.  The W_m chunk and the gathered expanded-cache
+//            halves reach LDS by LDS-DMA (buffer_load ... lds), issued while
+//            the previous chunk's phase 2 runs.
+//   phase 2  raw^T[D cols x 128 slots] += W2[:, chunk] . hidden chunk^T on
+//            32x32x16 MFMAs: wave (dg, rg) owns DTW 32-column tiles of D and
+//            RTW 32-slot tiles; W2 fragments come from L2 three k-steps ahead,
+//            hidden fragments from LDS one fragment ahead, and the raw
+//            accumulators stay in registers for the whole kernel.  The
+//            transposed product leaves one slot's columns in a lane.
+// Epilogue: + b2; LayerNorm moments per slot (in-lane sums, the two wave
+// halves, then the D-direction waves merged in LDS); partner weights and the
+// sum over a query's partners (in-lane over row tiles, then DPP / permlane
+// across the lanes of the query); 16-byte buffer stores.
 #include "rlm_common.hpp"
 
 namespace rlm {
@@ -37,12 +42,12 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kRows = 128;                 // (query, partner) rows per workgroup
-constexpr int kRowTiles = kRows / 16;
 constexpr int kHC = 128;                   // hidden columns per chunk
 constexpr int kMaxR = 128;
 constexpr int kMaxD = 512;
@@ -58,6 +63,10 @@ constexpr int kOffF32 = kOffHid + kRows * kLd * 2;
 constexpr int kF32Words = kRows + 2 * kRows + 2 * kWaves * kRows + 3 * kMaxD;
 constexpr int kOffRowOff = kOffF32 + kF32Words * 4;
 constexpr size_t kLdsBytes = static_cast<size_t>(kOffRowOff) + kRows * 2 * 4;
+#ifndef RLM_W2_AHEAD
+#define RLM_W2_AHEAD 3
+#endif
+constexpr int kW2Ahead = RLM_W2_AHEAD;      // phase-2 W2 prefetch distance (k-steps)
 constexpr int kWaitVm0 = 0x0F70;           // s_waitcnt vmcnt(0), other counters untouched
 
 struct FusedParams {
@@ -81,6 +90,7 @@ struct FusedParams {
   const void* pos;
   int pos_dtype;
   int64_t pos_sb, pos_sq;
+  uint32_t pos_count;    // elements of the positions tensor
   float eps;
   float* out;             // [B*Tq, D]
   uint32_t expanded_bytes, operand_bytes, wm_bytes, w2_bytes;
@@ -89,6 +99,47 @@ struct FusedParams {
 __device__ __forceinline__ f32x4 mfma_bf16(const u16x8& a, const u16x8& b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+// D[32x32] += A[32x16] B[16x32]: lane l holds A row l%32, k = 8(l/32)..+7, and
+// B column l%32, same k; D element 4i+j is row 8i + 4(l/32) + j, column l%32.
+__device__ __forceinline__ f32x16 mfma32_bf16(const u16x8& a, const u16x8& b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// Sum of lanes l and l +- N within each 16-lane row (DPP row_ror).
+template <int N>
+__device__ __forceinline__ float ror_sum(float v) {
+  return v + __uint_as_float(dpp_u32<0x120 + N>(__float_as_uint(v)));
+}
+
+__device__ __forceinline__ void buf_store_f32x4(float4 v, rsrc_t r, uint32_t off) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, 0);
+}
+
+// Phase 2 and the epilogue see the workgroup's 128 (query, partner) rows in
+// "slot" order: slot s = 32*rt + n is column n of 32-row tile rt, and a wave of
+// row group rg covers tiles RTW*rg .. RTW*rg + RTW-1.  The map keeps each
+// query inside one row group and puts its partners in as few lanes as
+// possible: K <= RTW -> one lane holds RTW/K whole queries (tile rt' of the
+// group = K*(query/32) + partner); K > RTW -> a query's partners sit in lanes
+// n = q, q + QG, q + 2QG, ... (QG = 32*RTW/K queries per group), RTW each.
+// Returns the local row (query*K + partner) of slot s.
+template <int RTW>
+__device__ __forceinline__ uint32_t slot_row(int s, uint32_t K, uint32_t k_log2) {
+  const int rt = s >> 5, n = s & 31;
+  const int rgs = rt / RTW, rtp = rt % RTW;
+  const int qg = (32 * RTW) >> k_log2;
+  int q_in, k;
+  if (static_cast<int>(K) <= RTW) {
+    q_in = 32 * (rtp >> k_log2) + n;
+    k = rtp & static_cast<int>(K - 1);
+  } else {
+    k = rtp + RTW * (n / qg);
+    q_in = n % qg;
+  }
+  return static_cast<uint32_t>((rgs * qg + q_in) * static_cast<int>(K) + k);
 }
 
 __device__ __forceinline__ u16x8 lds_frag(const unsigned char* p) {
@@ -112,22 +163,14 @@ __device__ __forceinline__ void lds_dma16(rsrc_t r, uint32_t lds_addr, uint32_t 
                : "memory");
 }
 
-// Weight p_k of row `grow` (< rows) in its query's partner mixture: softmax
-// over the active partners (rank < k_limit, score > -1e30; inactive scores
-// -1e4), renormalised by max(sum, 1e-9) -- relation_reduce.py:399-411.
-__device__ float row_weight(const FusedParams& p, uint32_t grow) {
-  const uint32_t K = p.K;
-  const uint32_t q = grow >> p.k_log2;
-  const uint32_t k = grow & (K - 1);
-  const uint32_t b = q / p.Tq;
-  const int64_t t = load_any_i(p.pos, p.pos_dtype, b * p.pos_sb + (q - b * p.Tq) * p.pos_sq);
+// Weight p_k of partner k in its query's mixture, from the query's K scores
+// and position t: softmax over the active partners (rank < k_limit, score >
+// -1e30; inactive scores -1e4), renormalised by max(sum, 1e-9) --
+// relation_reduce.py:399-411.
+__device__ float row_weight(const float (&sc)[16], int64_t t, uint32_t K, uint32_t k) {
   const int64_t n = t + 1;
   int k_limit = n > 0 ? 64 - __clzll(static_cast<unsigned long long>(n)) : 0;  // ceil(log2(t+2))
   k_limit = k_limit < 1 ? 1 : (k_limit > static_cast<int>(K) ? static_cast<int>(K) : k_limit);
-  const float* sq = p.scores + static_cast<size_t>(q) * K;
-  float sc[16];
-#pragma unroll
-  for (int c = 0; c < 16; ++c) sc[c] = c < static_cast<int>(K) ? sq[c] : -INFINITY;
   float m = -INFINITY;
 #pragma unroll
   for (int c = 0; c < 16; ++c)
@@ -140,6 +183,38 @@ __device__ float row_weight(const FusedParams& p, uint32_t grow) {
     mine = c == static_cast<int>(k) ? pc : mine;
   }
   return mine / fmaxf(total, 1.0e-9f);
+}
+
+// Branch-free loads of one int32 / int64 index (low word always, high word only
+// for int64: the other load gets an out-of-range offset and reads 0) and of one
+// fp32 / bf16 / fp16 element (the aligned dword holding it).  Issued early and
+// decoded after the round trip, so no load waits at a dtype branch.
+struct IndexWords {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ IndexWords issue_index(const void* base, int dtype, uint32_t count,
+                                                  uint32_t i, bool valid) {
+  const bool is64 = dtype == RLM_I64;
+  const rsrc_t r = make_rsrc(base, count * (is64 ? 8u : 4u));
+  return {buf_load_b32(r, valid ? i * (is64 ? 8u : 4u) : kNoOffset),
+          buf_load_b32(r, valid && is64 ? 8u * i + 4u : kNoOffset)};
+}
+__device__ __forceinline__ int64_t decode_index(IndexWords w, int dtype) {
+  return dtype == RLM_I64
+             ? static_cast<int64_t>((static_cast<uint64_t>(w.hi) << 32) | w.lo)
+             : static_cast<int64_t>(static_cast<int32_t>(w.lo));
+}
+__device__ __forceinline__ uint32_t issue_float(const void* base, int dtype, uint32_t count,
+                                                uint32_t i, bool valid) {
+  const uint32_t esz = dtype == RLM_F32 ? 4u : 2u;
+  const rsrc_t r = make_rsrc(base, count * esz);
+  return buf_load_b32(r, valid ? (i * esz) & ~3u : kNoOffset);
+}
+__device__ __forceinline__ float decode_float(uint32_t bits, int dtype, uint32_t i) {
+  const uint32_t half = (i & 1u) ? bits >> 16 : bits & 0xffffu;
+  const float fb = __uint_as_float(half << 16);
+  const float fh = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(half)));
+  return dtype == RLM_F32 ? __uint_as_float(bits) : (dtype == RLM_BF16 ? fb : fh);
 }
 
 __device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
@@ -199,6 +274,13 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
 
   constexpr int R = KS1 * 32;
   constexpr int QPR = R / 8;
+  // Phase 2 tiling: DG waves along D times RG along the rows; a wave owns DTW
+  // 32-wide column tiles of D and RTW 32-row tiles.
+  constexpr int DG = (DT % 2 == 0) ? 8 : 4;
+  constexpr int RG = kWaves / DG;
+  constexpr int DTW = 4 * DT / DG;
+  constexpr int RTW = 4 / RG;
+  static_assert(DG * DTW * 32 == 128 * DT && RG * RTW == 4, "phase-2 tiling");
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
@@ -211,13 +293,16 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
   const rsrc_t wmr = make_rsrc(p.wm, p.wm_bytes);
   const rsrc_t w2r = make_rsrc(p.w2, p.w2_bytes);
 
-  // ---- Set-up: two dependent round trips.  (1) this lane's row indices
-  // (beside the W_m DMA of chunk 0); (2) the wave's gather DMA of chunk 0, the
-  // operand rows, the row-weight inputs and b2 / gamma / beta, all in flight
-  // together.
+  // ---- Set-up: two dependent round trips.  (1) everything that does not
+  // depend on the row indices is issued together, branch-free (dtype
+  // dispatch by offset selection, so no load waits at a branch join): the
+  // W_m DMA of chunk 0, this lane's row indices, the row-weight inputs of slot
+  // tid and element tid of b2 / gamma / beta.  (2) the wave's gather DMA of
+  // chunk 0 and the operand rows.  Everything is decoded after the second
+  // round trip.
   dma_wm_chunk<KS1>(wmr, lds0, 0, wave, lane);
-  // This lane's phase-1 row: 16*wave + r16.
-  const int lrow = 16 * wave + r16;
+  // This lane's phase-1 slot: 16*wave + r16 (rows of the hidden chunk in LDS are slots).
+  const int lslot = 16 * wave + r16;
   u16x8 ph[KS1], pl[KS1];
   // Gather DMA sources of this lane (piece lane%32 of row 16*wave + 2i + lane/32), chunk 0.
   auto gather_src = [&](int i) {
@@ -232,21 +317,38 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
     for (int i = 0; i < kGatherInsts; ++i) src[i] = gather_src(i);
     dma_gather_chunk(xr, lds0 + kOffGather, src, chunk, wave);
   };
+  const uint32_t grow = row0 + slot_row<RTW>(lslot, p.K, p.k_log2);
+  const bool live = grow < p.rows;
+  const uint32_t q = grow >> p.k_log2;
+  const IndexWords ai = issue_index(p.anchor, p.index_dtype_a, p.queries, q, live);
+  const IndexWords pi = issue_index(p.partner, p.index_dtype_p, p.rows, grow, live);
+  // Row-weight inputs of slot tid (threads 0..127): its query's position and K scores.
+  const uint32_t wrow = row0 + slot_row<RTW>(tid & (kRows - 1), p.K, p.k_log2);
+  const bool wlive = tid < kRows && wrow < p.rows;
+  const uint32_t wq = wrow >> p.k_log2;
+  const uint32_t wb = wq / p.Tq;
+  const IndexWords wpos = issue_index(p.pos, p.pos_dtype, p.pos_count,
+                                      static_cast<uint32_t>(wb * p.pos_sb + (wq - wb * p.Tq) * p.pos_sq),
+                                      wlive);
+  const rsrc_t scr = make_rsrc(p.scores, p.rows * 4u);
+  uint32_t sc[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c)
+    sc[c] = buf_load_b32(scr, wlive && c < static_cast<int>(p.K) ? (wq * p.K + c) * 4u : kNoOffset);
+  // Element tid of b2 / gamma / beta (D <= kThreads).
+  const bool dlive = tid < static_cast<int>(p.D);
+  const uint32_t cb2 = issue_float(p.b2, p.b2_dtype, p.D, tid, dlive);
+  const uint32_t cgm = issue_float(p.gamma, p.gamma_dtype, p.D, tid, dlive);
+  const uint32_t cbt = issue_float(p.beta, p.beta_dtype, p.D, tid, dlive);
   {
-    const uint32_t grow = row0 + lrow;
-    int32_t a = -1, pp = -1;
-    uint32_t base = 0;
-    if (grow < p.rows) {
-      const uint32_t q = grow >> p.k_log2;
-      base = (q / p.Tq) * static_cast<uint32_t>(p.T);
-      const int64_t ai = load_any_i(p.anchor, p.index_dtype_a, q);
-      const int64_t pi = load_any_i(p.partner, p.index_dtype_p, grow);
-      a = (ai >= 0 && ai < p.T) ? static_cast<int32_t>(ai) : -1;
-      pp = (pi >= 0 && pi < p.T) ? static_cast<int32_t>(pi) : -1;
-    }
+    const int64_t a64 = decode_index(ai, p.index_dtype_a);
+    const int64_t p64 = decode_index(pi, p.index_dtype_p);
+    const int32_t a = live && a64 >= 0 && a64 < p.T ? static_cast<int32_t>(a64) : -1;
+    const int32_t pp = live && p64 >= 0 && p64 < p.T ? static_cast<int32_t>(p64) : -1;
+    const uint32_t base = (q / p.Tq) * static_cast<uint32_t>(p.T);
     if (g == 0) {
-      rowoff[2 * lrow] = a >= 0 ? (base + a) * (4u * H) : kNoOffset;               // anchor, first half
-      rowoff[2 * lrow + 1] = pp >= 0 ? (base + pp) * (4u * H) + 2u * H : kNoOffset;  // partner, second half
+      rowoff[2 * lslot] = a >= 0 ? (base + a) * (4u * H) : kNoOffset;               // anchor, first half
+      rowoff[2 * lslot + 1] = pp >= 0 ? (base + pp) * (4u * H) + 2u * H : kNoOffset;  // partner, second half
     }
     wave_sync();  // the wave's row offsets are in LDS (it reads only its own rows)
     gather_chunk(0);
@@ -258,12 +360,6 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
     for (int s = 0; s < KS1; ++s) {
       va[s] = buf_load_b128(opr, ok ? oa + 64u * s : kNoOffset);
       vp[s] = buf_load_b128(opr, ok ? op + 64u * s : kNoOffset);
-    }
-    if (tid < kRows) wts[tid] = row0 + tid < p.rows ? row_weight(p, row0 + tid) : 0.0f;
-    for (int i = tid; i < static_cast<int>(p.D); i += kThreads) {
-      cst[i] = load_any_f(p.b2, p.b2_dtype, i);
-      cst[kMaxD + i] = load_any_f(p.gamma, p.gamma_dtype, i);
-      cst[2 * kMaxD + i] = load_any_f(p.beta, p.beta_dtype, i);
     }
 #pragma unroll
     for (int s = 0; s < KS1; ++s) {
@@ -280,41 +376,63 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
       ph[s] = as_frag(make_uint4(h[0], h[1], h[2], h[3]));
       pl[s] = as_frag(make_uint4(l[0], l[1], l[2], l[3]));
     }
+    if (tid < kRows) {
+      float scf[16];
+#pragma unroll
+      for (int c = 0; c < 16; ++c) scf[c] = __uint_as_float(sc[c]);
+      wts[tid] = wlive ? row_weight(scf, decode_index(wpos, p.pos_dtype), p.K, wrow & (p.K - 1))
+                       : 0.0f;
+    }
+    if (dlive) {
+      cst[tid] = decode_float(cb2, p.b2_dtype, tid);
+      cst[kMaxD + tid] = decode_float(cgm, p.gamma_dtype, tid);
+      cst[2 * kMaxD + tid] = decode_float(cbt, p.beta_dtype, tid);
+    }
   }
 
-  // W2 fragments (B operand of phase 2) in groups of JC column tiles: rows
-  // dcol0 + 16(JC*jg + j) + r16, k = chunk*128 + 32s + 8g.
-  constexpr int JC = (DT % 2 == 0) ? DT / 2 : DT;
-  constexpr int NG = DT / JC;
-  const int dcol0 = wave * DT * 16;
-  const uint32_t w2_lane = (static_cast<uint32_t>(dcol0 + r16) * H + 8 * g) * 2u;
-  auto load_w2 = [&](u16x8 (&w)[JC], int chunk, int jg, int s) {
+  // W2 fragments (A operand of phase 2): rows d0 + 32j + n32 of W2, k = chunk*128
+  // + 16s + 8h (8 bf16 per lane).
+  const int dg = wave % DG, rg = wave / DG;
+  const int d0 = dg * DTW * 32;
+  const int n32 = lane & 31, h = lane >> 5;
+  const uint32_t w2_lane = (static_cast<uint32_t>(d0 + n32) * H + 8 * h) * 2u;
+  auto load_w2 = [&](u16x8 (&w)[DTW], int chunk, int s) {
 #pragma unroll
-    for (int j = 0; j < JC; ++j)
-      w[j] = as_frag(buf_load_b128(
-          w2r, w2_lane + (16u * (JC * jg + j) * H + chunk * kHC + 32 * s) * 2u));
+    for (int j = 0; j < DTW; ++j)
+      w[j] = as_frag(buf_load_b128(w2r, w2_lane + (32u * j * H + chunk * kHC + 16 * s) * 2u));
   };
 
-  f32x4 raw[kRowTiles][DT];
+  // raw[j][i][4ii + jj] = raw^T[d = d0 + 32j + 8ii + 4h + jj][slot 32(RTW rg + i) + n32].
+  f32x16 raw[DTW][RTW];
 #pragma unroll
-  for (int i = 0; i < kRowTiles; ++i)
+  for (int j = 0; j < DTW; ++j)
 #pragma unroll
-    for (int j = 0; j < DT; ++j) raw[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < RTW; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) raw[j][i][e] = 0.0f;
 
-  const unsigned char* my_gat = smem + kOffGather + lrow * kGatherRowBytes;
+  const unsigned char* my_gat = smem + kOffGather + lslot * kGatherRowBytes;
   // Constant A operand [I16 | I16]: lane (r16, g) holds row r16, k = 8g..8g+7,
   // 1.0 (bf16 0x3F80) where k % 16 == r16.
   u16x8 ident;
 #pragma unroll
   for (int k = 0; k < 8; ++k) ident[k] = (8 * (g & 1) + k == r16) ? 0x3F80 : 0;
-  unsigned char* my_hid = hid + lrow * (2 * kLd) + 8 * g;
+  unsigned char* my_hid = hid + lslot * (2 * kLd) + 8 * g;
+  // B operand of phase 2: hidden slot 32(RTW rg + i) + n32, k = 16s + 8h.
+  const unsigned char* brow = hid + (32 * RTW * rg + n32) * (2 * kLd) + 16 * h;
 
   const int nchunks = H / kHC;
   __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this lane's W_m and gather pieces of chunk 0 are in LDS
   __syncthreads();
 
   for (int c = 0; c < nchunks; ++c) {
-    // ---- Phase 1, two halves of 64 columns: hidden^T[cols x 16 rows of this wave].
+    // W2 fragments of this chunk's phase 2, k-step by k-step.  The first
+    // kW2Ahead are loaded before the last GELU of phase 1, while no LDS-DMA is
+    // in flight, and are complete before the next chunk's DMA is issued: loads
+    // return in issue order, so a wait for a load issued after a DMA also waits
+    // for the DMA.  The DMA is covered by the first kW2Ahead k-steps.
+    u16x8 wq[kHC / 16][DTW];
+    // ---- Phase 1, two halves of 64 columns: hidden^T[cols x 16 slots of this wave].
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       f32x4 acc[4];
@@ -342,197 +460,205 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
           acc[jj] = mfma_bf16(w[jj], pl[s], acc[jj]);
         }
       }
-      // acc[jj][e] = hidden[row lrow][col 16(4hh+jj) + 4g + e].
+      if (hh == 1) {
+#pragma unroll
+        for (int s = 0; s < kW2Ahead; ++s) load_w2(wq[s], c, s);
+      }
+      // acc[jj][e] = hidden[slot lslot][col 16(4hh+jj) + 4g + e].
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const f32x4 h = acc[jj];
+        const f32x4 hv = acc[jj];
         *reinterpret_cast<uint2*>(my_hid + 32 * (4 * hh + jj)) =
-            make_uint2(pack_bf16x2(gelu_erf(h[0]), gelu_erf(h[1])),
-                       pack_bf16x2(gelu_erf(h[2]), gelu_erf(h[3])));
+            make_uint2(pack_bf16x2(gelu_erf(hv[0]), gelu_erf(hv[1])),
+                       pack_bf16x2(gelu_erf(hv[2]), gelu_erf(hv[3])));
       }
     }
-    u16x8 b[JC];
-    load_w2(b, c, 0, 0);
     __syncthreads();  // hidden chunk complete; the W_m and gather tiles are free
     if (c + 1 < nchunks) {
+#pragma unroll
+      for (int s = 0; s < kW2Ahead; ++s)
+#pragma unroll
+        for (int j = 0; j < DTW; ++j) asm volatile("" ::"v"(wq[s][j]));  // landed before the DMA
       dma_wm_chunk<KS1>(wmr, lds0, c + 1, wave, lane);
       gather_chunk(c + 1);
     }
-    // ---- Phase 2: raw[128 x 16*DT] += hidden chunk . W2[cols, chunk]^T, JC column
-    // tiles at a time (W2 fragments of the next k-step in flight), row tile by
-    // row tile (the next hidden fragment in flight).
+    // ---- Phase 2: raw^T[32 DTW x 32 RTW] += W2[cols, chunk] . hidden chunk^T,
+    // k-step by k-step (W2 fragments kW2Ahead k-steps ahead), row tile by row
+    // tile (the next hidden fragment in flight).
+    u16x8 b = lds_frag(brow);
 #pragma unroll
-    for (int jg = 0; jg < NG; ++jg) {
+    for (int s = 0; s < kHC / 16; ++s) {
+      if (s + kW2Ahead < kHC / 16) load_w2(wq[s + kW2Ahead], c, s + kW2Ahead);
 #pragma unroll
-      for (int s = 0; s < kHC / 32; ++s) {
-        u16x8 bn[JC];
-        if (s + 1 < kHC / 32) load_w2(bn, c, jg, s + 1);
-        else if (jg + 1 < NG) load_w2(bn, c, jg + 1, 0);
-        const unsigned char* arow = hid + r16 * (2 * kLd) + 64 * s + 16 * g;
-        u16x8 a = lds_frag(arow);
+      for (int i = 0; i < RTW; ++i) {
+        // The next fragment in (k-step, row tile) order, across k-step boundaries.
+        const bool more = i + 1 < RTW || s + 1 < kHC / 16;
+        u16x8 bn;
+        if (more)
+          bn = lds_frag(i + 1 < RTW ? brow + (i + 1) * 32 * (2 * kLd) + 32 * s : brow + 32 * (s + 1));
 #pragma unroll
-        for (int i = 0; i < kRowTiles; ++i) {
-          u16x8 an;
-          if (i + 1 < kRowTiles) an = lds_frag(arow + (i + 1) * 16 * (2 * kLd));
-#pragma unroll
-          for (int j = 0; j < JC; ++j) raw[i][JC * jg + j] = mfma_bf16(a, b[j], raw[i][JC * jg + j]);
-          if (i + 1 < kRowTiles) a = an;
-        }
-        if (s + 1 < kHC / 32 || jg + 1 < NG) {
-#pragma unroll
-          for (int j = 0; j < JC; ++j) b[j] = bn[j];
-        }
-        __builtin_amdgcn_sched_barrier(0);  // keep each k-step's loads next to its products
+        for (int j = 0; j < DTW; ++j) raw[j][i] = mfma32_bf16(wq[s][j], b, raw[j][i]);
+        if (more) b = bn;
       }
+      __builtin_amdgcn_sched_barrier(0);  // keep each k-step's loads next to its products
     }
     __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this lane's pieces of chunk c+1 are in LDS
     __syncthreads();  // ... and everyone's; the hidden chunk is free again
   }
 
-  // ---- Epilogue.  raw[i][j][e] = row 16i+4g+e, column dcol0+16j+r16.
-  const float inv_d = 1.0f / static_cast<float>(p.D);
+  // ---- Epilogue.  A lane holds, for each of its RTW slots, 16*DTW of the
+  // wave's 32*DTW columns; the other 16*DTW are in lane ^ 32.
 #pragma unroll
-  for (int j = 0; j < DT; ++j) {
-    const float bias = cst[dcol0 + 16 * j + r16];
+  for (int j = 0; j < DTW; ++j)
 #pragma unroll
-    for (int i = 0; i < kRowTiles; ++i)
+    for (int ii = 0; ii < 4; ++ii) {
+      const float4 b4 = *reinterpret_cast<const float4*>(cst + d0 + 32 * j + 8 * ii + 4 * h);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) raw[i][j][e] += bias;
-  }
+      for (int i = 0; i < RTW; ++i) {
+        raw[j][i][4 * ii + 0] += b4.x;
+        raw[j][i][4 * ii + 1] += b4.y;
+        raw[j][i][4 * ii + 2] += b4.z;
+        raw[j][i][4 * ii + 3] += b4.w;
+      }
+    }
   // Row moments.  Each wave takes the mean and centred sum of squares of its
-  // 16*DT columns of every row (DPP sums over the 16 lanes of a column tile
-  // row); threads 0..127 merge the 8 waves' pairs (Chan, Golub and LeVeque's
-  // pairwise update, equal counts) -- one barrier round, no E[x^2]-mu^2.
-  constexpr float kInvCols = 1.0f / (16.0f * DT);
+  // 32*DTW columns of each of its slots (in-lane sums, then the two halves of
+  // the wave); threads 0..127 merge the DG waves of the slot's row group (Chan,
+  // Golub and LeVeque's pairwise update, equal counts) -- one barrier round, no
+  // E[x^2]-mu^2.
+  constexpr float kCols = 32.0f * DTW;
 #pragma unroll
-  for (int i = 0; i < kRowTiles; ++i)
+  for (int i = 0; i < RTW; ++i) {
+    float sum = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float sum = 0.0f;
+    for (int j = 0; j < DTW; ++j)
 #pragma unroll
-      for (int j = 0; j < DT; ++j) sum += raw[i][j][e];
-      const float mu = row16_sum(sum) * kInvCols;
-      float sq = 0.0f;
+      for (int e = 0; e < 16; ++e) sum += raw[j][i][e];
+    const float mu = swap32_sum(sum) * (1.0f / kCols);
+    float sq = 0.0f;
 #pragma unroll
-      for (int j = 0; j < DT; ++j) {
-        const float d = raw[i][j][e] - mu;
+    for (int j = 0; j < DTW; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float d = raw[j][i][e] - mu;
         sq = fmaf(d, d, sq);
       }
-      sq = row16_sum(sq);
-      if (r16 == 0) {
-        part[wave * kRows + 16 * i + 4 * g + e] = mu;
-        part[(kWaves + wave) * kRows + 16 * i + 4 * g + e] = sq;
-      }
+    sq = swap32_sum(sq);
+    if (h == 0) {
+      const int slot = 32 * (RTW * rg + i) + n32;
+      part[dg * kRows + slot] = mu;
+      part[(DG + dg) * kRows + slot] = sq;
     }
-  __syncthreads();
-  if (tid < kRows) {
-    float mw[kWaves], mu = 0.0f, m2 = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      mw[w] = part[w * kRows + tid];
-      mu += mw[w];
-      m2 += part[(kWaves + w) * kRows + tid];
-    }
-    mu *= 1.0f / kWaves;
-    float spread = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) spread = fmaf(mw[w] - mu, mw[w] - mu, spread);
-    mom[tid] = mu;
-    mom[kRows + tid] = rsqrtf(fmaf(spread, 16.0f * DT, m2) * inv_d + p.eps);
   }
   __syncthreads();
-  float4 mean[kRowTiles];
+  if (tid < kRows) {
+    float mw[DG], mu = 0.0f, m2 = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kRowTiles; ++i) mean[i] = *reinterpret_cast<const float4*>(mom + 16 * i + 4 * g);
-  // LayerNorm, weights, sum over each query's K consecutive rows, store:
+    for (int w = 0; w < DG; ++w) {
+      mw[w] = part[w * kRows + tid];
+      mu += mw[w];
+      m2 += part[(DG + w) * kRows + tid];
+    }
+    mu *= 1.0f / DG;
+    float spread = 0.0f;
+#pragma unroll
+    for (int w = 0; w < DG; ++w) spread = fmaf(mw[w] - mu, mw[w] - mu, spread);
+    mom[tid] = mu;
+    mom[kRows + tid] = rsqrtf(fmaf(spread, kCols, m2) * (1.0f / static_cast<float>(p.D)) + p.eps);
+  }
+  __syncthreads();
+  // LayerNorm, weights, sum over each query's K rows, store:
   //   out[q] = sum_k w_k (gamma (x_k - mu_k) rs_k + beta)
   //          = gamma * sum_k (A_k x_k - B_k) + beta * sum_k w_k,
-  // A_k = w_k rs_k, B_k = A_k mu_k, so each raw value costs one FMA.  Rows of
-  // one query: K <= 4 -> inside a lane group, K = 8 -> groups {0,1} / {2,3}
-  // (v_permlane16_swap), K = 16 -> all four (and v_permlane32_swap).  The
-  // store descriptor covers this workgroup's queries only, so rows past the end
-  // of the last workgroup are dropped by the buffer bounds check.
+  // A_k = w_k rs_k, B_k = A_k mu_k, so each raw value costs one FMA.  The
+  // store descriptor covers this workgroup's queries only, so queries past the
+  // end of the last workgroup are dropped by the buffer bounds check.
   const uint32_t K = p.K, D = p.D;
   const uint32_t q0 = row0 >> p.k_log2;
   const uint32_t nq = min(p.queries - q0, static_cast<uint32_t>(kRows) >> p.k_log2);
   const rsrc_t outr = make_rsrc(p.out + static_cast<size_t>(q0) * D, nq * D * 4u);
-  float gm[DT], bt[DT];
+  const int qg = (32 * RTW) >> p.k_log2;  // queries per row group
+  float A[RTW], nB[RTW], wk[RTW];
 #pragma unroll
-  for (int j = 0; j < DT; ++j) {
-    gm[j] = cst[kMaxD + dcol0 + 16 * j + r16];
-    bt[j] = cst[2 * kMaxD + dcol0 + 16 * j + r16];
+  for (int i = 0; i < RTW; ++i) {
+    const int slot = 32 * (RTW * rg + i) + n32;
+    wk[i] = wts[slot];
+    A[i] = wk[i] * mom[kRows + slot];
+    nB[i] = -A[i] * mom[slot];
   }
-  auto cross16 = [](float v) { return swap16_sum(v); };
-  auto cross32 = [](float v) { return swap32_sum(v); };
-  if (K >= 4) {
-    float v[kRowTiles][DT], W[kRowTiles];
+  // Stores the 16*DTW columns of one query: v holds sum_k (A_k x_k - B_k), W = sum_k w_k.
+  auto store_query = [&](const float (&v)[DTW][16], float W, uint32_t qloc) {
 #pragma unroll
-    for (int i = 0; i < kRowTiles; ++i) {
-      const float4 m4 = mean[i];
-      const float4 r4 = *reinterpret_cast<const float4*>(mom + kRows + 16 * i + 4 * g);
-      const float4 w4 = *reinterpret_cast<const float4*>(wts + 16 * i + 4 * g);
-      const float A[4] = {w4.x * r4.x, w4.y * r4.y, w4.z * r4.z, w4.w * r4.w};
-      const float nB[4] = {-A[0] * m4.x, -A[1] * m4.y, -A[2] * m4.z, -A[3] * m4.w};
-      W[i] = (w4.x + w4.y) + (w4.z + w4.w);
+    for (int j = 0; j < DTW; ++j)
 #pragma unroll
-      for (int j = 0; j < DT; ++j)
-        v[i][j] = (fmaf(raw[i][j][0], A[0], nB[0]) + fmaf(raw[i][j][1], A[1], nB[1])) +
-                  (fmaf(raw[i][j][2], A[2], nB[2]) + fmaf(raw[i][j][3], A[3], nB[3]));
-    }
-    if (K >= 8) {
-#pragma unroll
-      for (int i = 0; i < kRowTiles; ++i) {
-        W[i] = cross16(W[i]);
-#pragma unroll
-        for (int j = 0; j < DT; ++j) v[i][j] = cross16(v[i][j]);
+      for (int ii = 0; ii < 4; ++ii) {
+        const int d = d0 + 32 * j + 8 * ii + 4 * h;
+        const float4 g4 = *reinterpret_cast<const float4*>(cst + kMaxD + d);
+        const float4 b4 = *reinterpret_cast<const float4*>(cst + 2 * kMaxD + d);
+        const float4 o = make_float4(fmaf(g4.x, v[j][4 * ii + 0], b4.x * W),
+                                     fmaf(g4.y, v[j][4 * ii + 1], b4.y * W),
+                                     fmaf(g4.z, v[j][4 * ii + 2], b4.z * W),
+                                     fmaf(g4.w, v[j][4 * ii + 3], b4.w * W));
+        buf_store_f32x4(o, outr, (qloc * D + d) * 4u);
       }
-    }
-    if (K >= 16) {
+  };
+  if (static_cast<int>(K) >= RTW) {
+    // One query per lane; its partners also sit in lanes n32 + QG, + 2QG, ...
+    float v[DTW][16], W = 0.0f;
 #pragma unroll
-      for (int i = 0; i < kRowTiles; ++i) {
-        W[i] = cross32(W[i]);
+    for (int i = 0; i < RTW; ++i) W += wk[i];
 #pragma unroll
-        for (int j = 0; j < DT; ++j) v[i][j] = cross32(v[i][j]);
+    for (int j = 0; j < DTW; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < RTW; ++i) acc += fmaf(raw[j][i][e], A[i], nB[i]);
+        v[j][e] = acc;
       }
-    }
+    const int lanes = static_cast<int>(K) / RTW;  // lanes per query, QG apart
+    if (lanes >= 8) {
+      W = ror_sum<4>(W);
 #pragma unroll
-    for (int i = 0; i < kRowTiles; ++i) {
-      const uint32_t lrow = 16 * i + 4 * g;  // first local row of this lane group
-      if ((lrow & (K - 1)) != 0) continue;
-      const uint32_t obase = (lrow >> p.k_log2) * D + dcol0 + r16;
+      for (int j = 0; j < DTW; ++j)
 #pragma unroll
-      for (int j = 0; j < DT; ++j)
-        buf_store_f32(fmaf(gm[j], v[i][j], bt[j] * W[i]), outr, (obase + 16 * j) * 4u);
+        for (int e = 0; e < 16; ++e) v[j][e] = ror_sum<4>(v[j][e]);
     }
+    if (lanes >= 4) {
+      W = ror_sum<8>(W);
+#pragma unroll
+      for (int j = 0; j < DTW; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[j][e] = ror_sum<8>(v[j][e]);
+    }
+    if (lanes >= 2) {
+      W = swap16_sum(W);
+#pragma unroll
+      for (int j = 0; j < DTW; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[j][e] = swap16_sum(v[j][e]);
+    }
+    if (n32 < qg) store_query(v, W, static_cast<uint32_t>(rg * qg + n32));
   } else {
+    // K < RTW: this lane holds RTW/K whole queries, tiles K*qq .. K*qq + K-1.
 #pragma unroll
-    for (int i = 0; i < kRowTiles; ++i) {
-      const float4 m4 = mean[i];
-      const float4 r4 = *reinterpret_cast<const float4*>(mom + kRows + 16 * i + 4 * g);
-      const float4 w4 = *reinterpret_cast<const float4*>(wts + 16 * i + 4 * g);
-      const float A[4] = {w4.x * r4.x, w4.y * r4.y, w4.z * r4.z, w4.w * r4.w};
-      const float nB[4] = {-A[0] * m4.x, -A[1] * m4.y, -A[2] * m4.z, -A[3] * m4.w};
-      const uint32_t lrow = 16 * i + 4 * g;
-      if (K == 2) {
-        const float W0 = w4.x + w4.y, W1 = w4.z + w4.w;
-        const uint32_t obase = (lrow >> 1) * D + dcol0 + r16;
+    for (int qq = 0; qq < RTW; ++qq) {
+      if (qq * static_cast<int>(K) >= RTW) break;
+      float v[DTW][16], W = 0.0f;
 #pragma unroll
-        for (int j = 0; j < DT; ++j) {
-          const float v0 = fmaf(raw[i][j][0], A[0], nB[0]) + fmaf(raw[i][j][1], A[1], nB[1]);
-          const float v1 = fmaf(raw[i][j][2], A[2], nB[2]) + fmaf(raw[i][j][3], A[3], nB[3]);
-          buf_store_f32(fmaf(gm[j], v0, bt[j] * W0), outr, (obase + 16 * j) * 4u);
-          buf_store_f32(fmaf(gm[j], v1, bt[j] * W1), outr, (obase + D + 16 * j) * 4u);
-        }
-      } else {
-        const float Wk[4] = {w4.x, w4.y, w4.z, w4.w};
-        const uint32_t obase = lrow * D + dcol0 + r16;
+      for (int j = 0; j < DTW; ++j)
 #pragma unroll
-        for (int j = 0; j < DT; ++j)
+        for (int e = 0; e < 16; ++e) v[j][e] = 0.0f;
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            buf_store_f32(fmaf(gm[j], fmaf(raw[i][j][e], A[e], nB[e]), bt[j] * Wk[e]), outr,
-                          (obase + e * D + 16 * j) * 4u);
+      for (int i = 0; i < RTW; ++i) {
+        if (i / static_cast<int>(K) != qq) continue;
+        W += wk[i];
+#pragma unroll
+        for (int j = 0; j < DTW; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) v[j][e] += fmaf(raw[j][i][e], A[i], nB[i]);
       }
+      store_query(v, W, static_cast<uint32_t>(rg * qg + 32 * qq + n32));
     }
   }
 }
@@ -627,18 +753,20 @@ extern "C" hipError_t rlm_relation_reduce_fused_seq(
     RLM_TRY(check_dim(positions, "positions", 0, Tq));
     p.pos_sb = 0;
     p.pos_sq = 1;
+    p.pos_count = static_cast<uint32_t>(Tq);
   } else {
     RLM_TRY(check_tensor(positions, "positions", 2));
     RLM_TRY(check_dim(positions, "positions", 0, B));
     RLM_TRY(check_dim(positions, "positions", 1, Tq));
     p.pos_sb = Tq;
     p.pos_sq = 1;
+    p.pos_count = static_cast<uint32_t>(B * Tq);
   }
   constexpr int64_t kMaxBytes = int64_t(1) << 31;
   RLM_REQUIRE(B * T * 2 * H * 2 < kMaxBytes && B * T * R * 2 < kMaxBytes && D * H * 2 < kMaxBytes,
               "caches and weights must each be smaller than 2 GiB");
-  RLM_REQUIRE(B * Tq * K < kMaxBytes && B * Tq * D * 4 < kMaxBytes,
-              "fused relation reduce: B*Tq*K rows and the fp32 output must stay below 2^31");
+  RLM_REQUIRE(B * Tq * K * 8 < kMaxBytes && B * Tq * D * 4 < kMaxBytes,
+              "fused relation reduce: the index tensors and the fp32 output must stay below 2 GiB");
   for (const rlm_tensor* t : {operand_cache, product_weight, second_weight})
     RLM_REQUIRE((reinterpret_cast<uintptr_t>(t->data) & 15u) == 0,
                 "operand_cache, product_weight and second_weight must be 16-byte aligned");

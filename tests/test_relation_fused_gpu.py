@@ -109,8 +109,8 @@ def test_cfg2_fused_matches_unfused_and_oracle(device):
     assert abs_err(got, expected) <= TIGHT_ABS
 
 
-@pytest.mark.parametrize("k_out", [1, 2, 4, 16])
-@pytest.mark.parametrize("d_model", [256, 384])
+@pytest.mark.parametrize("k_out", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("d_model", [128, 256, 384])
 def test_fused_partner_counts_and_widths(device, k_out, d_model):
     cfg = RelationConfig("fused", 2, 96, d_model, 32, 64, 2, k_out, torch.bfloat16,
                          relation_dim=64, hidden_dim=256, seed=777 + k_out)
