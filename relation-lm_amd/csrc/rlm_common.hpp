@@ -121,6 +121,43 @@ __device__ __forceinline__ uint16_t buf_load_b16(rsrc_t r, uint32_t off) {
 __device__ __forceinline__ void buf_store_f32(float v, rsrc_t r, uint32_t off) {
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
 }
+// Branch-free loads of one int32 / int64 index (low word always, high word only
+// for int64: the other load gets an out-of-range offset and reads 0) and of one
+// fp32 / bf16 / fp16 element (a 4-byte and a 2-byte load, the one that does not
+// match the dtype out of range).  Issued early and decoded after the round
+// trip, so no load waits at a dtype branch.
+struct IndexWords {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ IndexWords issue_index(const void* base, int dtype, uint32_t count,
+                                                  uint32_t i, bool valid) {
+  const bool is64 = dtype == RLM_I64;
+  const rsrc_t r = make_rsrc(base, count * (is64 ? 8u : 4u));
+  return {buf_load_b32(r, valid ? i * (is64 ? 8u : 4u) : kNoOffset),
+          buf_load_b32(r, valid && is64 ? 8u * i + 4u : kNoOffset)};
+}
+__device__ __forceinline__ int64_t decode_index(IndexWords w, int dtype) {
+  return dtype == RLM_I64
+             ? static_cast<int64_t>((static_cast<uint64_t>(w.hi) << 32) | w.lo)
+             : static_cast<int64_t>(static_cast<int32_t>(w.lo));
+}
+struct FloatWords {
+  uint32_t w32;  // fp32 element (0 for 16-bit dtypes)
+  uint32_t w16;  // 16-bit element (0 for fp32)
+};
+__device__ __forceinline__ FloatWords issue_float(const void* base, int dtype, uint32_t count,
+                                                  uint32_t i, bool valid) {
+  const bool is32 = dtype == RLM_F32;
+  const rsrc_t r = make_rsrc(base, count * (is32 ? 4u : 2u));
+  return {buf_load_b32(r, valid && is32 ? 4u * i : kNoOffset),
+          static_cast<uint32_t>(buf_load_b16(r, valid && !is32 ? 2u * i : kNoOffset))};
+}
+__device__ __forceinline__ float decode_float(FloatWords w, int dtype) {
+  const float fh = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w.w16)));
+  return dtype == RLM_F32 ? __uint_as_float(w.w32)
+                          : (dtype == RLM_BF16 ? __uint_as_float(w.w16 << 16) : fh);
+}
+
 // One element of type T at byte offset `off`, as float.
 template <typename T>
 __device__ __forceinline__ float buf_load_elem(rsrc_t r, uint32_t off);
@@ -308,6 +345,8 @@ void clear_error();
 inline bool is_float_dtype(int d) { return d == RLM_F32 || d == RLM_BF16 || d == RLM_F16; }
 inline bool is_index_dtype(int d) { return d == RLM_I32 || d == RLM_I64; }
 const char* dtype_name(int d);
+// Bytes per element of an rlm dtype.
+inline int64_t dtype_size(int d) { return (d == RLM_F32 || d == RLM_I32) ? 4 : (d == RLM_I64 ? 8 : 2); }
 
 // Checks that `t` is a non-null, contiguous tensor of the given rank.
 bool check_tensor(const rlm_tensor* t, const char* name, int ndim);

@@ -185,38 +185,6 @@ __device__ float row_weight(const float (&sc)[16], int64_t t, uint32_t K, uint32
   return mine / fmaxf(total, 1.0e-9f);
 }
 
-// Branch-free loads of one int32 / int64 index (low word always, high word only
-// for int64: the other load gets an out-of-range offset and reads 0) and of one
-// fp32 / bf16 / fp16 element (the aligned dword holding it).  Issued early and
-// decoded after the round trip, so no load waits at a dtype branch.
-struct IndexWords {
-  uint32_t lo, hi;
-};
-__device__ __forceinline__ IndexWords issue_index(const void* base, int dtype, uint32_t count,
-                                                  uint32_t i, bool valid) {
-  const bool is64 = dtype == RLM_I64;
-  const rsrc_t r = make_rsrc(base, count * (is64 ? 8u : 4u));
-  return {buf_load_b32(r, valid ? i * (is64 ? 8u : 4u) : kNoOffset),
-          buf_load_b32(r, valid && is64 ? 8u * i + 4u : kNoOffset)};
-}
-__device__ __forceinline__ int64_t decode_index(IndexWords w, int dtype) {
-  return dtype == RLM_I64
-             ? static_cast<int64_t>((static_cast<uint64_t>(w.hi) << 32) | w.lo)
-             : static_cast<int64_t>(static_cast<int32_t>(w.lo));
-}
-__device__ __forceinline__ uint32_t issue_float(const void* base, int dtype, uint32_t count,
-                                                uint32_t i, bool valid) {
-  const uint32_t esz = dtype == RLM_F32 ? 4u : 2u;
-  const rsrc_t r = make_rsrc(base, count * esz);
-  return buf_load_b32(r, valid ? (i * esz) & ~3u : kNoOffset);
-}
-__device__ __forceinline__ float decode_float(uint32_t bits, int dtype, uint32_t i) {
-  const uint32_t half = (i & 1u) ? bits >> 16 : bits & 0xffffu;
-  const float fb = __uint_as_float(half << 16);
-  const float fh = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(half)));
-  return dtype == RLM_F32 ? __uint_as_float(bits) : (dtype == RLM_BF16 ? fb : fh);
-}
-
 __device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
 
@@ -337,9 +305,9 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
     sc[c] = buf_load_b32(scr, wlive && c < static_cast<int>(p.K) ? (wq * p.K + c) * 4u : kNoOffset);
   // Element tid of b2 / gamma / beta (D <= kThreads).
   const bool dlive = tid < static_cast<int>(p.D);
-  const uint32_t cb2 = issue_float(p.b2, p.b2_dtype, p.D, tid, dlive);
-  const uint32_t cgm = issue_float(p.gamma, p.gamma_dtype, p.D, tid, dlive);
-  const uint32_t cbt = issue_float(p.beta, p.beta_dtype, p.D, tid, dlive);
+  const FloatWords cb2 = issue_float(p.b2, p.b2_dtype, p.D, tid, dlive);
+  const FloatWords cgm = issue_float(p.gamma, p.gamma_dtype, p.D, tid, dlive);
+  const FloatWords cbt = issue_float(p.beta, p.beta_dtype, p.D, tid, dlive);
   {
     const int64_t a64 = decode_index(ai, p.index_dtype_a);
     const int64_t p64 = decode_index(pi, p.index_dtype_p);
@@ -384,9 +352,9 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
                        : 0.0f;
     }
     if (dlive) {
-      cst[tid] = decode_float(cb2, p.b2_dtype, tid);
-      cst[kMaxD + tid] = decode_float(cgm, p.gamma_dtype, tid);
-      cst[2 * kMaxD + tid] = decode_float(cbt, p.beta_dtype, tid);
+      cst[tid] = decode_float(cb2, p.b2_dtype);
+      cst[kMaxD + tid] = decode_float(cgm, p.gamma_dtype);
+      cst[2 * kMaxD + tid] = decode_float(cbt, p.beta_dtype);
     }
   }
 

@@ -16,10 +16,12 @@
 //                 tiles sharing an A row-block run on the same XCD (one L2),
 //                 which keeps A's HBM traffic at one read.
 //   smallk_kernel (M > 64, K in {32, 64, 96, 128})  e.g. the expanded-cache
-//                 projection (K = relation dim).  Each wave owns a 64x64 output
-//                 tile and loads all of its A and W fragments for the whole K
-//                 straight from L2 in MFMA operand layout -- one round trip,
-//                 no LDS staging and no barriers.
+//                 projection (K = relation dim).  A workgroup loads its 128-row
+//                 A and W tiles for the whole K once, in one round of
+//                 branch-free buffer loads, into swizzled LDS; each wave then
+//                 forms a 64x64 output tile as (W . A^T) so that a lane holds
+//                 four consecutive columns of a row (16-byte stores for fp32
+//                 output, 8-byte LDS staging then 16-byte row pieces for 16-bit).
 //   skinny_kernel (M <= 64)  decode shapes.  A workgroup owns one 16x16 output
 //                 tile; its eight waves split K, each issuing the W and A
 //                 fragment loads of up to six 32-wide slices at once straight
@@ -53,6 +55,7 @@ struct GemmParams {
   const void* bias;
   int bias_dtype;
   void* out;
+  uint32_t a_bytes, w_bytes;  // descriptor sizes of A and W (smallk_kernel; < 2 GiB)
   // Optional cache-row scatter (decode projection, skinny kernel only): output
   // columns [seg_lo[s], seg_hi[s]) of row m also go to row `position` of cache
   // s ([M, seg_rows[s], seg_hi[s] - seg_lo[s]], the output dtype); ring caches
@@ -260,83 +263,204 @@ __global__ void __launch_bounds__(256) tile_kernel(const GemmParams p) {
 // 16-bit weights, small K (K = 32*KS, KS <= 4)
 // ---------------------------------------------------------------------------
 
+// Eight consecutive elements at element offset `elem` of a TA buffer, as W
+// bit patterns, through a range-checked descriptor (`valid` false reads
+// zeros): no branch, so a wave's loads all issue back to back.
+template <typename TA, typename W>
+__device__ __forceinline__ uint4 load8_buf(rsrc_t r, uint32_t elem, bool valid) {
+  if constexpr (sizeof(TA) == 2) {
+    return buf_load_b128(r, valid ? elem * 2u : kNoOffset);
+  } else {
+    const uint4 x = buf_load_b128(r, valid ? elem * 4u : kNoOffset);
+    const uint4 y = buf_load_b128(r, valid ? elem * 4u + 16u : kNoOffset);
+    const float f[8] = {__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z),
+                        __uint_as_float(x.w), __uint_as_float(y.x), __uint_as_float(y.y),
+                        __uint_as_float(y.z), __uint_as_float(y.w)};
+    if constexpr (__is_same(W, bf16)) {
+      return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                        pack_bf16x2(f[6], f[7]));
+    } else {
+      return make_uint4(pack2(to_bits<W>(f[0]), to_bits<W>(f[1])), pack2(to_bits<W>(f[2]), to_bits<W>(f[3])),
+                        pack2(to_bits<W>(f[4]), to_bits<W>(f[5])), pack2(to_bits<W>(f[6]), to_bits<W>(f[7])));
+    }
+  }
+}
+
+// Four consecutive outputs of one row, packed for one LDS write.
+template <typename TO>
+__device__ __forceinline__ void put4(TO* dst, float v0, float v1, float v2, float v3) {
+  if constexpr (sizeof(TO) == 4) {
+    *reinterpret_cast<float4*>(dst) = make_float4(v0, v1, v2, v3);
+  } else if constexpr (__is_same(TO, bf16)) {
+    *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
+  } else {
+    *reinterpret_cast<uint2*>(dst) =
+        make_uint2(pack2(to_bits<f16>(v0), to_bits<f16>(v1)), pack2(to_bits<f16>(v2), to_bits<f16>(v3)));
+  }
+}
+
+// LDS of smallk_kernel: the workgroup's A and W tiles, 128 rows x K 16-bit
+// elements each, 16-byte piece q of row r stored at piece q ^ (r % SW) (SW
+// the largest of 16, 8, 4 dividing K/8) so that the rows of an MFMA fragment
+// read spread over the banks.  16-bit outputs are
+// staged after the tiles (4 waves x 64 rows x 72), so no wave waits for the
+// others before staging.
+template <typename TO, int KS>
+constexpr size_t smallk_tiles_bytes() {
+  return static_cast<size_t>(2 * 128 * 32 * KS * 2);
+}
+template <typename TO, int KS>
+constexpr size_t smallk_lds_bytes() {
+  return smallk_tiles_bytes<TO, KS>() + (sizeof(TO) == 2 ? 4 * 64 * 72 * 2 : 0);
+}
+
 template <typename TA, typename W, typename TO, int KS>
 __global__ void __launch_bounds__(256) smallk_kernel(const GemmParams p) {
-  constexpr int kLdo = 64 + 16 / static_cast<int>(sizeof(TO));  // staged row stride (elements)
-  __shared__ __align__(16) TO stage[4][64 * kLdo];
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  constexpr int K = 32 * KS;
+  constexpr int QPR = K / 8;                                // 16-byte pieces per tile row
+  // XOR swizzle width: a power of two dividing QPR (and 16), so that piece
+  // q ^ (row % SW) stays inside the row and a fragment's rows r16 use r16 % SW.
+  constexpr int SW = QPR % 16 == 0 ? 16 : (QPR % 8 == 0 ? 8 : 4);
+  constexpr int kVec = 16 / static_cast<int>(sizeof(TO));  // outputs per 16-byte store
+  constexpr int kLdo = 64 + kVec;                           // staged output row stride (elements)
+  extern __shared__ __align__(16) unsigned char smem[];
+  unsigned char* tile_a = smem;
+  unsigned char* tile_w = smem + 128 * K * 2;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
   const int64_t tiles_n = (p.N + 127) / 128;
   const int64_t tiles = tiles_n * ((p.M + 127) / 128);
   const int64_t tile = xcd_tile(blockIdx.x, tiles);
-  const int64_t m0 = (tile / tiles_n) * 128 + (wave >> 1) * 64;
-  const int64_t n0 = (tile % tiles_n) * 128 + (wave & 1) * 64;
+  const int64_t mt = (tile / tiles_n) * 128;
+  const int64_t nt = (tile % tiles_n) * 128;
+  const int64_t m0 = mt + (wave >> 1) * 64;
+  const int64_t n0 = nt + (wave & 1) * 64;
   const int r16 = lane & 15;
   const int g = lane >> 4;
-  const int kq = g * 8;
-  const TA* A = static_cast<const TA*>(p.a);
-  const W* Wt = static_cast<const W*>(p.w);
+  const rsrc_t ar = make_rsrc(p.a, p.a_bytes);
+  const rsrc_t wr = make_rsrc(p.w, p.w_bytes);
 
-  u16x8 a[KS][4], b[KS][4];
+  // The tiles, once per workgroup, all loads in flight together.
+  constexpr int kPer = 128 * QPR / 256;  // pieces per thread per tile
+  uint4 va[kPer], vw[kPer];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t m = m0 + 16 * i + r16;
-    const int64_t n = n0 + 16 * i + r16;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      a[s][i] = __builtin_bit_cast(
-          u16x8, m < p.M ? load8<TA, W>(A + m * p.lda, 32 * s + kq) : make_uint4(0, 0, 0, 0));
-      b[s][i] = __builtin_bit_cast(
-          u16x8, n < p.N ? load8<W, W>(Wt + n * p.K, 32 * s + kq) : make_uint4(0, 0, 0, 0));
-    }
+  for (int t = 0; t < kPer; ++t) {
+    const int piece = t * 256 + tid;
+    const int row = piece / QPR, q = piece % QPR;
+    const int64_t m = mt + row, n = nt + row;
+    va[t] = load8_buf<TA, W>(ar, static_cast<uint32_t>(m * p.lda + 8 * q), m < p.M);
+    vw[t] = load8_buf<W, W>(wr, static_cast<uint32_t>(n * K + 8 * q), n < p.N);
   }
+  TO* out = static_cast<TO*>(p.out);
+  const bool full = m0 + 64 <= p.M && n0 + 64 <= p.N && p.N % kVec == 0 &&
+                    (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+  // Bias of this lane's output columns n0 + 16j + 4g .. +3 on full tiles: one
+  // 16-byte (fp32) or 8-byte (16-bit) load per j, the other form out of range
+  // (edge tiles load theirs after the products).
+  const bool is32 = p.bias_dtype == RLM_F32;
+  const bool vec_bias = full && p.bias != nullptr;
+  const rsrc_t br = make_rsrc(p.bias, static_cast<uint32_t>(p.N * (is32 ? 4 : 2)));
+  uint4 bq[4];
+  uint2 bh[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t n = static_cast<uint32_t>(n0 + 16 * j + 4 * g);
+    bq[j] = buf_load_b128(br, vec_bias && is32 ? 4u * n : kNoOffset);
+    bh[j] = buf_load_b64(br, vec_bias && !is32 ? 2u * n : kNoOffset);
+  }
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const int piece = t * 256 + tid;
+    const int row = piece / QPR, q = piece % QPR;
+    const int at = row * (2 * K) + 16 * (q ^ (row % SW));
+    *reinterpret_cast<uint4*>(tile_a + at) = va[t];
+    *reinterpret_cast<uint4*>(tile_w + at) = vw[t];
+  }
+  __syncthreads();
+
+  // Transposed product: acc[i][j] = (W . A^T) tile, so lane (r16, g) holds
+  // out[m0 + 16i + r16][n0 + 16j + 4g + e], four consecutive columns of a row.
   f32x4 acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int ra = (wave >> 1) * 64 + r16, rw = (wave & 1) * 64 + r16;
 #pragma unroll
-  for (int s = 0; s < KS; ++s)
+  for (int s = 0; s < KS; ++s) {
+    const int q = 4 * s + g;  // piece of k = 32s + 8g
+    u16x8 a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[i] = *reinterpret_cast<const u16x8*>(tile_a + (ra + 16 * i) * (2 * K) + 16 * (q ^ (r16 % SW)));
+      b[i] = *reinterpret_cast<const u16x8*>(tile_w + (rw + 16 * i) * (2 * K) + 16 * (q ^ (r16 % SW)));
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<W>(a[s][i], b[s][j], acc[i][j]);
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<W>(b[j], a[i], acc[i][j]);
+  }
 
-  float bv[4];
+  float bv[4][4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int64_t n = n0 + 16 * j + r16;
-    bv[j] = (p.bias && n < p.N) ? load_any_f(p.bias, p.bias_dtype, n) : 0.0f;
+    const uint32_t w16[4] = {bh[j].x & 0xffffu, bh[j].x >> 16, bh[j].y & 0xffffu, bh[j].y >> 16};
+    const uint32_t w32[4] = {bq[j].x, bq[j].y, bq[j].z, bq[j].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (vec_bias) {
+        bv[j][e] = decode_float(FloatWords{w32[e], w16[e]}, p.bias_dtype);
+      } else {
+        const int64_t n = n0 + 16 * j + 4 * g + e;
+        bv[j][e] = (p.bias && n < p.N) ? load_any_f(p.bias, p.bias_dtype, n) : 0.0f;
+      }
+    }
   }
-  TO* out = static_cast<TO*>(p.out);
-  constexpr int kVec = 16 / static_cast<int>(sizeof(TO));  // elements per 16-byte store
-  const bool full = m0 + 64 <= p.M && n0 + 64 <= p.N && p.N % kVec == 0 &&
-                    (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
   if (!full) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int i = 0; i < 4; ++i) {
+      const int64_t m = m0 + 16 * i + r16;
+      if (m >= p.M) continue;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) store_tile<TO>(p, acc[i][j], m0 + 16 * i, n0 + 16 * j + r16, bv[j], lane);
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t n = n0 + 16 * j + 4 * g + e;
+          if (n < p.N) out[m * p.N + n] = from_f32<TO>(acc[i][j][e] + bv[j][e]);
+        }
+    }
     return;
   }
-  // Stage the wave's 64x64 tile in LDS, then write whole 16-byte row pieces.
-  TO* st = stage[wave];
+  if constexpr (sizeof(TO) == 4) {
+    // fp32: a lane's four columns are one 16-byte store.
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<float4*>(out + (m0 + 16 * i + r16) * p.N + n0 + 16 * j + 4 * g) =
+            make_float4(acc[i][j][0] + bv[j][0], acc[i][j][1] + bv[j][1], acc[i][j][2] + bv[j][2],
+                        acc[i][j][3] + bv[j][3]);
+  } else {
+    // 16-bit: stage the wave's 64x64 tile in LDS (8-byte writes), then write
+    // whole 16-byte row pieces.
+    TO* st = reinterpret_cast<TO*>(smem + smallk_tiles_bytes<TO, KS>()) + wave * 64 * kLdo;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        st[(16 * i + 4 * g + e) * kLdo + 16 * j + r16] = from_f32<TO>(acc[i][j][e] + bv[j]);
-  wave_sync();
-  constexpr int kPieces = 64 * 64 / kVec;
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-  for (int t = 0; t < kPieces / kWave; ++t) {
-    const int piece = t * kWave + lane;
-    const int row = piece / (64 / kVec);
-    const int col = (piece % (64 / kVec)) * kVec;
-    *reinterpret_cast<uint4*>(out + (m0 + row) * p.N + n0 + col) =
-        *reinterpret_cast<const uint4*>(st + row * kLdo + col);
+      for (int j = 0; j < 4; ++j)
+        put4<TO>(st + (16 * i + r16) * kLdo + 16 * j + 4 * g, acc[i][j][0] + bv[j][0],
+                 acc[i][j][1] + bv[j][1], acc[i][j][2] + bv[j][2], acc[i][j][3] + bv[j][3]);
+    wave_sync();
+    constexpr int kPieces = 64 * 64 / kVec;
+#pragma unroll
+    for (int t = 0; t < kPieces / kWave; ++t) {
+      const int piece = t * kWave + lane;
+      const int row = piece / (64 / kVec);
+      const int col = (piece % (64 / kVec)) * kVec;
+      *reinterpret_cast<uint4*>(out + (m0 + row) * p.N + n0 + col) =
+          *reinterpret_cast<const uint4*>(st + row * kLdo + col);
+    }
   }
 }
 
@@ -471,13 +595,58 @@ hipError_t launch_typed(const GemmParams& p, hipStream_t s) {
     return launch_status("linear");
   }
   const int64_t big = ((p.M + 127) / 128) * ((p.N + 127) / 128);
-  if (p.K <= 128 && p.K % 32 == 0) {
+  if (p.K <= 128 && p.K % 32 == 0 && p.a_bytes != 0) {
     const dim3 grid(static_cast<unsigned>(big));
     switch (p.K / 32) {
-      case 1: hipLaunchKernelGGL((smallk_kernel<TA, W, TO, 1>), grid, dim3(256), 0, s, p); break;
-      case 2: hipLaunchKernelGGL((smallk_kernel<TA, W, TO, 2>), grid, dim3(256), 0, s, p); break;
-      case 3: hipLaunchKernelGGL((smallk_kernel<TA, W, TO, 3>), grid, dim3(256), 0, s, p); break;
-      default: hipLaunchKernelGGL((smallk_kernel<TA, W, TO, 4>), grid, dim3(256), 0, s, p); break;
+      case 1: {
+        constexpr size_t lds = smallk_lds_bytes<TO, 1>();
+        // The LDS opt-in above 64 KiB is a per-process function attribute.
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&smallk_kernel<TA, W, TO, 1>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (attr != hipSuccess) {
+          set_error("linear: cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(attr));
+          return attr;
+        }
+        hipLaunchKernelGGL((smallk_kernel<TA, W, TO, 1>), grid, dim3(256), lds, s, p);
+        break;
+      }
+      case 2: {
+        constexpr size_t lds = smallk_lds_bytes<TO, 2>();
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&smallk_kernel<TA, W, TO, 2>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (attr != hipSuccess) {
+          set_error("linear: cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(attr));
+          return attr;
+        }
+        hipLaunchKernelGGL((smallk_kernel<TA, W, TO, 2>), grid, dim3(256), lds, s, p);
+        break;
+      }
+      case 3: {
+        constexpr size_t lds = smallk_lds_bytes<TO, 3>();
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&smallk_kernel<TA, W, TO, 3>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (attr != hipSuccess) {
+          set_error("linear: cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(attr));
+          return attr;
+        }
+        hipLaunchKernelGGL((smallk_kernel<TA, W, TO, 3>), grid, dim3(256), lds, s, p);
+        break;
+      }
+      default: {
+        constexpr size_t lds = smallk_lds_bytes<TO, 4>();
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&smallk_kernel<TA, W, TO, 4>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (attr != hipSuccess) {
+          set_error("linear: cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(attr));
+          return attr;
+        }
+        hipLaunchKernelGGL((smallk_kernel<TA, W, TO, 4>), grid, dim3(256), lds, s, p);
+        break;
+      }
     }
     return launch_status("linear");
   }
@@ -527,6 +696,15 @@ hipError_t linear_impl(const rlm_tensor* input, const rlm_tensor* weight, const 
   p.bias = bias ? bias->data : nullptr;
   p.bias_dtype = bias ? bias->dtype : RLM_F32;
   p.out = out->data;
+  {
+    // Byte extents of A (last row counts K elements) and W; 0 marks "too large
+    // for 32-bit buffer offsets" (the tile kernels take it then).
+    const int64_t ab = M > 0 ? ((M - 1) * p.lda + K) * dtype_size(input->dtype) : 0;
+    const int64_t wb = N * K * dtype_size(weight->dtype);
+    const bool fits = ab < (int64_t(1) << 31) && wb < (int64_t(1) << 31);
+    p.a_bytes = fits ? static_cast<uint32_t>(ab) : 0u;
+    p.w_bytes = fits ? static_cast<uint32_t>(wb) : 0u;
+  }
   if (scatter != nullptr) {
     RLM_REQUIRE(M <= kSkinnyM && weight->dtype != RLM_F32,
                 "%s: the cache-row scatter takes at most %d rows and 16-bit weights", what,

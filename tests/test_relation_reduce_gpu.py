@@ -376,17 +376,19 @@ def test_linear_shapes(device, m, n, k):
     assert rel_err(host(gotmix), expmix) <= FP32_REL
 
 
-@pytest.mark.parametrize("m,n,k", [(4096, 1024, 128), (200, 264, 64), (77, 48, 32)])
-def test_linear_small_k_bf16_out(device, m, n, k):
-    """K <= 128 takes the one-round-trip small-K kernel; bf16 output as the expanded cache."""
+@pytest.mark.parametrize("bias_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("m,n,k", [(4096, 1024, 128), (200, 264, 64), (77, 48, 32), (70, 77, 96)])
+def test_linear_small_k_bf16_out(device, m, n, k, bias_dtype):
+    """K <= 128 takes the one-round-trip small-K kernel; bf16 output as the expanded cache.
+    An odd N ends the 16-bit bias mid-dword and leaves partial edge tiles."""
     g = torch.Generator().manual_seed(m + 3 * n + k)
     x = torch.randn(m, k, generator=g).bfloat16()
     w = (torch.randn(n, k, generator=g) * k ** -0.5).bfloat16()
-    bias = torch.randn(n, generator=g) * 0.1
+    bias = (torch.randn(n, generator=g) * 0.1).to(bias_dtype)
     got = relation_linear(x.to(device), w.to(device), bias.to(device))
     torch.cuda.synchronize()
     assert got.dtype == torch.bfloat16 and got.shape == (m, n)
-    expected = ored.linear(x.float().numpy(), w.float().numpy(), bias.numpy())
+    expected = ored.linear(x.float().numpy(), w.float().numpy(), bias.float().numpy())
     assert abs_err(host(got), expected) <= BF16_ABS
     assert abs_err(host(got), ored.round_to(expected, "bfloat16")) <= 2 ** -7 * max(
         1.0, float(np.abs(expected).max()))
