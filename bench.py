@@ -70,6 +70,8 @@ def parse_args():
                     help="time only the cfg3 decode step (B=1 and B=8) and exit")
     ap.add_argument("--multi-only", action="store_true",
                     help="time only the cfg5 routed multi-anchor selection and exit")
+    ap.add_argument("--reduce-only", action="store_true",
+                    help="time only the cfg4 fused reduce in isolation and exit")
     ap.add_argument("--profile-kernels", type=int, default=0, metavar="N",
                     help="run a 256 MiB calibration copy, then each timed kernel N times, and "
                          "exit (the command profiled by rocprofv3 --kernel-trace / --pmc)")
@@ -168,6 +170,7 @@ def main() -> int:
         CONFIGS,
         MULTI_CONFIGS,
         RelationConfig,
+        causal_partner_indices,
         multi_select_args,
         multi_selection_inputs,
         packed_projection_inputs,
@@ -293,8 +296,59 @@ def main() -> int:
             "gathered_GBps": round(gathered / (us * 1e-6) / 1e9, 1),
         }
 
+    def run_reduce_cfg4(repeats=20):
+        """cfg4: the fused reduce in isolation (B=8, T=2048, d 512, hidden 1024, K=8),
+        partners uniform over the causal history, against the unfused three-op chain."""
+        rcfg = CONFIGS["cfg4"]
+        rred = reduce_inputs(rcfg, device=device)
+        rexp = relation_linear(rred["operand_cache"], rred["expanded_weight"],
+                               rred["expanded_bias"])
+        ra, rp, rs, rpos = (x.to(device) for x in causal_partner_indices(rcfg, seed=41))
+
+        def fused_once():
+            return relation_reduce_fused_seq(rexp, rred["operand_cache"], ra, rp,
+                                             rred["product_weight"], rred["second_weight"],
+                                             rred["second_bias"], rs, rred["norm_weight"],
+                                             rred["norm_bias"], rpos, 1e-5)
+
+        def unfused_once():
+            hid = relation_hidden_cached_seq(rexp, rred["operand_cache"], ra, rp,
+                                             rred["product_weight"])
+            raw = relation_linear(hid, rred["second_weight"], rred["second_bias"],
+                                  out_dtype=torch.float32)
+            return relation_norm_reduce_seq(raw, rs, rred["norm_weight"], rred["norm_bias"],
+                                            rpos, 1e-5)
+
+        out = {}
+        for name, fn in (("fused", fused_once), ("unfused", unfused_once)):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            start.record()
+            for _ in range(repeats):
+                fn()
+            end.record()
+            torch.cuda.synchronize()
+            out[name] = start.elapsed_time(end) * 1e3 / repeats
+        flops = algorithmic_flops(rcfg)["relation_reduce_fused"]
+        nbytes = algorithmic_bytes(rcfg)["relation_reduce_fused"]
+        return {
+            "workload": "cfg4 fused reduce in isolation: B=8 T=2048 d=512 hidden 1024 K=8 bf16, "
+                        "partners uniform over the causal history",
+            "us": round(out["fused"], 1),
+            "unfused_us": round(out["unfused"], 1),
+            "queries_per_s": round(rcfg.queries / (out["fused"] * 1e-6), 1),
+            "algorithmic_flops": flops,
+            "tflops": round(flops / (out["fused"] * 1e-6) / 1e12, 1),
+            "mfma_frac": round(flops / (out["fused"] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "algorithmic_bytes": nbytes,
+        }
+
     if args.multi_only:
         print(json.dumps({"multi_anchor_select": run_multi()}), flush=True)
+        return 0
+    if args.reduce_only:
+        print(json.dumps({"fused_reduce_cfg4": run_reduce_cfg4()}), flush=True)
         return 0
 
     if args.decode_only:
@@ -490,6 +544,7 @@ def main() -> int:
     decode = run_decode()
     ring_decode = run_decode(RING_POSITION)
     multi = run_multi()
+    reduce4 = run_reduce_cfg4()
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -531,6 +586,7 @@ def main() -> int:
         "decode_step_us": decode,
         "ring_decode_step_us": {"position": RING_POSITION, "cache_rows": 512, **ring_decode},
         "multi_anchor_select": multi,
+        "fused_reduce_cfg4": reduce4,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

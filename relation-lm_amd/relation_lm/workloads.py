@@ -255,3 +255,22 @@ def packed_projection_inputs(cfg: RelationConfig, *, device="cpu", seed: int | N
     weights = tuple(_randn(g, w, cfg.d_model, scale=cfg.d_model ** -0.5, dtype=cfg.dtype)
                     for w in widths)
     return memory.to(device), tuple(w.to(device) for w in weights)
+
+
+def causal_partner_indices(cfg: RelationConfig, seed: int):
+    """Config-4 style reduce inputs: per query one anchor and K partners drawn
+    uniformly over the causal history [0, t], partners distinct from the anchor,
+    and N(0,1) partner scores.  Query 0 has no position besides its anchor, so
+    its partner slots carry the select op's sentinel (t - local_window + 1, -inf).
+    Returns (anchor [B,T] int32, partner [B,T,K] int32, scores [B,T,K], positions [T])
+    on the CPU."""
+    g = _gen(seed)
+    B, T, K = cfg.batch, cfg.context, cfg.k_out
+    pos = torch.arange(T)
+    anchor = (torch.rand(B, T, generator=g) * (pos + 1)).long()
+    draw = (torch.rand(B, T, K, generator=g) * pos[None, :, None].clamp(min=1)).long()
+    partner = draw + (draw >= anchor[:, :, None]).long()  # uniform over [0, t] without the anchor
+    scores = torch.randn(B, T, K, generator=g)
+    partner[:, 0, :] = 0 - cfg.local_window + 1
+    scores[:, 0, :] = -torch.inf
+    return anchor.int(), partner.int(), scores, pos

@@ -23,7 +23,7 @@ from relation_lm.kernels.relation_reduce import (
     relation_norm_reduce_seq,
     relation_reduce_fused_seq,
 )
-from relation_lm.workloads import CONFIGS, RelationConfig, reduce_inputs
+from relation_lm.workloads import CONFIGS, RelationConfig, causal_partner_indices, reduce_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -159,3 +159,27 @@ def test_fused_rejects_unsupported_shapes(device):
                                   red["second_weight"].float(), red["second_bias"], scores,
                                   red["norm_weight"], red["norm_bias"],
                                   torch.arange(4, device=device), 1e-5)
+
+
+def test_cfg4_fused_reduce(device):
+    """Config 4 shape: B=8, T=2048, d_model 512, hidden 1024, K=8 -- the full run
+    against the unfused chain, a sample of queries against the float64 oracle."""
+    cfg = CONFIGS["cfg4"]
+    red = reduce_inputs(cfg, device=device)
+    expanded = relation_linear(red["operand_cache"], red["expanded_weight"], red["expanded_bias"])
+    anchor, partner, scores, pos = causal_partner_indices(cfg, seed=41)
+    assert bool((partner[:, 1:] != anchor[:, 1:, None]).all())
+    assert bool(((partner[:, 1:] >= 0) & (partner[:, 1:] <= pos[None, 1:, None])).all())
+    fused = run_fused(red, expanded, anchor, partner, scores, pos, device)
+    unfused = run_unfused(red, expanded, anchor, partner, scores, pos, device)
+    torch.cuda.synchronize()
+    assert fused.shape == (cfg.batch, cfg.context, cfg.d_model)
+    assert bool(torch.isfinite(fused).all())
+    assert abs_err(host(fused), host(unfused)) <= TIGHT_ABS
+    sample = np.array([0, 1, 2, 7, 8, 63, 64, 511, 1024, 1500, 2046, 2047])
+    for b in (0, cfg.batch - 1):
+        rows = slice(b, b + 1)
+        expected = oracle_chain(red, expanded, host(anchor)[:, sample], host(partner)[:, sample],
+                                host(scores)[:, sample], sample, rows)
+        got = host(fused)[b:b + 1, sample]
+        assert abs_err(got, expected) <= TIGHT_ABS, b
