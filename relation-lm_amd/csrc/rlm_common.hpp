@@ -121,6 +121,16 @@ __device__ __forceinline__ uint16_t buf_load_b16(rsrc_t r, uint32_t off) {
 __device__ __forceinline__ void buf_store_f32(float v, rsrc_t r, uint32_t off) {
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
 }
+// A wave-uniform condition that the compiler must treat as lane-varying.
+// Selects on a uniform condition may be turned into a branch with the loads
+// that feed one side sunk into it (each branch join then waits for its
+// load); on a lane-varying condition they stay v_cndmask.  Costs one v_mov.
+__device__ __forceinline__ bool varying(bool c) {
+  uint32_t z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return c != (z != 0u);
+}
+
 // Branch-free loads of one int32 / int64 index (low word always, high word only
 // for int64: the other load gets an out-of-range offset and reads 0) and of one
 // fp32 / bf16 / fp16 element (a 4-byte and a 2-byte load, the one that does not

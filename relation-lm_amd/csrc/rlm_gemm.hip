@@ -469,44 +469,78 @@ __global__ void __launch_bounds__(256) smallk_kernel(const GemmParams p) {
 // ---------------------------------------------------------------------------
 
 constexpr int kSkinnyWaves = 8;
-constexpr int kSkinnyBatch = 9;  // k-slices whose loads a wave issues together (K = 2304: one round trip)
+// k-slices whose loads a wave issues together: 9 covers K = 2304 in one round
+// trip; K <= 768 (the 576-wide packed projection) needs only 3 per wave.
+constexpr int kSkinnyBatchLong = 9;
+constexpr int kSkinnyBatchShort = 3;
 
 // One 16x16 output tile per workgroup (grid: N/16 x M/16).  The 8 waves split
 // K into 32-wide slices (wave w takes slices w, w+8, ...); each wave issues
 // the A and W fragment loads of up to kSkinnyBatch slices at once, so a wave
 // pays about one memory round trip per batch, and the 8 partial tiles are
 // summed in LDS in a fixed order.
-template <typename TA, typename W, typename TO>
+template <typename TA, typename W, typename TO, int kSkinnyBatch>
 __global__ void __launch_bounds__(kSkinnyWaves * kWave) skinny_kernel(const GemmParams p) {
   __shared__ f32x4 part[kSkinnyWaves][kWave];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform: scalar branches below
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 16;
   const int r16 = lane & 15;
   const int kq = (lane >> 4) * 8;
-  const TA* A = static_cast<const TA*>(p.a);
-  const W* Wt = static_cast<const W*>(p.w);
   const bool n_ok = n0 + r16 < p.N;
   const bool m_ok = m0 + r16 < p.M;
-  const W* wrow = Wt + (n_ok ? (n0 + r16) * p.K : 0);
-  const TA* arow = A + (m_ok ? (m0 + r16) * p.lda : 0);
+  const rsrc_t ar = make_rsrc(p.a, p.a_bytes);
+  const rsrc_t wr = make_rsrc(p.w, p.w_bytes);
+  const uint32_t arow = static_cast<uint32_t>((m0 + r16) * p.lda * static_cast<int64_t>(sizeof(TA)));
+  const uint32_t wrow = static_cast<uint32_t>((n0 + r16) * p.K * static_cast<int64_t>(sizeof(W)));
   f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const int64_t slices = (p.K + kBK - 1) / kBK;
   for (int64_t s0 = wave; s0 < slices; s0 += kSkinnyWaves * kSkinnyBatch) {
-    uint4 a[kSkinnyBatch], b[kSkinnyBatch];
+    // All raw loads of the batch first (from clamped, valid addresses: no
+    // branch), then the conversions and products, so the wave pays one memory
+    // round trip per batch.  fp32 inputs are two 16-byte loads per fragment.
+    constexpr int kAParts = sizeof(TA) == 4 ? 2 : 1;
+    // Range-checked buffer loads: rows past M or N and slots past K get an
+    // out-of-range offset (no memory access, zeros), so there is no branch and
+    // no dummy traffic.
+    uint4 araw[kSkinnyBatch][kAParts], braw[kSkinnyBatch];
 #pragma unroll
     for (int u = 0; u < kSkinnyBatch; ++u) {
       // K is a multiple of 8, so an 8-element chunk is either wholly inside or past K.
       const int64_t k = (s0 + u * kSkinnyWaves) * kBK + kq;
       const bool in = k < p.K;
-      b[u] = (n_ok && in) ? load8<W, W>(wrow, k) : make_uint4(0, 0, 0, 0);
-      a[u] = (m_ok && in) ? load8<TA, W>(arow, k) : make_uint4(0, 0, 0, 0);
-    }
+      const uint32_t kb = static_cast<uint32_t>(in ? k : 0);
+      braw[u] = buf_load_b128(wr, n_ok && in ? wrow + kb * static_cast<uint32_t>(sizeof(W)) : kNoOffset);
 #pragma unroll
-    for (int u = 0; u < kSkinnyBatch; ++u)
-      acc = mfma16<W>(__builtin_bit_cast(u16x8, a[u]), __builtin_bit_cast(u16x8, b[u]), acc);
+      for (int h = 0; h < kAParts; ++h)
+        araw[u][h] = buf_load_b128(
+            ar, m_ok && in ? arow + (kb + 4 * h) * static_cast<uint32_t>(sizeof(TA)) : kNoOffset);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kSkinnyBatch; ++u) {
+      uint4 av;
+      if constexpr (kAParts == 1) {
+        av = araw[u][0];
+      } else {
+        const uint4 x = araw[u][0], y = araw[u][1];
+        if constexpr (__is_same(W, bf16)) {
+          av = make_uint4(pack_bf16x2(__uint_as_float(x.x), __uint_as_float(x.y)),
+                          pack_bf16x2(__uint_as_float(x.z), __uint_as_float(x.w)),
+                          pack_bf16x2(__uint_as_float(y.x), __uint_as_float(y.y)),
+                          pack_bf16x2(__uint_as_float(y.z), __uint_as_float(y.w)));
+        } else {
+          av = make_uint4(pack2(to_bits<W>(__uint_as_float(x.x)), to_bits<W>(__uint_as_float(x.y))),
+                          pack2(to_bits<W>(__uint_as_float(x.z)), to_bits<W>(__uint_as_float(x.w))),
+                          pack2(to_bits<W>(__uint_as_float(y.x)), to_bits<W>(__uint_as_float(y.y))),
+                          pack2(to_bits<W>(__uint_as_float(y.z)), to_bits<W>(__uint_as_float(y.w))));
+        }
+      }
+      // Out-of-range loads already read zeros.
+      acc = mfma16<W>(__builtin_bit_cast(u16x8, av), __builtin_bit_cast(u16x8, braw[u]), acc);
+    }
   }
   part[wave][lane] = acc;
   __syncthreads();
@@ -589,9 +623,14 @@ __global__ void __launch_bounds__(256) f32_tile_kernel(const GemmParams p) {
 
 template <typename TA, typename W, typename TO>
 hipError_t launch_typed(const GemmParams& p, hipStream_t s) {
-  if (p.M <= kSkinnyM) {
+  if (p.M <= kSkinnyM && p.a_bytes != 0) {
     const dim3 grid(static_cast<unsigned>((p.N + 15) / 16), static_cast<unsigned>((p.M + 15) / 16));
-    hipLaunchKernelGGL((skinny_kernel<TA, W, TO>), grid, dim3(kSkinnyWaves * kWave), 0, s, p);
+    if (p.K <= kSkinnyWaves * kSkinnyBatchShort * kBK)
+      hipLaunchKernelGGL((skinny_kernel<TA, W, TO, kSkinnyBatchShort>), grid,
+                         dim3(kSkinnyWaves * kWave), 0, s, p);
+    else
+      hipLaunchKernelGGL((skinny_kernel<TA, W, TO, kSkinnyBatchLong>), grid,
+                         dim3(kSkinnyWaves * kWave), 0, s, p);
     return launch_status("linear");
   }
   const int64_t big = ((p.M + 127) / 128) * ((p.N + 127) / 128);
@@ -706,6 +745,7 @@ hipError_t linear_impl(const rlm_tensor* input, const rlm_tensor* weight, const 
     p.w_bytes = fits ? static_cast<uint32_t>(wb) : 0u;
   }
   if (scatter != nullptr) {
+    RLM_REQUIRE(p.a_bytes != 0, "%s: the cache-row scatter needs the input within 2 GiB", what);
     RLM_REQUIRE(M <= kSkinnyM && weight->dtype != RLM_F32,
                 "%s: the cache-row scatter takes at most %d rows and 16-bit weights", what,
                 kSkinnyM);

@@ -457,7 +457,47 @@ struct NormParams {
 // active = rank < k_limit and score > -1e30, p = softmax(where(active, s, -1e4)) * active,
 // renormalised by max(sum, 1e-9) (relation_reduce.py:399-411).
 __device__ __forceinline__ float partner_score(const NormParams& p, int64_t q, int lane) {
-  return lane < p.K ? p.scores[q * p.K + lane] : -INFINITY;
+  const float s = p.scores[q * p.K + (lane < p.K ? lane : 0)];  // unconditional: no branch
+  return lane < p.K ? s : -INFINITY;
+}
+
+// Unconditional (branch-free) loads of one int32/int64 index and of four
+// consecutive fp32/bf16/fp16 elements: both dtype interpretations are read
+// from in-bounds addresses (the unused one from element 0) and the result is
+// selected, so no load waits at a dtype branch.  `f4_issue` needs >= 4 elements.
+__device__ __forceinline__ int64_t index_at(const void* base, int dtype, int64_t i) {
+  const uint32_t* w = static_cast<const uint32_t*>(base);
+  const bool is64 = varying(dtype == RLM_I64);
+  const uint32_t lo = w[is64 ? 2 * i : i];
+  const uint32_t hi = w[is64 ? 2 * i + 1 : i];
+  // int32: the high word is lo's sign; one expression for both dtypes.
+  const uint32_t top = is64 ? hi : static_cast<uint32_t>(static_cast<int32_t>(lo) >> 31);
+  return static_cast<int64_t>((static_cast<uint64_t>(top) << 32) | lo);
+}
+struct F4Words {
+  uint2 a, b;  // fp32 reading (16 bytes)
+  uint2 h;     // 16-bit reading (8 bytes)
+};
+__device__ __forceinline__ F4Words f4_issue(const void* base, int dtype, int64_t i4) {
+  const bool is32 = varying(dtype == RLM_F32);
+  const uint2* w = static_cast<const uint2*>(base);
+  return {w[is32 ? 2 * i4 : 0], w[is32 ? 2 * i4 + 1 : 0], w[is32 ? 0 : i4]};
+}
+__device__ __forceinline__ float4 f4_decode(const F4Words& v, int dtype) {
+  // Both interpretations computed, one selected per element (selects, not
+  // branches, so the loads stay where they are issued).
+  const bool is32 = varying(dtype == RLM_F32);
+  const bool isbf = varying(dtype == RLM_BF16);
+  const uint32_t w32[4] = {v.a.x, v.a.y, v.b.x, v.b.y};
+  const uint32_t e[4] = {v.h.x & 0xffffu, v.h.x >> 16, v.h.y & 0xffffu, v.h.y >> 16};
+  float f[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float fb = __uint_as_float(e[k] << 16);
+    const float fh = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(e[k])));
+    f[k] = is32 ? __uint_as_float(w32[k]) : (isbf ? fb : fh);
+  }
+  return make_float4(f[0], f[1], f[2], f[3]);
 }
 // s: this lane's partner score (partner_score), loaded by the caller.
 __device__ __forceinline__ float partner_weight(const NormParams& p, float s, int64_t t,
@@ -497,43 +537,49 @@ __global__ void __launch_bounds__(256) norm_reduce_vec_kernel(const NormParams p
   const int64_t b = q / p.Tq;
   const int64_t tq = q - b * p.Tq;
   // Every load of the query is issued before any is used: position, scores,
-  // gamma / beta, and the first KB partner rows (one memory round trip).
-  const int64_t t = load_any_i(p.pos, p.pos_dtype, b * p.pos_sb + tq * p.pos_sq);
+  // gamma / beta, and the first KB partner rows (one memory round trip; the
+  // loads are unconditional, from in-bounds addresses, so none waits at a branch).
+  const int64_t t = index_at(p.pos, p.pos_dtype, b * p.pos_sb + tq * p.pos_sq);
   const float score = partner_score(p, q, lane);
   const int groups = p.D >> 2;
   const TR* raw = static_cast<const TR*>(p.raw) + q * p.K * static_cast<int64_t>(p.D);
 
-  float4 gam[G], bet[G], ctx[G];
+  F4Words gw[G], bw[G];
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int g = lane + kWave * i;
-    float4 w4 = make_float4(0.f, 0.f, 0.f, 0.f), b4 = w4;
-    if (g < groups) {
-      w4 = make_float4(load_any_f(p.w, p.w_dtype, 4 * g), load_any_f(p.w, p.w_dtype, 4 * g + 1),
-                       load_any_f(p.w, p.w_dtype, 4 * g + 2), load_any_f(p.w, p.w_dtype, 4 * g + 3));
-      b4 = make_float4(load_any_f(p.bias, p.b_dtype, 4 * g),
-                       load_any_f(p.bias, p.b_dtype, 4 * g + 1),
-                       load_any_f(p.bias, p.b_dtype, 4 * g + 2),
-                       load_any_f(p.bias, p.b_dtype, 4 * g + 3));
-    }
-    gam[i] = w4;
-    bet[i] = b4;
-    ctx[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    gw[i] = f4_issue(p.w, p.w_dtype, g < groups ? g : 0);
+    bw[i] = f4_issue(p.bias, p.b_dtype, g < groups ? g : 0);
   }
-  const float inv_d = 1.0f / static_cast<float>(p.D);
-  float prob = 0.0f;
-  for (int k0 = 0; k0 < p.K; k0 += KB) {
-    float4 x[KB][G];
+  // Partner rows in batches of KB; the first batch is issued before anything
+  // is decoded, so position, scores, gamma / beta and these rows share one
+  // memory round trip.
+  float4 x[KB][G];
+  auto load_batch = [&](int k0) {
 #pragma unroll
     for (int kk = 0; kk < KB; ++kk)
 #pragma unroll
       for (int i = 0; i < G; ++i) {
         const int g = lane + kWave * i;
-        x[kk][i] = (k0 + kk < p.K && g < groups)
-                       ? load_raw4(raw + static_cast<int64_t>(k0 + kk) * p.D + 4 * g)
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        const bool in = k0 + kk < p.K && g < groups;
+        const float4 v = load_raw4(raw + static_cast<int64_t>(in ? k0 + kk : 0) * p.D + 4 * (in ? g : 0));
+        x[kk][i] = in ? v : make_float4(0.f, 0.f, 0.f, 0.f);
       }
-    if (k0 == 0) prob = partner_weight(p, score, t, lane);
+  };
+  load_batch(0);
+  float4 gam[G], bet[G], ctx[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int g = lane + kWave * i;
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+    gam[i] = g < groups ? f4_decode(gw[i], p.w_dtype) : zero;
+    bet[i] = g < groups ? f4_decode(bw[i], p.b_dtype) : zero;
+    ctx[i] = zero;
+  }
+  const float inv_d = 1.0f / static_cast<float>(p.D);
+  const float prob = partner_weight(p, score, t, lane);
+  for (int k0 = 0; k0 < p.K; k0 += KB) {
+    if (k0 > 0) load_batch(k0);
 #pragma unroll
     for (int kk = 0; kk < KB; ++kk) {
       if (k0 + kk >= p.K) break;
