@@ -168,6 +168,45 @@ __device__ __forceinline__ float decode_float(FloatWords w, int dtype) {
                           : (dtype == RLM_BF16 ? __uint_as_float(w.w16 << 16) : fh);
 }
 
+// Unconditional (branch-free) loads of one int32/int64 index and of four
+// consecutive fp32/bf16/fp16 elements: both dtype interpretations are read
+// from in-bounds addresses (the unused one from element 0) and the result is
+// selected, so no load waits at a dtype branch.  `f4_issue` needs >= 4 elements.
+__device__ __forceinline__ int64_t index_at(const void* base, int dtype, int64_t i) {
+  const uint32_t* w = static_cast<const uint32_t*>(base);
+  const bool is64 = varying(dtype == RLM_I64);
+  const uint32_t lo = w[is64 ? 2 * i : i];
+  const uint32_t hi = w[is64 ? 2 * i + 1 : i];
+  // int32: the high word is lo's sign; one expression for both dtypes.
+  const uint32_t top = is64 ? hi : static_cast<uint32_t>(static_cast<int32_t>(lo) >> 31);
+  return static_cast<int64_t>((static_cast<uint64_t>(top) << 32) | lo);
+}
+struct F4Words {
+  uint2 a, b;  // fp32 reading (16 bytes)
+  uint2 h;     // 16-bit reading (8 bytes)
+};
+__device__ __forceinline__ F4Words f4_issue(const void* base, int dtype, int64_t i4) {
+  const bool is32 = varying(dtype == RLM_F32);
+  const uint2* w = static_cast<const uint2*>(base);
+  return {w[is32 ? 2 * i4 : 0], w[is32 ? 2 * i4 + 1 : 0], w[is32 ? 0 : i4]};
+}
+__device__ __forceinline__ float4 f4_decode(const F4Words& v, int dtype) {
+  // Both interpretations computed, one selected per element (selects, not
+  // branches, so the loads stay where they are issued).
+  const bool is32 = varying(dtype == RLM_F32);
+  const bool isbf = varying(dtype == RLM_BF16);
+  const uint32_t w32[4] = {v.a.x, v.a.y, v.b.x, v.b.y};
+  const uint32_t e[4] = {v.h.x & 0xffffu, v.h.x >> 16, v.h.y & 0xffffu, v.h.y >> 16};
+  float f[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float fb = __uint_as_float(e[k] << 16);
+    const float fh = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(e[k])));
+    f[k] = is32 ? __uint_as_float(w32[k]) : (isbf ? fb : fh);
+  }
+  return make_float4(f[0], f[1], f[2], f[3]);
+}
+
 // One element of type T at byte offset `off`, as float.
 template <typename T>
 __device__ __forceinline__ float buf_load_elem(rsrc_t r, uint32_t off);

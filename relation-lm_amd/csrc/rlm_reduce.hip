@@ -77,27 +77,29 @@ __device__ __forceinline__ void load_rows(const HiddenParams& p, int64_t r0, Row
   const int tid = threadIdx.x;
   if (tid < kRows) {
     const int64_t row = r0 + tid;
-    int32_t b = 0, a = -1, pp = -1;
-    if (row < p.rows) {
-      const int64_t q = row / p.K;
-      b = static_cast<int32_t>(q / p.Tq);
-      const int64_t ai = load_any_i(p.anchor, p.index_dtype_a, q);
-      const int64_t pi = load_any_i(p.partner, p.index_dtype_p, row);
-      // Valid index range [lo, hi).  Ring caches (row p mod T): any position
-      // below 2^31, and in the update form only the resident [t-T+1, t] --
-      // an older index would alias the row this launch rewrites.
-      int64_t lo = 0, hi = p.T;
-      if (p.ring) {
-        hi = int64_t(1) << 31;
-        if (p.pos != nullptr) {
-          const int64_t t = load_any_i(p.pos, p.pos_dtype, 0);
-          lo = t - p.T + 1 > 0 ? t - p.T + 1 : 0;
-          hi = t + 1 < hi ? t + 1 : hi;
-        }
+    // Unconditional loads (padding rows read row 0, the position a stand-in
+    // when there is none), decoded by selects: one round trip.
+    const bool live = row < p.rows;
+    const int64_t rowc = live ? row : 0;
+    const int64_t q = rowc / p.K;
+    const int32_t b = live ? static_cast<int32_t>(q / p.Tq) : 0;
+    const int64_t ai = index_at(p.anchor, p.index_dtype_a, q);
+    const int64_t pi = index_at(p.partner, p.index_dtype_p, rowc);
+    const bool has_pos = p.pos != nullptr;
+    const int64_t tp = index_at(has_pos ? p.pos : p.anchor, has_pos ? p.pos_dtype : p.index_dtype_a, 0);
+    // Valid index range [lo, hi).  Ring caches (row p mod T): any position
+    // below 2^31, and in the update form only the resident [t-T+1, t] --
+    // an older index would alias the row this launch rewrites.
+    int64_t lo = 0, hi = p.T;
+    if (p.ring) {
+      hi = int64_t(1) << 31;
+      if (has_pos) {
+        lo = tp - p.T + 1 > 0 ? tp - p.T + 1 : 0;
+        hi = tp + 1 < hi ? tp + 1 : hi;
       }
-      a = (ai >= lo && ai < hi) ? static_cast<int32_t>(ai) : -1;
-      pp = (pi >= lo && pi < hi) ? static_cast<int32_t>(pi) : -1;
     }
+    const int32_t a = (live && ai >= lo && ai < hi) ? static_cast<int32_t>(ai) : -1;
+    const int32_t pp = (live && pi >= lo && pi < hi) ? static_cast<int32_t>(pi) : -1;
     const uint32_t base = static_cast<uint32_t>(b) * static_cast<uint32_t>(p.T);
     const uint32_t mask = p.ring ? static_cast<uint32_t>(p.T - 1) : 0xffffffffu;
     const uint32_t ra = static_cast<uint32_t>(a) & mask, rp = static_cast<uint32_t>(pp) & mask;
@@ -121,37 +123,90 @@ __device__ __forceinline__ void load_rows(const HiddenParams& p, int64_t r0, Row
 template <typename T>
 __device__ void fresh_rows(const HiddenParams& p, int64_t t, int64_t b_first, int nb, int n0,
                            int cols, float* fresh) {
+  // Eight lanes share one dot; a lane takes 8-element chunks j, j+8, ...
+  // Every weight, operand-row and bias load of kIB items is issued before any
+  // is used (unconditional, from clamped addresses), so the items cost one
+  // memory round trip instead of one per chunk.
+  constexpr int EW = sizeof(T) == 4 ? 2 : 1;  // 16-byte pieces per 8-element chunk
+  constexpr int kIB = 4;                      // items per group in flight together
+  constexpr int kCH = 2;                      // chunks per lane per pass (R <= 128: one pass)
   const int tid = threadIdx.x;
   const int j = tid & 7;
   const int group = tid >> 3;
   const int groups = blockDim.x >> 3;
   const int items = nb * 2 * cols;
   const int chunks = p.R / 8;
-  for (int base = 0; base < items; base += groups) {
-    const int item = base + group;
-    const bool live = item < items;
-    const int c = live ? item % cols : 0;
-    const int half = live ? (item / cols) % 2 : 0;
-    const int bi = live ? item / (2 * cols) : 0;
-    const int n = n0 + c;
-    float acc = 0.0f;
-    if (live && n < p.H) {
-      const T* w = static_cast<const T*>(half == 0 ? p.wa : p.wp) + static_cast<int64_t>(n) * p.R;
-      const int64_t row = p.ring ? (t & (p.T - 1)) : t;
-      const T* op = static_cast<const T*>(p.operand) + ((b_first + bi) * p.T + row) * p.R;
-      for (int ch = j; ch < chunks; ch += 8) {
-        const float4 w0 = load4(w + 8 * ch), w1 = load4(w + 8 * ch + 4);
-        const float4 o0 = load4(op + 8 * ch), o1 = load4(op + 8 * ch + 4);
-        acc += w0.x * o0.x + w0.y * o0.y + w0.z * o0.z + w0.w * o0.w;
-        acc += w1.x * o1.x + w1.y * o1.y + w1.z * o1.z + w1.w * o1.w;
-      }
+  const int64_t row = p.ring ? (t & (p.T - 1)) : t;
+  for (int base = 0; base < items; base += groups * kIB) {
+    const unsigned char* wrow[kIB];
+    const unsigned char* orow[kIB];
+    bool ok[kIB];
+    int half[kIB];
+    float bias[kIB], acc[kIB];
+#pragma unroll
+    for (int ib = 0; ib < kIB; ++ib) {
+      const int item = base + group + groups * ib;
+      const int it = item < items ? item : 0;
+      const int c = it % cols;
+      half[ib] = (it / cols) % 2;
+      const int bi = it / (2 * cols);
+      const int n = n0 + c;
+      ok[ib] = item < items && n < p.H;
+      const int nc = n < p.H ? n : 0;
+      wrow[ib] = static_cast<const unsigned char*>(half[ib] == 0 ? p.wa : p.wp) +
+                 static_cast<int64_t>(nc) * p.R * sizeof(T);
+      orow[ib] = static_cast<const unsigned char*>(p.operand) +
+                 ((b_first + bi) * p.T + row) * p.R * sizeof(T);
+      bias[ib] = to_f32(static_cast<const T*>(p.b1)[nc]);
+      acc[ib] = 0.0f;
     }
-    acc += __shfl_xor(acc, 1, 8);
-    acc += __shfl_xor(acc, 2, 8);
-    acc += __shfl_xor(acc, 4, 8);
-    if (live && j == 0) {
-      if (half == 0 && n < p.H) acc += to_f32(static_cast<const T*>(p.b1)[n]);
-      fresh[item] = acc;
+    for (int c0 = 0; c0 < chunks; c0 += 8 * kCH) {
+      uint4 wv[kIB][kCH][EW], ov[kIB][kCH][EW];
+#pragma unroll
+      for (int ib = 0; ib < kIB; ++ib)
+#pragma unroll
+        for (int cc = 0; cc < kCH; ++cc) {
+          const int ch = c0 + j + 8 * cc;
+          const int chc = ch < chunks ? ch : 0;
+#pragma unroll
+          for (int e = 0; e < EW; ++e) {
+            wv[ib][cc][e] = *reinterpret_cast<const uint4*>(wrow[ib] + (chc * EW + e) * 16);
+            ov[ib][cc][e] = *reinterpret_cast<const uint4*>(orow[ib] + (chc * EW + e) * 16);
+          }
+        }
+#pragma unroll
+      for (int ib = 0; ib < kIB; ++ib)
+#pragma unroll
+        for (int cc = 0; cc < kCH; ++cc) {
+          const bool in = ok[ib] && c0 + j + 8 * cc < chunks;
+          float d = 0.0f;
+          if constexpr (EW == 1) {
+            const uint32_t w4[4] = {wv[ib][cc][0].x, wv[ib][cc][0].y, wv[ib][cc][0].z, wv[ib][cc][0].w};
+            const uint32_t o4[4] = {ov[ib][cc][0].x, ov[ib][cc][0].y, ov[ib][cc][0].z, ov[ib][cc][0].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              d += __uint_as_float(w4[k] << 16) * __uint_as_float(o4[k] << 16);
+              d += __uint_as_float(w4[k] & 0xffff0000u) * __uint_as_float(o4[k] & 0xffff0000u);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < EW; ++e) {
+              const uint4 w4 = wv[ib][cc][e], o4 = ov[ib][cc][e];
+              d += __uint_as_float(w4.x) * __uint_as_float(o4.x) + __uint_as_float(w4.y) * __uint_as_float(o4.y);
+              d += __uint_as_float(w4.z) * __uint_as_float(o4.z) + __uint_as_float(w4.w) * __uint_as_float(o4.w);
+            }
+          }
+          acc[ib] += in ? d : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int ib = 0; ib < kIB; ++ib) {
+      float v = acc[ib];
+      v += __shfl_xor(v, 1, 8);
+      v += __shfl_xor(v, 2, 8);
+      v += __shfl_xor(v, 4, 8);
+      const int item = base + group + groups * ib;
+      if (ok[ib] && j == 0) fresh[item] = half[ib] == 0 ? v + bias[ib] : v;
     }
   }
   __syncthreads();
@@ -217,11 +272,11 @@ __device__ __forceinline__ void store_hidden(const HiddenParams& p, rsrc_t outr,
 // Update-form set-up shared by both kernels: position, the batch range of the
 // tile and the fresh rows (computed, and stored to the cache by the owning tile).
 template <typename T, bool UPDATE>
-__device__ __forceinline__ int64_t update_setup(const HiddenParams& p, int64_t r0, int n0,
-                                                int cols, int64_t& b_first, float* fresh) {
+__device__ __forceinline__ int64_t update_setup(const HiddenParams& p, int64_t t, int64_t r0,
+                                                int n0, int cols, int64_t& b_first, float* fresh) {
+  // t: the position, loaded by the caller before the row table.
   b_first = 0;
   if (!UPDATE) return -1;
-  int64_t t = load_any_i(p.pos, p.pos_dtype, 0);
   // Out-of-range position: nothing to write or reuse (ring caches: t < 0 only).
   if (t < 0 || (!p.ring && t >= p.T) || t >= (int64_t(1) << 31)) t = -1;
   const int64_t QK = p.Tq * p.K;
@@ -255,9 +310,10 @@ __global__ void __launch_bounds__(256) hidden_bf16_kernel(const HiddenParams p) 
   const rsrc_t opr = make_rsrc(p.operand, p.operand_bytes);
   const rsrc_t wr_ = make_rsrc(p.wm, p.wm_bytes);
   const rsrc_t outr = make_rsrc(p.out, p.out_bytes);
+  const int64_t t_pos = UPDATE ? index_at(p.pos, p.pos_dtype, 0) : -1;  // beside the row loads
   load_rows<bf16>(p, r0, rt);
   int64_t b_first;
-  const int64_t t = update_setup<bf16, UPDATE>(p, r0, n0, BN, b_first, fresh);
+  const int64_t t = update_setup<bf16, UPDATE>(p, t_pos, r0, n0, BN, b_first, fresh);
   __syncthreads();
 
   const int wr = (wave >> 1) * 32;
@@ -377,9 +433,10 @@ __global__ void __launch_bounds__(256) hidden_f32_kernel(const HiddenParams p) {
   const rsrc_t opr = make_rsrc(p.operand, p.operand_bytes);
   const rsrc_t wr_ = make_rsrc(p.wm, p.wm_bytes);
   const rsrc_t outr = make_rsrc(p.out, p.out_bytes);
+  const int64_t t_pos = UPDATE ? index_at(p.pos, p.pos_dtype, 0) : -1;  // beside the row loads
   load_rows<T>(p, r0, rt);
   int64_t b_first;
-  const int64_t t = update_setup<T, UPDATE>(p, r0, n0, BN, b_first, fresh);
+  const int64_t t = update_setup<T, UPDATE>(p, t_pos, r0, n0, BN, b_first, fresh);
   __syncthreads();
 
   const int wr = (wave >> 1) * 32;
@@ -461,44 +518,6 @@ __device__ __forceinline__ float partner_score(const NormParams& p, int64_t q, i
   return lane < p.K ? s : -INFINITY;
 }
 
-// Unconditional (branch-free) loads of one int32/int64 index and of four
-// consecutive fp32/bf16/fp16 elements: both dtype interpretations are read
-// from in-bounds addresses (the unused one from element 0) and the result is
-// selected, so no load waits at a dtype branch.  `f4_issue` needs >= 4 elements.
-__device__ __forceinline__ int64_t index_at(const void* base, int dtype, int64_t i) {
-  const uint32_t* w = static_cast<const uint32_t*>(base);
-  const bool is64 = varying(dtype == RLM_I64);
-  const uint32_t lo = w[is64 ? 2 * i : i];
-  const uint32_t hi = w[is64 ? 2 * i + 1 : i];
-  // int32: the high word is lo's sign; one expression for both dtypes.
-  const uint32_t top = is64 ? hi : static_cast<uint32_t>(static_cast<int32_t>(lo) >> 31);
-  return static_cast<int64_t>((static_cast<uint64_t>(top) << 32) | lo);
-}
-struct F4Words {
-  uint2 a, b;  // fp32 reading (16 bytes)
-  uint2 h;     // 16-bit reading (8 bytes)
-};
-__device__ __forceinline__ F4Words f4_issue(const void* base, int dtype, int64_t i4) {
-  const bool is32 = varying(dtype == RLM_F32);
-  const uint2* w = static_cast<const uint2*>(base);
-  return {w[is32 ? 2 * i4 : 0], w[is32 ? 2 * i4 + 1 : 0], w[is32 ? 0 : i4]};
-}
-__device__ __forceinline__ float4 f4_decode(const F4Words& v, int dtype) {
-  // Both interpretations computed, one selected per element (selects, not
-  // branches, so the loads stay where they are issued).
-  const bool is32 = varying(dtype == RLM_F32);
-  const bool isbf = varying(dtype == RLM_BF16);
-  const uint32_t w32[4] = {v.a.x, v.a.y, v.b.x, v.b.y};
-  const uint32_t e[4] = {v.h.x & 0xffffu, v.h.x >> 16, v.h.y & 0xffffu, v.h.y >> 16};
-  float f[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const float fb = __uint_as_float(e[k] << 16);
-    const float fh = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(e[k])));
-    f[k] = is32 ? __uint_as_float(w32[k]) : (isbf ? fb : fh);
-  }
-  return make_float4(f[0], f[1], f[2], f[3]);
-}
 // s: this lane's partner score (partner_score), loaded by the caller.
 __device__ __forceinline__ float partner_weight(const NormParams& p, float s, int64_t t,
                                                 int lane) {
