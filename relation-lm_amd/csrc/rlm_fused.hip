@@ -230,7 +230,7 @@ __device__ __forceinline__ void dma_gather_chunk(rsrc_t xr, uint32_t tile,
 
 template <int DT, int KS1>
 __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParams p) {
-  // DT = 16-column tiles of D per wave in phase 2 (D = 128*DT); KS1 = R/32.
+  // DT = D / 128; KS1 = R / 32.
   extern __shared__ __align__(16) unsigned char smem[];
   unsigned char* hid = smem + kOffHid;                            // [kRows][kLd] bf16
   float* wts = reinterpret_cast<float*>(smem + kOffF32);           // [kRows]
