@@ -248,6 +248,16 @@ __device__ __forceinline__ float gelu_erf(float x) {
   return x < 0.0f ? xh : x - xh;
 }
 
+// Renumbers workgroup `i` of `count` so that each XCD (the hardware deals
+// workgroups round-robin over 8 XCDs) receives a contiguous range of logical
+// tile ids, so that workgroups with neighbouring logical ids share one L2.
+__device__ __forceinline__ int64_t xcd_tile(int64_t i, int64_t count) {
+  constexpr int kXcd = 8;
+  const int64_t per = count / kXcd, rem = count % kXcd;
+  const int64_t x = i % kXcd;
+  return x * per + (x < rem ? x : rem) + i / kXcd;
+}
+
 // ---------------------------------------------------------------------------
 // Wave-level primitives (wave64)
 // ---------------------------------------------------------------------------

@@ -254,7 +254,9 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
   const int wave = tid / kWave;
   const int r16 = lane & 15;
   const int g = lane >> 4;
-  const uint32_t row0 = blockIdx.x * kRows;
+  // Consecutive logical workgroups (the queries of one batch row) share an
+  // XCD, so the expanded-cache rows they gather are fetched into one L2.
+  const uint32_t row0 = static_cast<uint32_t>(xcd_tile(blockIdx.x, gridDim.x)) * kRows;
   const uint32_t H = p.H;
   const rsrc_t xr = make_rsrc(p.expanded, p.expanded_bytes);
   const rsrc_t opr = make_rsrc(p.operand, p.operand_bytes);

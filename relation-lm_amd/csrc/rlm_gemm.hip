@@ -113,16 +113,6 @@ __device__ __forceinline__ f32x4 mfma16<f16>(const u16x8& a, const u16x8& b, f32
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-// Renumbers workgroup `i` of `count` so that each XCD (the hardware deals
-// workgroups round-robin over 8 XCDs) receives a contiguous range of logical
-// tile ids.
-__device__ __forceinline__ int64_t xcd_tile(int64_t i, int64_t count) {
-  constexpr int kXcd = 8;
-  const int64_t per = count / kXcd, rem = count % kXcd;
-  const int64_t x = i % kXcd;
-  return x * per + (x < rem ? x : rem) + i / kXcd;
-}
-
 // Stores one 16x16 MFMA accumulator (lane holds rows 4*(lane/16)+e of column
 // lane%16) plus bias.
 template <typename TO>

@@ -121,8 +121,8 @@ __device__ __forceinline__ void load_rows(const HiddenParams& p, int64_t r0, Row
 // shuffle steps).  The tile holding row (b, k=0) then stores batch b's row.
 // fresh[(bi * 2 + half) * cols + c] for bi = b - b_first.
 template <typename T>
-__device__ void fresh_rows(const HiddenParams& p, int64_t t, int64_t b_first, int nb, int n0,
-                           int cols, float* fresh) {
+__device__ void fresh_rows(const HiddenParams& p, int64_t t, int64_t r0, int64_t b_first, int nb,
+                           int n0, int cols, float* fresh) {
   // Eight lanes share one dot; a lane takes 8-element chunks j, j+8, ...
   // Every weight, operand-row and bias load of kIB items is issued before any
   // is used (unconditional, from clamped addresses), so the items cost one
@@ -211,7 +211,6 @@ __device__ void fresh_rows(const HiddenParams& p, int64_t t, int64_t b_first, in
   }
   __syncthreads();
   const int64_t QK = p.Tq * p.K;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kRows;
   const int64_t b_lo = (r0 + QK - 1) / QK;
   int64_t b_hi = (r0 + kRows - 1) / QK;
   if (b_hi > p.B - 1) b_hi = p.B - 1;
@@ -283,7 +282,7 @@ __device__ __forceinline__ int64_t update_setup(const HiddenParams& p, int64_t t
   b_first = r0 / QK;
   int64_t b_last = (r0 + kRows - 1) / QK;
   if (b_last > p.B - 1) b_last = p.B - 1;
-  if (t >= 0) fresh_rows<T>(p, t, b_first, static_cast<int>(b_last - b_first + 1), n0, cols, fresh);
+  if (t >= 0) fresh_rows<T>(p, t, r0, b_first, static_cast<int>(b_last - b_first + 1), n0, cols, fresh);
   return t;
 }
 
@@ -304,8 +303,11 @@ __global__ void __launch_bounds__(256) hidden_bf16_kernel(const HiddenParams p) 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kRows;
-  const int n0 = blockIdx.x * BN;
+  // Row tiles of one batch row run on one XCD (one L2 for the rows they gather).
+  const int64_t wg = xcd_tile(static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x,
+                              static_cast<int64_t>(gridDim.x) * gridDim.y);
+  const int64_t r0 = wg / gridDim.x * kRows;
+  const int n0 = static_cast<int>(wg % gridDim.x) * BN;
   const rsrc_t xr = make_rsrc(p.expanded, p.expanded_bytes);
   const rsrc_t opr = make_rsrc(p.operand, p.operand_bytes);
   const rsrc_t wr_ = make_rsrc(p.wm, p.wm_bytes);
@@ -427,8 +429,11 @@ __global__ void __launch_bounds__(256) hidden_f32_kernel(const HiddenParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kRows;
-  const int n0 = blockIdx.x * BN;
+  // Row tiles of one batch row run on one XCD (one L2 for the rows they gather).
+  const int64_t wg = xcd_tile(static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x,
+                              static_cast<int64_t>(gridDim.x) * gridDim.y);
+  const int64_t r0 = wg / gridDim.x * kRows;
+  const int n0 = static_cast<int>(wg % gridDim.x) * BN;
   const rsrc_t xr = make_rsrc(p.expanded, p.expanded_bytes);
   const rsrc_t opr = make_rsrc(p.operand, p.operand_bytes);
   const rsrc_t wr_ = make_rsrc(p.wm, p.wm_bytes);

@@ -462,8 +462,11 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-  const int64_t b = blockIdx.x / p.tiles;
-  const int64_t tq0 = (blockIdx.x - b * p.tiles) * static_cast<int64_t>(p.W);
+  // Consecutive logical workgroups (one batch row's query tiles) share an XCD,
+  // so a batch row's keys and caches are fetched into one L2.
+  const int64_t wg = xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t b = wg / p.tiles;
+  const int64_t tq0 = (wg - b * p.tiles) * static_cast<int64_t>(p.W);
   const int64_t tq = tq0 + wave;
   const int RD = p.H * p.HD;
   constexpr bool kUseA = MODE != kPartnerOnly;
@@ -859,8 +862,11 @@ multi_select_kernel(const SelectParams p, const MultiParams m) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-  const int64_t b = blockIdx.x / p.tiles;
-  const int64_t tq0 = (blockIdx.x - b * p.tiles) * static_cast<int64_t>(p.W);
+  // Consecutive logical workgroups (one batch row's query tiles) share an XCD,
+  // so a batch row's keys and caches are fetched into one L2.
+  const int64_t wg = xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t b = wg / p.tiles;
+  const int64_t tq0 = (wg - b * p.tiles) * static_cast<int64_t>(p.W);
   const int64_t tq = tq0 + wave;
   const int RD = p.H * p.HD;
 
