@@ -73,7 +73,8 @@ struct SelectParams {
   int32_t* out_partner;
   float* out_partner_score;
   // launch geometry and LDS layout (bytes)
-  int W;            // queries (waves) per workgroup
+  int W;            // queries per workgroup
+  int split;        // waves per query (W == 1 only): candidate scoring split over them
   int tiles;        // workgroups per batch row
   int G;            // lanes per key row (E * sizeof / 16)
   int H_log2;       // heads is a power of two
@@ -298,9 +299,12 @@ __device__ __forceinline__ void candidate(const SelectParams& p, int c, const Qu
 // query's whole window lies inside it (a per-wave decision); other rows come
 // through range-checked buffer loads whose offset is pushed past the end for
 // invalid rows (they read zero and are masked to -inf).
+// `part` of `parts` waves sharing one query scores candidate passes part,
+// part + parts, ... into the shared ws.sc.
 template <typename TA, int NCL, bool RING = false>
 __device__ void candidate_scores(const SelectParams& p, const Stream& s, const unsigned char* win,
-                                 const Query& qy, int exclude, WaveScratch& ws, int lane) {
+                                 const Query& qy, int exclude, WaveScratch& ws, int lane,
+                                 int part = 0, int parts = 1) {
   constexpr int EPC = kEpc<TA>;
   const rsrc_t keys = make_rsrc(s.keys, p.key_bytes);
   const uint32_t row0 = static_cast<uint32_t>(qy.b * p.T);
@@ -311,7 +315,7 @@ __device__ void candidate_scores(const SelectParams& p, const Stream& s, const u
   const bool lds = win != nullptr && t - p.L + 1 >= qy.wbase && t < qy.wbase + p.WR;
   const int wb = static_cast<int>(qy.wbase);
   const int chunks = p.G;  // 16-byte chunks per row
-  for (int c0 = 0; c0 < p.CAP; c0 += kWave * NCL) {
+  for (int c0 = part * kWave * NCL; c0 < p.CAP; c0 += parts * kWave * NCL) {
     int pos[NCL];
     bool ok[NCL], from_lds[NCL];
 #pragma unroll
@@ -455,19 +459,26 @@ __device__ void stage_workgroup(const SelectParams& p, int64_t b, int64_t wbase,
 }
 
 // RING: ring-buffer caches (decode form only, no staged windows).
-template <typename TA, typename TS, int MODE, bool RING = false>
+// SPLIT: one query per workgroup (decode), its candidate scoring shared by
+// p.split waves.
+template <typename TA, typename TS, int MODE, bool RING = false, bool SPLIT = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) select_kernel(const SelectParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int EPC = kEpc<TA>;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
+  // split > 1 (one query per workgroup): waves wq*split .. +split-1 share
+  // query wq; sub-wave sw scores every split-th pass of 64 candidates.
+  const int split = SPLIT ? p.split : 1;
+  const int wq = wave / split;
+  const int sw = wave - wq * split;
   // Consecutive logical workgroups (one batch row's query tiles) share an XCD,
   // so a batch row's keys and caches are fetched into one L2.
   const int64_t wg = xcd_tile(blockIdx.x, gridDim.x);
   const int64_t b = wg / p.tiles;
   const int64_t tq0 = (wg - b * p.tiles) * static_cast<int64_t>(p.W);
-  const int64_t tq = tq0 + wave;
+  const int64_t tq = tq0 + wq;
   const int RD = p.H * p.HD;
   constexpr bool kUseA = MODE != kPartnerOnly;
   constexpr bool kUseP = MODE != kAnchorOnly;
@@ -533,6 +544,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
   ws.sel = reinterpret_cast<int*>(ws.blk + p.NB);
   ws.selv = ws.sel + p.TOP;
   ws.sc = reinterpret_cast<float*>(ws.selv + p.TOP);
+  // Candidate scores live in the region of the query's first wave.
+  ws.sc = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(ws.sc) - sw * p.wave_bytes);
 
   Query qy;
   qy.b = b;
@@ -569,7 +582,12 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
     wave_sync();
     block_scores<TS, RING>(p, p.as, stats_a, bias_a, sp_a, qy, ws, lane);
     pick_blocks<RING>(p, qy, ws, lane);
-    candidate_scores<TA, 3, RING>(p, p.as, win_a, qy, -1, ws, lane);
+    if constexpr (SPLIT) {
+      candidate_scores<TA, 1, RING>(p, p.as, win_a, qy, -1, ws, lane, sw, split);
+      __syncthreads();  // every wave of the query sees all candidate scores
+    } else {
+      candidate_scores<TA, 3, RING>(p, p.as, win_a, qy, -1, ws, lane);
+    }
     uint64_t best = 0;
     float best_score = -INFINITY;
     for (int c = lane; c < p.CAP; c += kWave) {
@@ -588,13 +606,13 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
     const uint64_t win = wave_max_u64(best);
     if (win == 0) {
       anchor = qy.t - p.L + 1;
-      if (lane == 0) {
+      if (lane == 0 && sw == 0) {
         p.out_anchor[qy.q] = static_cast<int32_t>(anchor);
         p.out_anchor_score[qy.q] = -INFINITY;
       }
     } else {
       anchor = key_index(win);
-      if (best == win) {
+      if (best == win && sw == 0) {
         p.out_anchor[qy.q] = static_cast<int32_t>(anchor);
         p.out_anchor_score[qy.q] = best_score;
       }
@@ -643,7 +661,14 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
   wave_sync();
   block_scores<TS, RING>(p, p.ps, stats_p, bias_p, sp_p, qy, ws, lane);
   pick_blocks<RING>(p, qy, ws, lane);
-  candidate_scores<TA, 3, RING>(p, p.ps, win_p, qy, static_cast<int>(anchor), ws, lane);
+  if constexpr (SPLIT) __syncthreads();  // every wave has read the anchor scores
+  if constexpr (SPLIT) {
+    candidate_scores<TA, 1, RING>(p, p.ps, win_p, qy, static_cast<int>(anchor), ws, lane, sw, split);
+    __syncthreads();
+  } else {
+    candidate_scores<TA, 3, RING>(p, p.ps, win_p, qy, static_cast<int>(anchor), ws, lane);
+  }
+  if (sw != 0) return;  // the query's first wave ranks the partners
 
   // K argmax passes (relation_select.py:298-308), ties to the lowest lane.
   // While finite scores remain, this is a stable descending order of the
@@ -1125,6 +1150,9 @@ hipError_t finish_params(SelectParams& p, const Geometry& g, int64_t local_windo
   p.H_log2 = 31 - __builtin_clz(static_cast<unsigned>(g.H));
   p.BS_log2 = 31 - __builtin_clz(static_cast<unsigned>(g.BS));
   p.W = g.Tq > 1 ? 8 : 1;
+  // One query per workgroup (decode): its candidate passes of 64 are shared
+  // by up to 4 waves.
+  p.split = p.W == 1 ? std::min(4, (p.CAP + kWave - 1) / kWave) : 1;
   p.tiles = static_cast<int>((g.Tq + p.W - 1) / p.W);
   p.WR = p.L + p.W - 1;
   p.row_bytes = g.E * elem + 16;
@@ -1154,13 +1182,13 @@ hipError_t finish_params(SelectParams& p, const Geometry& g, int64_t local_windo
   p.key_bytes = static_cast<uint32_t>(key_bytes);
   p.off_wave = off;
   p.wave_bytes = wave_region_bytes(g.E, g.NB, RD, p.TOP, p.CAP);
-  off += p.W * p.wave_bytes;
+  off += p.W * p.split * p.wave_bytes;
   if (p.stage && off > 96 * 1024) {
     // Too large to share: every wave reads statistics and keys from L2.
     p.stage = 0;
     off = 0;
     p.off_wave = 0;
-    off += p.W * p.wave_bytes;
+    off += p.W * p.split * p.wave_bytes;
   }
   RLM_REQUIRE(off <= 160 * 1024,
               "selection working set (%d bytes of LDS) exceeds the 160 KiB of one CU", off);
@@ -1173,13 +1201,18 @@ hipError_t launch_select(const SelectParams& p, int act_dtype, int stat_dtype,
                          hipStream_t stream) {
   const int64_t queries = p.B * p.Tq;
   if (queries == 0) return hipSuccess;
-  const dim3 block(p.W * kWave);
+  const dim3 block(p.W * p.split * kWave);
   const dim3 grid(static_cast<unsigned>(p.B * p.tiles));
   const size_t lds = static_cast<size_t>(p.lds_total);
-#define RLM_SELECT_CASE(TA_ID, TA, TS_ID, TS)                                          \
-  if (act_dtype == TA_ID && stat_dtype == TS_ID) {                                     \
-    hipLaunchKernelGGL((select_kernel<TA, TS, MODE, RING>), grid, block, lds, stream, p); \
-    return launch_status("relation_select");                                           \
+#define RLM_SELECT_CASE(TA_ID, TA, TS_ID, TS)                                             \
+  if (act_dtype == TA_ID && stat_dtype == TS_ID) {                                        \
+    if (p.split > 1)                                                                      \
+      hipLaunchKernelGGL((select_kernel<TA, TS, MODE, RING, true>), grid, block, lds, stream, p); \
+    else if constexpr (!RING)                                                             \
+      hipLaunchKernelGGL((select_kernel<TA, TS, MODE, RING, false>), grid, block, lds, stream, p); \
+    else                                                                                  \
+      return hipErrorInvalidValue;                                                        \
+    return launch_status("relation_select");                                              \
   }
   RLM_SELECT_CASE(RLM_F32, float, RLM_F32, float)
   RLM_SELECT_CASE(RLM_F32, float, RLM_BF16, bf16)
