@@ -1206,12 +1206,12 @@ hipError_t launch_select(const SelectParams& p, int act_dtype, int stat_dtype,
   const size_t lds = static_cast<size_t>(p.lds_total);
 #define RLM_SELECT_CASE(TA_ID, TA, TS_ID, TS)                                             \
   if (act_dtype == TA_ID && stat_dtype == TS_ID) {                                        \
-    if (p.split > 1)                                                                      \
+    /* ring caches are decode only (one query per workgroup): always the split */        \
+    /* form, which also serves split == 1 */                                              \
+    if (RING || p.split > 1)                                                              \
       hipLaunchKernelGGL((select_kernel<TA, TS, MODE, RING, true>), grid, block, lds, stream, p); \
     else if constexpr (!RING)                                                             \
       hipLaunchKernelGGL((select_kernel<TA, TS, MODE, RING, false>), grid, block, lds, stream, p); \
-    else                                                                                  \
-      return hipErrorInvalidValue;                                                        \
     return launch_status("relation_select");                                              \
   }
   RLM_SELECT_CASE(RLM_F32, float, RLM_F32, float)

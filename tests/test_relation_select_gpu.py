@@ -212,3 +212,23 @@ def test_errors_raise(device):
     bad[14] = inp["position"].cpu()
     with pytest.raises(RuntimeError, match="must be on"):
         relation_select_packed(*bad)
+
+
+# Decode candidate capacities L + TOP*BS of 64, 96, 192 and 320: one, two,
+# three and four waves per query (320 also takes the general top-K path).
+SPLIT_CASES = [(32, 2, 16), (32, 4, 16), (64, 4, 32), (64, 8, 32)]
+
+
+@pytest.mark.parametrize("local,top,block", SPLIT_CASES)
+@pytest.mark.parametrize("batch", [1, 5])
+def test_decode_candidate_capacities(device, local, top, block, batch):
+    base = CONFIGS["cfg2"]
+    cfg = RelationConfig(**{**base.__dict__, "batch": batch, "local_window": local,
+                            "top_blocks": top, "block_size": block})
+    inp = selection_inputs(cfg, queries=1, device=device)
+    for position in (0, local + 3, cfg.context - 1):
+        inp["position"] = torch.tensor(position, dtype=torch.int64, device=device)
+        got = relation_select_packed(*select_args(inp, cfg))
+        torch.cuda.synchronize()
+        assert_select_equal(got, oracle_packed(inp, cfg, seq=False),
+                            f"L={local} top={top} BS={block} t={position}")

@@ -220,3 +220,21 @@ def test_hidden_update_ring_matches_oracle(device, batch, position):
                                                   partner[:, :2].numpy(),
                                                   host(red["product_weight"]))
     assert rel_err(host(cached), exp_cached) <= FP32_REL
+
+
+@pytest.mark.parametrize("local,top,block", [(32, 2, 16), (32, 4, 16), (64, 8, 32)])
+@pytest.mark.parametrize("position", [40, 511, 1300])
+def test_select_ring_candidate_capacities(device, local, top, block, position):
+    # Capacities 64, 96 and 320: one, two and four waves per query.
+    cfg = dataclasses.replace(CONFIGS["cfg3"], batch=3, local_window=local, top_blocks=top,
+                              block_size=block)
+    inp = selection_inputs(cfg, queries=1, seed=cfg.seed + position)
+    inp["position"] = torch.tensor(position, dtype=torch.int64)
+    dev = {k: v.to(device) for k, v in inp.items()}
+    got = relation_select_packed_ring(*select_args(dev, cfg))
+    torch.cuda.synchronize()
+    h = {k: host(v) for k, v in inp.items()}
+    expected = osel.relation_select_packed_ring(*[h[k] for k in SELECT_ORDER], position,
+                                                cfg.local_window, cfg.top_blocks, cfg.k_out,
+                                                cfg.strict_valid)
+    assert_select_equal(got, expected, f"L={local} top={top} BS={block} t={position}")
