@@ -233,19 +233,20 @@ __device__ __forceinline__ float buf_load_elem<f16>(rsrc_t r, uint32_t off) {
 // |error| <= 1.5e-7), constants folded: for a = |x|,
 //   h = Phi(-a) = 0.5 * (1 - erf(a/sqrt2)) = t * poly(t) * exp(-x^2/2),
 //   t = 1/(1 + p a/sqrt2), poly with the A&S coefficients halved,
-// and GELU(x) = x h for x < 0, x - x h for x >= 0.  Forming x h directly keeps
-// the relative accuracy of the negative tail (no 1 + erf cancellation).
-// 12 VALU operations plus one v_rcp and one v_exp.
+// and GELU(x) = x h for x < 0, x - x h for x >= 0, i.e. max(x, 0) - a h: one
+// fused multiply-add.  Forming a h directly keeps the relative accuracy of the
+// negative tail (no 1 + erf cancellation).  10 VALU operations plus one v_rcp
+// and one v_exp.
 __device__ __forceinline__ float gelu_erf(float x) {
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f * 0.70710678118654752440f, fabsf(x), 1.0f));
+  const float a = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f * 0.70710678118654752440f, a, 1.0f));
   float y = fmaf(0.5f * 1.061405429f, t, 0.5f * -1.453152027f);
   y = fmaf(y, t, 0.5f * 1.421413741f);
   y = fmaf(y, t, 0.5f * -0.284496736f);
   y = fmaf(y, t, 0.5f * 0.254829592f);
   y *= t;
   const float e = __builtin_amdgcn_exp2f(x * (x * (-0.5f * 1.44269504088896340736f)));
-  const float xh = x * (y * e);
-  return x < 0.0f ? xh : x - xh;
+  return fmaf(-a, y * e, fmaxf(x, 0.0f));
 }
 
 // Renumbers workgroup `i` of `count` so that each XCD (the hardware deals
