@@ -239,19 +239,36 @@ __device__ __forceinline__ void gather_bases(const HiddenParams& p, rsrc_t xr, c
                                              int mrow, int n, int c, int64_t t, int64_t b_first,
                                              const float* fresh, int cols, int lane,
                                              float (&xs)[4]) {
-  const uint32_t col = (n < p.H ? static_cast<uint32_t>(n) : 0u) * sizeof(T);
+  // Branch-free: every row-table and `fresh` read is unconditional and the
+  // conditions only select between registers, so all the gathers are in
+  // flight together (a branch would make the compiler wait for each pair of
+  // loads at its join).
+  const bool in = n < p.H;
+  const uint32_t col = (in ? static_cast<uint32_t>(n) : 0u) * sizeof(T);
+  float xa[4], xp[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int m = mrow + (lane >> 4) * 4 + e;
-    const uint32_t oa = n < p.H ? rt.x_a[m] : kNoOffset;
-    const uint32_t op = n < p.H ? rt.x_p[m] : kNoOffset;
-    float xa = buf_load_elem<T>(xr, oa + col);
-    float xp = buf_load_elem<T>(xr, op + col);
-    if (UPDATE && t >= 0 && n < p.H) {
-      if (rt.a[m] == t) xa = fresh[((rt.b[m] - b_first) * 2 + 0) * cols + c];
-      if (rt.p[m] == t) xp = fresh[((rt.b[m] - b_first) * 2 + 1) * cols + c];
+    const uint32_t xam = rt.x_a[m], xpm = rt.x_p[m];
+    xa[e] = buf_load_elem<T>(xr, (in ? xam : kNoOffset) + col);
+    xp[e] = buf_load_elem<T>(xr, (in ? xpm : kNoOffset) + col);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float a = xa[e], b = xp[e];
+    if constexpr (UPDATE) {
+      // Row t comes from `fresh` (clamped index: always a valid LDS read).
+      const int m = mrow + (lane >> 4) * 4 + e;
+      const int32_t am = rt.a[m], pm = rt.p[m];
+      int64_t bi = rt.b[m] - b_first;
+      bi = bi < 0 ? 0 : (bi >= fresh_batches() ? fresh_batches() - 1 : bi);
+      const float fa = fresh[(bi * 2 + 0) * cols + c];
+      const float fp = fresh[(bi * 2 + 1) * cols + c];
+      const bool use = (t >= 0) & in;
+      a = (use & (am == t)) ? fa : a;
+      b = (use & (pm == t)) ? fp : b;
     }
-    xs[e] = xa + xp;
+    xs[e] = a + b;
   }
 }
 
