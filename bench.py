@@ -186,6 +186,23 @@ def main() -> int:
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
 
+    def windowed_us(fn, steps, windows=10):
+        """Per-step microseconds of `fn`: the median over `windows` back-to-back
+        windows of steps/windows calls each, so that one host-side stall in a
+        window (an eager step launches about ten kernels from Python) does not
+        move the figure."""
+        per = max(1, steps // windows)
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(windows + 1)]
+        torch.cuda.synchronize()
+        marks[0].record()
+        for w in range(windows):
+            for _ in range(per):
+                fn()
+            marks[w + 1].record()
+        torch.cuda.synchronize()
+        return statistics.median(marks[w].elapsed_time(marks[w + 1]) * 1e3 / per
+                                 for w in range(windows))
+
     def run_decode(ring_position=None):
         """Decode-step latency (cfg3) at B=1 and B=8, eager and from a HIP graph.
 
@@ -242,12 +259,7 @@ def main() -> int:
             for _ in range(20):
                 decode_step()
             torch.cuda.synchronize()
-            start.record()
-            for _ in range(args.decode_steps):
-                decode_step()
-            end.record()
-            torch.cuda.synchronize()
-            eager_us = start.elapsed_time(end) * 1e3 / args.decode_steps
+            eager_us = windowed_us(decode_step, args.decode_steps)
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(side):
@@ -259,12 +271,7 @@ def main() -> int:
             for _ in range(10):
                 graph.replay()
             torch.cuda.synchronize()
-            start.record()
-            for _ in range(args.decode_steps):
-                graph.replay()
-            end.record()
-            torch.cuda.synchronize()
-            graph_us = start.elapsed_time(end) * 1e3 / args.decode_steps
+            graph_us = windowed_us(graph.replay, args.decode_steps)
             decode[f"B{batch}"] = {"eager_us": round(eager_us, 2), "graph_us": round(graph_us, 2)}
 
         return decode

@@ -167,7 +167,7 @@ __device__ __forceinline__ int ring_block(const SelectParams& p, const Query& qy
 // DPP group reductions.  All in float64, rounded once.  Statistics and bias
 // come from LDS when the workgroup staged them, else from L2.  `sp` is
 // softplus(gamma_h) for this lane's head h = lane mod H.
-template <typename TS, bool RING = false>
+template <typename TS, bool RING = false, bool PRELOAD = false>
 __device__ void block_scores(const SelectParams& p, const Stream& s, const float* stats,
                              const float* bias_tab, double sp, const Query& qy, WaveScratch& ws,
                              int lane) {
@@ -195,7 +195,29 @@ __device__ void block_scores(const SelectParams& p, const Stream& s, const float
     } else {
       const TS* mr = static_cast<const TS*>(s.mean) + (qy.b * pairs + prc) * p.HD;
       const TS* sr = static_cast<const TS*>(s.stdev) + (qy.b * pairs + prc) * p.HD;
-      for (int d = 0; d < p.HD; d += 4) {
+      // PRELOAD (decode) and head dims up to 16: every statistics load of the
+      // lane is issued before the first is used (chunks past HD re-read chunk
+      // 0 and are not summed); otherwise the loop below.
+      constexpr int kQ = 4;
+      const int hd_pre = PRELOAD && p.HD <= 4 * kQ ? p.HD : 0;  // wave-uniform
+      float4 mq[kQ], sq[kQ];
+#pragma unroll
+      for (int q = 0; q < (PRELOAD ? kQ : 0); ++q) {
+        const int d = 4 * q < hd_pre ? 4 * q : 0;
+        mq[q] = load4(mr + d);
+        sq[q] = load4(sr + d);
+      }
+#pragma unroll
+      for (int q = 0; q < (PRELOAD ? kQ : 0); ++q) {
+        if (4 * q >= hd_pre) break;
+        const int d = 4 * q;
+        const float4 m = mq[q], sd = sq[q];
+        c += static_cast<double>(m.x) * qh[d] + static_cast<double>(m.y) * qh[d + 1] +
+             static_cast<double>(m.z) * qh[d + 2] + static_cast<double>(m.w) * qh[d + 3];
+        u += static_cast<double>(sd.x) * fabs(qh[d]) + static_cast<double>(sd.y) * fabs(qh[d + 1]) +
+             static_cast<double>(sd.z) * fabs(qh[d + 2]) + static_cast<double>(sd.w) * fabs(qh[d + 3]);
+      }
+      for (int d = hd_pre == 0 ? 0 : p.HD; d < p.HD; d += 4) {
         const float4 m = load4(mr + d);
         const float4 sd = load4(sr + d);
         c += static_cast<double>(m.x) * qh[d] + static_cast<double>(m.y) * qh[d + 1] +
@@ -209,8 +231,18 @@ __device__ void block_scores(const SelectParams& p, const Stream& s, const float
     const int dist = (qy.t > end ? static_cast<int>(qy.t - end) : 0) + 1;
     int bucket = 31 - __clz(dist);
     bucket = bucket < p.RB - 1 ? bucket : p.RB - 1;
-    const double bias = bias_tab != nullptr ? bias_tab[h * p.RB + bucket]
-                                            : load_any_f(s.bias, s.bias_dtype, h * p.RB + bucket);
+    // Unstaged: both dtype forms are loaded and one is kept (no branch, so the
+    // load is not waited for on its own).
+    double bias;
+    if constexpr (PRELOAD)
+      bias = bias_tab != nullptr
+                 ? bias_tab[h * p.RB + bucket]
+                 : decode_float(issue_float(s.bias, s.bias_dtype, static_cast<uint32_t>(p.H * p.RB),
+                                            static_cast<uint32_t>(h * p.RB + bucket), true),
+                                s.bias_dtype);
+    else
+      bias = bias_tab != nullptr ? bias_tab[h * p.RB + bucket]
+                                 : load_any_f(s.bias, s.bias_dtype, h * p.RB + bucket);
     double sv;
     {
 #pragma clang fp contract(off)
@@ -301,7 +333,10 @@ __device__ __forceinline__ void candidate(const SelectParams& p, int c, const Qu
 // invalid rows (they read zero and are masked to -inf).
 // `part` of `parts` waves sharing one query scores candidate passes part,
 // part + parts, ... into the shared ws.sc.
-template <typename TA, int NCL, bool RING = false>
+// STAGED = false (decode: no staged windows) reads every row from L2 with no
+// per-lane branch, so the compiler waits once per group of loads rather than
+// once per load.
+template <typename TA, int NCL, bool RING = false, bool STAGED = true>
 __device__ void candidate_scores(const SelectParams& p, const Stream& s, const unsigned char* win,
                                  const Query& qy, int exclude, WaveScratch& ws, int lane,
                                  int part = 0, int parts = 1) {
@@ -350,7 +385,7 @@ __device__ void candidate_scores(const SelectParams& p, const Stream& s, const u
           const int ch = ch0 + cc;
           if (ch >= chunks) {
             kc[u][cc] = make_uint4(0, 0, 0, 0);
-          } else if (from_lds[u]) {
+          } else if (STAGED && from_lds[u]) {
             const int wr = ok[u] ? pos[u] - wb : 0;
             kc[u][cc] = *reinterpret_cast<const uint4*>(win + wr * p.row_bytes + 16 * ch);
           } else {
@@ -487,7 +522,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
   // Waves past the last query read row tq0's vectors and leave after staging.
   const int64_t tq_ld = tq < p.Tq ? tq : tq0;
   const int64_t q_ld = b * p.Tq + tq_ld;
-  const int64_t t_own = load_any_i(p.pos, p.pos_dtype, b * p.pos_sb + tq_ld * p.pos_sq);
+  const int64_t t_own = SPLIT ? index_at(p.pos, p.pos_dtype, b * p.pos_sb + tq_ld * p.pos_sq)
+                              : load_any_i(p.pos, p.pos_dtype, b * p.pos_sb + tq_ld * p.pos_sq);
   const int jg = lane & (p.G - 1);
   const TA* q_exact = static_cast<const TA*>(kUseA ? p.aq : p.pq) +
                       q_ld * (kUseA ? static_cast<int64_t>(p.E) : p.pq_row);
@@ -502,8 +538,19 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
   {
 #pragma clang fp contract(off)
     const int h = lane & (p.H - 1);
-    if (kUseA) sp_a = log(1.0 + exp(static_cast<double>(load_any_f(p.as.gamma, p.as.gamma_dtype, h))));
-    if (kUseP) sp_p = log(1.0 + exp(static_cast<double>(load_any_f(p.ps.gamma, p.ps.gamma_dtype, h))));
+    if constexpr (SPLIT) {
+      // Decode: both dtype forms loaded, one kept -- no branch for the loads to
+      // wait at (a lone wave's chain has nothing else to hide that latency).
+      const FloatWords ga = issue_float(p.as.gamma, p.as.gamma_dtype, static_cast<uint32_t>(p.H),
+                                        static_cast<uint32_t>(h), kUseA);
+      const FloatWords gp = issue_float(p.ps.gamma, p.ps.gamma_dtype, static_cast<uint32_t>(p.H),
+                                        static_cast<uint32_t>(h), kUseP);
+      if (kUseA) sp_a = log(1.0 + exp(static_cast<double>(decode_float(ga, p.as.gamma_dtype))));
+      if (kUseP) sp_p = log(1.0 + exp(static_cast<double>(decode_float(gp, p.ps.gamma_dtype))));
+    } else {
+      if (kUseA) sp_a = log(1.0 + exp(static_cast<double>(load_any_f(p.as.gamma, p.as.gamma_dtype, h))));
+      if (kUseP) sp_p = log(1.0 + exp(static_cast<double>(load_any_f(p.ps.gamma, p.ps.gamma_dtype, h))));
+    }
   }
   constexpr int kRq = 4;  // router-query elements held per lane (RD <= 256)
   float rq_a[kRq], rq_p[kRq];
@@ -514,8 +561,17 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
 #pragma unroll
     for (int i = 0; i < kRq; ++i) {
       const int d = lane + kWave * i;
-      rq_a[i] = d < RD ? to_f32(ra[d]) : 0.0f;
-      rq_p[i] = (MODE == kPacked && d < RD) ? to_f32(rp[d]) : 0.0f;
+      if constexpr (SPLIT) {
+        // Decode: unconditional loads (index clamped) and selects.
+        const int dc = d < RD ? d : 0;
+        const float va = to_f32(ra[dc]);
+        rq_a[i] = d < RD ? va : 0.0f;
+        const float vp = MODE == kPacked ? to_f32(rp[dc]) : 0.0f;
+        rq_p[i] = (MODE == kPacked && d < RD) ? vp : 0.0f;
+      } else {
+        rq_a[i] = d < RD ? to_f32(ra[d]) : 0.0f;
+        rq_p[i] = (MODE == kPacked && d < RD) ? to_f32(rp[d]) : 0.0f;
+      }
     }
   }
 
@@ -580,10 +636,10 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
     put_exact();
     put_router(rq_a, static_cast<const TA*>(p.arq), RD);
     wave_sync();
-    block_scores<TS, RING>(p, p.as, stats_a, bias_a, sp_a, qy, ws, lane);
+    block_scores<TS, RING, SPLIT>(p, p.as, stats_a, bias_a, sp_a, qy, ws, lane);
     pick_blocks<RING>(p, qy, ws, lane);
     if constexpr (SPLIT) {
-      candidate_scores<TA, 1, RING>(p, p.as, win_a, qy, -1, ws, lane, sw, split);
+      candidate_scores<TA, 1, RING, false>(p, p.as, win_a, qy, -1, ws, lane, sw, split);
       __syncthreads();  // every wave of the query sees all candidate scores
     } else {
       candidate_scores<TA, 3, RING>(p, p.as, win_a, qy, -1, ws, lane);
@@ -638,7 +694,12 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
 #pragma unroll
       for (int i = 0; i < kRq; ++i) {
         const int d = lane + kWave * i;
-        cr[i] = d < RD ? to_f32(pc[p.E + d]) : 0.0f;
+        if constexpr (SPLIT) {
+          const float v = to_f32(pc[p.E + (d < RD ? d : 0)]);
+          cr[i] = d < RD ? v : 0.0f;
+        } else {
+          cr[i] = d < RD ? to_f32(pc[p.E + d]) : 0.0f;
+        }
       }
       chunk_to_f64<TA>(cc, cache_q);
 #pragma unroll
@@ -659,11 +720,12 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) s
     put_exact();
   }
   wave_sync();
-  block_scores<TS, RING>(p, p.ps, stats_p, bias_p, sp_p, qy, ws, lane);
+  block_scores<TS, RING, SPLIT>(p, p.ps, stats_p, bias_p, sp_p, qy, ws, lane);
   pick_blocks<RING>(p, qy, ws, lane);
   if constexpr (SPLIT) __syncthreads();  // every wave has read the anchor scores
   if constexpr (SPLIT) {
-    candidate_scores<TA, 1, RING>(p, p.ps, win_p, qy, static_cast<int>(anchor), ws, lane, sw, split);
+    candidate_scores<TA, 1, RING, false>(p, p.ps, win_p, qy, static_cast<int>(anchor), ws, lane, sw,
+                                         split);
     __syncthreads();
   } else {
     candidate_scores<TA, 3, RING>(p, p.ps, win_p, qy, static_cast<int>(anchor), ws, lane);
