@@ -374,8 +374,13 @@ __device__ void candidate_scores(const SelectParams& p, const Stream& s, const u
     double acc[NCL];
 #pragma unroll
     for (int u = 0; u < NCL; ++u) acc[u] = 0.0;
-    // Rows in groups of CG chunks: all loads of a group in flight.
-    constexpr int CG = 4;
+    // Rows in groups of CG chunks: all loads of a group in flight.  With
+    // staged windows both sources are read for every row (the L2 read of a
+    // window row goes out of range and returns zeros, the LDS read of a remote
+    // row reads window row 0) and a select keeps the right one: a per-lane
+    // branch between them would make the compiler wait for each L2 load before
+    // the next.  Two chunks per group keep the registers of four.
+    constexpr int CG = STAGED ? 2 : 4;
     for (int ch0 = 0; ch0 < chunks; ch0 += CG) {
       uint4 kc[NCL][CG];
 #pragma unroll
@@ -383,15 +388,20 @@ __device__ void candidate_scores(const SelectParams& p, const Stream& s, const u
 #pragma unroll
         for (int cc = 0; cc < CG; ++cc) {
           const int ch = ch0 + cc;
-          if (ch >= chunks) {
-            kc[u][cc] = make_uint4(0, 0, 0, 0);
-          } else if (STAGED && from_lds[u]) {
-            const int wr = ok[u] ? pos[u] - wb : 0;
-            kc[u][cc] = *reinterpret_cast<const uint4*>(win + wr * p.row_bytes + 16 * ch);
+          const bool in = ch < chunks;  // wave-uniform
+          const bool l2 = !STAGED || !from_lds[u];
+          const uint4 g = buf_load_b128(
+              keys, in && ok[u] && l2 ? (row0 + static_cast<uint32_t>(pos[u])) * row_bytes + 16u * ch
+                                      : kNoOffset);
+          if constexpr (STAGED) {
+            uint4 l = make_uint4(0, 0, 0, 0);
+            if (win != nullptr && in) {  // wave-uniform
+              const int wr = ok[u] && from_lds[u] ? pos[u] - wb : 0;
+              l = *reinterpret_cast<const uint4*>(win + wr * p.row_bytes + 16 * ch);
+            }
+            kc[u][cc] = from_lds[u] ? l : g;
           } else {
-            kc[u][cc] = buf_load_b128(
-                keys, ok[u] ? (row0 + static_cast<uint32_t>(pos[u])) * row_bytes + 16u * ch
-                            : kNoOffset);
+            kc[u][cc] = g;
           }
         }
 #pragma unroll
