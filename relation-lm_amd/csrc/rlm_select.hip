@@ -207,15 +207,19 @@ __device__ void block_scores(const SelectParams& p, const Stream& s, const float
         mq[q] = load4(mr + d);
         sq[q] = load4(sr + d);
       }
+      // Every chunk is used (a select drops those past HD): a load used only
+      // under a condition would be sunk into that branch and waited for there.
 #pragma unroll
       for (int q = 0; q < (PRELOAD ? kQ : 0); ++q) {
-        if (4 * q >= hd_pre) break;
-        const int d = 4 * q;
+        const bool use = 4 * q < hd_pre;
+        const int d = use ? 4 * q : 0;
         const float4 m = mq[q], sd = sq[q];
-        c += static_cast<double>(m.x) * qh[d] + static_cast<double>(m.y) * qh[d + 1] +
-             static_cast<double>(m.z) * qh[d + 2] + static_cast<double>(m.w) * qh[d + 3];
-        u += static_cast<double>(sd.x) * fabs(qh[d]) + static_cast<double>(sd.y) * fabs(qh[d + 1]) +
-             static_cast<double>(sd.z) * fabs(qh[d + 2]) + static_cast<double>(sd.w) * fabs(qh[d + 3]);
+        const double cq = static_cast<double>(m.x) * qh[d] + static_cast<double>(m.y) * qh[d + 1] +
+                          static_cast<double>(m.z) * qh[d + 2] + static_cast<double>(m.w) * qh[d + 3];
+        const double uq = static_cast<double>(sd.x) * fabs(qh[d]) + static_cast<double>(sd.y) * fabs(qh[d + 1]) +
+                          static_cast<double>(sd.z) * fabs(qh[d + 2]) + static_cast<double>(sd.w) * fabs(qh[d + 3]);
+        c += use ? cq : 0.0;
+        u += use ? uq : 0.0;
       }
       for (int d = hd_pre == 0 ? 0 : p.HD; d < p.HD; d += 4) {
         const float4 m = load4(mr + d);
@@ -404,10 +408,12 @@ __device__ void candidate_scores(const SelectParams& p, const Stream& s, const u
             kc[u][cc] = g;
           }
         }
+      // Chunks past the row end were loaded as zeros and add exact zeros, so
+      // every chunk is used unconditionally (a load used only under a
+      // condition would be sunk into that branch and waited for there).
 #pragma unroll
       for (int cc = 0; cc < CG; ++cc) {
-        const int ch = ch0 + cc;
-        if (ch >= chunks) break;
+        const int ch = ch0 + cc < chunks ? ch0 + cc : 0;
         double q[EPC];
 #pragma unroll
         for (int e = 0; e < EPC; e += 2) {
