@@ -485,6 +485,11 @@ __global__ void __launch_bounds__(kSkinnyWaves * kWave) skinny_kernel(const Gemm
   const rsrc_t wr = make_rsrc(p.w, p.w_bytes);
   const uint32_t arow = static_cast<uint32_t>((m0 + r16) * p.lda * static_cast<int64_t>(sizeof(TA)));
   const uint32_t wrow = static_cast<uint32_t>((n0 + r16) * p.K * static_cast<int64_t>(sizeof(W)));
+  // The bias of this lane's column, issued now (both dtype forms, one kept)
+  // and used after the reduction: no load waits at the end on its own.
+  const bool has_bias = p.bias != nullptr && n_ok && wave == 0;
+  const FloatWords bias_w = issue_float(p.bias, p.bias_dtype, static_cast<uint32_t>(p.N),
+                                        static_cast<uint32_t>(n_ok ? n0 + r16 : 0), has_bias);
   f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const int64_t slices = (p.K + kBK - 1) / kBK;
   for (int64_t s0 = wave; s0 < slices; s0 += kSkinnyWaves * kSkinnyBatch) {
@@ -539,7 +544,7 @@ __global__ void __launch_bounds__(kSkinnyWaves * kWave) skinny_kernel(const Gemm
 #pragma unroll
   for (int w = 1; w < kSkinnyWaves; ++w) sum += part[w][lane];
   const int64_t n = n0 + r16;
-  const float bv = (p.bias && n < p.N) ? load_any_f(p.bias, p.bias_dtype, n) : 0.0f;
+  const float bv = has_bias ? decode_float(bias_w, p.bias_dtype) : 0.0f;
   store_tile<TO>(p, sum, m0, n, bv, lane);
   scatter_tile<TO>(p, sum, m0, n, bv, lane);
 }
