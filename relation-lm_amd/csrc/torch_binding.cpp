@@ -10,7 +10,10 @@
 //   relation_lm::router_cache_update         (router_cache.py:181)
 // plus the sequence forms, the fused reduce, the packed sparse-cache
 // projection and the linear.
-// Only a CUDA-key (ROCm device) implementation exists: CPU tensors raise.
+// Every op has a CUDA-key (ROCm device) implementation over the C ABI.  The
+// one exception to "CPU tensors raise" is packed_sparse_cache_projection: the
+// reference's project() is F.linear and runs on any device, so its CPU-key
+// implementation is at::linear (device tensors never reach it).
 // Outputs are allocated with the caching allocator on the input device and
 // every kernel is enqueued on the current HIP stream, so the ops compose
 // with graph capture.
@@ -610,8 +613,8 @@ TORCH_LIBRARY(relation_lm, m) {
       "router_cache_update(Tensor anchor_raw, Tensor partner_raw, Tensor(a!) anchor_raw_cache, "
       "Tensor(b!) partner_raw_cache, Tensor(c!) anchor_conv_cache, Tensor(d!) partner_conv_cache, "
       "Tensor(e!) anchor_mean, Tensor(f!) anchor_std, Tensor(g!) partner_mean, Tensor(h!) "
-      "partner_std, Tensor anchor_conv_weight, Tensor partner_conv_weight, Tensor position, int "
-      "block_size) -> Tensor");
+      "partner_std, Tensor anchor_conv_weight, Tensor partner_conv_weight, Tensor position, "
+      "SymInt block_size) -> Tensor");
   // Ring-buffer forms (no reference op): the schemas of the linear ops.
   m.def(
       "relation_select_packed_ring(Tensor anchor_query, Tensor anchor_keys, Tensor "
@@ -632,7 +635,7 @@ TORCH_LIBRARY(relation_lm, m) {
       "anchor_raw_cache, Tensor(b!) partner_raw_cache, Tensor(c!) anchor_conv_cache, Tensor(d!) "
       "partner_conv_cache, Tensor(e!) anchor_mean, Tensor(f!) anchor_std, Tensor(g!) "
       "partner_mean, Tensor(h!) partner_std, Tensor anchor_conv_weight, Tensor "
-      "partner_conv_weight, Tensor position, int block_size) -> Tensor");
+      "partner_conv_weight, Tensor position, SymInt block_size) -> Tensor");
   m.def("packed_sparse_cache_projection(Tensor memory, Tensor weight) -> Tensor");
   m.def(
       "packed_projection_to_caches(Tensor memory, Tensor weight, Tensor(a!) anchor_keys, "
@@ -673,6 +676,16 @@ TORCH_LIBRARY_IMPL(relation_lm, CUDA, m) {
   m.impl("packed_sparse_cache_projection", TORCH_FN(packed_sparse_cache_projection));
   m.impl("packed_projection_to_caches", TORCH_FN(packed_projection_to_caches));
   m.impl("relation_linear", TORCH_FN(relation_linear));
+}
+
+// CPU tensors: the reference's PackedSparseCacheProjection.project is F.linear
+// (src/relation_lm/inference/packed_cache.py:52-57), which runs on the CPU.
+TORCH_LIBRARY_IMPL(relation_lm, CPU, m) {
+  m.impl("packed_sparse_cache_projection", [](const at::Tensor& memory, const at::Tensor& weight) {
+    TORCH_CHECK(weight.device() == memory.device(),
+                "relation_lm::packed_sparse_cache_projection: memory and weight must share a device");
+    return at::linear(memory, weight);
+  });
 }
 
 TORCH_LIBRARY_IMPL(relationlex, CUDA, m) {

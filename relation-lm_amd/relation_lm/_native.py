@@ -3,7 +3,9 @@
 Importing this module makes ``torch.ops.relation_lm.*`` and
 ``torch.ops.relationlex.*`` available.  There is no fallback: when the built
 library is missing the import fails with instructions to build it, and calling
-an op with CPU tensors raises (only the ROCm-device implementation exists).
+an op with CPU tensors raises (only the ROCm-device implementation exists) --
+except ``packed_sparse_cache_projection``, whose CPU tensors take ``at::linear``
+as the reference's ``F.linear`` does.
 """
 from __future__ import annotations
 

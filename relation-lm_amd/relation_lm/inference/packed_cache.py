@@ -5,7 +5,9 @@ the order ``SPARSE_CACHE_NAMES``.  The dataclass, its properties, validation
 errors and the packing helper keep the reference contract (:10-94); the GEMM
 behind ``project`` is the gfx950 MFMA kernel registered as
 ``relation_lm::packed_sparse_cache_projection`` (the reference calls
-``F.linear``; the op has no name there).
+``F.linear``; the op has no name there).  CPU tensors take the op's CPU
+implementation, ``at::linear``, so ``project`` runs on any device as the
+reference's does.
 """
 from __future__ import annotations
 

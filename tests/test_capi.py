@@ -169,6 +169,9 @@ def test_torch_ops_registered_with_reference_schemas():
         torch.ops.relation_lm.relation_hidden_cache_update.default._schema)
     assert "SymInt k_out" in str(torch.ops.relationlex.partner_topk.default._schema)
     assert "float norm_eps" in str(torch.ops.relation_lm.relation_norm_reduce.default._schema)
+    # triton_op infers SymInt for the reference's `block_size: int` (router_cache.py:188-203).
+    for op in (torch.ops.relation_lm.router_cache_update, torch.ops.relation_lm.router_cache_update_ring):
+        assert str(op.default._schema).endswith("Tensor position, SymInt block_size) -> Tensor")
 
 
 def test_cpu_tensors_fail_loudly():
