@@ -94,7 +94,7 @@ def _hidden_flat(expanded, operand, batch_of, anchor, partner, product_weight,
         op_a = _gather_rows(operand, b, a).astype(np.float32)          # [q,R]
         op_p = _gather_rows(operand, b, p).astype(np.float32)          # [q,K,R]
         product = (op_p * op_a[:, None, :]).astype(np.float32)          # fp32 product (:129)
-        pre = np.einsum("qkr,nr->qkn", _f64(product), wm)
+        pre = (_f64(product).reshape(-1, wm.shape[1]) @ wm.T).reshape(len(a), k, hidden_dim)
         base_a = _gather_rows(expanded, b, a)[:, :hidden_dim]            # [q,H]
         base_p = _gather_rows(expanded, b, p)[..., hidden_dim:]          # [q,K,H]
         if anchor_current is not None:

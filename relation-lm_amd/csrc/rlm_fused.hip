@@ -151,15 +151,13 @@ __device__ __forceinline__ u16x8 as_frag(uint4 v) { return __builtin_bit_cast(u1
 // 16 bytes per lane from global memory straight into LDS: lane i's bytes land
 // at lds_addr + 16*i.  Issued as inline assembly so that the compiler does not
 // follow it with a full vmcnt(0) before the next LDS access; the caller waits
-// (s_waitcnt vmcnt(0) + barrier) before the tile is read.  M0 (the LDS base of
-// the transfer) is set inside the same asm statement.  M0 is a reserved
-// register that a clobber list cannot name; nothing else in this kernel uses
-// it (the compiler emits no M0 access of its own here), so the write cannot
-// disturb compiler-generated code.
+// (s_waitcnt vmcnt(0) + barrier) before the tile is read.  The LDS base of the
+// transfer travels in M0, passed as an operand bound to that register ("{m0}"),
+// so the compiler writes M0 itself and knows it holds this value.
 __device__ __forceinline__ void lds_dma16(rsrc_t r, uint32_t lds_addr, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds"
                :
-               : "s"(lds_addr), "v"(voff), "s"(r)
+               : "v"(voff), "s"(r), "{m0}"(lds_addr)
                : "memory");
 }
 
