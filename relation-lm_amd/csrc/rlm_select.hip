@@ -28,7 +28,10 @@
 // candidate lane (local window first, then picked blocks in pick order).
 // Each rule is one 64-bit key (order-preserving score bits above the
 // complemented tie index), so one wave max-reduction yields the winner.
+#include <cstdlib>
+
 #include "rlm_common.hpp"
+#include "rlm_select_tile.hpp"
 
 namespace rlm {
 namespace {
@@ -1352,6 +1355,77 @@ bool check_outputs(const rlm_tensor* idx, const rlm_tensor* score, const char* w
   return true;
 }
 
+// The sequence form takes the matrix-core-filtered kernel where it applies
+// unless RLM_SELECT_TILE=0 (both kernels give identical results; the switch
+// exists to compare them).
+bool tile_path_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("RLM_SELECT_TILE");
+    return v == nullptr || v[0] != '0';
+  }();
+  return on;
+}
+
+// Fills the tile kernel's parameters when the shapes fit it.
+bool tile_params(const SelectParams& p, const Geometry& g, int act, int stat,
+                 const rlm_tensor* position, const rlm_tensor* aq, const rlm_tensor* arq,
+                 const rlm_tensor* pbase, const rlm_tensor* pcache, const rlm_tensor* akeys,
+                 const rlm_tensor* pkeys, const rlm_tensor* amean, const rlm_tensor* astd,
+                 const rlm_tensor* agamma, const rlm_tensor* abias, const rlm_tensor* pmean,
+                 const rlm_tensor* pstd, const rlm_tensor* pgamma, const rlm_tensor* pbias,
+                 TileParams& tp) {
+  if (act != RLM_BF16 || (stat != RLM_F32 && stat != RLM_BF16)) return false;
+  if (g.E != 64 || g.H * g.HD != 64 || g.H > kTileMaxHeads || g.HD % 4 != 0) return false;
+  if (g.T % 16 != 0 || g.T > kTileMaxRows || static_cast<int64_t>(g.NB) * g.BS != g.T) return false;
+  if (g.NB > 64 || g.NB % 4 != 0 || p.CAP > 256 || p.TOP > kTileMaxTop || p.K < 1 || p.K > kTileMaxK) return false;
+  if (g.H * g.RB > 1024) return false;
+  tp.B = g.B;
+  tp.Tq = g.Tq;
+  tp.T = g.T;
+  tp.NB = g.NB;
+  tp.BS = g.BS;
+  tp.BS_log2 = p.BS_log2;
+  tp.L = p.L;
+  tp.TOP = p.TOP;
+  tp.K = p.K;
+  tp.CAP = p.CAP;
+  tp.NCL = (p.CAP + 15) / 16;
+  tp.H = g.H;
+  tp.HD = g.HD;
+  tp.RB = g.RB;
+  tp.strict = p.strict;
+  tp.exact_scale = p.exact_scale;
+  tp.head_scale = p.head_scale;
+  tp.pos = position->data;
+  tp.pos_dtype = position->dtype;
+  tp.pos_sb = p.pos_sb;
+  tp.pos_sq = p.pos_sq;
+  tp.aq = static_cast<const bf16*>(aq->data);
+  tp.arq = static_cast<const bf16*>(arq->data);
+  tp.pbase = static_cast<const bf16*>(pbase->data);
+  tp.pcache = static_cast<const bf16*>(pcache->data);
+  tp.akeys = static_cast<const bf16*>(akeys->data);
+  tp.pkeys = static_cast<const bf16*>(pkeys->data);
+  tp.amean = amean->data;
+  tp.astd = astd->data;
+  tp.pmean = pmean->data;
+  tp.pstd = pstd->data;
+  tp.agamma = agamma->data;
+  tp.pgamma = pgamma->data;
+  tp.abias = abias->data;
+  tp.pbias = pbias->data;
+  tp.agamma_dtype = agamma->dtype;
+  tp.pgamma_dtype = pgamma->dtype;
+  tp.abias_dtype = abias->dtype;
+  tp.pbias_dtype = pbias->dtype;
+  tp.out_anchor = p.out_anchor;
+  tp.out_anchor_score = p.out_anchor_score;
+  tp.out_partner = p.out_partner;
+  tp.out_partner_score = p.out_partner_score;
+  tp.tiles = static_cast<int>((g.Tq + 15) / 16);
+  return select_tile_layout(tp);
+}
+
 hipError_t select_packed_impl(
     bool seq, bool ring, const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
     const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
@@ -1435,6 +1509,16 @@ hipError_t select_packed_impl(
   p.out_anchor_score = static_cast<float*>(out_anchor_score->data);
   p.out_partner = static_cast<int32_t*>(out_partner->data);
   p.out_partner_score = static_cast<float*>(out_partner_score->data);
+  if (seq && !ring && tile_path_enabled()) {
+    // bf16 activations, 64-wide exact and router vectors, caches of at most 512
+    // rows: the matrix-core-filtered kernel (rlm_select_tile.hip).
+    TileParams tp{};
+    if (tile_params(p, g, act, stat, position, anchor_query, anchor_router_query,
+                    partner_base, partner_anchor_cache, anchor_keys, partner_keys,
+                    anchor_block_mean, anchor_block_std, anchor_gamma, anchor_bias,
+                    partner_block_mean, partner_block_std, partner_gamma, partner_bias, tp))
+      return select_tile_launch(tp, stat, stream);
+  }
   if (ring) {
     RLM_REQUIRE(!seq, "ring-buffer caches are supported by the decode form only");
     RLM_REQUIRE((g.T & (g.T - 1)) == 0 && static_cast<int64_t>(g.NB) * g.BS == g.T,
