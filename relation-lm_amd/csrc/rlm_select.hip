@@ -1375,7 +1375,9 @@ bool tile_params(const SelectParams& p, const Geometry& g, int act, int stat,
                  const rlm_tensor* pstd, const rlm_tensor* pgamma, const rlm_tensor* pbias,
                  TileParams& tp) {
   if (act != RLM_BF16 || (stat != RLM_F32 && stat != RLM_BF16)) return false;
-  if (g.E != 64 || g.H * g.HD != 64 || g.H > kTileMaxHeads || g.HD % 4 != 0) return false;
+  if (g.E != 64 || g.H * g.HD != 64 || g.H > kTileMaxHeads || g.HD % 4 != 0 ||
+      (g.H & (g.H - 1)) != 0)
+    return false;
   if (g.T % 16 != 0 || g.T > kTileMaxRows || static_cast<int64_t>(g.NB) * g.BS != g.T) return false;
   if (g.NB > 64 || g.NB % 4 != 0 || p.CAP > 256 || p.TOP > kTileMaxTop || p.K < 1 || p.K > kTileMaxK) return false;
   if (g.H * g.RB > 1024) return false;
@@ -1391,6 +1393,7 @@ bool tile_params(const SelectParams& p, const Geometry& g, int act, int stat,
   tp.CAP = p.CAP;
   tp.NCL = (p.CAP + 15) / 16;
   tp.H = g.H;
+  tp.H_log2 = p.H_log2;
   tp.HD = g.HD;
   tp.RB = g.RB;
   tp.strict = p.strict;
@@ -1400,6 +1403,7 @@ bool tile_params(const SelectParams& p, const Geometry& g, int act, int stat,
   tp.pos_dtype = position->dtype;
   tp.pos_sb = p.pos_sb;
   tp.pos_sq = p.pos_sq;
+  tp.pos_count = p.pos_sb == 0 ? g.Tq : g.B * g.Tq;
   tp.aq = static_cast<const bf16*>(aq->data);
   tp.arq = static_cast<const bf16*>(arq->data);
   tp.pbase = static_cast<const bf16*>(pbase->data);

@@ -14,12 +14,13 @@ constexpr int kTileMaxRows = 512;  // cache rows staged in LDS
 
 struct TileParams {
   int64_t B, Tq, T;
-  int NB, BS, BS_log2, L, TOP, K, CAP, NCL, H, HD, RB;
+  int NB, BS, BS_log2, L, TOP, K, CAP, NCL, H, H_log2, HD, RB;
   int strict;
   double exact_scale, head_scale;
   const void* pos;
   int pos_dtype;
   int64_t pos_sb, pos_sq;
+  int64_t pos_count;  // elements of the position tensor
   const bf16* aq;      // [B*Tq, 64]
   const bf16* arq;     // [B*Tq, 64]
   const bf16* pbase;   // [B*Tq, 128]: exact half, router half
