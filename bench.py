@@ -301,11 +301,64 @@ def main() -> int:
                         "top 8, bf16, every position a query",
             "us": round(us, 1),
             "queries_per_s": round(mcfg.queries / (us * 1e-6), 1),
-            "stack_select_us": round(us * mcfg.layers, 1),
             "algorithmic_bytes": nbytes,
             "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "gathered_key_bytes": gathered,
             "gathered_GBps": round(gathered / (us * 1e-6) / 1e9, 1),
+            "stack": run_stack(mcfg),
+        }
+
+    def run_stack(mcfg, repeats=3):
+        """The cfg5 RelationBlockStack (4 routed multi-anchor blocks + final norm) on
+        the HIP path, random-init bf16 weights, synthetic N(0,1) hidden / memory:
+        the whole forward timed, and one block split into its selection half
+        (input norm, projections, router statistics, routed selection) and its
+        relation half (MLP hidden, second linear, LayerNorm / softmax / slot mix)."""
+        from relation_lm.models import MultiRelationBlockConfig, RelationBlockStack
+
+        bcfg = MultiRelationBlockConfig(
+            d_model=mcfg.d_model, gate_dim=mcfg.exact_dim, relation_dim=128, ff_mult=4,
+            anchors_per_block=mcfg.slots, partners_per_anchor=mcfg.k_out,
+            block_size=mcfg.block_size, local_window=mcfg.local_window,
+            top_blocks=mcfg.top_blocks, router_heads=mcfg.heads, router_head_dim=mcfg.head_dim,
+            rel_buckets=mcfg.rel_buckets)
+        torch.manual_seed(mcfg.seed)
+        stack = RelationBlockStack(bcfg, mcfg.layers).to(device=device, dtype=torch.bfloat16)
+        g = torch.Generator().manual_seed(mcfg.seed + 1)
+        shape = (mcfg.batch, mcfg.context, mcfg.d_model)
+        hidden = torch.randn(shape, generator=g).to(device=device, dtype=torch.bfloat16)
+        memory = torch.randn(shape, generator=g).to(device=device, dtype=torch.bfloat16)
+        block = stack.blocks[0]
+        with torch.no_grad():
+            for _ in range(2):
+                stack(hidden, memory)
+            torch.cuda.synchronize()
+            start.record()
+            for _ in range(repeats):
+                stack(hidden, memory)
+            end.record()
+            torch.cuda.synchronize()
+            stack_ms = start.elapsed_time(end) / repeats
+            marks = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            marks[0].record()
+            sel = block.select(hidden, memory)
+            marks[1].record()
+            block.relate(hidden, sel)
+            marks[2].record()
+            torch.cuda.synchronize()
+        layer_flops = 2 * mcfg.queries * mcfg.slots * mcfg.k_out * (
+            bcfg.relation_dim * bcfg.ff_mult * bcfg.d_model
+            + bcfg.ff_mult * bcfg.d_model * bcfg.d_model)
+        return {
+            "workload": (f"cfg5 RelationBlockStack: {mcfg.layers} routed multi-anchor blocks + "
+                         f"final norm, B={mcfg.batch} T={mcfg.context} d={mcfg.d_model}, "
+                         f"{mcfg.slots} slots x K={mcfg.k_out}, relation dim 128, MLP hidden "
+                         f"{bcfg.ff_mult * bcfg.d_model}, bf16, random-init weights"),
+            "stack_ms": round(stack_ms, 3),
+            "tokens_per_s": round(mcfg.queries / (stack_ms * 1e-3), 1),
+            "layer0_select_ms": round(marks[0].elapsed_time(marks[1]), 3),
+            "layer0_relate_ms": round(marks[1].elapsed_time(marks[2]), 3),
+            "relation_mlp_tflop_per_layer": round(layer_flops / 1e12, 3),
         }
 
     def run_reduce_cfg4(repeats=20):

@@ -387,6 +387,55 @@ hipError_t rlm_linear(const rlm_tensor* input, const rlm_tensor* weight,
                       const rlm_tensor* bias, const rlm_tensor* out,
                       hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Multi-anchor relation block (the cfg5 RelationBlockStack)
+ * ---------------------------------------------------------------------- */
+
+/*
+ * Replaces the post-selection half of MultiAnchorRelationBlock.forward
+ *   (src/relation_lm/models/multi_relation_blocks.py:163-178): the relation
+ * MLP's closing LayerNorm per (query, slot, partner) row (:51), the per-slot
+ * partner softmax without k_limit (:164-168), the slot context (:169-170), the
+ * slot mix (:172-177) and the residual gate (:178).  The MLP's two Linears run
+ * before it (rlm_relation_hidden_cached_seq over the S*K rows of each query,
+ * then rlm_linear).
+ *   raw [B,Tq,S*K,D] (row s*K + k; f32/bf16/f16), partner_scores f32
+ *   [B,Tq,S,K] (-inf marks an inactive partner), norm_weight / norm_bias [D],
+ *   slot_mix_logits [S], residual_gate 0-d, hidden [B,Tq,D] (the block input),
+ *   positions [Tq] or [B,Tq] (slot s is active iff s <= t).
+ *   S*K <= 64; D a multiple of 4, at most 2048.
+ * Outputs: out [B,Tq,D] in hidden's dtype = hidden + sigmoid(gate) * context;
+ *          context f32 [B,Tq,D] (the block's relation_context), or NULL.
+ */
+hipError_t rlm_multi_relation_reduce_seq(
+    const rlm_tensor* raw, const rlm_tensor* partner_scores, const rlm_tensor* norm_weight,
+    const rlm_tensor* norm_bias, const rlm_tensor* slot_mix_logits,
+    const rlm_tensor* residual_gate, const rlm_tensor* hidden, const rlm_tensor* positions,
+    double norm_eps, const rlm_tensor* out, const rlm_tensor* context, hipStream_t stream);
+
+/*
+ * Replaces nn.LayerNorm over the last dimension: the block's input_norm and
+ * the stack's final_norm (multi_relation_blocks.py:39, :111, :198, :207).
+ *   input [..., D] (1-4 dims, f32/bf16/f16), weight / bias [D].  D a multiple
+ *   of 4, at most 2048.  Statistics in fp32.
+ * Output: out, input's shape and dtype.
+ */
+hipError_t rlm_layer_norm(const rlm_tensor* input, const rlm_tensor* weight,
+                          const rlm_tensor* bias, double eps, const rlm_tensor* out,
+                          hipStream_t stream);
+
+/*
+ * Replaces DistilledBlockRouter.block_statistics
+ *   (src/relation_lm/routing/block_router.py:54-68): mean and biased std of
+ * the router keys over each block of block_size positions, per channel.
+ *   keys [B,T,C] (f32/bf16/f16), T a multiple of block_size.
+ * Outputs: out_mean, out_std f32 [B,T/block_size,C] (the [B,NB,H,HD] block
+ * statistics of the selection ops with C = H*HD).
+ */
+hipError_t rlm_block_statistics(const rlm_tensor* keys, int64_t block_size,
+                                const rlm_tensor* out_mean, const rlm_tensor* out_std,
+                                hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -564,6 +564,63 @@ at::Tensor packed_projection_to_caches(const at::Tensor& memory, const at::Tenso
   return out;
 }
 
+at::Tensor multi_relation_reduce_seq(const at::Tensor& raw, const at::Tensor& partner_scores,
+                                    const at::Tensor& norm_weight, const at::Tensor& norm_bias,
+                                    const at::Tensor& slot_mix_logits,
+                                    const at::Tensor& residual_gate, const at::Tensor& hidden,
+                                    const at::Tensor& positions, double norm_eps) {
+  const char* op = "relation_lm::multi_relation_reduce_seq";
+  c10::DeviceGuard guard(raw.device());
+  hipStream_t stream = device_stream(op, {&raw, &partner_scores, &norm_weight, &norm_bias,
+                                          &slot_mix_logits, &residual_gate, &hidden, &positions});
+  TORCH_CHECK(raw.dim() == 5 && partner_scores.dim() == 4, op,
+              ": raw must be [B,Tq,S,K,D] and partner_scores [B,Tq,S,K]");
+  const at::Tensor rows = raw.reshape({raw.size(0), raw.size(1), raw.size(2) * raw.size(3),
+                                       raw.size(4)});
+  at::Tensor out = at::empty_like(hidden, hidden.options().memory_format(at::MemoryFormat::Contiguous));
+  rlm_tensor d[9] = {desc(rows, "raw"),
+                     desc(partner_scores, "partner_scores"),
+                     desc(norm_weight, "norm_weight"),
+                     desc(norm_bias, "norm_bias"),
+                     desc(slot_mix_logits, "slot_mix_logits"),
+                     desc(residual_gate, "residual_gate"),
+                     desc(hidden, "hidden"),
+                     desc(positions, "positions"),
+                     desc(out, "out")};
+  check(rlm_multi_relation_reduce_seq(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7],
+                                      norm_eps, &d[8], nullptr, stream),
+        op);
+  return out;
+}
+
+at::Tensor layer_norm(const at::Tensor& input, const at::Tensor& weight, const at::Tensor& bias,
+                      double eps) {
+  const char* op = "relation_lm::layer_norm";
+  c10::DeviceGuard guard(input.device());
+  hipStream_t stream = device_stream(op, {&input, &weight, &bias});
+  TORCH_CHECK(input.dim() >= 1, op, ": input must have at least one dimension");
+  const at::Tensor x = input.reshape({-1, input.size(-1)});
+  at::Tensor out = at::empty(x.sizes(), x.options().memory_format(at::MemoryFormat::Contiguous));
+  rlm_tensor d[4] = {desc(x, "input"), desc(weight, "weight"), desc(bias, "bias"),
+                     desc(out, "out")};
+  check(rlm_layer_norm(&d[0], &d[1], &d[2], eps, &d[3], stream), op);
+  return out.view(input.sizes());
+}
+
+std::tuple<at::Tensor, at::Tensor> block_statistics(const at::Tensor& keys, int64_t block_size) {
+  const char* op = "relation_lm::block_statistics";
+  c10::DeviceGuard guard(keys.device());
+  hipStream_t stream = device_stream(op, {&keys});
+  TORCH_CHECK(keys.dim() == 3 && block_size > 0, op,
+              ": keys must be [B,T,C] and block_size positive");
+  const int64_t nb = keys.size(1) / block_size;
+  at::Tensor mean = at::empty({keys.size(0), nb, keys.size(2)}, f32(keys));
+  at::Tensor std_ = at::empty({keys.size(0), nb, keys.size(2)}, f32(keys));
+  rlm_tensor d[3] = {desc(keys, "keys"), desc(mean, "out_mean"), desc(std_, "out_std")};
+  check(rlm_block_statistics(&d[0], block_size, &d[1], &d[2], stream), op);
+  return {mean, std_};
+}
+
 }  // namespace
 
 TORCH_LIBRARY(relation_lm, m) {
@@ -644,6 +701,14 @@ TORCH_LIBRARY(relation_lm, m) {
   m.def(
       "relation_linear(Tensor input, Tensor weight, Tensor? bias=None, ScalarType? "
       "out_dtype=None) -> Tensor");
+  // Multi-anchor relation block (no reference op: the reference runs these in
+  // eager torch inside MultiAnchorRelationBlock / DistilledBlockRouter).
+  m.def(
+      "multi_relation_reduce_seq(Tensor raw, Tensor partner_scores, Tensor norm_weight, Tensor "
+      "norm_bias, Tensor slot_mix_logits, Tensor residual_gate, Tensor hidden, Tensor positions, "
+      "float norm_eps) -> Tensor");
+  m.def("layer_norm(Tensor input, Tensor weight, Tensor bias, float eps) -> Tensor");
+  m.def("block_statistics(Tensor keys, SymInt block_size) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY(relationlex, m) {
@@ -676,6 +741,9 @@ TORCH_LIBRARY_IMPL(relation_lm, CUDA, m) {
   m.impl("packed_sparse_cache_projection", TORCH_FN(packed_sparse_cache_projection));
   m.impl("packed_projection_to_caches", TORCH_FN(packed_projection_to_caches));
   m.impl("relation_linear", TORCH_FN(relation_linear));
+  m.impl("multi_relation_reduce_seq", TORCH_FN(multi_relation_reduce_seq));
+  m.impl("layer_norm", TORCH_FN(layer_norm));
+  m.impl("block_statistics", TORCH_FN(block_statistics));
 }
 
 // CPU tensors: the reference's PackedSparseCacheProjection.project is F.linear

@@ -113,5 +113,20 @@ def _register_fakes() -> None:
         return input.new_empty(tuple(input.shape[:-1]) + (weight.shape[0],),
                                dtype=out_dtype or input.dtype)
 
+    @torch.library.register_fake("relation_lm::multi_relation_reduce_seq")
+    def _(raw, partner_scores, norm_weight, norm_bias, slot_mix_logits, residual_gate, hidden,
+          positions, norm_eps):
+        return torch.empty_like(hidden, memory_format=torch.contiguous_format)
+
+    @torch.library.register_fake("relation_lm::layer_norm")
+    def _(input, weight, bias, eps):
+        return torch.empty_like(input, memory_format=torch.contiguous_format)
+
+    @torch.library.register_fake("relation_lm::block_statistics")
+    def _(keys, block_size):
+        shape = (keys.shape[0], keys.shape[1] // block_size, keys.shape[2])
+        return (keys.new_empty(shape, dtype=torch.float32),
+                keys.new_empty(shape, dtype=torch.float32))
+
 
 load()
