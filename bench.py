@@ -20,8 +20,8 @@ Also reported:
     roofline fraction of the dominant kernel (HBM bytes at the operator
     contract, or matrix-core FLOPs for the fused reduce);
   * decode-step latency (cfg3: packed 576->512 projection, router cache update,
-    cache-row writes, select, reduce) at B=1 and B=8, eager and replayed from a
-    HIP graph; the same step at position 4095 over 512-row ring-buffer caches;
+    cache-row writes, select, reduce, output-head preparation) at B=1 and B=8,
+    eager and replayed from a HIP graph; the same step at position 4095 over 512-row ring-buffer caches;
   * routed multi-anchor selection at cfg5 (B=4, T=4096, 4 anchor slots x K=6,
     block 64, local 128, top 8): one layer's selection over all 16384 queries;
   * the CPU baseline: the path restated in eager fp32 torch (oracle/eager.py),
@@ -154,7 +154,9 @@ def main() -> int:
         relation_hidden_cached,
         relation_hidden_cached_seq,
         relation_linear,
+        relation_linear_out,
         relation_norm_reduce,
+        relation_norm_reduce_output,
         relation_norm_reduce_seq,
         relation_reduce_fused_seq,
     )
@@ -232,9 +234,17 @@ def main() -> int:
             dargs = select_args(dsel, dcfg)
             t = (ring_position if ring else dcfg.context - 1) % dcfg.context  # cache row
             position = dsel["position"]
+            # Output-head preparation inputs (relation_lm.py:203-206): the token's
+            # query stream, the relation mix logit and output_norm.
+            gq = torch.Generator().manual_seed(dcfg.seed + 3)
+            head = {"query": torch.randn(batch, dcfg.d_model, generator=gq).to(device, dcfg.dtype),
+                    "mix": torch.tensor(-1.0, device=device),
+                    "weight": (1 + 0.1 * torch.randn(dcfg.d_model, generator=gq)).to(device, dcfg.dtype),
+                    "bias": (0.1 * torch.randn(dcfg.d_model, generator=gq)).to(device, dcfg.dtype)}
 
             def decode_step(dsel=dsel, dred=dred, dexp=dexp, memory=memory, projection=projection,
-                            dargs=dargs, t=t, position=position, batch=batch, rc=rc, dcfg=dcfg):
+                            dargs=dargs, t=t, position=position, batch=batch, rc=rc, dcfg=dcfg,
+                            head=head):
                 # projection + the token's key / operand / partner-anchor cache rows
                 parts = projection.project_into(memory, dsel["anchor_keys"], dsel["partner_keys"],
                                                 dred["operand_cache"],
@@ -250,15 +260,17 @@ def main() -> int:
                     hid = update_op(
                         dexp, dred["operand_cache"], a_, p_, dred["anchor_weight"],
                         dred["partner_weight"], dred["product_weight"], dred["first_bias"], position)
-                else:
-                    row = relation_linear(dred["operand_cache"][:, t], dred["expanded_weight"],
-                                          dred["expanded_bias"])
-                    dexp[:, t] = row
+                else:  # separate update: the row is written straight into the cache
+                    relation_linear_out(dred["operand_cache"][:, t], dred["expanded_weight"],
+                                        dred["expanded_bias"], dexp[:, t])
                     hid = cached_op(dexp, dred["operand_cache"], a_, p_, dred["product_weight"])
                 raw_ = relation_linear(hid, dred["second_weight"], dred["second_bias"],
                                        out_dtype=torch.float32)
-                return relation_norm_reduce(raw_, ps_, dred["norm_weight"], dred["norm_bias"],
-                                            position, 1e-5)
+                # norm-reduce with the output-head preparation as its epilogue
+                return relation_norm_reduce_output(raw_, ps_, dred["norm_weight"],
+                                                   dred["norm_bias"], position, 1e-5,
+                                                   head["query"], head["mix"], head["weight"],
+                                                   head["bias"], 1e-5)[1]
 
             for _ in range(20):
                 decode_step()

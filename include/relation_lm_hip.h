@@ -238,6 +238,36 @@ hipError_t rlm_relation_norm_reduce_seq(
     hipStream_t stream);
 
 /*
+ * rlm_relation_norm_reduce with the last-token output preparation fused as
+ * its epilogue (the reference's roadmap item "fuse last-token output
+ * preparation", README.md:150-151; the computation is RelationLexLM.forward's
+ * output_norm(query + sigmoid(relation_mix_logit) * context),
+ * src/relation_lm/models/relation_lm.py:203-206):
+ *   query [B,D] (f32/bf16/f16), mix_logit 0-d, output_weight/output_bias [D]
+ *   (output_norm), output_eps.
+ * Outputs: out_context f32 [B,D] (bit-identical to rlm_relation_norm_reduce),
+ *          out_final [B,D] in query's dtype = LayerNorm_out(query + sigmoid(mix) ctx).
+ */
+hipError_t rlm_relation_norm_reduce_output(
+    const rlm_tensor* raw, const rlm_tensor* partner_scores, const rlm_tensor* norm_weight,
+    const rlm_tensor* norm_bias, const rlm_tensor* position, double norm_eps,
+    const rlm_tensor* query, const rlm_tensor* mix_logit, const rlm_tensor* output_weight,
+    const rlm_tensor* output_bias, double output_eps, const rlm_tensor* out_context,
+    const rlm_tensor* out_final, hipStream_t stream);
+
+/*
+ * Sequence form of rlm_relation_norm_reduce_output: raw [B,Tq,K,D],
+ * partner_scores [B,Tq,K], positions [Tq] or [B,Tq], query [B,Tq,D];
+ * out_context f32 [B,Tq,D], out_final [B,Tq,D].
+ */
+hipError_t rlm_relation_norm_reduce_output_seq(
+    const rlm_tensor* raw, const rlm_tensor* partner_scores, const rlm_tensor* norm_weight,
+    const rlm_tensor* norm_bias, const rlm_tensor* positions, double norm_eps,
+    const rlm_tensor* query, const rlm_tensor* mix_logit, const rlm_tensor* output_weight,
+    const rlm_tensor* output_bias, double output_eps, const rlm_tensor* out_context,
+    const rlm_tensor* out_final, hipStream_t stream);
+
+/*
  * Fused relation reduce, sequence form (no reference counterpart: the
  * reference runs relation_hidden_cached -> F.linear -> relation_norm_reduce,
  * src/relation_lm/kernels/relation_reduce.py:149,420 and the call sequence of
@@ -379,9 +409,12 @@ hipError_t rlm_packed_projection_to_caches(
  * out = input @ weight^T (+ bias), the library GEMM behind the expanded-cache
  * projection (tests/test_relation_reduce_gpu.py:64-68 in the reference) and
  * the relation MLP's second linear (benchmarks/benchmark_relation_reduce.py:63).
- *   input [M,Kd] (f32/bf16/f16), weight [N,Kd] (same dtype), bias [N] or NULL.
- * Output: out [M,N] (f32/bf16/f16).  bf16/f16 inputs use MFMA with fp32
- * accumulation; f32 inputs use fp32 arithmetic throughout.
+ *   input [M,Kd] (f32/bf16/f16; rows may be strided), weight [N,Kd] (16-bit
+ *   weights take a 16-bit input of their dtype or f32, rounded on load; f32
+ *   weights take f32), bias [N] or NULL.
+ * Output: out [M,N] (f32/bf16/f16; unit column stride, rows may be strided,
+ * e.g. a cache column cache[:, t]).  16-bit weights use MFMA with fp32
+ * accumulation; f32 weights use fp32 arithmetic throughout.
  */
 hipError_t rlm_linear(const rlm_tensor* input, const rlm_tensor* weight,
                       const rlm_tensor* bias, const rlm_tensor* out,

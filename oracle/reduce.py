@@ -7,6 +7,7 @@ Restates in numpy:
   * ``_relation_hidden_cache_update_kernel``   relation_reduce.py:186-309
   * ``_relation_norm_reduce_kernel``           relation_reduce.py:360-417
   * ``PackedSparseCacheProjection.project``    inference/packed_cache.py:52-57
+  * the last-token output preparation          models/relation_lm.py:203-206
   * the caller's second linear                 benchmarks/benchmark_relation_reduce.py:63
 
 Everything is evaluated in float64 and rounded once to float32 (or to the
@@ -22,7 +23,9 @@ Parity pins (tests/test_oracle_reduce.py):
     dense weights of relation_lm.py:171-177;
   * packed projection == six separate torch linears
     (tests/test_packed_cache_projection.py:17-23);
-  * k_limit == ceil(log2(t + 2)) evaluated in float for every t < 2**20.
+  * k_limit == ceil(log2(t + 2)) evaluated in float for every t < 2**20;
+  * output_prep == torch F.layer_norm(query + sigmoid(mix) * context), and with
+    the mix logit at -inf equals the LayerNorm of the query alone.
 """
 from __future__ import annotations
 
@@ -222,6 +225,16 @@ def relation_norm_reduce_seq(raw, partner_scores, norm_weight, norm_bias, positi
                             np.asarray(partner_scores).reshape(-1, k), norm_weight, norm_bias,
                             np.ascontiguousarray(pos).reshape(-1), norm_eps)
     return out.reshape(batch, queries, d)
+
+
+def output_prep(query, context, mix_logit, output_weight, output_bias, eps) -> np.ndarray:
+    """output_norm(query + sigmoid(mix_logit) * context) in float64
+    (RelationLexLM.forward, relation_lm.py:203-206)."""
+    gate = 1.0 / (1.0 + np.exp(-float(mix_logit)))
+    y = _f64(query) + gate * _f64(context)
+    mean = y.mean(axis=-1, keepdims=True)
+    var = ((y - mean) ** 2).mean(axis=-1, keepdims=True)
+    return (y - mean) / np.sqrt(var + float(eps)) * _f64(output_weight) + _f64(output_bias)
 
 
 def packed_sparse_cache_projection(memory, weight) -> np.ndarray:

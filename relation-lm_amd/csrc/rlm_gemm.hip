@@ -55,6 +55,7 @@ struct GemmParams {
   const void* bias;
   int bias_dtype;
   void* out;
+  int64_t ldo;  // output row stride in elements (>= N)
   uint32_t a_bytes, w_bytes;  // descriptor sizes of A and W (smallk_kernel; < 2 GiB)
   // Optional cache-row scatter (decode projection, skinny kernel only): output
   // columns [seg_lo[s], seg_hi[s]) of row m also go to row `position` of cache
@@ -124,7 +125,7 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const f32x4& acc
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int64_t m = m0 + e;
-    if (m < p.M) out[m * p.N + n] = from_f32<TO>(acc[e] + bv);
+    if (m < p.M) out[m * p.ldo + n] = from_f32<TO>(acc[e] + bv);
   }
 }
 
@@ -343,7 +344,7 @@ __global__ void __launch_bounds__(256) smallk_kernel(const GemmParams p) {
     vw[t] = load8_buf<W, W>(wr, static_cast<uint32_t>(n * K + 8 * q), n < p.N);
   }
   TO* out = static_cast<TO*>(p.out);
-  const bool full = m0 + 64 <= p.M && n0 + 64 <= p.N && p.N % kVec == 0 &&
+  const bool full = m0 + 64 <= p.M && n0 + 64 <= p.N && p.ldo % kVec == 0 &&
                     (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
   // Bias of this lane's output columns n0 + 16j + 4g .. +3 on full tiles: one
   // 16-byte (fp32) or 8-byte (16-bit) load per j, the other form out of range
@@ -417,7 +418,7 @@ __global__ void __launch_bounds__(256) smallk_kernel(const GemmParams p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int64_t n = n0 + 16 * j + 4 * g + e;
-          if (n < p.N) out[m * p.N + n] = from_f32<TO>(acc[i][j][e] + bv[j][e]);
+          if (n < p.N) out[m * p.ldo + n] = from_f32<TO>(acc[i][j][e] + bv[j][e]);
         }
     }
     return;
@@ -428,7 +429,7 @@ __global__ void __launch_bounds__(256) smallk_kernel(const GemmParams p) {
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        *reinterpret_cast<float4*>(out + (m0 + 16 * i + r16) * p.N + n0 + 16 * j + 4 * g) =
+        *reinterpret_cast<float4*>(out + (m0 + 16 * i + r16) * p.ldo + n0 + 16 * j + 4 * g) =
             make_float4(acc[i][j][0] + bv[j][0], acc[i][j][1] + bv[j][1], acc[i][j][2] + bv[j][2],
                         acc[i][j][3] + bv[j][3]);
   } else {
@@ -448,7 +449,7 @@ __global__ void __launch_bounds__(256) smallk_kernel(const GemmParams p) {
       const int piece = t * kWave + lane;
       const int row = piece / (64 / kVec);
       const int col = (piece % (64 / kVec)) * kVec;
-      *reinterpret_cast<uint4*>(out + (m0 + row) * p.N + n0 + col) =
+      *reinterpret_cast<uint4*>(out + (m0 + row) * p.ldo + n0 + col) =
           *reinterpret_cast<const uint4*>(st + row * kLdo + col);
     }
   }
@@ -707,7 +708,7 @@ hipError_t linear_impl(const rlm_tensor* input, const rlm_tensor* weight, const 
                        const GemmParams* scatter = nullptr) {
   RLM_TRY(check_rows(input, "input"));
   RLM_TRY(check_tensor(weight, "weight", 2));
-  RLM_TRY(check_tensor(out, "out", 2));
+  RLM_TRY(check_rows(out, "out"));
   RLM_TRY(check_dtype_float(input, "input"));
   RLM_TRY(check_dtype_float(weight, "weight"));
   RLM_TRY(check_dtype_float(out, "out"));
@@ -730,6 +731,7 @@ hipError_t linear_impl(const rlm_tensor* input, const rlm_tensor* weight, const 
   p.bias = bias ? bias->data : nullptr;
   p.bias_dtype = bias ? bias->dtype : RLM_F32;
   p.out = out->data;
+  p.ldo = M > 1 ? out->stride[0] : N;
   {
     // Byte extents of A (last row counts K elements) and W; 0 marks "too large
     // for 32-bit buffer offsets" (the tile kernels take it then).

@@ -529,7 +529,41 @@ struct NormParams {
   int64_t pos_sb, pos_sq;
   float eps;
   float* out;           // [Q,D]
+  // Output-head preparation (relation_lm.py:203-206), when `prep` is set:
+  //   final = LayerNorm_out(query + sigmoid(mix) * context), in the query's dtype.
+  // Unset, every pointer below aliases `w` (D elements of w_dtype), so the
+  // epilogue's loads stay unconditional and in bounds.
+  int prep;
+  const void* query;    // [Q,D]
+  const void* mix;      // 0-d mix logit
+  const void* ow;       // [D] output_norm weight
+  const void* ob;       // [D] output_norm bias
+  int query_dtype, mix_dtype, ow_dtype, ob_dtype;
+  float out_eps;
+  void* final;          // [Q,D], query_dtype
 };
+
+__device__ __forceinline__ void store_any4(void* base, int dtype, int64_t i4, float4 v) {
+  if (dtype == RLM_F32) {
+    reinterpret_cast<float4*>(base)[i4] = v;
+  } else if (dtype == RLM_BF16) {
+    reinterpret_cast<uint2*>(base)[i4] = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+  } else {
+    f16* h = static_cast<f16*>(base) + 4 * i4;
+    h[0] = static_cast<f16>(v.x);
+    h[1] = static_cast<f16>(v.y);
+    h[2] = static_cast<f16>(v.z);
+    h[3] = static_cast<f16>(v.w);
+  }
+}
+__device__ __forceinline__ void store_any(void* base, int dtype, int64_t i, float v) {
+  if (dtype == RLM_F32)
+    static_cast<float*>(base)[i] = v;
+  else if (dtype == RLM_BF16)
+    static_cast<bf16*>(base)[i] = f32_to_bf16(v);
+  else
+    static_cast<f16*>(base)[i] = static_cast<f16>(v);
+}
 
 // Softmax weight of partner `lane` (lanes 0..K-1; K <= 64) for the query at
 // position t: k_limit = clamp(ceil(log2(t + 2)), 1, K) == clamp(bit_length(t + 1), 1, K),
@@ -585,13 +619,19 @@ __global__ void __launch_bounds__(256) norm_reduce_vec_kernel(const NormParams p
   const int groups = p.D >> 2;
   const TR* raw = static_cast<const TR*>(p.raw) + q * p.K * static_cast<int64_t>(p.D);
 
-  F4Words gw[G], bw[G];
+  F4Words gw[G], bw[G], qw[G], ow[G], obw[G];
+  const int64_t qoff = p.prep ? q * (p.D >> 2) : 0;
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int g = lane + kWave * i;
-    gw[i] = f4_issue(p.w, p.w_dtype, g < groups ? g : 0);
-    bw[i] = f4_issue(p.bias, p.b_dtype, g < groups ? g : 0);
+    const int gs = g < groups ? g : 0;
+    gw[i] = f4_issue(p.w, p.w_dtype, gs);
+    bw[i] = f4_issue(p.bias, p.b_dtype, gs);
+    qw[i] = f4_issue(p.query, p.query_dtype, qoff + gs);
+    ow[i] = f4_issue(p.ow, p.ow_dtype, gs);
+    obw[i] = f4_issue(p.ob, p.ob_dtype, gs);
   }
+  const float mix = load_any_f(p.mix, p.mix_dtype, 0);
   // Partner rows in batches of KB; the first batch is issued before anything
   // is decoded, so position, scores, gamma / beta and these rows share one
   // memory round trip.
@@ -657,6 +697,43 @@ __global__ void __launch_bounds__(256) norm_reduce_vec_kernel(const NormParams p
     const int g = lane + kWave * i;
     if (g < groups) *reinterpret_cast<float4*>(out + 4 * g) = ctx[i];
   }
+  if (p.prep) {  // wave-uniform
+    // Output-head preparation: LayerNorm_out(query + sigmoid(mix) * context).
+    const float gate = 1.0f / (1.0f + expf(-mix));
+    float4 y[G];
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const bool in = lane + kWave * i < groups;
+      const float4 qv = f4_decode(qw[i], p.query_dtype);
+      y[i] = in ? make_float4(fmaf(gate, ctx[i].x, qv.x), fmaf(gate, ctx[i].y, qv.y),
+                              fmaf(gate, ctx[i].z, qv.z), fmaf(gate, ctx[i].w, qv.w))
+                : make_float4(0.f, 0.f, 0.f, 0.f);
+      sum += (y[i].x + y[i].y) + (y[i].z + y[i].w);
+    }
+    const float mean = wave_sum_f32(sum) * inv_d;
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      if (lane + kWave * i < groups) {
+        const float dx = y[i].x - mean, dy = y[i].y - mean, dz = y[i].z - mean, dw = y[i].w - mean;
+        sq += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+      }
+    }
+    const float rstd = rsqrtf(wave_sum_f32(sq) * inv_d + p.out_eps);
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int g = lane + kWave * i;
+      if (g >= groups) continue;
+      const float4 w4 = f4_decode(ow[i], p.ow_dtype);
+      const float4 b4 = f4_decode(obw[i], p.ob_dtype);
+      store_any4(p.final, p.query_dtype, q * (p.D >> 2) + g,
+                 make_float4(fmaf((y[i].x - mean) * rstd, w4.x, b4.x),
+                             fmaf((y[i].y - mean) * rstd, w4.y, b4.y),
+                             fmaf((y[i].z - mean) * rstd, w4.z, b4.z),
+                             fmaf((y[i].w - mean) * rstd, w4.w, b4.w)));
+    }
+  }
 }
 
 template <typename TR, int VPL>
@@ -669,14 +746,20 @@ __global__ void __launch_bounds__(256) norm_reduce_kernel(const NormParams p) {
   const int64_t t = load_any_i(p.pos, p.pos_dtype, b * p.pos_sb + tq * p.pos_sq);
   const float prob = partner_weight(p, partner_score(p, q, lane), t, lane);
 
-  float gam[VPL], bet[VPL], ctx[VPL];
+  float gam[VPL], bet[VPL], ctx[VPL], qv[VPL], ow[VPL], obv[VPL];
+  const int64_t qoff = p.prep ? q * p.D : 0;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int d = lane + kWave * i;
+    const int ds = d < p.D ? d : 0;
     gam[i] = d < p.D ? load_any_f(p.w, p.w_dtype, d) : 0.0f;
     bet[i] = d < p.D ? load_any_f(p.bias, p.b_dtype, d) : 0.0f;
+    qv[i] = load_any_f(p.query, p.query_dtype, qoff + ds);
+    ow[i] = load_any_f(p.ow, p.ow_dtype, ds);
+    obv[i] = load_any_f(p.ob, p.ob_dtype, ds);
     ctx[i] = 0.0f;
   }
+  const float mix = load_any_f(p.mix, p.mix_dtype, 0);
   const float inv_d = 1.0f / static_cast<float>(p.D);
   const TR* raw = static_cast<const TR*>(p.raw) + q * p.K * static_cast<int64_t>(p.D);
   for (int k = 0; k < p.K; ++k) {
@@ -709,6 +792,28 @@ __global__ void __launch_bounds__(256) norm_reduce_kernel(const NormParams p) {
   for (int i = 0; i < VPL; ++i) {
     const int d = lane + kWave * i;
     if (d < p.D) out[d] = ctx[i];
+  }
+  if (p.prep) {  // wave-uniform: output-head preparation, as the vector kernel
+    const float gate = 1.0f / (1.0f + expf(-mix));
+    float y[VPL], sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      y[i] = lane + kWave * i < p.D ? fmaf(gate, ctx[i], qv[i]) : 0.0f;
+      sum += y[i];
+    }
+    const float mean = wave_sum_f32(sum) * inv_d;
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const float dv = lane + kWave * i < p.D ? y[i] - mean : 0.0f;
+      sq += dv * dv;
+    }
+    const float rstd = rsqrtf(wave_sum_f32(sq) * inv_d + p.out_eps);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int d = lane + kWave * i;
+      if (d < p.D) store_any(p.final, p.query_dtype, q * p.D + d, fmaf((y[i] - mean) * rstd, ow[i], obv[i]));
+    }
   }
 }
 
@@ -856,10 +961,20 @@ hipError_t launch_norm_vpl(const NormParams& p, int dtype, hipStream_t stream) {
   return hipErrorInvalidValue;
 }
 
+// Output-head preparation arguments of norm_impl (all null: context only).
+struct OutputPrep {
+  const rlm_tensor* query = nullptr;
+  const rlm_tensor* mix_logit = nullptr;
+  const rlm_tensor* weight = nullptr;
+  const rlm_tensor* bias = nullptr;
+  double eps = 0.0;
+  const rlm_tensor* final = nullptr;
+};
+
 hipError_t norm_impl(bool seq, const rlm_tensor* raw, const rlm_tensor* partner_scores,
                      const rlm_tensor* norm_weight, const rlm_tensor* norm_bias,
                      const rlm_tensor* position, double norm_eps, const rlm_tensor* out,
-                     hipStream_t stream) {
+                     hipStream_t stream, const OutputPrep& prep = OutputPrep()) {
   clear_error();
   const int qd = seq ? 2 : 1;
   RLM_TRY(check_tensor(raw, "raw", qd + 2));
@@ -921,8 +1036,48 @@ hipError_t norm_impl(bool seq, const rlm_tensor* raw, const rlm_tensor* partner_
   p.pos_dtype = position->dtype;
   p.eps = static_cast<float>(norm_eps);
   p.out = static_cast<float*>(out->data);
+  p.prep = prep.query != nullptr;
+  p.query = p.mix = p.ow = p.ob = p.w;
+  p.query_dtype = p.mix_dtype = p.ow_dtype = p.ob_dtype = p.w_dtype;
+  p.final = nullptr;
+  if (p.prep) {
+    const int qd = seq ? 2 : 1;
+    RLM_TRY(check_tensor(prep.query, "query", qd + 1));
+    RLM_TRY(check_dtype_float(prep.query, "query"));
+    RLM_TRY(check_dim(prep.query, "query", 0, B));
+    if (seq) RLM_TRY(check_dim(prep.query, "query", 1, Tq));
+    RLM_TRY(check_dim(prep.query, "query", qd, D));
+    RLM_TRY(check_tensor(prep.mix_logit, "mix_logit", 0));
+    RLM_TRY(check_dtype_float(prep.mix_logit, "mix_logit"));
+    RLM_TRY(check_tensor(prep.weight, "output_weight", 1));
+    RLM_TRY(check_dtype_float(prep.weight, "output_weight"));
+    RLM_TRY(check_dim(prep.weight, "output_weight", 0, D));
+    RLM_TRY(check_tensor(prep.bias, "output_bias", 1));
+    RLM_TRY(check_dtype_float(prep.bias, "output_bias"));
+    RLM_TRY(check_dim(prep.bias, "output_bias", 0, D));
+    RLM_TRY(check_tensor(prep.final, "out_final", qd + 1));
+    RLM_TRY(check_same_dtype(prep.final, "out_final", prep.query, "query"));
+    RLM_TRY(check_dim(prep.final, "out_final", 0, B));
+    if (seq) RLM_TRY(check_dim(prep.final, "out_final", 1, Tq));
+    RLM_TRY(check_dim(prep.final, "out_final", qd, D));
+    for (const rlm_tensor* t : {prep.query, prep.weight, prep.bias, prep.final})
+      RLM_REQUIRE((reinterpret_cast<uintptr_t>(t->data) & 15u) == 0,
+                  "query, output_weight, output_bias and out_final must be 16-byte aligned");
+    p.query = prep.query->data;
+    p.query_dtype = prep.query->dtype;
+    p.mix = prep.mix_logit->data;
+    p.mix_dtype = prep.mix_logit->dtype;
+    p.ow = prep.weight->data;
+    p.ow_dtype = prep.weight->dtype;
+    p.ob = prep.bias->data;
+    p.ob_dtype = prep.bias->dtype;
+    p.out_eps = static_cast<float>(prep.eps);
+    p.final = prep.final->data;
+  }
   if (p.Q == 0) return hipSuccess;
-  if (D % 4 == 0 && (reinterpret_cast<uintptr_t>(raw->data) & 15u) == 0) {
+  if (D % 4 == 0 && (reinterpret_cast<uintptr_t>(raw->data) & 15u) == 0 &&
+      (reinterpret_cast<uintptr_t>(norm_weight->data) & 15u) == 0 &&
+      (reinterpret_cast<uintptr_t>(norm_bias->data) & 15u) == 0) {
     const int groups = static_cast<int>((D / 4 + kWave - 1) / kWave);
     if (groups <= 1) return launch_norm_vec<1, 8>(p, raw->dtype, stream);
     if (groups <= 2) return launch_norm_vec<2, 8>(p, raw->dtype, stream);
@@ -1070,6 +1225,42 @@ extern "C" hipError_t rlm_relation_norm_reduce(const rlm_tensor* raw,
                                                const rlm_tensor* out, hipStream_t stream) {
   return norm_impl(false, raw, partner_scores, norm_weight, norm_bias, position, norm_eps, out,
                    stream);
+}
+
+extern "C" hipError_t rlm_relation_norm_reduce_output(
+    const rlm_tensor* raw, const rlm_tensor* partner_scores, const rlm_tensor* norm_weight,
+    const rlm_tensor* norm_bias, const rlm_tensor* position, double norm_eps,
+    const rlm_tensor* query, const rlm_tensor* mix_logit, const rlm_tensor* output_weight,
+    const rlm_tensor* output_bias, double output_eps, const rlm_tensor* out_context,
+    const rlm_tensor* out_final, hipStream_t stream) {
+  RLM_REQUIRE(query != nullptr, "query: missing tensor");
+  OutputPrep prep;
+  prep.query = query;
+  prep.mix_logit = mix_logit;
+  prep.weight = output_weight;
+  prep.bias = output_bias;
+  prep.eps = output_eps;
+  prep.final = out_final;
+  return norm_impl(false, raw, partner_scores, norm_weight, norm_bias, position, norm_eps,
+                   out_context, stream, prep);
+}
+
+extern "C" hipError_t rlm_relation_norm_reduce_output_seq(
+    const rlm_tensor* raw, const rlm_tensor* partner_scores, const rlm_tensor* norm_weight,
+    const rlm_tensor* norm_bias, const rlm_tensor* positions, double norm_eps,
+    const rlm_tensor* query, const rlm_tensor* mix_logit, const rlm_tensor* output_weight,
+    const rlm_tensor* output_bias, double output_eps, const rlm_tensor* out_context,
+    const rlm_tensor* out_final, hipStream_t stream) {
+  RLM_REQUIRE(query != nullptr, "query: missing tensor");
+  OutputPrep prep;
+  prep.query = query;
+  prep.mix_logit = mix_logit;
+  prep.weight = output_weight;
+  prep.bias = output_bias;
+  prep.eps = output_eps;
+  prep.final = out_final;
+  return norm_impl(true, raw, partner_scores, norm_weight, norm_bias, positions, norm_eps,
+                   out_context, stream, prep);
 }
 
 extern "C" hipError_t rlm_relation_norm_reduce_seq(const rlm_tensor* raw,

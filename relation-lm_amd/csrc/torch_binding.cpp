@@ -413,6 +413,59 @@ at::Tensor relation_norm_reduce_seq(const at::Tensor& raw, const at::Tensor& par
   return norm_common(true, raw, partner_scores, norm_weight, norm_bias, positions, norm_eps);
 }
 
+std::tuple<at::Tensor, at::Tensor> norm_output_common(
+    bool seq, const at::Tensor& raw, const at::Tensor& partner_scores,
+    const at::Tensor& norm_weight, const at::Tensor& norm_bias, const at::Tensor& position,
+    double norm_eps, const at::Tensor& query, const at::Tensor& mix_logit,
+    const at::Tensor& output_weight, const at::Tensor& output_bias, double output_eps) {
+  const char* op = seq ? "relation_lm::relation_norm_reduce_output_seq"
+                       : "relation_lm::relation_norm_reduce_output";
+  c10::DeviceGuard guard(raw.device());
+  hipStream_t stream =
+      device_stream(op, {&raw, &partner_scores, &norm_weight, &norm_bias, &position, &query,
+                         &mix_logit, &output_weight, &output_bias});
+  TORCH_CHECK(raw.dim() == (seq ? 4 : 3), op, ": raw must be ", seq ? "[B,Tq,K,D]" : "[B,K,D]");
+  std::vector<int64_t> shape{raw.size(0)};
+  if (seq) shape.push_back(raw.size(1));
+  shape.push_back(raw.size(raw.dim() - 1));
+  at::Tensor context = at::empty(shape, f32(raw));
+  at::Tensor final = at::empty(shape, query.options().memory_format(at::MemoryFormat::Contiguous));
+  rlm_tensor d[11] = {desc(raw, "raw"),
+                      desc(partner_scores, "partner_scores"),
+                      desc(norm_weight, "norm_weight"),
+                      desc(norm_bias, "norm_bias"),
+                      desc(position, "position"),
+                      desc(query, "query"),
+                      desc(mix_logit, "mix_logit"),
+                      desc(output_weight, "output_weight"),
+                      desc(output_bias, "output_bias"),
+                      desc(context, "out_context"),
+                      desc(final, "out_final")};
+  auto fn = seq ? rlm_relation_norm_reduce_output_seq : rlm_relation_norm_reduce_output;
+  check(fn(&d[0], &d[1], &d[2], &d[3], &d[4], norm_eps, &d[5], &d[6], &d[7], &d[8], output_eps,
+           &d[9], &d[10], stream),
+        op);
+  return {context, final};
+}
+
+std::tuple<at::Tensor, at::Tensor> relation_norm_reduce_output(
+    const at::Tensor& raw, const at::Tensor& partner_scores, const at::Tensor& norm_weight,
+    const at::Tensor& norm_bias, const at::Tensor& position, double norm_eps,
+    const at::Tensor& query, const at::Tensor& mix_logit, const at::Tensor& output_weight,
+    const at::Tensor& output_bias, double output_eps) {
+  return norm_output_common(false, raw, partner_scores, norm_weight, norm_bias, position,
+                            norm_eps, query, mix_logit, output_weight, output_bias, output_eps);
+}
+
+std::tuple<at::Tensor, at::Tensor> relation_norm_reduce_output_seq(
+    const at::Tensor& raw, const at::Tensor& partner_scores, const at::Tensor& norm_weight,
+    const at::Tensor& norm_bias, const at::Tensor& positions, double norm_eps,
+    const at::Tensor& query, const at::Tensor& mix_logit, const at::Tensor& output_weight,
+    const at::Tensor& output_bias, double output_eps) {
+  return norm_output_common(true, raw, partner_scores, norm_weight, norm_bias, positions,
+                            norm_eps, query, mix_logit, output_weight, output_bias, output_eps);
+}
+
 at::Tensor relation_reduce_fused_seq(const at::Tensor& expanded_cache,
                                      const at::Tensor& operand_cache,
                                      const at::Tensor& anchor_index,
@@ -472,6 +525,22 @@ at::Tensor linear_common(const char* op, const at::Tensor& input, const at::Tens
   }
   check(err, op);
   return out.view(shape);
+}
+
+// out = input @ weight^T (+ bias) written into a caller-provided 2-d view whose
+// rows may be strided (a cache column such as expanded_cache[:, t]).
+void relation_linear_out(const at::Tensor& input, const at::Tensor& weight,
+                         const c10::optional<at::Tensor>& bias, at::Tensor& out) {
+  const char* op = "relation_lm::relation_linear_out";
+  c10::DeviceGuard guard(input.device());
+  at::Tensor b = bias.has_value() ? *bias : at::Tensor();
+  hipStream_t stream = device_stream(op, {&input, &weight, &b, &out});
+  TORCH_CHECK(input.dim() == 2 && weight.dim() == 2 && out.dim() == 2, op,
+              ": input, weight and out must be 2-D");
+  rlm_tensor dx = desc(input, "input"), dw = desc(weight, "weight"), dout = desc(out, "out");
+  rlm_tensor db{};
+  if (b.defined()) db = desc(b, "bias");
+  check(rlm_linear(&dx, &dw, b.defined() ? &db : nullptr, &dout, stream), op);
 }
 
 at::Tensor packed_sparse_cache_projection(const at::Tensor& memory, const at::Tensor& weight) {
@@ -701,6 +770,8 @@ TORCH_LIBRARY(relation_lm, m) {
   m.def(
       "relation_linear(Tensor input, Tensor weight, Tensor? bias=None, ScalarType? "
       "out_dtype=None) -> Tensor");
+  m.def(
+      "relation_linear_out(Tensor input, Tensor weight, Tensor? bias, Tensor(a!) out) -> ()");
   // Multi-anchor relation block (no reference op: the reference runs these in
   // eager torch inside MultiAnchorRelationBlock / DistilledBlockRouter).
   m.def(
@@ -708,6 +779,16 @@ TORCH_LIBRARY(relation_lm, m) {
       "norm_bias, Tensor slot_mix_logits, Tensor residual_gate, Tensor hidden, Tensor positions, "
       "float norm_eps) -> Tensor");
   m.def("layer_norm(Tensor input, Tensor weight, Tensor bias, float eps) -> Tensor");
+  // Norm-reduce with the last-token output preparation as its epilogue
+  // (roadmap item of the reference, README.md:150-151; relation_lm.py:203-206).
+  m.def(
+      "relation_norm_reduce_output(Tensor raw, Tensor partner_scores, Tensor norm_weight, Tensor "
+      "norm_bias, Tensor position, float norm_eps, Tensor query, Tensor mix_logit, Tensor "
+      "output_weight, Tensor output_bias, float output_eps) -> (Tensor, Tensor)");
+  m.def(
+      "relation_norm_reduce_output_seq(Tensor raw, Tensor partner_scores, Tensor norm_weight, "
+      "Tensor norm_bias, Tensor positions, float norm_eps, Tensor query, Tensor mix_logit, Tensor "
+      "output_weight, Tensor output_bias, float output_eps) -> (Tensor, Tensor)");
   m.def("block_statistics(Tensor keys, SymInt block_size) -> (Tensor, Tensor)");
 }
 
@@ -741,8 +822,11 @@ TORCH_LIBRARY_IMPL(relation_lm, CUDA, m) {
   m.impl("packed_sparse_cache_projection", TORCH_FN(packed_sparse_cache_projection));
   m.impl("packed_projection_to_caches", TORCH_FN(packed_projection_to_caches));
   m.impl("relation_linear", TORCH_FN(relation_linear));
+  m.impl("relation_linear_out", TORCH_FN(relation_linear_out));
   m.impl("multi_relation_reduce_seq", TORCH_FN(multi_relation_reduce_seq));
   m.impl("layer_norm", TORCH_FN(layer_norm));
+  m.impl("relation_norm_reduce_output", TORCH_FN(relation_norm_reduce_output));
+  m.impl("relation_norm_reduce_output_seq", TORCH_FN(relation_norm_reduce_output_seq));
   m.impl("block_statistics", TORCH_FN(block_statistics));
 }
 

@@ -113,10 +113,23 @@ def _register_fakes() -> None:
         return input.new_empty(tuple(input.shape[:-1]) + (weight.shape[0],),
                                dtype=out_dtype or input.dtype)
 
+    @torch.library.register_fake("relation_lm::relation_linear_out")
+    def _(input, weight, bias, out):
+        return None
+
     @torch.library.register_fake("relation_lm::multi_relation_reduce_seq")
     def _(raw, partner_scores, norm_weight, norm_bias, slot_mix_logits, residual_gate, hidden,
           positions, norm_eps):
         return torch.empty_like(hidden, memory_format=torch.contiguous_format)
+
+    def fake_norm_output(raw, partner_scores, norm_weight, norm_bias, position, norm_eps, query,
+                         mix_logit, output_weight, output_bias, output_eps):
+        shape = tuple(raw.shape[:-2]) + (raw.shape[-1],)
+        return (raw.new_empty(shape, dtype=torch.float32),
+                query.new_empty(shape))
+
+    torch.library.register_fake("relation_lm::relation_norm_reduce_output")(fake_norm_output)
+    torch.library.register_fake("relation_lm::relation_norm_reduce_output_seq")(fake_norm_output)
 
     @torch.library.register_fake("relation_lm::layer_norm")
     def _(input, weight, bias, eps):

@@ -142,6 +142,47 @@ def relation_norm_reduce_seq(
         raw, partner_scores, norm_weight, norm_bias, positions, float(norm_eps))
 
 
+def relation_norm_reduce_output(
+    raw: Tensor,
+    partner_scores: Tensor,
+    norm_weight: Tensor,
+    norm_bias: Tensor,
+    position: Tensor,
+    norm_eps: float,
+    query: Tensor,
+    mix_logit: Tensor,
+    output_weight: Tensor,
+    output_bias: Tensor,
+    output_eps: float,
+) -> tuple[Tensor, Tensor]:
+    """relation_norm_reduce with the last-token output preparation fused in (the
+    reference's roadmap item, README.md:150-151): returns (context f32 [B,D],
+    final [B,D]) with final = output_norm(query + sigmoid(mix_logit) * context)
+    as RelationLexLM.forward (relation_lm.py:203-206), in query's dtype."""
+    return torch.ops.relation_lm.relation_norm_reduce_output(
+        raw, partner_scores, norm_weight, norm_bias, position, float(norm_eps), query, mix_logit,
+        output_weight, output_bias, float(output_eps))
+
+
+def relation_norm_reduce_output_seq(
+    raw: Tensor,
+    partner_scores: Tensor,
+    norm_weight: Tensor,
+    norm_bias: Tensor,
+    positions: Tensor,
+    norm_eps: float,
+    query: Tensor,
+    mix_logit: Tensor,
+    output_weight: Tensor,
+    output_bias: Tensor,
+    output_eps: float,
+) -> tuple[Tensor, Tensor]:
+    """Sequence form of relation_norm_reduce_output: query [B,Tq,D]."""
+    return torch.ops.relation_lm.relation_norm_reduce_output_seq(
+        raw, partner_scores, norm_weight, norm_bias, positions, float(norm_eps), query,
+        mix_logit, output_weight, output_bias, float(output_eps))
+
+
 def relation_reduce_fused_seq(
     expanded_cache: Tensor,
     operand_cache: Tensor,
@@ -173,3 +214,10 @@ def relation_linear(input: Tensor, weight: Tensor, bias: Tensor | None = None,
                     out_dtype: torch.dtype | None = None) -> Tensor:
     """``input @ weight.T + bias`` on MFMA (bf16/f16 weights) or fp32 FMA (fp32 weights)."""
     return torch.ops.relation_lm.relation_linear(input, weight, bias, out_dtype)
+
+
+def relation_linear_out(input: Tensor, weight: Tensor, bias: Tensor | None, out: Tensor) -> None:
+    """``out[:] = input @ weight.T + bias`` into a 2-d view whose rows may be strided
+    (e.g. ``expanded_cache[:, t]``: the decode step's separate cache-row update
+    written in place, relation_reduce.py:60-69's "separate_update" mode)."""
+    torch.ops.relation_lm.relation_linear_out(input, weight, bias, out)

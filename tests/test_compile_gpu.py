@@ -244,6 +244,30 @@ def op_cases(device):
                   (memory, weight) + caches + (pos, False)))
     cases.append(("relation_linear", ops.relation_linear.default,
                   (red["operand_cache"], red["expanded_weight"], red["expanded_bias"], None)))
+    cases.append(("relation_linear_out", ops.relation_linear_out.default,
+                  (red["operand_cache"][:, 3], red["expanded_weight"], red["expanded_bias"],
+                   expanded.clone()[:, 3])))
+    d = cfg.d_model
+    query_dec = torch.randn(b, d, generator=g).to(device, torch.bfloat16)
+    query_seq = torch.randn(b, t, d, generator=g).to(device, torch.bfloat16)
+    head = (torch.tensor(0.2, device=device), red["norm_weight"], red["norm_bias"], 1e-5)
+    cases.append(("relation_norm_reduce_output", ops.relation_norm_reduce_output.default,
+                  (raw_dec, scores_dec, red["norm_weight"], red["norm_bias"], pos, 1e-5,
+                   query_dec) + head))
+    cases.append(("relation_norm_reduce_output_seq", ops.relation_norm_reduce_output_seq.default,
+                  (raw_seq, scores_seq, red["norm_weight"], red["norm_bias"], positions, 1e-5,
+                   query_seq) + head))
+    slots, kk = 2, 3
+    raw_multi = torch.randn(b, t, slots, kk, d, generator=g).to(device)
+    scores_multi = torch.randn(b, t, slots, kk, generator=g).to(device)
+    cases.append(("multi_relation_reduce_seq", ops.multi_relation_reduce_seq.default,
+                  (raw_multi, scores_multi, red["norm_weight"], red["norm_bias"],
+                   torch.zeros(slots, device=device), torch.tensor(-1.5, device=device),
+                   query_seq, positions, 1e-5)))
+    cases.append(("layer_norm", ops.layer_norm.default,
+                  (query_seq, red["norm_weight"], red["norm_bias"], 1e-5)))
+    keys = torch.randn(b, t, 64, generator=g).to(device, torch.bfloat16)
+    cases.append(("block_statistics", ops.block_statistics.default, (keys, cfg.block_size)))
     return cases
 
 
@@ -254,7 +278,9 @@ OP_NAMES = ("relation_select_packed", "relation_select_packed_seq",
             "relation_hidden_cache_update_ring", "relation_norm_reduce",
             "relation_norm_reduce_seq", "relation_reduce_fused_seq", "router_cache_update",
             "router_cache_update_ring", "packed_sparse_cache_projection",
-            "packed_projection_to_caches", "relation_linear")
+            "packed_projection_to_caches", "relation_linear", "relation_linear_out",
+            "relation_norm_reduce_output", "relation_norm_reduce_output_seq",
+            "multi_relation_reduce_seq", "layer_norm", "block_statistics")
 
 
 def test_opcheck_every_registered_op(device):

@@ -130,3 +130,18 @@ def test_bf16_rounding_matches_torch():
     x = (rng.standard_normal(100000) * 10.0 ** rng.integers(-5, 5, 100000)).astype(np.float32)
     expected = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     assert np.array_equal(ored.round_to(x, "bfloat16").astype(np.float32), expected)
+
+
+def test_output_prep_matches_torch_layer_norm():
+    rng = np.random.default_rng(31)
+    query, context = rng.normal(size=(3, 40)), rng.normal(size=(3, 40))
+    w, b = rng.normal(1.0, 0.1, 40), rng.normal(0.0, 0.1, 40)
+    got = ored.output_prep(query, context, 0.35, w, b, 1e-5)
+    tq = torch.from_numpy(query) + torch.sigmoid(torch.tensor(0.35, dtype=torch.float64)) * torch.from_numpy(context)
+    ref = torch.nn.functional.layer_norm(tq, (40,), torch.from_numpy(w), torch.from_numpy(b), 1e-5)
+    np.testing.assert_allclose(got, ref.numpy(), rtol=0, atol=1e-12)
+    # A mix logit of -inf gates the context out: the LayerNorm of the query alone.
+    only_query = ored.output_prep(query, 1e3 * context, -np.inf, w, b, 1e-5)
+    ref = torch.nn.functional.layer_norm(torch.from_numpy(query), (40,), torch.from_numpy(w),
+                                         torch.from_numpy(b), 1e-5)
+    np.testing.assert_allclose(only_query, ref.numpy(), rtol=0, atol=1e-12)

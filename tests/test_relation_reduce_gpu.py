@@ -23,6 +23,7 @@ from relation_lm.kernels.relation_reduce import (
     relation_hidden_cached,
     relation_hidden_cached_seq,
     relation_linear,
+    relation_linear_out,
     relation_norm_reduce,
     relation_norm_reduce_seq,
 )
@@ -458,3 +459,24 @@ def test_linear_second_linear_shape(device):
     x16 = hidden[rows].bfloat16().float().numpy()
     expected = ored.linear(x16, w.float().numpy(), bias.float().numpy())
     assert rel_err(host(got)[rows.numpy()], expected) <= FP32_REL
+
+
+@pytest.mark.parametrize("dtype,batch", [(torch.bfloat16, 8), (torch.bfloat16, 1), (torch.float32, 3)])
+def test_linear_out_into_cache_column(device, dtype, batch):
+    """relation_linear_out writes a cache column (rows strided by the cache row
+    pitch) in place: the decode step's separate expanded-row update.  Equal to
+    relation_linear's result; every other cache row is untouched."""
+    g = torch.Generator().manual_seed(41 + batch)
+    operand = torch.randn(batch, 64, 128, generator=g).to(device=device, dtype=dtype)
+    weight = (torch.randn(2 * 2304, 128, generator=g) * 0.08).to(device=device, dtype=dtype)
+    bias = torch.randn(2 * 2304, generator=g).to(device=device, dtype=dtype)
+    cache = torch.randn(batch, 64, 2 * 2304, generator=g).to(device=device, dtype=dtype)
+    before = cache.clone()
+    t = 37
+    relation_linear_out(operand[:, t], weight, bias, cache[:, t])
+    expected = relation_linear(operand[:, t].contiguous(), weight, bias)
+    torch.cuda.synchronize()
+    assert torch.equal(cache[:, t], expected)
+    keep = torch.ones(64, dtype=torch.bool)
+    keep[t] = False
+    assert torch.equal(cache[:, keep], before[:, keep])
