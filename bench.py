@@ -52,7 +52,7 @@ CPU_SAMPLES = 9                 # CPU baseline: timed calls per shape (median)  
 # Kernel-name prefixes (as rocprofv3 reports them) of the timed kernels.
 KERNEL_SYMBOLS = {
     "expanded_projection": "smallk_kernel<rlm::bf16, rlm::bf16, rlm::bf16",
-    "relation_select": "::select_kernel<",
+    "relation_select": "select_tile_kernel<",
     "relation_reduce_fused": "fused_reduce_kernel<",
     "relation_hidden": "hidden_bf16_kernel<",
     "second_linear": "tile_kernel<float, rlm::bf16, float",
