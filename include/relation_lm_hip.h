@@ -278,7 +278,7 @@ hipError_t rlm_relation_norm_reduce_output_seq(
  *   expanded_cache [B,T,2H], operand_cache [B,T,R], product_weight [H,R],
  *   second_weight [D,H] (all bf16), second_bias [D], partner_scores f32
  *   [B,Tq,K], norm_weight/norm_bias [D], anchor_index [B,Tq], partner_index
- *   [B,Tq,K], positions [Tq] or [B,Tq].  K in {1,2,4,8,16}, R in {32,64,128},
+ *   [B,Tq,K], positions [Tq] or [B,Tq].  1 <= K <= 16, R in {32,64,128},
  *   H a multiple of 128, D in {128, 256, 384, 512}.
  * Output: out f32 [B,Tq,D].
  */

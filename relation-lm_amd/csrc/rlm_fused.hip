@@ -8,7 +8,8 @@
 // [K,D] raw rows of a query never leave the CU.
 //
 // Mapping: a workgroup of 8 waves (2 per SIMD) owns 128 consecutive
-// (query, partner) rows, so it holds whole queries (K in {1, 2, 4, 8, 16}).
+// (query, partner) rows, so it holds whole queries (K rounded up to a power
+// of two, at most 16; the padding rows of a query carry weight 0).
 // Inside the workgroup the rows are kept in "slot" order (slot_row below),
 // chosen so that phase 2 leaves each query's partners in as few lanes as
 // possible.
@@ -72,6 +73,7 @@ constexpr int kWaitVm0 = 0x0F70;           // s_waitcnt vmcnt(0), other counters
 struct FusedParams {
   int64_t T;
   uint32_t Tq, K, k_log2, R, H, D;
+  uint32_t Kr;         // partners per query in the inputs (K is Kr rounded up to a power of two)
   uint32_t rows;       // B*Tq*K
   uint32_t queries;    // B*Tq
   const void* expanded;   // [B,T,2H] bf16
@@ -285,11 +287,15 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
     for (int i = 0; i < kGatherInsts; ++i) src[i] = gather_src(i);
     dma_gather_chunk(xr, lds0 + kOffGather, src, chunk, wave);
   };
+  // Rows are numbered query*K + k with K a power of two; rows k >= Kr (padding
+  // of a non-power-of-two partner count) read no index: zero operands, weight 0.
   const uint32_t grow = row0 + slot_row<RTW>(lslot, p.K, p.k_log2);
-  const bool live = grow < p.rows;
   const uint32_t q = grow >> p.k_log2;
+  const uint32_t kr = grow & (p.K - 1);
+  const bool live = grow < p.rows && kr < p.Kr;
   const IndexWords ai = issue_index(p.anchor, p.index_dtype_a, p.queries, q, live);
-  const IndexWords pi = issue_index(p.partner, p.index_dtype_p, p.rows, grow, live);
+  const IndexWords pi = issue_index(p.partner, p.index_dtype_p, p.queries * p.Kr, q * p.Kr + kr,
+                                    live);
   // Row-weight inputs of slot tid (threads 0..127): its query's position and K scores.
   const uint32_t wrow = row0 + slot_row<RTW>(tid & (kRows - 1), p.K, p.k_log2);
   const bool wlive = tid < kRows && wrow < p.rows;
@@ -298,11 +304,11 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
   const IndexWords wpos = issue_index(p.pos, p.pos_dtype, p.pos_count,
                                       static_cast<uint32_t>(wb * p.pos_sb + (wq - wb * p.Tq) * p.pos_sq),
                                       wlive);
-  const rsrc_t scr = make_rsrc(p.scores, p.rows * 4u);
+  const rsrc_t scr = make_rsrc(p.scores, p.queries * p.Kr * 4u);
   uint32_t sc[16];
 #pragma unroll
   for (int c = 0; c < 16; ++c)
-    sc[c] = buf_load_b32(scr, wlive && c < static_cast<int>(p.K) ? (wq * p.K + c) * 4u : kNoOffset);
+    sc[c] = buf_load_b32(scr, wlive && c < static_cast<int>(p.Kr) ? (wq * p.Kr + c) * 4u : kNoOffset);
   // Element tid of b2 / gamma / beta (D <= kThreads).
   const bool dlive = tid < static_cast<int>(p.D);
   const FloatWords cb2 = issue_float(p.b2, p.b2_dtype, p.D, tid, dlive);
@@ -348,7 +354,8 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
       float scf[16];
 #pragma unroll
       for (int c = 0; c < 16; ++c) scf[c] = __uint_as_float(sc[c]);
-      wts[tid] = wlive ? row_weight(scf, decode_index(wpos, p.pos_dtype), p.K, wrow & (p.K - 1))
+      // Padding rows (k >= Kr) get weight 0: row_weight only weighs k < Kr.
+      wts[tid] = wlive ? row_weight(scf, decode_index(wpos, p.pos_dtype), p.Kr, wrow & (p.K - 1))
                        : 0.0f;
     }
     if (dlive) {
@@ -688,8 +695,8 @@ extern "C" hipError_t rlm_relation_reduce_fused_seq(
   RLM_TRY(check_dim(partner_index, "partner_index", 0, B));
   RLM_TRY(check_dim(partner_index, "partner_index", 1, Tq));
   const int64_t K = partner_index->shape[2];
-  RLM_REQUIRE(K == 1 || K == 2 || K == 4 || K == 8 || K == 16,
-              "fused relation reduce supports K in {1, 2, 4, 8, 16}, got %lld", (long long)K);
+  RLM_REQUIRE(K >= 1 && K <= 16, "fused relation reduce supports 1 <= K <= 16, got %lld",
+              (long long)K);
   RLM_REQUIRE(R == 32 || R == 64 || R == 128,
               "fused relation reduce needs relation dim 32, 64 or 128, got %lld", (long long)R);
   RLM_REQUIRE(H % kHC == 0 && H > 0, "fused relation reduce needs hidden dim a multiple of %d",
@@ -743,9 +750,12 @@ extern "C" hipError_t rlm_relation_reduce_fused_seq(
   p.R = static_cast<uint32_t>(R);
   p.H = static_cast<uint32_t>(H);
   p.D = static_cast<uint32_t>(D);
-  p.K = static_cast<uint32_t>(K);
-  p.k_log2 = static_cast<uint32_t>(__builtin_ctzll(static_cast<unsigned long long>(K)));
-  p.rows = static_cast<uint32_t>(B * Tq * K);
+  // A non-power-of-two K runs as the next power of two with zero-weight padding rows.
+  const int64_t Kp = K <= 1 ? 1 : int64_t(1) << (64 - __builtin_clzll(static_cast<unsigned long long>(K - 1)));
+  p.Kr = static_cast<uint32_t>(K);
+  p.K = static_cast<uint32_t>(Kp);
+  p.k_log2 = static_cast<uint32_t>(__builtin_ctzll(static_cast<unsigned long long>(Kp)));
+  p.rows = static_cast<uint32_t>(B * Tq * Kp);
   p.queries = static_cast<uint32_t>(B * Tq);
   p.expanded = expanded_cache->data;
   p.operand = operand_cache->data;

@@ -109,7 +109,7 @@ def test_cfg2_fused_matches_unfused_and_oracle(device):
     assert abs_err(got, expected) <= TIGHT_ABS
 
 
-@pytest.mark.parametrize("k_out", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("k_out", [1, 2, 3, 4, 5, 6, 7, 8, 12, 16])
 @pytest.mark.parametrize("d_model", [128, 256, 384])
 def test_fused_partner_counts_and_widths(device, k_out, d_model):
     cfg = RelationConfig("fused", 2, 96, d_model, 32, 64, 2, k_out, torch.bfloat16,
