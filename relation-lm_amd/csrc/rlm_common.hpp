@@ -335,6 +335,56 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return best;
 }
 
+// Maximum over the wave held in every lane, all in VALU: DPP steps within the
+// 16-lane rows, then v_permlane16/32_swap between rows (no SGPR round trips).
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint64_t wave_max_u64_v(uint64_t v) {
+  v = umax64(v, dpp_u64<kDppXor1>(v));
+  v = umax64(v, dpp_u64<kDppXor2>(v));
+  v = umax64(v, dpp_u64<kDppHalfMirror>(v));
+  v = umax64(v, dpp_u64<kDppMirror>(v));
+  auto lo = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(v), static_cast<uint32_t>(v),
+                                             false, false);
+  auto hi = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(v >> 32),
+                                             static_cast<uint32_t>(v >> 32), false, false);
+  v = umax64(static_cast<uint64_t>(lo[0]) | (static_cast<uint64_t>(hi[0]) << 32),
+             static_cast<uint64_t>(lo[1]) | (static_cast<uint64_t>(hi[1]) << 32));
+  lo = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(v), static_cast<uint32_t>(v), false,
+                                        false);
+  hi = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(v >> 32),
+                                        static_cast<uint32_t>(v >> 32), false, false);
+  return umax64(static_cast<uint64_t>(lo[0]) | (static_cast<uint64_t>(hi[0]) << 32),
+                static_cast<uint64_t>(lo[1]) | (static_cast<uint64_t>(hi[1]) << 32));
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32_v(uint32_t v) {
+  v = max(v, dpp_u32<kDppXor1>(v));
+  v = max(v, dpp_u32<kDppXor2>(v));
+  v = max(v, dpp_u32<kDppHalfMirror>(v));
+  v = max(v, dpp_u32<kDppMirror>(v));
+  auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max(r[0], r[1]);
+  r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max(r[0], r[1]);
+}
+
+// Maximum 64-bit selection key over the wave, returned in every lane: the
+// score half first (32-bit steps), then -- only when several lanes share the
+// top score -- the tie half among those lanes.
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t v) {
+  const uint32_t hi = static_cast<uint32_t>(v >> 32);
+  const uint32_t lo = static_cast<uint32_t>(v);
+  const uint32_t mhi = wave_max_u32_v(hi);
+  const uint64_t tied = __builtin_amdgcn_ballot_w64(hi == mhi);
+  uint32_t mlo;
+  if (__builtin_popcountll(tied) == 1)
+    mlo = static_cast<uint32_t>(
+        __builtin_amdgcn_readlane(static_cast<int>(lo), static_cast<int>(__builtin_ctzll(tied))));
+  else
+    mlo = wave_max_u32_v(hi == mhi ? lo : 0u);
+  return (static_cast<uint64_t>(mhi) << 32) | mlo;
+}
+
 // Sum over the 16 lanes of a DPP row; every lane of the row gets the same bits
 // (each step adds a pair in both orders, and float addition commutes).
 __device__ __forceinline__ float row16_sum(float v) {

@@ -31,6 +31,7 @@
 #include <cstdlib>
 
 #include "rlm_common.hpp"
+#include "rlm_select_decode.hpp"
 #include "rlm_select_tile.hpp"
 
 namespace rlm {
@@ -1430,6 +1431,68 @@ bool tile_params(const SelectParams& p, const Geometry& g, int act, int stat,
   return select_tile_layout(tp);
 }
 
+// The decode form takes the latency-oriented kernel where it applies unless
+// RLM_SELECT_DECODE=0 (both kernels give identical results; the switch exists
+// to compare them).
+bool decode_path_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("RLM_SELECT_DECODE");
+    return v == nullptr || v[0] != '0';
+  }();
+  return on;
+}
+
+// Fills the decode kernel's parameters when the shapes fit it.
+bool decode_params(const SelectParams& p, const Geometry& g, int act, int stat,
+                   const rlm_tensor* position, const rlm_tensor* aq, const rlm_tensor* arq,
+                   const rlm_tensor* pbase, const rlm_tensor* pcache, const rlm_tensor* akeys,
+                   const rlm_tensor* pkeys, const rlm_tensor* amean, const rlm_tensor* astd,
+                   const rlm_tensor* agamma, const rlm_tensor* abias, const rlm_tensor* pmean,
+                   const rlm_tensor* pstd, const rlm_tensor* pgamma, const rlm_tensor* pbias,
+                   DecodeParams& dp) {
+  const bool dtypes = (act == RLM_BF16 && (stat == RLM_F32 || stat == RLM_BF16)) ||
+                      (act == RLM_F16 && (stat == RLM_F32 || stat == RLM_F16));
+  if (!dtypes || g.E != 64 || g.H != 4 || g.HD != 16) return false;
+  dp.B = g.B;
+  dp.T = g.T;
+  dp.NB = g.NB;
+  dp.BS = g.BS;
+  dp.BS_log2 = p.BS_log2;
+  dp.L = p.L;
+  dp.TOP = p.TOP;
+  dp.K = p.K;
+  dp.CAP = p.CAP;
+  dp.RB = g.RB;
+  dp.strict = p.strict;
+  dp.exact_scale = p.exact_scale;
+  dp.head_scale = p.head_scale;
+  dp.pos = position->data;
+  dp.pos_dtype = position->dtype;
+  dp.aq = aq->data;
+  dp.arq = arq->data;
+  dp.pbase = pbase->data;
+  dp.pcache = pcache->data;
+  dp.akeys = akeys->data;
+  dp.pkeys = pkeys->data;
+  dp.amean = amean->data;
+  dp.astd = astd->data;
+  dp.pmean = pmean->data;
+  dp.pstd = pstd->data;
+  dp.agamma = agamma->data;
+  dp.pgamma = pgamma->data;
+  dp.abias = abias->data;
+  dp.pbias = pbias->data;
+  dp.agamma_dtype = agamma->dtype;
+  dp.pgamma_dtype = pgamma->dtype;
+  dp.abias_dtype = abias->dtype;
+  dp.pbias_dtype = pbias->dtype;
+  dp.out_anchor = p.out_anchor;
+  dp.out_anchor_score = p.out_anchor_score;
+  dp.out_partner = p.out_partner;
+  dp.out_partner_score = p.out_partner_score;
+  return select_decode_layout(dp);
+}
+
 hipError_t select_packed_impl(
     bool seq, bool ring, const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
     const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
@@ -1529,8 +1592,18 @@ hipError_t select_packed_impl(
                 "ring-buffer caches need a power-of-two cache length split into whole blocks "
                 "(cache length %lld, %d blocks)",
                 (long long)g.T, g.NB);
-    return launch_select<kPacked, true>(p, act, stat, stream);
   }
+  if (!seq && decode_path_enabled()) {
+    // 16-bit activations, 4 router heads of 16, caches of at most 512 rows:
+    // the latency-oriented decode kernel (rlm_select_decode.hip).
+    DecodeParams dp{};
+    if (decode_params(p, g, act, stat, position, anchor_query, anchor_router_query, partner_base,
+                      partner_anchor_cache, anchor_keys, partner_keys, anchor_block_mean,
+                      anchor_block_std, anchor_gamma, anchor_bias, partner_block_mean,
+                      partner_block_std, partner_gamma, partner_bias, dp))
+      return select_decode_launch(dp, act, stat, ring, stream);
+  }
+  if (ring) return launch_select<kPacked, true>(p, act, stat, stream);
   return launch_select<kPacked>(p, act, stat, stream);
 }
 

@@ -162,6 +162,50 @@ def test_duplicate_keys_tie_rules(device):
     assert expected[0][0] == 5
 
 
+@pytest.mark.parametrize("strict", [False, True])
+def test_decode_duplicate_keys_tie_rules_bf16(device, strict):
+    """The bf16 decode form (the staged-cache decode kernel): exact ties between
+    anchor candidates (lowest position wins) and between partner lanes (local
+    window first, then picks in pick order), plus all-zero key rows whose scores
+    are signed zeros."""
+    cfg = RelationConfig(**{**CONFIGS["cfg2"].__dict__, "batch": 3, "strict_valid": strict})
+    inp = selection_inputs(cfg, queries=1, device="cpu")
+    t = cfg.context - 1
+    for b in range(3):
+        strong = inp["anchor_query"][b] * 4.0
+        inp["anchor_keys"][b, 70] = strong
+        inp["anchor_keys"][b, t - 3] = strong
+        inp["anchor_block_mean"][b, 2] = 20.0
+    inp["partner_keys"][:, 100:140] = inp["partner_keys"][:, 100:101]
+    inp["partner_keys"][:, t - 20:t] = inp["partner_keys"][:, 100:101]
+    inp["partner_keys"][:, 200:232] = 0.0
+    inp["partner_block_mean"][:, 6] = 15.0
+    dev = {k: v.to(device) for k, v in inp.items()}
+    got = relation_select_packed(*select_args(dev, cfg))
+    torch.cuda.synchronize()
+    assert_select_equal(got, oracle_packed(dev, cfg, seq=False), f"bf16 ties strict={strict}")
+
+
+# Decode-form routing parameters inside the decode kernel's limits
+# (candidates <= 256): no remote blocks, k above the candidate count, more
+# picks than blocks, k = 1.
+DECODE_ROUTING = [(8, 0, 8, 512), (16, 1, 40, 512), (4, 7, 16, 512), (32, 2, 1, 512),
+                  (32, 6, 8, 128), (64, 4, 64, 512)]
+
+
+@pytest.mark.parametrize("local,top,k,context", DECODE_ROUTING)
+def test_decode_unusual_routing_parameters_bf16(device, local, top, k, context):
+    cfg = RelationConfig(**{**CONFIGS["cfg2"].__dict__, "batch": 2, "local_window": local,
+                            "top_blocks": top, "k_out": k, "context": context})
+    inp = selection_inputs(cfg, queries=1, device=device)
+    for position in (0, 5, local + 40, context - 1):
+        inp["position"] = torch.tensor(position, dtype=torch.int64, device=device)
+        got = relation_select_packed(*select_args(inp, cfg))
+        torch.cuda.synchronize()
+        assert_select_equal(got, oracle_packed(inp, cfg, seq=False),
+                            f"L={local} top={top} k={k} T={context} t={position}")
+
+
 @pytest.mark.parametrize("local,top,k", [(8, 0, 8), (16, 1, 40), (4, 8, 16), (32, 2, 1)])
 def test_unusual_routing_parameters(device, local, top, k):
     cfg = RelationConfig(**{**CONFIGS["cfg1"].__dict__, "batch": 2, "local_window": local,
