@@ -736,6 +736,189 @@ __global__ void __launch_bounds__(256) norm_reduce_vec_kernel(const NormParams p
   }
 }
 
+// Decode shapes (a few queries): one workgroup of four waves per query, so
+// that the query's latency chain is short.  Wave w normalises partner rows w,
+// w + 4, ... (RPW of them side by side, so their reductions interleave); the
+// parameter vectors (norm weight and bias, and for the output-head
+// preparation the query, output weight and bias) are loaded as one 4-element
+// chunk per thread and staged in LDS as fp32; the waves' weighted row sums
+// meet in LDS:  context = gamma * sum_k p_k xhat_k + beta * sum_k p_k.
+// fp32 raw rows, D % 4 == 0, D <= 256 * GI.
+constexpr int kQWaves = 4;
+constexpr int kQMaxD = 1024;
+constexpr int64_t kQueryKernelMaxQ = 256;  // queries below which a workgroup per query pays
+
+// Four consecutive elements c*4.. of a parameter vector of `dtype`: a 16-byte
+// and an 8-byte load are both issued, the one that does not match the dtype
+// out of range (no memory access).
+struct Chunk4 {
+  uint4 w32;
+  uint2 w16;
+};
+__device__ __forceinline__ Chunk4 chunk4_issue(const void* base, int dtype, int D, int c, bool live) {
+  const bool is32 = dtype == RLM_F32;
+  const rsrc_t r = make_rsrc(base, static_cast<uint32_t>(D) * (is32 ? 4u : 2u));
+  return {buf_load_b128(r, live && is32 ? 16u * c : kNoOffset),
+          buf_load_b64(r, live && !is32 ? 8u * c : kNoOffset)};
+}
+__device__ __forceinline__ float4 chunk4_decode(const Chunk4& v, int dtype) {
+  if (dtype == RLM_F32)
+    return make_float4(__uint_as_float(v.w32.x), __uint_as_float(v.w32.y),
+                       __uint_as_float(v.w32.z), __uint_as_float(v.w32.w));
+  const uint32_t e[4] = {v.w16.x & 0xffffu, v.w16.x >> 16, v.w16.y & 0xffffu, v.w16.y >> 16};
+  float f[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    f[k] = dtype == RLM_BF16
+               ? __uint_as_float(e[k] << 16)
+               : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(e[k])));
+  return make_float4(f[0], f[1], f[2], f[3]);
+}
+
+template <int RPW, int GI>
+__global__ void __launch_bounds__(kQWaves * kWave) norm_reduce_query_kernel(const NormParams p) {
+  __shared__ float4 par[5][kQMaxD / 4];         // w, b, query, ow, ob as fp32
+  __shared__ float4 part[kQWaves][kQMaxD / 4];  // each wave's sum_k p_k xhat_k
+  __shared__ float red[2][kQWaves];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int64_t q = blockIdx.x;
+  const int64_t b = q / p.Tq;
+  const int64_t tq = q - b * p.Tq;
+  const int groups = p.D >> 2;
+  // ---- Every load of the query at once: position, scores, mix logit, the
+  // wave's partner rows and one chunk of each parameter vector per thread.
+  const int64_t t = index_at(p.pos, p.pos_dtype, b * p.pos_sb + tq * p.pos_sq);
+  const float score = partner_score(p, q, lane);
+  const float mix = load_any_f(p.mix, p.mix_dtype, 0);
+  const float* raw = static_cast<const float*>(p.raw) + q * p.K * static_cast<int64_t>(p.D);
+  float4 x[RPW][GI];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int i = 0; i < GI; ++i) {
+      const int k = wave + kQWaves * r;
+      const int g = lane + kWave * i;
+      const bool in = k < p.K && g < groups;
+      const float4 v = *reinterpret_cast<const float4*>(raw + static_cast<int64_t>(in ? k : 0) * p.D +
+                                                        4 * (in ? g : 0));
+      x[r][i] = in ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  const bool cl = tid < groups;
+  const Chunk4 cw = chunk4_issue(p.w, p.w_dtype, p.D, tid, cl);
+  const Chunk4 cb = chunk4_issue(p.bias, p.b_dtype, p.D, tid, cl);
+  const Chunk4 cq = chunk4_issue(static_cast<const unsigned char*>(p.query) +
+                                     (p.prep ? q * p.D * (p.query_dtype == RLM_F32 ? 4 : 2) : 0),
+                                 p.query_dtype, p.D, tid, cl);
+  const Chunk4 cow = chunk4_issue(p.ow, p.ow_dtype, p.D, tid, cl);
+  const Chunk4 cob = chunk4_issue(p.ob, p.ob_dtype, p.D, tid, cl);
+
+  // ---- Partner weights (every wave computes the same ones).
+  const float prob = partner_weight(p, score, t, lane);
+  const float psum = wave_sum_f32(prob);
+  const float inv_d = 1.0f / static_cast<float>(p.D);
+  // ---- Row statistics, the wave's rows side by side.
+  float mean[RPW], rstd[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < GI; ++i) s += (x[r][i].x + x[r][i].y) + (x[r][i].z + x[r][i].w);
+    mean[r] = wave_sum_f32(s) * inv_d;
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < GI; ++i) {
+      const bool in = lane + kWave * i < groups;
+      float4& v = x[r][i];
+      v.x = in ? v.x - mean[r] : 0.0f;
+      v.y = in ? v.y - mean[r] : 0.0f;
+      v.z = in ? v.z - mean[r] : 0.0f;
+      v.w = in ? v.w - mean[r] : 0.0f;
+      sq += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+    }
+    rstd[r] = rsqrtf(wave_sum_f32(sq) * inv_d + p.eps);
+  }
+  // Weighted sum of the wave's normalised rows; an inactive row (weight 0)
+  // adds exactly 0.
+  float4 acc[GI];
+#pragma unroll
+  for (int i = 0; i < GI; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int k = wave + kQWaves * r;
+    const float pk = __uint_as_float(
+        __builtin_amdgcn_readlane(__float_as_uint(prob), k < p.K ? k : 0));
+    const bool use = k < p.K && pk != 0.0f;
+#pragma unroll
+    for (int i = 0; i < GI; ++i) {
+      acc[i].x += use ? pk * (x[r][i].x * rstd[r]) : 0.0f;
+      acc[i].y += use ? pk * (x[r][i].y * rstd[r]) : 0.0f;
+      acc[i].z += use ? pk * (x[r][i].z * rstd[r]) : 0.0f;
+      acc[i].w += use ? pk * (x[r][i].w * rstd[r]) : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < GI; ++i) {
+    const int g = lane + kWave * i;
+    if (g < groups) part[wave][g] = acc[i];
+  }
+  if (cl) {
+    par[0][tid] = chunk4_decode(cw, p.w_dtype);
+    par[1][tid] = chunk4_decode(cb, p.b_dtype);
+    par[2][tid] = chunk4_decode(cq, p.query_dtype);
+    par[3][tid] = chunk4_decode(cow, p.ow_dtype);
+    par[4][tid] = chunk4_decode(cob, p.ob_dtype);
+  }
+  __syncthreads();
+  // ---- Column phase: thread tid owns columns 4 tid .. 4 tid + 3.
+  float4 ctx = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (cl) {
+    float4 s = part[0][tid];
+#pragma unroll
+    for (int w = 1; w < kQWaves; ++w) {
+      const float4 o = part[w][tid];
+      s.x += o.x;
+      s.y += o.y;
+      s.z += o.z;
+      s.w += o.w;
+    }
+    const float4 gm = par[0][tid], bt = par[1][tid];
+    ctx = make_float4(fmaf(gm.x, s.x, bt.x * psum), fmaf(gm.y, s.y, bt.y * psum),
+                      fmaf(gm.z, s.z, bt.z * psum), fmaf(gm.w, s.w, bt.w * psum));
+    reinterpret_cast<float4*>(p.out + q * static_cast<int64_t>(p.D))[tid] = ctx;
+  }
+  if (!p.prep) return;  // uniform
+  // ---- Output-head preparation: LayerNorm_out(query + sigmoid(mix) * context).
+  const float gate = 1.0f / (1.0f + expf(-mix));
+  float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (cl) {
+    const float4 qv = par[2][tid];
+    y = make_float4(fmaf(gate, ctx.x, qv.x), fmaf(gate, ctx.y, qv.y), fmaf(gate, ctx.z, qv.z),
+                    fmaf(gate, ctx.w, qv.w));
+  }
+  float s = wave_sum_f32((y.x + y.y) + (y.z + y.w));
+  if (lane == 0) red[0][wave] = s;
+  __syncthreads();
+  const float ymean = ((red[0][0] + red[0][1]) + (red[0][2] + red[0][3])) * inv_d;
+  const float4 dy = cl ? make_float4(y.x - ymean, y.y - ymean, y.z - ymean, y.w - ymean)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+  s = wave_sum_f32((dy.x * dy.x + dy.y * dy.y) + (dy.z * dy.z + dy.w * dy.w));
+  if (lane == 0) red[1][wave] = s;
+  __syncthreads();
+  const float yrstd =
+      rsqrtf(((red[1][0] + red[1][1]) + (red[1][2] + red[1][3])) * inv_d + p.out_eps);
+  if (cl) {
+    const float4 w4 = par[3][tid], b4 = par[4][tid];
+    store_any4(p.final, p.query_dtype, q * groups + tid,
+               make_float4(fmaf(dy.x * yrstd, w4.x, b4.x), fmaf(dy.y * yrstd, w4.y, b4.y),
+                           fmaf(dy.z * yrstd, w4.z, b4.z), fmaf(dy.w * yrstd, w4.w, b4.w)));
+  }
+}
+
 template <typename TR, int VPL>
 __global__ void __launch_bounds__(256) norm_reduce_kernel(const NormParams p) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -944,6 +1127,34 @@ hipError_t launch_norm_vec(const NormParams& p, int dtype, hipStream_t stream) {
   return hipErrorInvalidValue;
 }
 
+template <int RPW>
+hipError_t launch_norm_query_rpw(const NormParams& p, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(p.Q));
+  const int gi = (p.D / 4 + kWave - 1) / kWave;
+#define RLM_NORMQ_CASE(GI)                                                                    \
+  if (gi <= GI) {                                                                             \
+    hipLaunchKernelGGL((norm_reduce_query_kernel<RPW, GI>), grid, dim3(kQWaves * kWave), 0,  \
+                       stream, p);                                                            \
+    return launch_status("relation_norm_reduce");                                            \
+  }
+  RLM_NORMQ_CASE(1)
+  RLM_NORMQ_CASE(2)
+  RLM_NORMQ_CASE(3)
+  RLM_NORMQ_CASE(4)
+#undef RLM_NORMQ_CASE
+  set_error("relation_norm_reduce: width %d too large for the per-query kernel", p.D);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_norm_query(const NormParams& p, hipStream_t stream) {
+  switch ((p.K + kQWaves - 1) / kQWaves) {
+    case 1: return launch_norm_query_rpw<1>(p, stream);
+    case 2: return launch_norm_query_rpw<2>(p, stream);
+    case 3: return launch_norm_query_rpw<3>(p, stream);
+    default: return launch_norm_query_rpw<4>(p, stream);
+  }
+}
+
 template <int VPL>
 hipError_t launch_norm_vpl(const NormParams& p, int dtype, hipStream_t stream) {
   const int waves = 4;
@@ -1075,9 +1286,13 @@ hipError_t norm_impl(bool seq, const rlm_tensor* raw, const rlm_tensor* partner_
     p.final = prep.final->data;
   }
   if (p.Q == 0) return hipSuccess;
-  if (D % 4 == 0 && (reinterpret_cast<uintptr_t>(raw->data) & 15u) == 0 &&
-      (reinterpret_cast<uintptr_t>(norm_weight->data) & 15u) == 0 &&
-      (reinterpret_cast<uintptr_t>(norm_bias->data) & 15u) == 0) {
+  const bool vec_ok = D % 4 == 0 && (reinterpret_cast<uintptr_t>(raw->data) & 15u) == 0 &&
+                      (reinterpret_cast<uintptr_t>(norm_weight->data) & 15u) == 0 &&
+                      (reinterpret_cast<uintptr_t>(norm_bias->data) & 15u) == 0;
+  // A few queries (decode): one workgroup per query.
+  if (vec_ok && p.Q <= kQueryKernelMaxQ && raw->dtype == RLM_F32 && D <= kQMaxD && K <= 16)
+    return launch_norm_query(p, stream);
+  if (vec_ok) {
     const int groups = static_cast<int>((D / 4 + kWave - 1) / kWave);
     if (groups <= 1) return launch_norm_vec<1, 8>(p, raw->dtype, stream);
     if (groups <= 2) return launch_norm_vec<2, 8>(p, raw->dtype, stream);
