@@ -44,11 +44,11 @@ for _p in (ROOT, os.path.join(ROOT, "relation-lm_amd")):
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-CALIBRATION_BYTES = 256 << 20
+CALIBRATION_BYTES = 256 << 20  # plain copy whose counter readings scale FETCH/WRITE_SIZE
 RING_POSITION = 4095            # decode position of the ring-buffer step (512-row caches)
 MALL_BYTES = 256 * 2**20        # MI355X last-level (Infinity) cache
 CPU_WARMUP = 3                  # CPU baseline: warm-up calls per shape
-CPU_SAMPLES = 9                 # CPU baseline: timed calls per shape (median)   # plain copy whose counter readings scale FETCH/WRITE_SIZE
+CPU_SAMPLES = 9                 # CPU baseline: timed calls per shape (median)
 # Kernel-name prefixes (as rocprofv3 reports them) of the timed kernels.
 KERNEL_SYMBOLS = {
     "expanded_projection": "smallk_kernel<rlm::bf16, rlm::bf16, rlm::bf16",
@@ -170,9 +170,7 @@ def main() -> int:
         relation_hidden_cache_update_ring,
         relation_hidden_cached_ring,
         relation_select_packed_ring,
-        router_cache_update_ring,
     )
-    from relation_lm.kernels.router_cache import router_cache_update
     from relation_lm.workloads import (
         CONFIGS,
         MULTI_CONFIGS,
@@ -216,7 +214,6 @@ def main() -> int:
         the cfg3 length (the *_ring ops; rows written at position mod length)."""
         ring = ring_position is not None
         select_op = relation_select_packed_ring if ring else relation_select_packed
-        router_op = router_cache_update_ring if ring else router_cache_update
         update_op = relation_hidden_cache_update_ring if ring else relation_hidden_cache_update
         cached_op = relation_hidden_cached_ring if ring else relation_hidden_cached
         decode = {}
@@ -245,16 +242,16 @@ def main() -> int:
             def decode_step(dsel=dsel, dred=dred, dexp=dexp, memory=memory, projection=projection,
                             dargs=dargs, t=t, position=position, batch=batch, rc=rc, dcfg=dcfg,
                             head=head):
-                # projection + the token's key / operand / partner-anchor cache rows
-                parts = projection.project_into(memory, dsel["anchor_keys"], dsel["partner_keys"],
-                                                dred["operand_cache"],
-                                                dsel["partner_anchor_cache"], position, ring=ring)
-                router_op(parts[4], parts[5], rc["anchor_raw_cache"], rc["partner_raw_cache"],
-                          rc["anchor_conv_cache"], rc["partner_conv_cache"],
-                          dsel["anchor_block_mean"], dsel["anchor_block_std"],
-                          dsel["partner_block_mean"], dsel["partner_block_std"],
-                          rc["anchor_conv_weight"], rc["partner_conv_weight"], position,
-                          dcfg.block_size)
+                # projection + the token's key / operand / partner-anchor cache rows, with
+                # the router cache update folded in (one launch)
+                projection.project_into_routed(
+                    memory, dsel["anchor_keys"], dsel["partner_keys"], dred["operand_cache"],
+                    dsel["partner_anchor_cache"], position, rc["anchor_raw_cache"],
+                    rc["partner_raw_cache"], rc["anchor_conv_cache"], rc["partner_conv_cache"],
+                    dsel["anchor_block_mean"], dsel["anchor_block_std"],
+                    dsel["partner_block_mean"], dsel["partner_block_std"],
+                    rc["anchor_conv_weight"], rc["partner_conv_weight"], dcfg.block_size,
+                    ring=ring)
                 a_, s_, p_, ps_ = select_op(*dargs)
                 if batch == 1:
                     hid = update_op(

@@ -406,6 +406,29 @@ hipError_t rlm_packed_projection_to_caches(
     const rlm_tensor* position, int32_t ring, hipStream_t stream);
 
 /*
+ * rlm_packed_projection_to_caches and rlm_router_cache_update(_ring) on its
+ * router segments in one launch: the reference's roadmap item "fold the
+ * router cache update into the packed projection" (README.md:148-149); no
+ * reference op.  The router segments are the last two of the packed output
+ * (widths D each, the router caches' last dim); the router tensors are those of
+ * rlm_router_cache_update with the raw rows taken from `out`.  Results are
+ * bit-identical to the two calls.  16-bit memory/weight/out, B <= 16, Din <= 768,
+ * D <= 64, block_size 8/16/32/64 and one fp32 or bf16 dtype for the router
+ * state take the single launch; other shapes run the two calls in turn.
+ * router_out [B,2,D] fp32 receives the conv rows.
+ */
+hipError_t rlm_packed_projection_router_update(
+    const rlm_tensor* memory, const rlm_tensor* weight, const rlm_tensor* out,
+    const rlm_tensor* anchor_keys, const rlm_tensor* partner_keys,
+    const rlm_tensor* operand_cache, const rlm_tensor* partner_anchor_cache,
+    const rlm_tensor* position, int32_t ring, const rlm_tensor* anchor_raw_cache,
+    const rlm_tensor* partner_raw_cache, const rlm_tensor* anchor_conv_cache,
+    const rlm_tensor* partner_conv_cache, const rlm_tensor* anchor_mean,
+    const rlm_tensor* anchor_std, const rlm_tensor* partner_mean, const rlm_tensor* partner_std,
+    const rlm_tensor* anchor_conv_weight, const rlm_tensor* partner_conv_weight,
+    int64_t block_size, const rlm_tensor* router_out, hipStream_t stream);
+
+/*
  * out = input @ weight^T (+ bias), the library GEMM behind the expanded-cache
  * projection (tests/test_relation_reduce_gpu.py:64-68 in the reference) and
  * the relation MLP's second linear (benchmarks/benchmark_relation_reduce.py:63).

@@ -633,6 +633,55 @@ at::Tensor packed_projection_to_caches(const at::Tensor& memory, const at::Tenso
   return out;
 }
 
+// Packed projection with its cache-row writes and the router cache update as
+// one launch (the reference's roadmap item, README.md:148-149; no reference op).
+std::tuple<at::Tensor, at::Tensor> packed_projection_router_update(
+    const at::Tensor& memory, const at::Tensor& weight, at::Tensor& anchor_keys,
+    at::Tensor& partner_keys, at::Tensor& operand_cache, at::Tensor& partner_anchor_cache,
+    const at::Tensor& position, bool ring, at::Tensor& anchor_raw_cache,
+    at::Tensor& partner_raw_cache, at::Tensor& anchor_conv_cache, at::Tensor& partner_conv_cache,
+    at::Tensor& anchor_mean, at::Tensor& anchor_std, at::Tensor& partner_mean,
+    at::Tensor& partner_std, const at::Tensor& anchor_conv_weight,
+    const at::Tensor& partner_conv_weight, int64_t block_size) {
+  const char* op = "relation_lm::packed_projection_router_update";
+  c10::DeviceGuard guard(memory.device());
+  hipStream_t stream = device_stream(
+      op, {&memory, &weight, &anchor_keys, &partner_keys, &operand_cache, &partner_anchor_cache,
+           &position, &anchor_raw_cache, &partner_raw_cache, &anchor_conv_cache,
+           &partner_conv_cache, &anchor_mean, &anchor_std, &partner_mean, &partner_std,
+           &anchor_conv_weight, &partner_conv_weight});
+  TORCH_CHECK(memory.dim() == 2, op, ": memory must be [B, Din]");
+  TORCH_CHECK(weight.dim() == 2, op, ": weight must be [Dout, Din]");
+  TORCH_CHECK(anchor_raw_cache.dim() == 3, op, ": router caches must be [B, T, D]");
+  at::Tensor out = at::empty({memory.size(0), weight.size(0)}, memory.options());
+  at::Tensor rout = at::empty({memory.size(0), 2, anchor_raw_cache.size(2)}, f32(memory));
+  rlm_tensor d[19] = {desc(memory, "memory"),
+                      desc(weight, "weight"),
+                      desc(out, "out"),
+                      desc(anchor_keys, "anchor_keys"),
+                      desc(partner_keys, "partner_keys"),
+                      desc(operand_cache, "operand_cache"),
+                      desc(partner_anchor_cache, "partner_anchor_cache"),
+                      desc(position, "position"),
+                      desc(anchor_raw_cache, "anchor_raw_cache"),
+                      desc(partner_raw_cache, "partner_raw_cache"),
+                      desc(anchor_conv_cache, "anchor_conv_cache"),
+                      desc(partner_conv_cache, "partner_conv_cache"),
+                      desc(anchor_mean, "anchor_mean"),
+                      desc(anchor_std, "anchor_std"),
+                      desc(partner_mean, "partner_mean"),
+                      desc(partner_std, "partner_std"),
+                      desc(anchor_conv_weight, "anchor_conv_weight"),
+                      desc(partner_conv_weight, "partner_conv_weight"),
+                      desc(rout, "router_out")};
+  check(rlm_packed_projection_router_update(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6],
+                                            &d[7], ring ? 1 : 0, &d[8], &d[9], &d[10], &d[11],
+                                            &d[12], &d[13], &d[14], &d[15], &d[16], &d[17],
+                                            block_size, &d[18], stream),
+        op);
+  return {out, rout};
+}
+
 at::Tensor multi_relation_reduce_seq(const at::Tensor& raw, const at::Tensor& partner_scores,
                                     const at::Tensor& norm_weight, const at::Tensor& norm_bias,
                                     const at::Tensor& slot_mix_logits,
@@ -768,6 +817,13 @@ TORCH_LIBRARY(relation_lm, m) {
       "Tensor(b!) partner_keys, Tensor(c!) operand_cache, Tensor(d!) partner_anchor_cache, "
       "Tensor position, bool ring=False) -> Tensor");
   m.def(
+      "packed_projection_router_update(Tensor memory, Tensor weight, Tensor(a!) anchor_keys, "
+      "Tensor(b!) partner_keys, Tensor(c!) operand_cache, Tensor(d!) partner_anchor_cache, "
+      "Tensor position, bool ring, Tensor(e!) anchor_raw_cache, Tensor(f!) partner_raw_cache, "
+      "Tensor(g!) anchor_conv_cache, Tensor(h!) partner_conv_cache, Tensor(i!) anchor_block_mean, "
+      "Tensor(j!) anchor_block_std, Tensor(k!) partner_block_mean, Tensor(l!) partner_block_std, "
+      "Tensor anchor_conv_weight, Tensor partner_conv_weight, SymInt block_size) -> (Tensor, Tensor)");
+  m.def(
       "relation_linear(Tensor input, Tensor weight, Tensor? bias=None, ScalarType? "
       "out_dtype=None) -> Tensor");
   m.def(
@@ -821,6 +877,7 @@ TORCH_LIBRARY_IMPL(relation_lm, CUDA, m) {
   m.impl("router_cache_update_ring", TORCH_FN(router_cache_update_ring));
   m.impl("packed_sparse_cache_projection", TORCH_FN(packed_sparse_cache_projection));
   m.impl("packed_projection_to_caches", TORCH_FN(packed_projection_to_caches));
+  m.impl("packed_projection_router_update", TORCH_FN(packed_projection_router_update));
   m.impl("relation_linear", TORCH_FN(relation_linear));
   m.impl("relation_linear_out", TORCH_FN(relation_linear_out));
   m.impl("multi_relation_reduce_seq", TORCH_FN(multi_relation_reduce_seq));

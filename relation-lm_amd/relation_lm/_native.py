@@ -104,6 +104,13 @@ def _register_fakes() -> None:
     def _(memory, weight, *rest):
         return memory.new_empty((memory.shape[0], weight.shape[0]))
 
+    @torch.library.register_fake("relation_lm::packed_projection_router_update")
+    def _(memory, weight, anchor_keys, partner_keys, operand_cache, partner_anchor_cache,
+          position, ring, anchor_raw_cache, *rest):
+        return (memory.new_empty((memory.shape[0], weight.shape[0])),
+                memory.new_empty((memory.shape[0], 2, anchor_raw_cache.shape[2]),
+                                 dtype=torch.float32))
+
     @torch.library.register_fake("relation_lm::packed_sparse_cache_projection")
     def _(memory, weight):
         return memory.new_empty(tuple(memory.shape[:-1]) + (weight.shape[0],))

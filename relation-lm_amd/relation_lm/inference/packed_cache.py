@@ -83,6 +83,37 @@ class PackedSparseCacheProjection:
             memory, self.weight, *caches, position, ring)
         return packed.split(self.split_sizes, dim=-1)
 
+    def project_into_routed(self, memory: Tensor, anchor_keys: Tensor, partner_keys: Tensor,
+                            operand_cache: Tensor, partner_anchor_cache: Tensor,
+                            position: Tensor, anchor_raw_cache: Tensor,
+                            partner_raw_cache: Tensor, anchor_conv_cache: Tensor,
+                            partner_conv_cache: Tensor, anchor_block_mean: Tensor,
+                            anchor_block_std: Tensor, partner_block_mean: Tensor,
+                            partner_block_std: Tensor, anchor_conv_weight: Tensor,
+                            partner_conv_weight: Tensor, block_size: int, *,
+                            ring: bool = False) -> tuple[tuple[Tensor, ...], Tensor]:
+        """``project_into`` with the router cache update of the last two segments
+        (anchor_router_key, partner_router_key) folded in -- the reference's roadmap
+        item "fold the router cache update into the packed projection"
+        (README.md:148-149); no reference counterpart.
+
+        Same results as ``project_into(...)`` followed by
+        ``router_cache_update(parts[4], parts[5], <router tensors>, position,
+        block_size)`` (``router_cache_update_ring`` when ``ring``), in one launch for
+        decode shapes.  Returns (the ``project`` views, the router's conv rows
+        [B, 2, D] fp32)."""
+        if memory.size(-1) != self.input_width:
+            raise ValueError("memory width does not match packed projection input")
+        caches = (anchor_keys, partner_keys, operand_cache, partner_anchor_cache)
+        if tuple(int(c.size(-1)) for c in caches) != tuple(self.split_sizes[:4]):
+            raise ValueError("cache widths must equal the first four split sizes")
+        packed, router_out = torch.ops.relation_lm.packed_projection_router_update(
+            memory, self.weight, *caches, position, ring, anchor_raw_cache, partner_raw_cache,
+            anchor_conv_cache, partner_conv_cache, anchor_block_mean, anchor_block_std,
+            partner_block_mean, partner_block_std, anchor_conv_weight, partner_conv_weight,
+            block_size)
+        return packed.split(self.split_sizes, dim=-1), router_out
+
     def project_dict(self, memory: Tensor) -> dict[str, Tensor]:
         """Project ``memory`` and return a name-to-tensor mapping."""
         return dict(zip(self.names, self.project(memory), strict=True))

@@ -242,6 +242,11 @@ def op_cases(device):
                    for w in (64, 64, 128, 128))
     cases.append(("packed_projection_to_caches", ops.packed_projection_to_caches.default,
                   (memory, weight) + caches + (pos, False)))
+    cases.append(("packed_projection_router_update",
+                  ops.packed_projection_router_update.default,
+                  (memory, weight) + tuple(c.clone() for c in caches) + (rdev["position"], False)
+                  + tuple(rdev[n].clone() for n in ROUTER_BUFFERS)
+                  + (rdev["anchor_weight"], rdev["partner_weight"], 8)))
     cases.append(("relation_linear", ops.relation_linear.default,
                   (red["operand_cache"], red["expanded_weight"], red["expanded_bias"], None)))
     cases.append(("relation_linear_out", ops.relation_linear_out.default,
@@ -278,7 +283,8 @@ OP_NAMES = ("relation_select_packed", "relation_select_packed_seq",
             "relation_hidden_cache_update_ring", "relation_norm_reduce",
             "relation_norm_reduce_seq", "relation_reduce_fused_seq", "router_cache_update",
             "router_cache_update_ring", "packed_sparse_cache_projection",
-            "packed_projection_to_caches", "relation_linear", "relation_linear_out",
+            "packed_projection_to_caches", "packed_projection_router_update",
+            "relation_linear", "relation_linear_out",
             "relation_norm_reduce_output", "relation_norm_reduce_output_seq",
             "multi_relation_reduce_seq", "layer_norm", "block_statistics")
 
