@@ -156,7 +156,7 @@ def main() -> int:
         relation_linear,
         relation_linear_out,
         relation_norm_reduce,
-        relation_norm_reduce_output,
+        relation_linear_norm_reduce_output,
         relation_norm_reduce_seq,
         relation_reduce_fused_seq,
     )
@@ -261,13 +261,12 @@ def main() -> int:
                     relation_linear_out(dred["operand_cache"][:, t], dred["expanded_weight"],
                                         dred["expanded_bias"], dexp[:, t])
                     hid = cached_op(dexp, dred["operand_cache"], a_, p_, dred["product_weight"])
-                raw_ = relation_linear(hid, dred["second_weight"], dred["second_bias"],
-                                       out_dtype=torch.float32)
-                # norm-reduce with the output-head preparation as its epilogue
-                return relation_norm_reduce_output(raw_, ps_, dred["norm_weight"],
-                                                   dred["norm_bias"], position, 1e-5,
-                                                   head["query"], head["mix"], head["weight"],
-                                                   head["bias"], 1e-5)[1]
+                # second linear (split over the hidden dim) and norm-reduce with the
+                # output-head preparation as its epilogue, the partials summed there
+                return relation_linear_norm_reduce_output(
+                    hid, dred["second_weight"], dred["second_bias"], ps_, dred["norm_weight"],
+                    dred["norm_bias"], position, 1e-5, head["query"], head["mix"],
+                    head["weight"], head["bias"], 1e-5)[1]
 
             for _ in range(20):
                 decode_step()

@@ -256,6 +256,29 @@ hipError_t rlm_relation_norm_reduce_output(
     const rlm_tensor* out_final, hipStream_t stream);
 
 /*
+ * The decode step's second linear and norm-reduce with the output-head
+ * preparation (the reference's roadmap item "fold norm-reduce into the second
+ * linear", README.md:148-151; no reference op): the same result as
+ *   raw = hidden @ second_weight^T + second_bias   (rlm_linear)
+ *   rlm_relation_norm_reduce_output(raw, ...)
+ * within fp32 rounding (the reduction is summed in a different order).  The
+ * linear runs split-K over `partials` [S, B*K, D] fp32 (a caller-owned
+ * workspace; S splits of the hidden dim, each written whole) and the per-query
+ * norm-reduce kernel adds the S partial products in order plus the bias as it
+ * loads the rows -- deterministic, no atomics.
+ *   hidden [B,K,H] f32/bf16/f16, second_weight [D,H] bf16/f16, second_bias [D].
+ *   query NULL: context only (out_final unused).  Decode shapes only: B <= 256
+ *   queries, B*K <= 64 rows, D % 4 == 0, D <= 1024, K <= 16.
+ */
+hipError_t rlm_relation_linear_norm_reduce_output(
+    const rlm_tensor* hidden, const rlm_tensor* second_weight, const rlm_tensor* second_bias,
+    const rlm_tensor* partner_scores, const rlm_tensor* norm_weight,
+    const rlm_tensor* norm_bias, const rlm_tensor* position, double norm_eps,
+    const rlm_tensor* query, const rlm_tensor* mix_logit, const rlm_tensor* output_weight,
+    const rlm_tensor* output_bias, double output_eps, const rlm_tensor* partials,
+    const rlm_tensor* out_context, const rlm_tensor* out_final, hipStream_t stream);
+
+/*
  * Sequence form of rlm_relation_norm_reduce_output: raw [B,Tq,K,D],
  * partner_scores [B,Tq,K], positions [Tq] or [B,Tq], query [B,Tq,D];
  * out_context f32 [B,Tq,D], out_final [B,Tq,D].

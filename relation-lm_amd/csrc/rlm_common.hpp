@@ -485,4 +485,8 @@ bool check_same_dtype(const rlm_tensor* a, const char* an, const rlm_tensor* b, 
 // Launch status of the last kernel, with the error message recorded.
 hipError_t launch_status(const char* what);
 
+// Split-K partial products of the decode GEMM (rlm_gemm.hip): part[z] [M,N] fp32.
+hipError_t linear_partials_impl(const rlm_tensor* input, const rlm_tensor* weight,
+                                const rlm_tensor* part, hipStream_t stream);
+
 }  // namespace rlm

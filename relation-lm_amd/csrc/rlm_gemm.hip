@@ -67,6 +67,11 @@ struct GemmParams {
   const void* pos;
   int pos_dtype;
   int ring;
+  // Optional split-K (skinny kernel only): grid.z = splits, split z takes
+  // slices [z * split_slices, (z + 1) * split_slices) and writes its fp32
+  // partial tile, without bias, to part[z][M][N] (the consumer adds the splits).
+  int64_t split_slices;
+  float* part;
 };
 
 // 16-bit bit pattern of v in the MFMA input type W (bf16 or f16).
@@ -492,8 +497,11 @@ __global__ void __launch_bounds__(kSkinnyWaves * kWave) skinny_kernel(const Gemm
   const FloatWords bias_w = issue_float(p.bias, p.bias_dtype, static_cast<uint32_t>(p.N),
                                         static_cast<uint32_t>(n_ok ? n0 + r16 : 0), has_bias);
   f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  const int64_t slices = (p.K + kBK - 1) / kBK;
-  for (int64_t s0 = wave; s0 < slices; s0 += kSkinnyWaves * kSkinnyBatch) {
+  const int64_t all_slices = (p.K + kBK - 1) / kBK;
+  // Split-K: this workgroup's slices [s_lo, slices).
+  const int64_t s_lo = p.part != nullptr ? static_cast<int64_t>(blockIdx.z) * p.split_slices : 0;
+  const int64_t slices = p.part != nullptr ? min(all_slices, s_lo + p.split_slices) : all_slices;
+  for (int64_t s0 = s_lo + wave; s0 < slices; s0 += kSkinnyWaves * kSkinnyBatch) {
     // All raw loads of the batch first (from clamped, valid addresses: no
     // branch), then the conversions and products, so the wave pays one memory
     // round trip per batch.  fp32 inputs are two 16-byte loads per fragment.
@@ -505,8 +513,9 @@ __global__ void __launch_bounds__(kSkinnyWaves * kWave) skinny_kernel(const Gemm
 #pragma unroll
     for (int u = 0; u < kSkinnyBatch; ++u) {
       // K is a multiple of 8, so an 8-element chunk is either wholly inside or past K.
-      const int64_t k = (s0 + u * kSkinnyWaves) * kBK + kq;
-      const bool in = k < p.K;
+      const int64_t su = s0 + u * kSkinnyWaves;
+      const int64_t k = su * kBK + kq;
+      const bool in = su < slices && k < p.K;
       const uint32_t kb = static_cast<uint32_t>(in ? k : 0);
       braw[u] = buf_load_b128(wr, n_ok && in ? wrow + kb * static_cast<uint32_t>(sizeof(W)) : kNoOffset);
 #pragma unroll
@@ -545,6 +554,17 @@ __global__ void __launch_bounds__(kSkinnyWaves * kWave) skinny_kernel(const Gemm
 #pragma unroll
   for (int w = 1; w < kSkinnyWaves; ++w) sum += part[w][lane];
   const int64_t n = n0 + r16;
+  if (p.part != nullptr) {  // split-K partial: fp32, no bias
+    if (n < p.N) {
+      float* dst = p.part + static_cast<int64_t>(blockIdx.z) * p.M * p.N;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t m = m0 + (lane >> 4) * 4 + e;
+        if (m < p.M) dst[m * p.N + n] = sum[e];
+      }
+    }
+    return;
+  }
   const float bv = has_bias ? decode_float(bias_w, p.bias_dtype) : 0.0f;
   store_tile<TO>(p, sum, m0, n, bv, lane);
   scatter_tile<TO>(p, sum, m0, n, bv, lane);
@@ -788,6 +808,75 @@ hipError_t linear_impl(const rlm_tensor* input, const rlm_tensor* weight, const 
 }
 
 }  // namespace
+
+// Split-K partial products of the skinny GEMM: part[z] = input @ weight^T over
+// reduction slices [z * split_slices * 32, ...), fp32, no bias (declared in
+// rlm_common.hpp; the consumer sums the splits).  input [M<=64, K] fp32 or
+// 16-bit, weight [N, K] bf16/f16, part [splits, M, N] fp32.
+hipError_t linear_partials_impl(const rlm_tensor* input, const rlm_tensor* weight,
+                                const rlm_tensor* part, hipStream_t stream) {
+  const char* what = "linear partials";
+  RLM_TRY(check_rows(input, "input"));
+  RLM_TRY(check_tensor(weight, "weight", 2));
+  RLM_TRY(check_tensor(part, "partials", 3));
+  RLM_TRY(check_dtype_is(part, "partials", RLM_F32));
+  const int64_t M = input->shape[0], K = input->shape[1], N = weight->shape[0];
+  const int64_t splits = part->shape[0];
+  RLM_TRY(check_dim(weight, "weight", 1, K));
+  RLM_TRY(check_dim(part, "partials", 1, M));
+  RLM_TRY(check_dim(part, "partials", 2, N));
+  RLM_REQUIRE(weight->dtype == RLM_BF16 || weight->dtype == RLM_F16,
+              "%s: 16-bit weights required", what);
+  RLM_REQUIRE(input->dtype == RLM_F32 || input->dtype == weight->dtype,
+              "%s: input must be fp32 or share the weight dtype", what);
+  RLM_REQUIRE(M >= 1 && M <= kSkinnyM && splits >= 1 && splits <= 64,
+              "%s: 1..%d rows and 1..64 splits", what, kSkinnyM);
+  const int64_t lda = M > 1 ? input->stride[0] : K;
+  RLM_REQUIRE(K % 8 == 0 && lda % 8 == 0, "%s: reduction dim and row stride must be multiples of 8", what);
+  RLM_REQUIRE((reinterpret_cast<uintptr_t>(input->data) & 15u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(weight->data) & 15u) == 0,
+              "%s: input and weight must be 16-byte aligned", what);
+  const int64_t ab = ((M - 1) * lda + K) * dtype_size(input->dtype);
+  const int64_t wb = N * K * dtype_size(weight->dtype);
+  RLM_REQUIRE(ab < (int64_t(1) << 31) && wb < (int64_t(1) << 31), "%s: operands over 2 GiB", what);
+  GemmParams p{};
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.lda = lda;
+  p.a = input->data;
+  p.w = weight->data;
+  p.bias_dtype = RLM_F32;
+  p.out = part->data;
+  p.ldo = N;
+  p.a_bytes = static_cast<uint32_t>(ab);
+  p.w_bytes = static_cast<uint32_t>(wb);
+  const int64_t slices = (K + kBK - 1) / kBK;
+  p.split_slices = (slices + splits - 1) / splits;
+  p.part = static_cast<float*>(part->data);
+  if (N == 0) return hipSuccess;
+  RLM_REQUIRE(p.split_slices <= kSkinnyWaves * kSkinnyBatchLong,
+              "%s: %lld slices per split exceed one round of loads", what,
+              (long long)p.split_slices);
+  const dim3 grid(static_cast<unsigned>((N + 15) / 16), static_cast<unsigned>((M + 15) / 16),
+                  static_cast<unsigned>(splits));
+  const bool short_batch = p.split_slices <= kSkinnyWaves * kSkinnyBatchShort;
+#define RLM_PART_CASE(TA, W)                                                                   \
+  if (short_batch)                                                                             \
+    hipLaunchKernelGGL((skinny_kernel<TA, W, float, kSkinnyBatchShort>), grid,                \
+                       dim3(kSkinnyWaves * kWave), 0, stream, p);                              \
+  else                                                                                         \
+    hipLaunchKernelGGL((skinny_kernel<TA, W, float, kSkinnyBatchLong>), grid,                 \
+                       dim3(kSkinnyWaves * kWave), 0, stream, p);
+  if (weight->dtype == RLM_BF16) {
+    if (input->dtype == RLM_F32) { RLM_PART_CASE(float, bf16) } else { RLM_PART_CASE(bf16, bf16) }
+  } else {
+    if (input->dtype == RLM_F32) { RLM_PART_CASE(float, f16) } else { RLM_PART_CASE(f16, f16) }
+  }
+#undef RLM_PART_CASE
+  return launch_status(what);
+}
+
 }  // namespace rlm
 
 using namespace rlm;

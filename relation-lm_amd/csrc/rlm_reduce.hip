@@ -541,6 +541,12 @@ struct NormParams {
   int query_dtype, mix_dtype, ow_dtype, ob_dtype;
   float out_eps;
   void* final;          // [Q,D], query_dtype
+  // Raw rows given as split-K partial products (the per-query kernel only):
+  // raw = sum_z parts[z] + b2, the splits added in order.
+  const float* parts;   // [nparts][Q*K][D] fp32
+  int nparts;
+  const void* b2;       // [D]
+  int b2_dtype;
 };
 
 __device__ __forceinline__ void store_any4(void* base, int dtype, int64_t i4, float4 v) {
@@ -631,7 +637,7 @@ __global__ void __launch_bounds__(256) norm_reduce_vec_kernel(const NormParams p
     ow[i] = f4_issue(p.ow, p.ow_dtype, gs);
     obw[i] = f4_issue(p.ob, p.ob_dtype, gs);
   }
-  const float mix = load_any_f(p.mix, p.mix_dtype, 0);
+  const FloatWords mixw = issue_float(p.mix, p.mix_dtype, 1, 0, p.prep != 0);
   // Partner rows in batches of KB; the first batch is issued before anything
   // is decoded, so position, scores, gamma / beta and these rows share one
   // memory round trip.
@@ -699,7 +705,7 @@ __global__ void __launch_bounds__(256) norm_reduce_vec_kernel(const NormParams p
   }
   if (p.prep) {  // wave-uniform
     // Output-head preparation: LayerNorm_out(query + sigmoid(mix) * context).
-    const float gate = 1.0f / (1.0f + expf(-mix));
+    const float gate = 1.0f / (1.0f + expf(-decode_float(mixw, p.mix_dtype)));
     float4 y[G];
     float sum = 0.0f;
 #pragma unroll
@@ -747,6 +753,7 @@ __global__ void __launch_bounds__(256) norm_reduce_vec_kernel(const NormParams p
 constexpr int kQWaves = 4;
 constexpr int kQMaxD = 1024;
 constexpr int64_t kQueryKernelMaxQ = 256;  // queries below which a workgroup per query pays
+constexpr int kMaxParts = 4;                // split-K partial products summed on load
 
 // Four consecutive elements c*4.. of a parameter vector of `dtype`: a 16-byte
 // and an 8-byte load are both issued, the one that does not match the dtype
@@ -775,8 +782,10 @@ __device__ __forceinline__ float4 chunk4_decode(const Chunk4& v, int dtype) {
   return make_float4(f[0], f[1], f[2], f[3]);
 }
 
-template <int RPW, int GI>
-__global__ void __launch_bounds__(kQWaves * kWave) norm_reduce_query_kernel(const NormParams p) {
+// NP > 0: the raw rows are the sum of NP split-K partial products plus b2.
+template <int RPW, int GI, int NP>
+__global__ void __launch_bounds__(kQWaves * kWave) __attribute__((amdgpu_waves_per_eu(1, 1)))
+norm_reduce_query_kernel(const NormParams p) {
   __shared__ float4 par[5][kQMaxD / 4];         // w, b, query, ow, ob as fp32
   __shared__ float4 part[kQWaves][kQMaxD / 4];  // each wave's sum_k p_k xhat_k
   __shared__ float red[2][kQWaves];
@@ -791,20 +800,10 @@ __global__ void __launch_bounds__(kQWaves * kWave) norm_reduce_query_kernel(cons
   // wave's partner rows and one chunk of each parameter vector per thread.
   const int64_t t = index_at(p.pos, p.pos_dtype, b * p.pos_sb + tq * p.pos_sq);
   const float score = partner_score(p, q, lane);
-  const float mix = load_any_f(p.mix, p.mix_dtype, 0);
+  const FloatWords mixw = issue_float(p.mix, p.mix_dtype, 1, 0, p.prep != 0);
   const float* raw = static_cast<const float*>(p.raw) + q * p.K * static_cast<int64_t>(p.D);
-  float4 x[RPW][GI];
-#pragma unroll
-  for (int r = 0; r < RPW; ++r)
-#pragma unroll
-    for (int i = 0; i < GI; ++i) {
-      const int k = wave + kQWaves * r;
-      const int g = lane + kWave * i;
-      const bool in = k < p.K && g < groups;
-      const float4 v = *reinterpret_cast<const float4*>(raw + static_cast<int64_t>(in ? k : 0) * p.D +
-                                                        4 * (in ? g : 0));
-      x[r][i] = in ? v : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+  // The parameter chunks go first: the row statistics below wait for the rows,
+  // and with the chunks already in flight that wait covers them too.
   const bool cl = tid < groups;
   const Chunk4 cw = chunk4_issue(p.w, p.w_dtype, p.D, tid, cl);
   const Chunk4 cb = chunk4_issue(p.bias, p.b_dtype, p.D, tid, cl);
@@ -813,6 +812,66 @@ __global__ void __launch_bounds__(kQWaves * kWave) norm_reduce_query_kernel(cons
                                  p.query_dtype, p.D, tid, cl);
   const Chunk4 cow = chunk4_issue(p.ow, p.ow_dtype, p.D, tid, cl);
   const Chunk4 cob = chunk4_issue(p.ob, p.ob_dtype, p.D, tid, cl);
+  float4 x[RPW][GI];
+  if constexpr (NP > 0) {
+    // raw = (sum of the split-K partial products, in split order) + b2.  Every
+    // partial of the wave's rows is loaded before any is added, so the
+    // partials cost one memory round trip.
+    const uint32_t pstride = static_cast<uint32_t>(p.Q * p.K * p.D) * 4u;  // bytes per split
+    const rsrc_t prs = make_rsrc(p.parts, pstride * static_cast<uint32_t>(NP));
+    const uint32_t qoff = static_cast<uint32_t>(q * p.K * p.D) * 4u;
+    F4Words bw[GI];
+#pragma unroll
+    for (int i = 0; i < GI; ++i) {
+      const int g = lane + kWave * i;
+      bw[i] = f4_issue(p.b2, p.b2_dtype, g < groups ? g : 0);
+    }
+    uint4 w[RPW][GI][NP];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int i = 0; i < GI; ++i) {
+        const int k = wave + kQWaves * r;
+        const int g = lane + kWave * i;
+        const bool in = k < p.K && g < groups;
+        // Lanes past the row and rows past K read nothing.
+        const uint32_t off = qoff + static_cast<uint32_t>((in ? k : 0) * p.D + 4 * (in ? g : 0)) * 4u;
+#pragma unroll
+        for (int z = 0; z < NP; ++z) w[r][i][z] = buf_load_b128(prs, in ? off + z * pstride : kNoOffset);
+      }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int i = 0; i < GI; ++i) {
+        const int k = wave + kQWaves * r;
+        const int g = lane + kWave * i;
+        const bool in = k < p.K && g < groups;
+        float4 v = make_float4(__uint_as_float(w[r][i][0].x), __uint_as_float(w[r][i][0].y),
+                               __uint_as_float(w[r][i][0].z), __uint_as_float(w[r][i][0].w));
+#pragma unroll
+        for (int z = 1; z < NP; ++z) {
+          v.x += __uint_as_float(w[r][i][z].x);
+          v.y += __uint_as_float(w[r][i][z].y);
+          v.z += __uint_as_float(w[r][i][z].z);
+          v.w += __uint_as_float(w[r][i][z].w);
+        }
+        const float4 b4 = f4_decode(bw[i], p.b2_dtype);
+        x[r][i] = in ? make_float4(v.x + b4.x, v.y + b4.y, v.z + b4.z, v.w + b4.w)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+  } else {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int i = 0; i < GI; ++i) {
+        const int k = wave + kQWaves * r;
+        const int g = lane + kWave * i;
+        const bool in = k < p.K && g < groups;
+        const float4 v = *reinterpret_cast<const float4*>(raw + static_cast<int64_t>(in ? k : 0) * p.D +
+                                                          4 * (in ? g : 0));
+        x[r][i] = in ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+  }
 
   // ---- Partner weights (every wave computes the same ones).
   const float prob = partner_weight(p, score, t, lane);
@@ -893,7 +952,7 @@ __global__ void __launch_bounds__(kQWaves * kWave) norm_reduce_query_kernel(cons
   }
   if (!p.prep) return;  // uniform
   // ---- Output-head preparation: LayerNorm_out(query + sigmoid(mix) * context).
-  const float gate = 1.0f / (1.0f + expf(-mix));
+  const float gate = 1.0f / (1.0f + expf(-decode_float(mixw, p.mix_dtype)));
   float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
   if (cl) {
     const float4 qv = par[2][tid];
@@ -942,7 +1001,7 @@ __global__ void __launch_bounds__(256) norm_reduce_kernel(const NormParams p) {
     obv[i] = load_any_f(p.ob, p.ob_dtype, ds);
     ctx[i] = 0.0f;
   }
-  const float mix = load_any_f(p.mix, p.mix_dtype, 0);
+  const FloatWords mixw = issue_float(p.mix, p.mix_dtype, 1, 0, p.prep != 0);
   const float inv_d = 1.0f / static_cast<float>(p.D);
   const TR* raw = static_cast<const TR*>(p.raw) + q * p.K * static_cast<int64_t>(p.D);
   for (int k = 0; k < p.K; ++k) {
@@ -977,7 +1036,7 @@ __global__ void __launch_bounds__(256) norm_reduce_kernel(const NormParams p) {
     if (d < p.D) out[d] = ctx[i];
   }
   if (p.prep) {  // wave-uniform: output-head preparation, as the vector kernel
-    const float gate = 1.0f / (1.0f + expf(-mix));
+    const float gate = 1.0f / (1.0f + expf(-decode_float(mixw, p.mix_dtype)));
     float y[VPL], sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
@@ -1131,10 +1190,18 @@ template <int RPW>
 hipError_t launch_norm_query_rpw(const NormParams& p, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.Q));
   const int gi = (p.D / 4 + kWave - 1) / kWave;
+#define RLM_NORMQ_NP(GI, NP)                                                                  \
+  hipLaunchKernelGGL((norm_reduce_query_kernel<RPW, GI, NP>), grid, dim3(kQWaves * kWave), 0, \
+                     stream, p)
 #define RLM_NORMQ_CASE(GI)                                                                    \
   if (gi <= GI) {                                                                             \
-    hipLaunchKernelGGL((norm_reduce_query_kernel<RPW, GI>), grid, dim3(kQWaves * kWave), 0,  \
-                       stream, p);                                                            \
+    switch (p.nparts) {                                                                       \
+      case 0: RLM_NORMQ_NP(GI, 0); break;                                                     \
+      case 1: RLM_NORMQ_NP(GI, 1); break;                                                     \
+      case 2: RLM_NORMQ_NP(GI, 2); break;                                                     \
+      case 3: RLM_NORMQ_NP(GI, 3); break;                                                     \
+      default: RLM_NORMQ_NP(GI, 4); break;                                                    \
+    }                                                                                         \
     return launch_status("relation_norm_reduce");                                            \
   }
   RLM_NORMQ_CASE(1)
@@ -1142,6 +1209,7 @@ hipError_t launch_norm_query_rpw(const NormParams& p, hipStream_t stream) {
   RLM_NORMQ_CASE(3)
   RLM_NORMQ_CASE(4)
 #undef RLM_NORMQ_CASE
+#undef RLM_NORMQ_NP
   set_error("relation_norm_reduce: width %d too large for the per-query kernel", p.D);
   return hipErrorInvalidValue;
 }
@@ -1174,6 +1242,10 @@ hipError_t launch_norm_vpl(const NormParams& p, int dtype, hipStream_t stream) {
 
 // Output-head preparation arguments of norm_impl (all null: context only).
 struct OutputPrep {
+  // Raw rows as split-K partial products [S, Q*K, D] fp32 plus the second
+  // linear's bias (the raw tensor then only describes the shape).
+  const rlm_tensor* parts = nullptr;
+  const rlm_tensor* b2 = nullptr;
   const rlm_tensor* query = nullptr;
   const rlm_tensor* mix_logit = nullptr;
   const rlm_tensor* weight = nullptr;
@@ -1284,6 +1356,31 @@ hipError_t norm_impl(bool seq, const rlm_tensor* raw, const rlm_tensor* partner_
     p.ob_dtype = prep.bias->dtype;
     p.out_eps = static_cast<float>(prep.eps);
     p.final = prep.final->data;
+  }
+  if (prep.parts != nullptr) {
+    RLM_TRY(check_tensor(prep.parts, "partials", 3));
+    RLM_TRY(check_dtype_is(prep.parts, "partials", RLM_F32));
+    RLM_TRY(check_dim(prep.parts, "partials", 1, p.Q * K));
+    RLM_TRY(check_dim(prep.parts, "partials", 2, D));
+    RLM_TRY(check_tensor(prep.b2, "second_bias", 1));
+    RLM_TRY(check_dtype_float(prep.b2, "second_bias"));
+    RLM_TRY(check_dim(prep.b2, "second_bias", 0, D));
+    RLM_REQUIRE(prep.parts->shape[0] >= 1 && prep.parts->shape[0] <= kMaxParts,
+                "relation_linear_norm_reduce: 1..%d hidden-dim splits", kMaxParts);
+    RLM_REQUIRE(p.Q <= kQueryKernelMaxQ && D % 4 == 0 && D <= kQMaxD && K <= 16 &&
+                    (reinterpret_cast<uintptr_t>(prep.parts->data) & 15u) == 0 &&
+                    (reinterpret_cast<uintptr_t>(norm_weight->data) & 15u) == 0 &&
+                    (reinterpret_cast<uintptr_t>(norm_bias->data) & 15u) == 0 &&
+                    (reinterpret_cast<uintptr_t>(prep.b2->data) & 15u) == 0,
+                "relation_linear_norm_reduce: decode shapes only (at most %lld queries, "
+                "D %% 4 == 0, D <= %d, K <= 16, 16-byte aligned vectors)",
+                (long long)kQueryKernelMaxQ, kQMaxD);
+    p.parts = static_cast<const float*>(prep.parts->data);
+    p.nparts = static_cast<int>(prep.parts->shape[0]);
+    p.b2 = prep.b2->data;
+    p.b2_dtype = prep.b2->dtype;
+    if (p.Q == 0) return hipSuccess;
+    return launch_norm_query(p, stream);
   }
   if (p.Q == 0) return hipSuccess;
   const bool vec_ok = D % 4 == 0 && (reinterpret_cast<uintptr_t>(raw->data) & 15u) == 0 &&
@@ -1457,6 +1554,53 @@ extern "C" hipError_t rlm_relation_norm_reduce_output(
   prep.eps = output_eps;
   prep.final = out_final;
   return norm_impl(false, raw, partner_scores, norm_weight, norm_bias, position, norm_eps,
+                   out_context, stream, prep);
+}
+
+extern "C" hipError_t rlm_relation_linear_norm_reduce_output(
+    const rlm_tensor* hidden, const rlm_tensor* second_weight, const rlm_tensor* second_bias,
+    const rlm_tensor* partner_scores, const rlm_tensor* norm_weight, const rlm_tensor* norm_bias,
+    const rlm_tensor* position, double norm_eps, const rlm_tensor* query,
+    const rlm_tensor* mix_logit, const rlm_tensor* output_weight, const rlm_tensor* output_bias,
+    double output_eps, const rlm_tensor* partials, const rlm_tensor* out_context,
+    const rlm_tensor* out_final, hipStream_t stream) {
+  clear_error();
+  RLM_TRY(check_tensor(hidden, "hidden", 3));
+  RLM_REQUIRE(second_bias != nullptr, "second_bias: missing tensor");
+  const int64_t B = hidden->shape[0], K = hidden->shape[1], H = hidden->shape[2];
+  // The hidden rows as a [B*K, H] matrix (contiguous rows).
+  rlm_tensor rows = *hidden;
+  rows.ndim = 2;
+  rows.shape[0] = B * K;
+  rows.shape[1] = H;
+  rows.stride[0] = hidden->stride[1];
+  rows.stride[1] = hidden->stride[2];
+  RLM_REQUIRE(B <= 1 || hidden->stride[0] == K * hidden->stride[1],
+              "hidden: rows of consecutive batch entries must be contiguous");
+  RLM_TRY(check_tensor(partials, "partials", 3));
+  hipError_t err = linear_partials_impl(&rows, second_weight, partials, stream);
+  if (err != hipSuccess) return err;
+  // The raw shape [B, K, D] for norm_impl's checks; the values come from the partials.
+  rlm_tensor raw = *partials;
+  raw.ndim = 3;
+  raw.shape[0] = B;
+  raw.shape[1] = K;
+  raw.shape[2] = partials->shape[2];
+  raw.stride[2] = 1;
+  raw.stride[1] = raw.shape[2];
+  raw.stride[0] = K * raw.shape[2];
+  OutputPrep prep;
+  prep.parts = partials;
+  prep.b2 = second_bias;
+  if (query != nullptr) {
+    prep.query = query;
+    prep.mix_logit = mix_logit;
+    prep.weight = output_weight;
+    prep.bias = output_bias;
+    prep.eps = output_eps;
+    prep.final = out_final;
+  }
+  return norm_impl(false, &raw, partner_scores, norm_weight, norm_bias, position, norm_eps,
                    out_context, stream, prep);
 }
 

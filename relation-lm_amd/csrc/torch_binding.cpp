@@ -466,6 +466,78 @@ std::tuple<at::Tensor, at::Tensor> relation_norm_reduce_output_seq(
                             norm_eps, query, mix_logit, output_weight, output_bias, output_eps);
 }
 
+// The decode step's second linear and norm-reduce with the output-head
+// preparation (no reference op): split-K partial products in a workspace, summed
+// by the per-query norm kernel; other shapes run relation_linear then
+// relation_norm_reduce_output.
+std::tuple<at::Tensor, at::Tensor> relation_linear_norm_reduce_output(
+    const at::Tensor& hidden, const at::Tensor& second_weight, const at::Tensor& second_bias,
+    const at::Tensor& partner_scores, const at::Tensor& norm_weight, const at::Tensor& norm_bias,
+    const at::Tensor& position, double norm_eps, const at::Tensor& query,
+    const at::Tensor& mix_logit, const at::Tensor& output_weight, const at::Tensor& output_bias,
+    double output_eps) {
+  const char* op = "relation_lm::relation_linear_norm_reduce_output";
+  c10::DeviceGuard guard(hidden.device());
+  hipStream_t stream = device_stream(
+      op, {&hidden, &second_weight, &second_bias, &partner_scores, &norm_weight, &norm_bias,
+           &position, &query, &mix_logit, &output_weight, &output_bias});
+  TORCH_CHECK(hidden.dim() == 3, op, ": hidden must be [B,K,H]");
+  TORCH_CHECK(second_weight.dim() == 2, op, ": second_weight must be [D,H]");
+  const int64_t B = hidden.size(0), K = hidden.size(1), H = hidden.size(2);
+  const int64_t D = second_weight.size(0);
+  at::Tensor context = at::empty({B, D}, f32(hidden));
+  at::Tensor final = at::empty({B, D}, query.options().memory_format(at::MemoryFormat::Contiguous));
+  const bool fused = B * K <= 64 && B <= 256 && K <= 16 && D % 4 == 0 && D <= 1024 &&
+                     H <= 4 * 72 * 32 && second_weight.scalar_type() != at::kFloat &&
+                     hidden.is_contiguous();
+  if (!fused) {
+    at::Tensor raw = at::empty({B, K, D}, f32(hidden));
+    at::Tensor h2 = hidden.reshape({B * K, H});
+    at::Tensor r2 = raw.view({B * K, D});
+    rlm_tensor l[4] = {desc(h2, "input"), desc(second_weight, "weight"),
+                       desc(second_bias, "bias"), desc(r2, "out")};
+    check(rlm_linear(&l[0], &l[1], &l[2], &l[3], stream), op);
+    rlm_tensor d[11] = {desc(raw, "raw"),          desc(partner_scores, "partner_scores"),
+                        desc(norm_weight, "norm_weight"), desc(norm_bias, "norm_bias"),
+                        desc(position, "position"), desc(query, "query"),
+                        desc(mix_logit, "mix_logit"), desc(output_weight, "output_weight"),
+                        desc(output_bias, "output_bias"), desc(context, "out_context"),
+                        desc(final, "out_final")};
+    check(rlm_relation_norm_reduce_output(&d[0], &d[1], &d[2], &d[3], &d[4], norm_eps, &d[5],
+                                          &d[6], &d[7], &d[8], output_eps, &d[9], &d[10], stream),
+          op);
+    return {context, final};
+  }
+  // Splits of the hidden dim (at most four): enough that each split's 32-wide
+  // slices fit the short load batch (24), then one more while the grid stays
+  // within one workgroup per CU (256).
+  const int64_t slices = (H + 31) / 32;
+  const int64_t tiles = ((D + 15) / 16) * ((B * K + 15) / 16);
+  int64_t splits = std::min<int64_t>(4, (slices + 23) / 24);
+  while (splits < 4 && tiles * (splits + 1) <= 256 && slices >= 8 * (splits + 1)) ++splits;
+  splits = std::max<int64_t>(1, splits);
+  at::Tensor partials = at::empty({splits, B * K, D}, f32(hidden));
+  rlm_tensor d[16] = {desc(hidden, "hidden"),
+                      desc(second_weight, "second_weight"),
+                      desc(second_bias, "second_bias"),
+                      desc(partner_scores, "partner_scores"),
+                      desc(norm_weight, "norm_weight"),
+                      desc(norm_bias, "norm_bias"),
+                      desc(position, "position"),
+                      desc(query, "query"),
+                      desc(mix_logit, "mix_logit"),
+                      desc(output_weight, "output_weight"),
+                      desc(output_bias, "output_bias"),
+                      desc(partials, "partials"),
+                      desc(context, "out_context"),
+                      desc(final, "out_final")};
+  check(rlm_relation_linear_norm_reduce_output(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6],
+                                               norm_eps, &d[7], &d[8], &d[9], &d[10], output_eps,
+                                               &d[11], &d[12], &d[13], stream),
+        op);
+  return {context, final};
+}
+
 at::Tensor relation_reduce_fused_seq(const at::Tensor& expanded_cache,
                                      const at::Tensor& operand_cache,
                                      const at::Tensor& anchor_index,
@@ -824,6 +896,11 @@ TORCH_LIBRARY(relation_lm, m) {
       "Tensor(j!) anchor_block_std, Tensor(k!) partner_block_mean, Tensor(l!) partner_block_std, "
       "Tensor anchor_conv_weight, Tensor partner_conv_weight, SymInt block_size) -> (Tensor, Tensor)");
   m.def(
+      "relation_linear_norm_reduce_output(Tensor hidden, Tensor second_weight, Tensor "
+      "second_bias, Tensor partner_scores, Tensor norm_weight, Tensor norm_bias, Tensor "
+      "position, float norm_eps, Tensor query, Tensor mix_logit, Tensor output_weight, Tensor "
+      "output_bias, float output_eps) -> (Tensor, Tensor)");
+  m.def(
       "relation_linear(Tensor input, Tensor weight, Tensor? bias=None, ScalarType? "
       "out_dtype=None) -> Tensor");
   m.def(
@@ -878,6 +955,7 @@ TORCH_LIBRARY_IMPL(relation_lm, CUDA, m) {
   m.impl("packed_sparse_cache_projection", TORCH_FN(packed_sparse_cache_projection));
   m.impl("packed_projection_to_caches", TORCH_FN(packed_projection_to_caches));
   m.impl("packed_projection_router_update", TORCH_FN(packed_projection_router_update));
+  m.impl("relation_linear_norm_reduce_output", TORCH_FN(relation_linear_norm_reduce_output));
   m.impl("relation_linear", TORCH_FN(relation_linear));
   m.impl("relation_linear_out", TORCH_FN(relation_linear_out));
   m.impl("multi_relation_reduce_seq", TORCH_FN(multi_relation_reduce_seq));

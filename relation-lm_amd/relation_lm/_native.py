@@ -138,6 +138,12 @@ def _register_fakes() -> None:
     torch.library.register_fake("relation_lm::relation_norm_reduce_output")(fake_norm_output)
     torch.library.register_fake("relation_lm::relation_norm_reduce_output_seq")(fake_norm_output)
 
+    @torch.library.register_fake("relation_lm::relation_linear_norm_reduce_output")
+    def _(hidden, second_weight, second_bias, partner_scores, norm_weight, norm_bias, position,
+          norm_eps, query, mix_logit, output_weight, output_bias, output_eps):
+        shape = (hidden.shape[0], second_weight.shape[0])
+        return (hidden.new_empty(shape, dtype=torch.float32), query.new_empty(shape))
+
     @torch.library.register_fake("relation_lm::layer_norm")
     def _(input, weight, bias, eps):
         return torch.empty_like(input, memory_format=torch.contiguous_format)

@@ -183,6 +183,37 @@ def relation_norm_reduce_output_seq(
         mix_logit, output_weight, output_bias, float(output_eps))
 
 
+def relation_linear_norm_reduce_output(
+    hidden: Tensor,
+    second_weight: Tensor,
+    second_bias: Tensor,
+    partner_scores: Tensor,
+    norm_weight: Tensor,
+    norm_bias: Tensor,
+    position: Tensor,
+    norm_eps: float,
+    query: Tensor,
+    mix_logit: Tensor,
+    output_weight: Tensor,
+    output_bias: Tensor,
+    output_eps: float,
+) -> tuple[Tensor, Tensor]:
+    """The decode step's second linear folded into relation_norm_reduce_output:
+    hidden [B,K,H] -> (context f32 [B,D], final [B,D]), the result of
+    ``relation_norm_reduce_output(relation_linear(hidden, second_weight, second_bias,
+    torch.float32), ...)`` (benchmarks/benchmark_relation_reduce.py:80-81 then
+    relation_lm.py:203-206).
+
+    With bf16/f16 weights and at most 64 hidden rows the linear writes fp32 partial
+    products of a few hidden-dim splits into a workspace and the per-query norm kernel
+    adds them (and the bias) in split order as it loads them; the summation order is
+    then not the one-launch linear's, so the raw rows agree with it to fp32 rounding,
+    not bit for bit.  Other shapes run the two ops."""
+    return torch.ops.relation_lm.relation_linear_norm_reduce_output(
+        hidden, second_weight, second_bias, partner_scores, norm_weight, norm_bias, position,
+        float(norm_eps), query, mix_logit, output_weight, output_bias, float(output_eps))
+
+
 def relation_reduce_fused_seq(
     expanded_cache: Tensor,
     operand_cache: Tensor,

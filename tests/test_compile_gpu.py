@@ -262,6 +262,12 @@ def op_cases(device):
     cases.append(("relation_norm_reduce_output_seq", ops.relation_norm_reduce_output_seq.default,
                   (raw_seq, scores_seq, red["norm_weight"], red["norm_bias"], positions, 1e-5,
                    query_seq) + head))
+    hidden_dec = torch.randn(b, k, red["second_weight"].shape[1], generator=g).to(
+        device, red["second_weight"].dtype)
+    cases.append(("relation_linear_norm_reduce_output",
+                  ops.relation_linear_norm_reduce_output.default,
+                  (hidden_dec, red["second_weight"], red["second_bias"], scores_dec,
+                   red["norm_weight"], red["norm_bias"], pos, 1e-5, query_dec) + head))
     slots, kk = 2, 3
     raw_multi = torch.randn(b, t, slots, kk, d, generator=g).to(device)
     scores_multi = torch.randn(b, t, slots, kk, generator=g).to(device)
@@ -286,7 +292,7 @@ OP_NAMES = ("relation_select_packed", "relation_select_packed_seq",
             "packed_projection_to_caches", "packed_projection_router_update",
             "relation_linear", "relation_linear_out",
             "relation_norm_reduce_output", "relation_norm_reduce_output_seq",
-            "multi_relation_reduce_seq", "layer_norm", "block_statistics")
+            "relation_linear_norm_reduce_output", "multi_relation_reduce_seq", "layer_norm", "block_statistics")
 
 
 def test_opcheck_every_registered_op(device):
