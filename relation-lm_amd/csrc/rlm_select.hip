@@ -31,6 +31,7 @@
 #include <cstdlib>
 
 #include "rlm_common.hpp"
+#include "rlm_multi_tile.hpp"
 #include "rlm_select_decode.hpp"
 #include "rlm_select_tile.hpp"
 
@@ -1381,7 +1382,7 @@ bool tile_params(const SelectParams& p, const Geometry& g, int act, int stat,
     return false;
   if (g.T % 16 != 0 || g.T > kTileMaxRows || static_cast<int64_t>(g.NB) * g.BS != g.T) return false;
   if (g.NB > 64 || g.NB % 4 != 0 || p.CAP > 256 || p.TOP > kTileMaxTop || p.K < 1 || p.K > kTileMaxK) return false;
-  if (g.H * g.RB > 1024) return false;
+  if (g.H * g.RB > 512) return false;  // both sides' bias tables staged by one thread each
   tp.B = g.B;
   tp.Tq = g.Tq;
   tp.T = g.T;
@@ -1613,6 +1614,81 @@ bool check_slot_rows(const rlm_tensor* t, const char* name, int64_t d0, int64_t 
          check_dim(t, name, 2, S) && check_dim(t, name, 3, width) && check_dtype_is(t, name, act);
 }
 
+// The multi-anchor selection takes the matrix-core-filtered kernel where it
+// applies unless RLM_MULTI_TILE=0 (both kernels give identical results; the
+// switch exists for comparisons).
+bool multi_tile_path_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("RLM_MULTI_TILE");
+    return v == nullptr || v[0] != '0';
+  }();
+  return on;
+}
+
+// Fills the multi-anchor tile kernel's parameters when the shapes fit it:
+// bf16 activations, 64-wide exact and router vectors, whole blocks of at least
+// 16 rows, at most 64 blocks and 1024 candidates.
+bool multi_tile_params(const SelectParams& p, const MultiParams& m, const Geometry& g, int act,
+                       int stat, const rlm_tensor* positions, MultiTileParams& tp) {
+  if (act != RLM_BF16 || (stat != RLM_F32 && stat != RLM_BF16)) return false;
+  if (g.E != 64 || g.H * g.HD != 64 || g.H > kMultiTileMaxHeads || g.HD % 4 != 0 ||
+      (g.H & (g.H - 1)) != 0)
+    return false;
+  if (static_cast<int64_t>(g.NB) * g.BS != g.T || g.BS < 16 || g.BS % 16 != 0) return false;
+  if (g.NB > kMultiTileMaxBlocks || g.NB % 4 != 0) return false;
+  if (p.CAP > kMultiTileMaxCap || p.TOP > kMultiTileMaxTop || p.K < 1 || p.K > kMultiTileMaxK)
+    return false;
+  if (m.S > kMultiTileMaxSlots || g.H * g.RB > 512) return false;
+  tp.B = g.B;
+  tp.Tq = g.Tq;
+  tp.T = g.T;
+  tp.S = m.S;
+  tp.NB = g.NB;
+  tp.BS = g.BS;
+  tp.BS_log2 = p.BS_log2;
+  tp.L = p.L;
+  tp.TOP = p.TOP;
+  tp.K = p.K;
+  tp.CAP = p.CAP;
+  tp.H = g.H;
+  tp.H_log2 = p.H_log2;
+  tp.HD = g.HD;
+  tp.RB = g.RB;
+  tp.strict = p.strict;
+  tp.exact_scale = p.exact_scale;
+  tp.head_scale = p.head_scale;
+  tp.pos = positions->data;
+  tp.pos_dtype = positions->dtype;
+  tp.pos_sb = p.pos_sb;
+  tp.pos_sq = p.pos_sq;
+  tp.pos_count = p.pos_sb == 0 ? g.Tq : g.B * g.Tq;
+  tp.aq = static_cast<const bf16*>(p.aq);
+  tp.arq = static_cast<const bf16*>(p.arq);
+  tp.pbase = static_cast<const bf16*>(p.pq);
+  tp.pcache = static_cast<const bf16*>(p.pcache);
+  tp.akeys = static_cast<const bf16*>(p.as.keys);
+  tp.pkeys = static_cast<const bf16*>(p.ps.keys);
+  tp.key_bytes = p.key_bytes;
+  tp.amean = p.as.mean;
+  tp.astd = p.as.stdev;
+  tp.pmean = p.ps.mean;
+  tp.pstd = p.ps.stdev;
+  tp.agamma = p.as.gamma;
+  tp.pgamma = p.ps.gamma;
+  tp.abias = p.as.bias;
+  tp.pbias = p.ps.bias;
+  tp.agamma_dtype = p.as.gamma_dtype;
+  tp.pgamma_dtype = p.ps.gamma_dtype;
+  tp.abias_dtype = p.as.bias_dtype;
+  tp.pbias_dtype = p.ps.bias_dtype;
+  tp.out_anchor = p.out_anchor;
+  tp.out_anchor_score = p.out_anchor_score;
+  tp.out_partner = p.out_partner;
+  tp.out_partner_score = p.out_partner_score;
+  tp.tiles = static_cast<int>((g.Tq + 15) / 16);
+  return multi_tile_layout(tp);
+}
+
 hipError_t multi_select_impl(
     const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
     const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
@@ -1731,6 +1807,11 @@ hipError_t multi_select_impl(
   m.qrow = g.E + RD;
   const int64_t queries = g.B * g.Tq;
   if (queries == 0) return hipSuccess;
+  if (multi_tile_path_enabled()) {
+    MultiTileParams tp{};
+    if (multi_tile_params(p, m, g, act, stat, positions, tp))
+      return multi_tile_launch(tp, stat, stream);
+  }
   const dim3 block(p.W * kWave);
   const dim3 grid(static_cast<unsigned>(g.B * p.tiles));
   const size_t lds = static_cast<size_t>(p.lds_total);
