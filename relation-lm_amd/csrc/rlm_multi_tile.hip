@@ -46,7 +46,7 @@ namespace rlm {
 namespace {
 
 constexpr int kMQ = 16;          // queries per workgroup
-constexpr int kMWaves = 8;       // waves per workgroup: wave w owns queries w and w + 8
+constexpr int kMWaves = 16;      // waves per workgroup: wave w owns query w
 constexpr int kMThreads = kMWaves * kWave;
 constexpr int kMStatRow = 68;    // floats per staged statistics row (64 + 4)
 constexpr int kMQRow = 66;       // doubles per staged query row (64 + 2)
@@ -216,27 +216,30 @@ __device__ void block_picks(const MultiTileParams& p, const MLds& L, int qi, int
   uint64_t* row = L.blk + qi * p.NB;
   {
     // Lane j: block j's heads, summed pairwise (((h0 + h1) + (h2 + h3)) + ...),
-    // the order of a lane-group tree reduction over the heads.
+    // the order of a lane-group tree reduction over the heads.  One exp at a
+    // time: s0..s2 hold the pending left halves of the tree (H a power of two).
     const int j = lane;
     const bool live = j < p.NB;
-    double v[kMultiTileMaxHeads], e[kMultiTileMaxHeads];
+    const double* shj = L.sh + qi * p.NB + (live ? j : 0);
     double m = -INFINITY;
-#pragma unroll
-    for (int h = 0; h < kMultiTileMaxHeads; ++h) {
-      v[h] = h < p.H && live ? L.sh[(h * kMQ + qi) * p.NB + j] : 0.0;
-      if (h < p.H) m = fmax(m, v[h]);
-    }
-#pragma unroll
-    for (int h = 0; h < kMultiTileMaxHeads; ++h) e[h] = h < p.H ? exp(v[h] - m) : 0.0;
-    double sum;
-    if (p.H == 1) {
-      sum = e[0];
-    } else if (p.H == 2) {
-      sum = e[0] + e[1];
-    } else if (p.H == 4) {
-      sum = (e[0] + e[1]) + (e[2] + e[3]);
-    } else {
-      sum = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+    for (int h = 0; h < p.H; ++h) m = fmax(m, shj[h * kMQ * p.NB]);
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, sum = 0.0;
+#pragma unroll 1
+    for (int h = 0; h < p.H; ++h) {
+      double x = exp(shj[h * kMQ * p.NB] - m);
+      if (h & 1) {
+        x = s0 + x;
+        if (h & 2) {
+          x = s1 + x;
+          if (h & 4) x = s2 + x;
+          else s2 = x;
+        } else {
+          s1 = x;
+        }
+      } else {
+        s0 = x;
+      }
+      sum = x;
     }
     if (live) {
       const double lse = m + log(sum);
@@ -305,7 +308,7 @@ __device__ __forceinline__ uint64_t member_key(const MultiTileParams& p, const M
 #pragma unroll
   for (int ch = 0; ch < 2; ++ch) kv[ch] = buf_load_b128(keys, base + 16u * (2 * sub + ch));
   double acc[4] = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll
+#pragma unroll 1
   for (int ch = 0; ch < 2; ++ch) {
     const int chunk = 2 * sub + ch;
     const uint32_t w[4] = {kv[ch].x, kv[ch].y, kv[ch].z, kv[ch].w};
@@ -372,35 +375,25 @@ __device__ int exact_select(const MultiTileParams& p, const MLds& L, int qi, int
   for (int x = 0; x < kMultiTileMaxSlots; ++x) excl[x] = x < nex ? R.taken[x] : -1;
   const int K = ANCHOR ? 1 : p.K;
   const float* sc = L.sc + qi * sc_row(p.CAP);
-  // The lane's candidates lane + 64 i: every LDS read (score, pick) issued
-  // first, then validity, exclusion and the lane maximum without branches.
-  float scv[kMNCL];
-  int pkv[kMNCL];
-#pragma unroll
-  for (int i = 0; i < kMNCL; ++i) {
-    if (kWave * i >= p.CAP) break;  // uniform
-    const int c = lane + kWave * i;
-    const bool in = c < p.CAP;
-    scv[i] = sc[in ? c : 0];
-    pkv[i] = R.pick[in && c >= p.L ? (c - p.L) >> p.BS_log2 : 0];
-  }
-  uint32_t vmask = 0;
-  float lm = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < kMNCL; ++i) {
-    if (kWave * i >= p.CAP) break;  // uniform
-    const int c = lane + kWave * i;
+  // Candidate lane c: valid, not excluded, and its approximate score.  The
+  // passes below stream over the lanes (nothing per candidate is held).
+  auto candidate_score = [&](int c, bool& v) {
     const bool local = c < p.L;
-    const int pos = local ? t - p.L + 1 + c : pkv[i] * p.BS + ((c - p.L) & (p.BS - 1));
-    bool v = c < p.CAP && pos <= t && pos < p.T &&
-             (local ? pos >= 0 : (pkv[i] >= 0 && pos < ls));
+    const int pk = R.pick[!local && c < p.CAP ? (c - p.L) >> p.BS_log2 : 0];
+    const int pos = local ? t - p.L + 1 + c : pk * p.BS + ((c - p.L) & (p.BS - 1));
+    v = c < p.CAP && pos <= t && pos < p.T && (local ? pos >= 0 : (pk >= 0 && pos < ls));
 #pragma unroll
     for (int x = 0; x < kMultiTileMaxSlots; ++x) {
       if (x >= nex) break;  // uniform
       v = v && pos != excl[x];
     }
-    lm = v ? fmaxf(lm, scv[i]) : lm;
-    vmask |= v ? 1u << i : 0u;
+    return sc[c < p.CAP ? c : p.CAP];
+  };
+  float lm = -INFINITY;
+  for (int c0 = 0; c0 < p.CAP; c0 += kWave) {
+    bool v;
+    const float x = candidate_score(c0 + lane, v);
+    lm = v ? fmaxf(lm, x) : lm;
   }
   // theta: a lower bound of the k-th largest approximate score.
   float theta;
@@ -421,25 +414,31 @@ __device__ int exact_select(const MultiTileParams& p, const MLds& L, int qi, int
   }
   const float eps = kErrScale * qn1 * kmax;
   const float thr = theta - (2.0f * eps + kErrAbs);
-  uint32_t mask = 0;
-#pragma unroll
-  for (int i = 0; i < kMNCL; ++i) {
-    if (kWave * i >= p.CAP) break;  // uniform
-    mask |= ((vmask >> i) & 1u) && scv[i] > -INFINITY && scv[i] >= thr ? 1u << i : 0u;
-  }
-  int mi[kMNCL];
-  const int members = number_members<kMNCL>(mask, mi);
+  // Members (valid candidates with s~ >= thr) numbered in candidate order;
+  // those of window [lo, lo + 64) go to the list (others to its trash entry).
   uint64_t* list = L.list + qi * kMListRow;
+  auto list_members = [&](int lo) {
+    int n = 0;
+    for (int c0 = 0; c0 < p.CAP; c0 += kWave) {
+      bool v;
+      const float x = candidate_score(c0 + lane, v);
+      const bool mem = v && x > -INFINITY && x >= thr;
+      const uint64_t bal = __builtin_amdgcn_ballot_w64(mem);
+      const int mi = n + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                             static_cast<uint32_t>(bal >> 32),
+                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u)));
+      list[mem && mi >= lo && mi < lo + kMListCap ? mi - lo : kMListCap] =
+          static_cast<uint64_t>(c0 + lane);
+      n += __builtin_popcountll(bal);
+    }
+    return n;
+  };
+  const int members = list_members(0);
   const int sub = lane & 3;
   int anchor = -1;
 
   if (members <= 16) {
     // Every member scored in one pass (4 lanes each), ranked, emitted.
-#pragma unroll
-    for (int i = 0; i < kMNCL; ++i) {
-      if (kWave * i >= p.CAP) break;  // uniform
-      list[(mask >> i) & 1u ? mi[i] : kMListCap] = static_cast<uint64_t>(lane + kWave * i);
-    }
     wave_sync();
     {
       const int m = lane >> 2;
@@ -454,7 +453,7 @@ __device__ int exact_select(const MultiTileParams& p, const MLds& L, int qi, int
     if (lane < members) {
       ke = list[lane];
       rank = 0;
-#pragma unroll
+#pragma unroll 2
       for (int f = 0; f < 16; f += 2) {
         const uint4 kk = *reinterpret_cast<const uint4*>(list + f);
         const uint64_t k0 = (static_cast<uint64_t>(kk.y) << 32) | kk.x;
@@ -477,12 +476,7 @@ __device__ int exact_select(const MultiTileParams& p, const MLds& L, int qi, int
   for (int w = 0; w < nwin; ++w) {
     const int lo = w * kMListCap;
     const int nw = min(members - lo, kMListCap);
-#pragma unroll
-    for (int i = 0; i < kMNCL; ++i) {
-      if (kWave * i >= p.CAP) break;  // uniform
-      const bool put = ((mask >> i) & 1u) && mi[i] >= lo && mi[i] < lo + kMListCap;
-      list[put ? mi[i] - lo : kMListCap] = static_cast<uint64_t>(lane + kWave * i);
-    }
+    if (w > 0) list_members(lo);  // window 0 is in the list already
     wave_sync();
     for (int m0 = 0; m0 < nw; m0 += 16) {
       const int m = m0 + (lane >> 2);
@@ -560,7 +554,7 @@ __device__ uint32_t score_tiles(const MultiTileParams& p, const MLds& L, rsrc_t 
   const int ntiles = (u.hi + 16) >> 4;
   // kTB tiles per round: every key load of the round is issued before the
   // first product (a tile outside the union reads nothing and files nothing).
-  constexpr int kTB = 4;
+  constexpr int kTB = 2;
   for (int t0 = wave; t0 < ntiles; t0 += kMWaves * kTB) {
     uint4 b0[kTB], b1[kTB];
     bool rel[kTB];
