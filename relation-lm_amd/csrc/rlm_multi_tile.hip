@@ -390,10 +390,12 @@ __device__ int exact_select(const MultiTileParams& p, const MLds& L, int qi, int
     return sc[c < p.CAP ? c : p.CAP];
   };
   float lm = -INFINITY;
-  for (int c0 = 0; c0 < p.CAP; c0 += kWave) {
+  uint32_t vmask = 0;  // bit i: candidate lane + 64 i is valid
+  for (int c0 = 0, i = 0; c0 < p.CAP; c0 += kWave, ++i) {
     bool v;
     const float x = candidate_score(c0 + lane, v);
     lm = v ? fmaxf(lm, x) : lm;
+    vmask |= v ? 1u << i : 0u;
   }
   // theta: a lower bound of the k-th largest approximate score.
   float theta;
@@ -419,10 +421,10 @@ __device__ int exact_select(const MultiTileParams& p, const MLds& L, int qi, int
   uint64_t* list = L.list + qi * kMListRow;
   auto list_members = [&](int lo) {
     int n = 0;
-    for (int c0 = 0; c0 < p.CAP; c0 += kWave) {
-      bool v;
-      const float x = candidate_score(c0 + lane, v);
-      const bool mem = v && x > -INFINITY && x >= thr;
+    for (int c0 = 0, i = 0; c0 < p.CAP; c0 += kWave, ++i) {
+      const int c = c0 + lane;
+      const float x = sc[c < p.CAP ? c : p.CAP];
+      const bool mem = ((vmask >> i) & 1u) && x > -INFINITY && x >= thr;
       const uint64_t bal = __builtin_amdgcn_ballot_w64(mem);
       const int mi = n + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
                              static_cast<uint32_t>(bal >> 32),
