@@ -56,6 +56,7 @@ struct HiddenParams {
   float* out;             // [rows, H]
   // Byte sizes of the buffers addressed through range-checked descriptors.
   uint32_t expanded_bytes, operand_bytes, wm_bytes, out_bytes;
+  int out_bf16;           // hidden stored as bf16 (round to nearest even), else fp32
 };
 
 
@@ -273,15 +274,21 @@ __device__ __forceinline__ void gather_bases(const HiddenParams& p, rsrc_t xr, c
 }
 
 // GELU(acc + bases) for the lane's four rows of column n; rows past the end
-// fall outside the output descriptor and are dropped.
+// fall outside the output descriptor and are dropped.  A bf16 output holds
+// the value a bf16 consumer would round the fp32 one to (the same conversion).
 __device__ __forceinline__ void store_hidden(const HiddenParams& p, rsrc_t outr, const f32x4& acc,
                                              const float (&xs)[4], int64_t r0, int mrow, int n,
                                              int lane) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const uint32_t grow = static_cast<uint32_t>(r0 + mrow + (lane >> 4) * 4 + e);
-    const uint32_t off = n < p.H ? (grow * static_cast<uint32_t>(p.H) + n) * 4u : kNoOffset;
-    buf_store_f32(gelu_erf(acc[e] + xs[e]), outr, off);
+    const uint32_t idx = grow * static_cast<uint32_t>(p.H) + n;
+    const float v = gelu_erf(acc[e] + xs[e]);
+    if (p.out_bf16)  // uniform
+      __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(pack_bf16x2(v, 0.0f)), outr,
+                                            n < p.H ? idx * 2u : kNoOffset, 0, 0);
+    else
+      buf_store_f32(v, outr, n < p.H ? idx * 4u : kNoOffset);
   }
 }
 
@@ -1138,7 +1145,7 @@ hipError_t hidden_impl(bool seq, const rlm_tensor* expanded_cache,
                   (reinterpret_cast<uintptr_t>(product_weight->data) & 15u) == 0,
               "operand_cache and product_weight must be 16-byte aligned");
   RLM_TRY(check_tensor(out, "out", qd + 2));
-  RLM_TRY(check_dtype_is(out, "out", RLM_F32));
+  RLM_REQUIRE(out->dtype == RLM_F32 || out->dtype == RLM_BF16, "out must be float32 or bfloat16");
   RLM_TRY(check_dim(out, "out", 0, B));
   if (seq) RLM_TRY(check_dim(out, "out", 1, Tq));
   RLM_TRY(check_dim(out, "out", qd, K));
@@ -1159,12 +1166,14 @@ hipError_t hidden_impl(bool seq, const rlm_tensor* expanded_cache,
   p.index_dtype_p = partner_index->dtype;
   p.wm = product_weight->data;
   p.out = static_cast<float*>(out->data);
-  RLM_REQUIRE(p.rows * H * 4 + 64 * H * 4 < kMaxBytes,
+  p.out_bf16 = out->dtype == RLM_BF16 ? 1 : 0;
+  const int64_t os = p.out_bf16 ? 2 : 4;
+  RLM_REQUIRE(p.rows * H * os + 64 * H * 4 < kMaxBytes,
               "relation hidden output must be smaller than 2 GiB");
   p.expanded_bytes = static_cast<uint32_t>(B * T * 2 * H * es);
   p.operand_bytes = static_cast<uint32_t>(B * T * R * es);
   p.wm_bytes = static_cast<uint32_t>(H * R * es);
-  p.out_bytes = static_cast<uint32_t>(p.rows * H * 4);
+  p.out_bytes = static_cast<uint32_t>(p.rows * H * os);
   return hipSuccess;
 }
 

@@ -325,6 +325,25 @@ at::Tensor relation_hidden_cached_seq(const at::Tensor& expanded_cache,
                        product_weight);
 }
 
+// relation_hidden_cached_seq into a caller's [B,Tq,K,H] tensor, fp32 or bf16
+// (bf16: the value a bf16 consumer rounds the fp32 hidden to).  No reference
+// counterpart: the multi-anchor relation MLP feeds it to a bf16 Linear.
+void relation_hidden_cached_seq_out(const at::Tensor& expanded_cache,
+                                    const at::Tensor& operand_cache,
+                                    const at::Tensor& anchor_index,
+                                    const at::Tensor& partner_index,
+                                    const at::Tensor& product_weight, at::Tensor& out) {
+  const char* op = "relation_lm::relation_hidden_cached_seq_out";
+  c10::DeviceGuard guard(operand_cache.device());
+  hipStream_t stream = device_stream(
+      op, {&operand_cache, &expanded_cache, &anchor_index, &partner_index, &product_weight, &out});
+  TORCH_CHECK(out.is_contiguous(), op, ": out must be contiguous");
+  rlm_tensor d[6] = {desc(expanded_cache, "expanded_cache"), desc(operand_cache, "operand_cache"),
+                     desc(anchor_index, "anchor_index"),     desc(partner_index, "partner_index"),
+                     desc(product_weight, "product_weight"), desc(out, "out")};
+  check(rlm_relation_hidden_cached_seq(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], stream), op);
+}
+
 at::Tensor hidden_update_common(bool ring, at::Tensor& expanded_cache,
                                 const at::Tensor& operand_cache, const at::Tensor& anchor_index,
                                 const at::Tensor& partner_index, const at::Tensor& anchor_weight,
@@ -905,6 +924,9 @@ TORCH_LIBRARY(relation_lm, m) {
       "out_dtype=None) -> Tensor");
   m.def(
       "relation_linear_out(Tensor input, Tensor weight, Tensor? bias, Tensor(a!) out) -> ()");
+  m.def(
+      "relation_hidden_cached_seq_out(Tensor expanded_cache, Tensor operand_cache, Tensor "
+      "anchor_index, Tensor partner_index, Tensor product_weight, Tensor(a!) out) -> ()");
   // Multi-anchor relation block (no reference op: the reference runs these in
   // eager torch inside MultiAnchorRelationBlock / DistilledBlockRouter).
   m.def(
@@ -958,6 +980,7 @@ TORCH_LIBRARY_IMPL(relation_lm, CUDA, m) {
   m.impl("relation_linear_norm_reduce_output", TORCH_FN(relation_linear_norm_reduce_output));
   m.impl("relation_linear", TORCH_FN(relation_linear));
   m.impl("relation_linear_out", TORCH_FN(relation_linear_out));
+  m.impl("relation_hidden_cached_seq_out", TORCH_FN(relation_hidden_cached_seq_out));
   m.impl("multi_relation_reduce_seq", TORCH_FN(multi_relation_reduce_seq));
   m.impl("layer_norm", TORCH_FN(layer_norm));
   m.impl("relation_norm_reduce_output", TORCH_FN(relation_norm_reduce_output));

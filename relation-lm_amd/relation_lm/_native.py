@@ -124,6 +124,10 @@ def _register_fakes() -> None:
     def _(input, weight, bias, out):
         return None
 
+    @torch.library.register_fake("relation_lm::relation_hidden_cached_seq_out")
+    def _(expanded_cache, operand_cache, anchor_index, partner_index, product_weight, out):
+        return None
+
     @torch.library.register_fake("relation_lm::multi_relation_reduce_seq")
     def _(raw, partner_scores, norm_weight, norm_bias, slot_mix_logits, residual_gate, hidden,
           positions, norm_eps):

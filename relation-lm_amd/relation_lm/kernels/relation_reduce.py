@@ -99,6 +99,21 @@ def relation_hidden_cached_seq(
         expanded_cache, operand_cache, anchor_index, partner_index, product_weight)
 
 
+def relation_hidden_cached_seq_out(
+    expanded_cache: Tensor,
+    operand_cache: Tensor,
+    anchor_index: Tensor,
+    partner_index: Tensor,
+    product_weight: Tensor,
+    out: Tensor,
+) -> None:
+    """relation_hidden_cached_seq into ``out`` [B,Tq,K,H], fp32 or bf16.  A bf16
+    ``out`` holds each value rounded to nearest even -- the operand a bf16 Linear
+    rounds the fp32 hidden to, so the Linear's result is the same either way."""
+    torch.ops.relation_lm.relation_hidden_cached_seq_out(
+        expanded_cache, operand_cache, anchor_index, partner_index, product_weight, out)
+
+
 def relation_hidden_cache_update(
     expanded_cache: Tensor,
     operand_cache: Tensor,

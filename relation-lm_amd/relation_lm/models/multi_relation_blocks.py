@@ -11,8 +11,9 @@ multi-anchor selection (local window plus the top blocks of a block router,
   projections of hidden / memory  relation_lm::relation_linear (MFMA)
   router block statistics         relation_lm::block_statistics
   distinct anchors, partners      relation_lm::multi_relation_select_seq
-  relation MLP Linear -> GELU     relation_lm::relation_hidden_cached_seq
-    (factorized: operand cache, expanded cache = [W_a+W_d; W_p-W_d] op + [b; 0])
+  relation MLP Linear -> GELU     relation_lm::relation_hidden_cached_seq_out
+    (factorized: operand cache, expanded cache = [W_a+W_d; W_p-W_d] op + [b; 0];
+    stored in bf16 when the second Linear is bf16)
   relation MLP second Linear      relation_lm::relation_linear
   LayerNorm, partner softmax,     relation_lm::multi_relation_reduce_seq
     slot mix, residual gate
@@ -198,13 +199,20 @@ class MultiAnchorRelationBlock(nn.Module):
         h, k_count = cfg.anchors_per_block, cfg.partners_per_anchor
         mlp = self.relation_mlp
         outputs = []
-        # One batch row at a time: the [T*S, K, hidden] fp32 MLP hidden of a row
-        # stays below the 2 GiB a kernel addresses.
+        # The MLP hidden in the second Linear's operand dtype: a bf16 Linear
+        # rounds an fp32 hidden to bf16 before its products, so storing bf16
+        # gives the same result at half the bytes.  One batch row at a time:
+        # the [T*S, K, hidden] hidden of a row stays below the 2 GiB a kernel
+        # addresses.
+        hid_dtype = torch.bfloat16 if mlp[2].weight.dtype == torch.bfloat16 else torch.float32
+        rows = torch.empty((1, length * h, k_count, mlp[2].weight.shape[1]), dtype=hid_dtype,
+                           device=hidden.device)
         for b in range(batch):
-            rows = ops.relation_hidden_cached_seq(
+            ops.relation_hidden_cached_seq_out(
                 sel["expanded_cache"][b:b + 1], sel["operand_cache"][b:b + 1],
                 sel["anchor"][b:b + 1].reshape(1, length * h),
-                sel["partner"][b:b + 1].reshape(1, length * h, k_count), sel["product_weight"])
+                sel["partner"][b:b + 1].reshape(1, length * h, k_count), sel["product_weight"],
+                rows)
             raw = ops.relation_linear(rows, mlp[2].weight, mlp[2].bias, torch.float32)
             outputs.append(ops.multi_relation_reduce_seq(
                 raw.view(1, length, h, k_count, d), sel["partner_score"][b:b + 1], mlp[3].weight,

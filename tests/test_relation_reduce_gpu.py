@@ -480,3 +480,33 @@ def test_linear_out_into_cache_column(device, dtype, batch):
     keep = torch.ones(64, dtype=torch.bool)
     keep[t] = False
     assert torch.equal(cache[:, keep], before[:, keep])
+
+
+@pytest.mark.parametrize("hidden_dim,relation_dim", [(3072, 128), (512, 64)])
+def test_hidden_seq_out_bf16_feeds_the_linear_unchanged(device, hidden_dim, relation_dim):
+    """relation_hidden_cached_seq_out with a bf16 out: every element is the fp32
+    hidden rounded to nearest even, so a bf16 second Linear (which rounds its
+    fp32 input the same way before the products) gives bit-identical raw rows
+    from either hidden -- the multi-anchor relation MLP stores bf16."""
+    from relation_lm.kernels.relation_reduce import relation_hidden_cached_seq_out
+    g = torch.Generator().manual_seed(hidden_dim)
+    b, t, k = 1, 256, 6
+    operand = torch.randn(b, t, relation_dim, generator=g).to(device, torch.bfloat16)
+    expanded = torch.randn(b, t, 2 * hidden_dim, generator=g).to(device, torch.bfloat16)
+    wm = (torch.randn(hidden_dim, relation_dim, generator=g) * relation_dim ** -0.5).to(
+        device, torch.bfloat16)
+    a = torch.randint(0, t, (b, 4 * t), generator=g).to(device)
+    p = torch.randint(0, t, (b, 4 * t, k), generator=g).to(device)
+    w2 = (torch.randn(768, hidden_dim, generator=g) * hidden_dim ** -0.5).to(device, torch.bfloat16)
+    b2 = torch.randn(768, generator=g).to(device, torch.bfloat16)
+    h32 = relation_hidden_cached_seq(expanded, operand, a, p, wm)
+    h16 = torch.empty(h32.shape, dtype=torch.bfloat16, device=device)
+    relation_hidden_cached_seq_out(expanded, operand, a, p, wm, h16)
+    h32b = torch.empty_like(h32)
+    relation_hidden_cached_seq_out(expanded, operand, a, p, wm, h32b)
+    raw32 = relation_linear(h32, w2, b2, out_dtype=torch.float32)
+    raw16 = relation_linear(h16, w2, b2, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(h32b, h32)
+    assert torch.equal(h16, h32.to(torch.bfloat16))
+    assert torch.equal(raw16, raw32)
