@@ -52,7 +52,6 @@ constexpr int kMStatRow = 68;    // floats per staged statistics row (64 + 4)
 constexpr int kMQRow = 66;       // doubles per staged query row (64 + 2)
 constexpr int kMListCap = 64;    // members per query per window
 constexpr int kMListRow = kMListCap + 2;  // + a trash entry (branch-free stores), 16-byte rows
-constexpr int kMNCL = kMultiTileMaxCap / kWave;  // candidate lanes per lane
 constexpr int kKeyRow = 128;     // bytes of one slot vector (64 bf16)
 
 // Per-query record of the current routing.
