@@ -257,8 +257,9 @@ hipError_t rlm_relation_norm_reduce_output(
 
 /*
  * The decode step's second linear and norm-reduce with the output-head
- * preparation (the reference's roadmap item "fold norm-reduce into the second
- * linear", README.md:148-151; no reference op): the same result as
+ * preparation (no reference op: the reference calls F.linear then
+ * relation_norm_reduce, benchmarks/benchmark_relation_reduce.py:80-81; the
+ * output-head preparation is its roadmap item 3, README.md:151): the same result as
  *   raw = hidden @ second_weight^T + second_bias   (rlm_linear)
  *   rlm_relation_norm_reduce_output(raw, ...)
  * within fp32 rounding (the reduction is summed in a different order).  The
@@ -276,6 +277,25 @@ hipError_t rlm_relation_linear_norm_reduce_output(
     const rlm_tensor* norm_bias, const rlm_tensor* position, double norm_eps,
     const rlm_tensor* query, const rlm_tensor* mix_logit, const rlm_tensor* output_weight,
     const rlm_tensor* output_bias, double output_eps, const rlm_tensor* partials,
+    const rlm_tensor* out_context, const rlm_tensor* out_final, hipStream_t stream);
+
+/*
+ * rlm_relation_linear_norm_reduce_output without the `partials` workspace,
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc); no counterpart in
+ * the reference.  The partials live in a static per-GPU device array of
+ * 4 x 64 x 1024 fp32 (1 MiB): splits * B*K * D must not exceed that, or the
+ * call fails with hipErrorInvalidValue.  `splits` (1..4) is the S of the
+ * workspace form; the result equals that form's with the same S.  Allocates
+ * nothing; call with the stream's device current.  Calls that overlap on one
+ * GPU share the array and race.
+ */
+hipError_t rlm_relation_linear_norm_reduce_output_noalloc(
+    const rlm_tensor* hidden, const rlm_tensor* second_weight, const rlm_tensor* second_bias,
+    const rlm_tensor* partner_scores, const rlm_tensor* norm_weight,
+    const rlm_tensor* norm_bias, const rlm_tensor* position, double norm_eps,
+    const rlm_tensor* query, const rlm_tensor* mix_logit, const rlm_tensor* output_weight,
+    const rlm_tensor* output_bias, double output_eps, int32_t splits,
     const rlm_tensor* out_context, const rlm_tensor* out_final, hipStream_t stream);
 
 /*

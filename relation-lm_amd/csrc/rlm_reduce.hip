@@ -20,6 +20,8 @@
 // norm_reduce_kernel: one wavefront per query; each lane owns D/64 columns,
 //   LayerNorm moments are wave64 reductions, the K softmax weights live in
 //   lanes 0..K-1 and are broadcast by shuffles.
+#include <mutex>
+
 #include "rlm_common.hpp"
 
 namespace rlm {
@@ -1639,4 +1641,89 @@ extern "C" hipError_t rlm_relation_norm_reduce_seq(const rlm_tensor* raw,
                                                    const rlm_tensor* out, hipStream_t stream) {
   return norm_impl(true, raw, partner_scores, norm_weight, norm_bias, positions, norm_eps, out,
                    stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free form of rlm_relation_linear_norm_reduce_output.  The split-K
+// partials live in `scratch`, a file-scope device array (one copy per GPU, held
+// until the process ends) of at most 4 splits x 64 rows x 1024 columns fp32
+// (1 MiB).  Host code never passes the array's name to a kernel: its device
+// address is taken once per device with hipGetSymbolAddress and kept.  Every
+// partial the norm kernel reads is written by the linear first, so nothing is
+// cleared.  Calls that overlap on one GPU share the array and race.
+// ---------------------------------------------------------------------------
+
+constexpr int64_t kScratchFloats = int64_t(4) * 64 * 1024;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+namespace {
+constexpr int kScratchMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kScratchMaxDevices] = {};
+
+// The current device's copy of `scratch` (its address taken on first use).
+hipError_t scratch_for_current_device(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    rlm::set_error("relation_linear_norm_reduce (no-alloc): hipGetDevice failed: %s",
+                   hipGetErrorString(e));
+    return e;
+  }
+  if (dev < 0 || dev >= kScratchMaxDevices) {
+    rlm::set_error("relation_linear_norm_reduce (no-alloc): device %d beyond the %d supported",
+                   dev, kScratchMaxDevices);
+    return hipErrorInvalidDevice;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      rlm::set_error("relation_linear_norm_reduce (no-alloc): hipGetSymbolAddress failed: %s",
+                     hipGetErrorString(e));
+      return e != hipSuccess ? e : hipErrorInvalidSymbol;
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+}  // namespace
+
+extern "C" hipError_t rlm_relation_linear_norm_reduce_output_noalloc(
+    const rlm_tensor* hidden, const rlm_tensor* second_weight, const rlm_tensor* second_bias,
+    const rlm_tensor* partner_scores, const rlm_tensor* norm_weight, const rlm_tensor* norm_bias,
+    const rlm_tensor* position, double norm_eps, const rlm_tensor* query,
+    const rlm_tensor* mix_logit, const rlm_tensor* output_weight, const rlm_tensor* output_bias,
+    double output_eps, int32_t splits, const rlm_tensor* out_context, const rlm_tensor* out_final,
+    hipStream_t stream) {
+  clear_error();
+  RLM_TRY(check_tensor(hidden, "hidden", 3));
+  RLM_TRY(check_tensor(second_weight, "second_weight", 2));
+  const int64_t rows = hidden->shape[0] * hidden->shape[1];
+  const int64_t D = second_weight->shape[0];
+  RLM_REQUIRE(splits >= 1 && splits <= 4, "relation_linear_norm_reduce (no-alloc): splits must "
+              "be in [1, 4], got %d", splits);
+  RLM_REQUIRE(static_cast<int64_t>(splits) * rows * D <= kScratchFloats,
+              "relation_linear_norm_reduce (no-alloc): %d splits x %lld rows x %lld columns "
+              "exceed the static workspace of %lld fp32 values",
+              splits, (long long)rows, (long long)D, (long long)kScratchFloats);
+  float* ws = nullptr;
+  const hipError_t e = scratch_for_current_device(&ws);
+  if (e != hipSuccess) return e;
+  rlm_tensor part{};
+  part.data = ws;
+  part.dtype = RLM_F32;
+  part.ndim = 3;
+  part.shape[0] = splits;
+  part.shape[1] = rows;
+  part.shape[2] = D;
+  part.stride[2] = 1;
+  part.stride[1] = D;
+  part.stride[0] = rows * D;
+  return rlm_relation_linear_norm_reduce_output(
+      hidden, second_weight, second_bias, partner_scores, norm_weight, norm_bias, position,
+      norm_eps, query, mix_logit, output_weight, output_bias, output_eps, &part, out_context,
+      out_final, stream);
 }
