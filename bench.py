@@ -57,7 +57,7 @@ KERNEL_SYMBOLS = {
     "relation_hidden": "hidden_bf16_kernel<",
     "second_linear": "tile_kernel<float, rlm::bf16, float",
     "norm_reduce": "norm_reduce_vec_kernel<",
-    "multi_anchor_select": "multi_select_kernel<",
+    "multi_anchor_select": "multi_tile_kernel<",
 }
 
 
@@ -119,9 +119,11 @@ def multi_select_bytes(cfg):
     return query_side + memory_side + outputs
 
 
-def multi_select_gathered_bytes(cfg):
-    """Key bytes the candidate passes read (each slot's vector of every candidate,
-    anchor and partner side): what the kernel streams from L2 per launch."""
+def multi_select_candidate_bytes(cfg):
+    """Key bytes of the candidate vectors the queries score (each slot's vector of
+    every candidate, anchor and partner side).  A per-query kernel streams all of
+    them; the tile kernel reads each 16-row tile once for the 16 queries of a
+    workgroup, so this is an effective figure, not its traffic."""
     cap = cfg.local_window + cfg.top_blocks * cfg.block_size
     return cfg.batch * cfg.context * 2 * cfg.slots * cap * cfg.exact_dim * 2
 
@@ -303,7 +305,7 @@ def main() -> int:
         torch.cuda.synchronize()
         us = start.elapsed_time(end) * 1e3 / repeats
         nbytes = multi_select_bytes(mcfg)
-        gathered = multi_select_gathered_bytes(mcfg)
+        scored = multi_select_candidate_bytes(mcfg)
         return {
             "workload": "cfg5 one layer: B=4 T=4096 4 anchor slots x K=6, block 64, local 128, "
                         "top 8, bf16, every position a query",
@@ -311,8 +313,8 @@ def main() -> int:
             "queries_per_s": round(mcfg.queries / (us * 1e-6), 1),
             "algorithmic_bytes": nbytes,
             "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "gathered_key_bytes": gathered,
-            "gathered_GBps": round(gathered / (us * 1e-6) / 1e9, 1),
+            "candidate_vector_bytes": scored,
+            "candidate_vector_GBps_effective": round(scored / (us * 1e-6) / 1e9, 1),
             "stack": run_stack(mcfg),
         }
 
