@@ -60,11 +60,13 @@ constexpr int kQRow = 66;       // doubles per staged query row (64 + 2)
 constexpr int kListCap = 64;    // members per query per window
 constexpr int kMaxNCL = 4;      // candidates per lane (CAP <= 256)
 
-// Per-query record in LDS.
+// Per-query record in LDS: the position and the candidate table, entry 0 the
+// local window, entry 1 + r the block of pick r, each (first position,
+// position limit): a candidate at offset o of an entry is position x + o,
+// valid when 0 <= x + o < limit (and inside the cache).
 struct QRec {
   int t, pad0, pad1, pad2;
-  int sel[kTileMaxTop];
-  int selv[kTileMaxTop];
+  int2 ent[1 + kTileMaxTop];
 };
 
 struct Lds {
@@ -77,6 +79,7 @@ struct Lds {
   uint64_t* blk;        // [16][NB]: block selection keys
   uint64_t* list;       // [16][kListCap]
   uint64_t* top;        // [2][16][kTileMaxK]
+  uint16_t* frag;       // [hi, lo][16][64] bf16 partner query (aliases `top`)
   QRec* qr;             // [16]
   double* bias;         // [2 sides][H*RB]
   double* sp;           // [2 sides][16]
@@ -94,6 +97,7 @@ __device__ __forceinline__ Lds carve(const TileParams& p, unsigned char* smem) {
   s.sh = reinterpret_cast<double*>(smem + p.off_list);
   s.blk = reinterpret_cast<uint64_t*>(smem + p.off_blk);
   s.top = reinterpret_cast<uint64_t*>(smem + p.off_top);
+  s.frag = reinterpret_cast<uint16_t*>(smem + p.off_top);
   s.qr = reinterpret_cast<QRec*>(smem + p.off_qrec);
   s.bias = reinterpret_cast<double*>(smem + p.off_bias);
   s.sp = reinterpret_cast<double*>(smem + p.off_sp);
@@ -105,52 +109,112 @@ __device__ __forceinline__ int key_chunk_offset(int row, int ch) {
   return row * kRowBytes + 16 * (ch ^ ((row >> 1) & 7));
 }
 
-// Both streams' block statistics (mean and std, NB*64 <= 4096 elements each)
-// into LDS as fp32 rows of kStatRow: thread tid < NB*8 moves 8 consecutive
-// elements of each tensor.
+// Element e of query row r in the partner fragment table (16-byte chunks
+// XOR-swizzled by row, so that the fragment reads of 16 rows do not conflict).
+// The table lives in the running top-k lists, which are dead from the anchor's
+// last use of them until the partner side's block picks.
+__device__ __forceinline__ int frag_offset(int r, int e) {
+  return r * 64 + 8 * ((e >> 3) ^ (r & 7)) + (e & 7);
+}
+static_assert(2 * kQ * 64 * 2 <= 2 * kQ * kTileMaxK * 8, "fragment table exceeds the top-k lists");
+
+// Both streams' block statistics (mean and std, NB*64 <= 4096 elements each),
+// staged as fp32 rows of kStatRow by every wave alike: wave w reads tensor
+// w & 3 (amean, astd, pmean, pstd), four elements per lane per round, rounds
+// of 256 groups of four.  The loads are issued first (issue_stats) and stored
+// once they are needed (put_stats), so no wave waits for them on its own.
 template <typename TS>
-__device__ void stage_stats(const TileParams& p, const Lds& L, int64_t b, int tid) {
-  const int per = p.NB * 64;
-  const void* const src_of[4] = {p.amean, p.astd, p.pmean, p.pstd};
-  const bool mine = 8 * tid < per;
-  const int e = mine ? 8 * tid : 0;
-  float v[4][8];
+struct StatGroup;
+template <>
+struct StatGroup<float> {
+  uint4 v[4];
+  __device__ __forceinline__ void issue(rsrc_t r, int u, uint32_t grp, bool live) {
+    v[u] = buf_load_b128(r, live ? grp * 16u : kNoOffset);
+  }
+  __device__ __forceinline__ float4 at(int u) const {
+    return make_float4(__uint_as_float(v[u].x), __uint_as_float(v[u].y), __uint_as_float(v[u].z),
+                       __uint_as_float(v[u].w));
+  }
+};
+template <>
+struct StatGroup<bf16> {
+  uint2 v[4];
+  __device__ __forceinline__ void issue(rsrc_t r, int u, uint32_t grp, bool live) {
+    v[u] = buf_load_b64(r, live ? grp * 8u : kNoOffset);
+  }
+  __device__ __forceinline__ float4 at(int u) const {
+    return make_float4(__uint_as_float(v[u].x << 16), __uint_as_float(v[u].x & 0xffff0000u),
+                       __uint_as_float(v[u].y << 16), __uint_as_float(v[u].y & 0xffff0000u));
+  }
+};
+
+template <typename TS>
+__device__ __forceinline__ void issue_stats(const TileParams& p, int64_t b, int wave, int lane,
+                                            StatGroup<TS>& g) {
+  const int w = wave & 3;
+  const void* src = w == 0 ? p.amean : w == 1 ? p.astd : w == 2 ? p.pmean : p.pstd;
+  const uint32_t groups = static_cast<uint32_t>(p.NB) * 16u;  // per batch row
+  const rsrc_t r = make_rsrc(static_cast<const TS*>(src) + b * p.NB * 64,
+                             groups * 4u * static_cast<uint32_t>(sizeof(TS)));
 #pragma unroll
-  for (int w = 0; w < 4; ++w)
-    load_stat8<TS>(static_cast<const TS*>(src_of[w]) + b * per + e, v[w]);
-  if (!mine) return;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    float* dst = L.stats + (w * p.NB + (e >> 6)) * kStatRow + (e & 63);
-    *reinterpret_cast<float4*>(dst) = make_float4(v[w][0], v[w][1], v[w][2], v[w][3]);
-    *reinterpret_cast<float4*>(dst + 4) = make_float4(v[w][4], v[w][5], v[w][6], v[w][7]);
+  for (int u = 0; u < 4; ++u) {
+    const uint32_t grp = static_cast<uint32_t>((wave >> 2) * kWave + lane + 256 * u);
+    if (256 * u < static_cast<int>(groups)) g.issue(r, u, grp, grp < groups);
   }
 }
 
-// Bias tables and softplus(gamma) of both streams into LDS (float64).
-__device__ void stage_router_consts(const TileParams& p, const Lds& L, int tid) {
-  // Every thread issues its loads (both dtype forms, out-of-range ones read 0)
-  // before decoding any: no load waits at a dtype branch.
+template <typename TS>
+__device__ __forceinline__ void put_stats(const TileParams& p, const Lds& L, int wave, int lane,
+                                          const StatGroup<TS>& g) {
+  const int w = wave & 3;
+  const int groups = p.NB * 16;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int grp = (wave >> 2) * kWave + lane + 256 * u;
+    if (256 * u < groups && grp < groups)
+      *reinterpret_cast<float4*>(L.stats + (w * p.NB + (grp >> 4)) * kStatRow + 4 * (grp & 15)) =
+          g.at(u);
+  }
+}
+
+// Router constants of both streams: thread i < 2 H*RB one relative-bias entry
+// (anchor table, then partner), the next 2 H threads one gamma each.  Issued
+// before any other load of the kernel (both dtype forms; out-of-range lanes
+// read 0), so that the decode and the softplus wait for these loads only and
+// run while the key rows are still in flight.
+struct RouterWords {
+  FloatWords ab, pb, ag, pg;
+};
+
+__device__ __forceinline__ void issue_router_consts(const TileParams& p, int tid, RouterWords& w) {
   const uint32_t n = static_cast<uint32_t>(p.H * p.RB);
+  const uint32_t H = static_cast<uint32_t>(p.H);
   const uint32_t i = static_cast<uint32_t>(tid);
-  const bool is_bias = i < 2 * n;
-  const uint32_t kb = i < n ? i : i - n;
-  const FloatWords ab = issue_float(p.abias, p.abias_dtype, n, kb, is_bias && i < n);
-  const FloatWords pb = issue_float(p.pbias, p.pbias_dtype, n, kb, is_bias && i >= n);
-  const uint32_t h = i < static_cast<uint32_t>(p.H) ? i : i - static_cast<uint32_t>(p.H);
-  const bool is_gamma = i < 2u * static_cast<uint32_t>(p.H);
-  const FloatWords ag = issue_float(p.agamma, p.agamma_dtype, static_cast<uint32_t>(p.H), h,
-                                    is_gamma && i < static_cast<uint32_t>(p.H));
-  const FloatWords pg = issue_float(p.pgamma, p.pgamma_dtype, static_cast<uint32_t>(p.H), h,
-                                    is_gamma && i >= static_cast<uint32_t>(p.H));
-  if (is_bias)
-    L.bias[i] = static_cast<double>(i < n ? decode_float(ab, p.abias_dtype)
-                                          : decode_float(pb, p.pbias_dtype));
-  if (is_gamma) {
+  if (i < 2 * n + 2 * H) {
+    const uint32_t kb = i < n ? i : i - n;
+    const uint32_t h = i - 2 * n < H ? i - 2 * n : i - 2 * n - H;
+    w.ab = issue_float(p.abias, p.abias_dtype, n, kb, i < n);
+    w.pb = issue_float(p.pbias, p.pbias_dtype, n, kb, i >= n && i < 2 * n);
+    w.ag = issue_float(p.agamma, p.agamma_dtype, H, h, i >= 2 * n && i < 2 * n + H);
+    w.pg = issue_float(p.pgamma, p.pgamma_dtype, H, h, i >= 2 * n + H);
+  }
+}
+
+// Bias tables (float64) and softplus(gamma) (float64) of both streams into LDS.
+__device__ __forceinline__ void put_router_consts(const TileParams& p, const Lds& L, int tid,
+                                                  const RouterWords& w) {
+  const uint32_t n = static_cast<uint32_t>(p.H * p.RB);
+  const uint32_t H = static_cast<uint32_t>(p.H);
+  const uint32_t i = static_cast<uint32_t>(tid);
+  if (i < 2 * n) {
+    L.bias[i] = static_cast<double>(i < n ? decode_float(w.ab, p.abias_dtype)
+                                          : decode_float(w.pb, p.pbias_dtype));
+  } else if (i < 2 * n + 2 * H) {
 #pragma clang fp contract(off)
-    const bool partner = i >= static_cast<uint32_t>(p.H);
-    const double g = static_cast<double>(partner ? decode_float(pg, p.pgamma_dtype)
-                                                 : decode_float(ag, p.agamma_dtype));
+    const bool partner = i >= 2 * n + H;
+    const uint32_t h = partner ? i - 2 * n - H : i - 2 * n;
+    const double g = static_cast<double>(partner ? decode_float(w.pg, p.pgamma_dtype)
+                                                 : decode_float(w.ag, p.agamma_dtype));
     L.sp[(partner ? 16 : 0) + h] = log(1.0 + exp(g));  // softplus without threshold, relation_select.py:87
   }
 }
@@ -172,10 +236,25 @@ __device__ void head_scores(const TileParams& p, const Lds& L, int side, int wav
     const int h = item / nbt;
     const int jt = item - h * nbt;
     const int j = jt * 16 + c16;
-    const int jc = j < p.NB ? j : 0;
+    const bool jv = j < p.NB;
+    const int jc = jv ? j : 0;
+    // The epilogue's operands first (query positions, then the bucket biases),
+    // so that their LDS round trips overlap the matrix-core chain.
+    const int end = (j + 1) * p.BS - 1;
+    double bv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = L.qr[4 * r + kq].t;
+      const int dist = (t > end ? t - end : 0) + 1;
+      int bucket = 31 - __clz(dist);
+      bucket = bucket < p.RB - 1 ? bucket : p.RB - 1;
+      bv[r] = bias[h * p.RB + bucket];
+    }
+    const double sph = sp[h];
     f64x4_t content = {0.0, 0.0, 0.0, 0.0}, unc = {0.0, 0.0, 0.0, 0.0};
     for (int ks0 = 0; ks0 < p.HD; ks0 += 16) {
-      // Up to four k-steps: every operand is read before the first MFMA.
+      // Four k-steps, every operand read before the first MFMA; k-steps past
+      // the head's HD dims (HD = 8) get zero B operands instead of a branch.
       double a[4];
       float bm[4], bs[4];
 #pragma unroll
@@ -187,28 +266,22 @@ __device__ void head_scores(const TileParams& p, const Lds& L, int side, int wav
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        if (ks0 + 4 * u >= p.HD) break;  // uniform
-        const double m = j < p.NB ? static_cast<double>(bm[u]) : 0.0;
-        const double sd = j < p.NB ? static_cast<double>(bs[u]) : 0.0;
+        const bool live = jv && ks0 + 4 * u < p.HD;
+        const double m = live ? static_cast<double>(bm[u]) : 0.0;
+        const double sd = live ? static_cast<double>(bs[u]) : 0.0;
         content = __builtin_amdgcn_mfma_f64_16x16x4f64(a[u], m, content, 0, 0, 0);
         unc = __builtin_amdgcn_mfma_f64_16x16x4f64(fabs(a[u]), sd, unc, 0, 0, 0);
       }
     }
-    const int end = (j + 1) * p.BS - 1;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int q = 4 * r + kq;
-      const int t = L.qr[q].t;
-      const int dist = (t > end ? t - end : 0) + 1;
-      int bucket = 31 - __clz(dist);
-      bucket = bucket < p.RB - 1 ? bucket : p.RB - 1;
       double v;
       {
 #pragma clang fp contract(off)
-        const double c = content[r] + sp[h] * unc[r];
-        v = c * p.head_scale + bias[h * p.RB + bucket];
+        const double c = content[r] + sph * unc[r];
+        v = c * p.head_scale + bv[r];
       }
-      if (j < p.NB) L.sh[(h * kQ + q) * p.NB + j] = v;
+      if (jv) L.sh[(h * kQ + 4 * r + kq) * p.NB + j] = v;
     }
   }
 }
@@ -237,10 +310,8 @@ __device__ void block_picks(const TileParams& p, const Lds& L, int qi, int lane,
       row[j] = select_key(eligible ? static_cast<float>(lse) : -INFINITY, static_cast<uint32_t>(j));
     }
   }
-  if (lane < p.TOP) {
-    R.sel[lane] = 0;
-    R.selv[lane] = 0;
-  }
+  if (lane < p.TOP) R.ent[1 + lane] = make_int2(0, 0);
+  if (lane == kWave - 1) R.ent[0] = make_int2(t - p.L + 1, t + 1);
   wave_sync();
   for (int j = lane; j < p.NB; j += kWave) {
     const uint64_t kj = row[j];
@@ -250,27 +321,31 @@ __device__ void block_picks(const TileParams& p, const Lds& L, int qi, int lane,
       rank += ((static_cast<uint64_t>(o.y) << 32) | o.x) > kj;
       rank += ((static_cast<uint64_t>(o.w) << 32) | o.z) > kj;
     }
-    if (rank < p.TOP) {
-      R.sel[rank] = j;
-      R.selv[rank] = key_score(kj) > -1.0e30f ? 1 : 0;
-    }
+    if (rank < p.TOP)
+      R.ent[1 + rank] = make_int2(j << p.BS_log2, key_score(kj) > -1.0e30f ? min(t + 1, ls) : 0);
   }
   wave_sync();
 }
 
-// Position and validity of candidate lane c (relation_select.py:244-284):
-// local window first, then the picks' blocks in pick order.
-__device__ __forceinline__ int cand_pos(const TileParams& p, const QRec& R, int c, int t, int ls,
-                                        bool& valid) {
-  if (c < p.L) {
-    const int pos = t - p.L + 1 + c;
-    valid = pos >= 0 && pos <= t && pos < p.T;
-    return pos;
-  }
-  const int r = (c - p.L) >> p.BS_log2;
-  const int o = (c - p.L) & (p.BS - 1);
-  const int pos = R.sel[r] * p.BS + o;
-  valid = R.selv[r] != 0 && pos <= t && pos < ls && pos < p.T;
+// Candidate-table entry and offset of candidate lane c (relation_select.py:
+// 244-284): the local window first, then the picks' blocks in pick order.  The
+// local window's positions t - L + 1 + c are valid up to t; a pick's up to
+// min(t, ls - 1), none for an invalid pick.
+__device__ __forceinline__ void cand_slot(const TileParams& p, int c, int& e, int& off) {
+  const bool local = c < p.L;
+  int r = (c - p.L) >> p.BS_log2;
+  r = r < kTileMaxTop - 1 ? r : kTileMaxTop - 1;
+  e = local ? 0 : 1 + r;
+  off = local ? c : (c - p.L) & (p.BS - 1);
+}
+
+// Position and validity of candidate lane c.
+__device__ __forceinline__ int cand_pos(const TileParams& p, const QRec& R, int c, bool& valid) {
+  int e, off;
+  cand_slot(p, c, e, off);
+  const int2 en = R.ent[e];
+  const int pos = en.x + off;
+  valid = (pos >= 0) & (pos < en.y) & (pos < static_cast<int>(p.T));
   return pos;
 }
 
@@ -280,9 +355,9 @@ __device__ __forceinline__ int cand_pos(const TileParams& p, const QRec& R, int 
 // key (score, tie index), the same in the member's 4 lanes.
 template <bool ANCHOR>
 __device__ __forceinline__ uint64_t member_key(const TileParams& p, const Lds& L, const QRec& R,
-                                               int c, int t, int ls, int s, const double* qrow) {
+                                               int c, int s, const double* qrow) {
   bool v;
-  const int pos = cand_pos(p, R, c, t, ls, v);
+  const int pos = cand_pos(p, R, c, v);
   const int row = v ? pos : 0;
   double acc[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
@@ -319,7 +394,7 @@ __device__ __forceinline__ int emit(const TileParams& p, const QRec& R, int64_t 
       pos = tie;
     } else {
       bool v;
-      pos = cand_pos(p, R, tie, t, ls, v);
+      pos = cand_pos(p, R, tie, v);
     }
   }
   if (active) {
@@ -344,19 +419,36 @@ __device__ int exact_select(const TileParams& p, const Lds& L, int qi, int lane,
                             int64_t qrow_out) {
   QRec& R = L.qr[qi];
   const int K = ANCHOR ? 1 : p.K;
+  // s~ of the lane's candidates (positions as cand_pos gives them), without
+  // branches: every candidate's table entry is read, then every s~ entry
+  // (row 0 for invalid candidates, masked after).
+  const int T32 = static_cast<int>(p.T);
+  int2 en[kMaxNCL];
+  int off[kMaxNCL];
+#pragma unroll
+  for (int i = 0; i < kMaxNCL; ++i) {
+    int e;
+    cand_slot(p, lane + kWave * i, e, off[i]);
+    en[i] = R.ent[e];
+  }
+  int row[kMaxNCL];
+  bool ok[kMaxNCL];
+#pragma unroll
+  for (int i = 0; i < kMaxNCL; ++i) {
+    const int pos = en[i].x + off[i];
+    bool v = (pos >= 0) & (pos < en[i].y) & (pos < T32) & (lane + kWave * i < p.CAP) & active;
+    if (!ANCHOR) v = v & (pos != exclude);
+    ok[i] = v;
+    row[i] = v ? pos : 0;
+  }
   float st[kMaxNCL];
+#pragma unroll
+  for (int i = 0; i < kMaxNCL; ++i) st[i] = L.sc[row[i] * kSQ + qi];
   float lm = -INFINITY;
 #pragma unroll
   for (int i = 0; i < kMaxNCL; ++i) {
-    st[i] = -INFINITY;
-    const int c = lane + kWave * i;
-    if (c < p.CAP && active) {
-      bool v;
-      const int pos = cand_pos(p, R, c, t, ls, v);
-      if (!ANCHOR) v = v && pos != exclude;
-      if (v) st[i] = L.sc[pos * kSQ + qi];
-      lm = fmaxf(lm, st[i]);
-    }
+    st[i] = ok[i] ? st[i] : -INFINITY;
+    lm = fmaxf(lm, st[i]);
   }
   // theta: a lower bound of the k-th largest approximate score.
   float theta;
@@ -365,13 +457,15 @@ __device__ int exact_select(const TileParams& p, const Lds& L, int qi, int lane,
   } else {
     // The k-th largest lane maximum, bit by bit from the top of its
     // order-preserving key: the largest key with at least k lanes at or above it.
+    // The top 20 bits suffice: a lower bound is all theta must be.  A prefix
+    // in the -inf / NaN part of the key range means no k-th candidate: -inf.
     const uint32_t key = ordered_key(lm);
     uint32_t prefix = 0;
-    for (int bit = 31; bit >= 0; --bit) {
+    for (int bit = 31; bit >= 12; --bit) {
       const uint32_t cand = prefix | (1u << bit);
       if (__builtin_popcountll(__builtin_amdgcn_ballot_w64(key >= cand)) >= K) prefix = cand;
     }
-    theta = key_to_float(prefix);
+    theta = prefix >= 0x00800000u ? key_to_float(prefix) : -INFINITY;  // key of -FLT_MAX
   }
   const float eps = kErrScale * qn1 * kmax;
   const float thr = theta - (2.0f * eps + kErrAbs);
@@ -395,7 +489,7 @@ __device__ int exact_select(const TileParams& p, const Lds& L, int qi, int lane,
       const int m = lane >> 2;
       const bool act = m < members;
       const int c = act ? static_cast<int>(list[m]) : 0;
-      const uint64_t key = member_key<ANCHOR>(p, L, R, c, t, ls, s, qrow);
+      const uint64_t key = member_key<ANCHOR>(p, L, R, c, s, qrow);
       if (act && s == 0) list[m] = key;
     }
     wave_sync();
@@ -436,7 +530,7 @@ __device__ int exact_select(const TileParams& p, const Lds& L, int qi, int lane,
       const int m = m0 + (lane >> 2);
       const bool act = m < nw;
       const int c = act ? static_cast<int>(list[m]) : 0;
-      const uint64_t key = member_key<ANCHOR>(p, L, R, c, t, ls, s, qrow);
+      const uint64_t key = member_key<ANCHOR>(p, L, R, c, s, qrow);
       if (act && s == 0) list[m] = key;
     }
     wave_sync();
@@ -509,8 +603,11 @@ __global__ void __launch_bounds__(kThreads) select_tile_kernel(const TileParams 
   const int nchunks = T * 8;
   const uint32_t side_bytes = static_cast<uint32_t>(T) * kRowBytes;
 
-  // ---- One round of loads: the anchor keys (every row), the statistics of
-  //      both streams, the query-side rows and the position. ----
+  // ---- One round of loads: the router constants, the anchor keys (every
+  //      row), the query-side rows, the position and the statistics of both
+  //      streams. ----
+  RouterWords rw;
+  issue_router_consts(p, tid, rw);
   const rsrc_t akr = make_rsrc(p.akeys + b * p.T * 64, side_bytes);
   uint4 kv[4];
 #pragma unroll
@@ -528,8 +625,10 @@ __global__ void __launch_bounds__(kThreads) select_tile_kernel(const TileParams 
   // Exact and router query element `lane` of this wave's query.
   const float aqe = to_f32(p.aq[qrow * 64 + lane]);
   const float arqe = to_f32(p.arq[qrow * 64 + lane]);
-  stage_stats<TS>(p, L, b, tid);
-  stage_router_consts(p, L, tid);
+  StatGroup<TS> sg;
+  issue_stats<TS>(p, b, wave, lane, sg);
+  put_router_consts(p, L, tid, rw);
+  put_stats<TS>(p, L, wave, lane, sg);
 
   put_keys(L, kv, tid, nchunks, wave, lane);
   L.eq[qi * kQRow + lane] = static_cast<double>(aqe);
@@ -564,9 +663,14 @@ __global__ void __launch_bounds__(kThreads) select_tile_kernel(const TileParams 
   const bool have = anchor >= 0 && anchor < T;
   const float pbe = to_f32(p.pbase[qrow * 128 + lane]);
   const float pbr = to_f32(p.pbase[qrow * 128 + 64 + lane]);
-  const bf16* pcrow = p.pcache + (b * p.T + (have ? anchor : 0)) * 128;
-  const float pce = have ? to_f32(pcrow[lane]) : 0.0f;
-  const float pcr = have ? to_f32(pcrow[64 + lane]) : 0.0f;
+  // The anchor's cached partner row: branch-free buffer loads (no anchor reads
+  // 0), issued together and ahead of the partner keys.
+  const rsrc_t pcr_r = make_rsrc(p.pcache + b * p.T * 128, side_bytes * 2u);
+  const uint32_t pco = have ? static_cast<uint32_t>(anchor * 128 + lane) * 2u : kNoOffset;
+  const uint32_t pce_w = buf_load_b16(pcr_r, pco);
+  const uint32_t pcr_w = buf_load_b16(pcr_r, have ? pco + 128u : kNoOffset);
+  const float pce = __uint_as_float(pce_w << 16);
+  const float pcr = __uint_as_float(pcr_w << 16);
   const rsrc_t pkr = make_rsrc(p.pkeys + b * p.T * 64, side_bytes);
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
@@ -580,22 +684,24 @@ __global__ void __launch_bounds__(kThreads) select_tile_kernel(const TileParams 
   const float pqr = pbr + pcr;
   L.eq[qi * kQRow + lane] = static_cast<double>(pqe);
   L.rq[qi * kQRow + lane] = static_cast<double>(pqr);
+  {
+    // bf16 hi (round to nearest even) + lo = bf16(x - hi) of the wave's own
+    // query element, for every wave's MFMA A fragments.
+    const uint32_t hl = pack_bf16x2(pqe, 0.0f) & 0xffffu;
+    const uint32_t ll = pack_bf16x2(pqe - __uint_as_float(hl << 16), 0.0f) & 0xffffu;
+    const int o = frag_offset(qi, lane);
+    L.frag[o] = static_cast<uint16_t>(hl);
+    L.frag[kQ * 64 + o] = static_cast<uint16_t>(ll);
+  }
   qn1 = wave_sum_f32(fabsf(pqe)) * (1.0f + 1.0f / 1024.0f);
   __syncthreads();  // B3
 
   kmax = staged_kmax(L);
   // Partner A fragments: bf16 hi + lo of the fp32 query, row lane%16.
-  uint4 ah0, al0, ah1, al1;
-  {
-    const double* src = L.eq + c16 * kQRow;
-    float x[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = static_cast<float>(src[8 * g4 + e]);
-    split_hi_lo(x, ah0, al0);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = static_cast<float>(src[32 + 8 * g4 + e]);
-    split_hi_lo(x, ah1, al1);
-  }
+  const uint4 ah0 = *reinterpret_cast<const uint4*>(L.frag + frag_offset(c16, 8 * g4));
+  const uint4 al0 = *reinterpret_cast<const uint4*>(L.frag + kQ * 64 + frag_offset(c16, 8 * g4));
+  const uint4 ah1 = *reinterpret_cast<const uint4*>(L.frag + frag_offset(c16, 32 + 8 * g4));
+  const uint4 al1 = *reinterpret_cast<const uint4*>(L.frag + kQ * 64 + frag_offset(c16, 32 + 8 * g4));
   for (int tt = wave; tt < ntiles; tt += kQ) {
     const int row = tt * 16 + c16;
     const uint4 b0 = *reinterpret_cast<const uint4*>(L.keys + key_chunk_offset(row, g4));
