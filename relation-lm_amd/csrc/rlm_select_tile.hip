@@ -56,7 +56,7 @@ constexpr int kThreads = 1024;
 constexpr int kRowBytes = 128;  // one staged key row (64 bf16)
 constexpr int kSQ = 16;         // floats per s~ row (one per query)
 constexpr int kStatRow = 68;    // floats per staged statistics row (64 + 4: conflict-free MFMA operand reads)
-constexpr int kQRow = 66;       // doubles per staged query row (64 + 2)
+constexpr int kQRow = 68;       // doubles per staged query row (64 + 4 zeros: dead k-steps of a head)
 constexpr int kListCap = 64;    // members per query per window
 constexpr int kMaxNCL = 4;      // candidates per lane (CAP <= 256)
 
@@ -220,19 +220,21 @@ __device__ __forceinline__ void put_router_consts(const TileParams& p, const Lds
 }
 
 // Per-head block scores of the 16 queries (relation_select.py:70-96) on
-// float64 MFMA, one (head, block tile) per wave:
+// float64 MFMA, one (head, block tile) per wave of the first `hw` waves (the
+// others score the keys meanwhile):
 //   content[q][j] = sum_d mean[j][h,d] q[q][h,d],  unc[q][j] = sum_d std[j][h,d] |q[q][h,d]|
 //   s_h = (content + softplus(gamma_h) unc) * HD^-0.5 + bias[h, bucket(t_q, j)]
 // into sh[h][q][j].  v_mfma_f64_16x16x4f64 takes A[i = lane%16][k = lane/16],
 // B[k = lane/16][j = lane%16] and leaves D[4r + lane/16][lane%16] in register r.
-__device__ void head_scores(const TileParams& p, const Lds& L, int side, int wave, int lane) {
+__device__ void head_scores(const TileParams& p, const Lds& L, int side, int wave, int hw,
+                            int lane) {
   const float* mean = L.stats + (2 * side) * p.NB * kStatRow;
   const float* stdv = L.stats + (2 * side + 1) * p.NB * kStatRow;
   const double* sp = L.sp + 16 * side;
   const double* bias = L.bias + side * p.H * p.RB;
   const int kq = lane >> 4, c16 = lane & 15;
   const int nbt = (p.NB + 15) >> 4;
-  for (int item = wave; item < p.H * nbt; item += kQ) {
+  for (int item = wave; item < p.H * nbt; item += hw) {
     const int h = item / nbt;
     const int jt = item - h * nbt;
     const int j = jt * 16 + c16;
@@ -253,24 +255,27 @@ __device__ void head_scores(const TileParams& p, const Lds& L, int side, int wav
     const double sph = sp[h];
     f64x4_t content = {0.0, 0.0, 0.0, 0.0}, unc = {0.0, 0.0, 0.0, 0.0};
     for (int ks0 = 0; ks0 < p.HD; ks0 += 16) {
-      // Four k-steps, every operand read before the first MFMA; k-steps past
-      // the head's HD dims (HD = 8) get zero B operands instead of a branch.
+      // Four k-steps, every operand read before the first MFMA and no operand
+      // masked: a k-step past the head's HD dims (HD = 8) takes its query
+      // values from the zero pad of the query row, a block past NB reads
+      // block 0 (its column is not stored).
       double a[4];
       float bm[4], bs[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int d = h * p.HD + (ks0 + 4 * u < p.HD ? ks0 + 4 * u : 0) + kq;
-        a[u] = L.rq[c16 * kQRow + d];
+        const bool live = ks0 + 4 * u < p.HD;
+        const int d = h * p.HD + (live ? ks0 + 4 * u : 0) + kq;
+        a[u] = L.rq[c16 * kQRow + (live ? d : 64 + kq)];
         bm[u] = mean[jc * kStatRow + d];
         bs[u] = stdv[jc * kStatRow + d];
       }
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the chain
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const bool live = jv && ks0 + 4 * u < p.HD;
-        const double m = live ? static_cast<double>(bm[u]) : 0.0;
-        const double sd = live ? static_cast<double>(bs[u]) : 0.0;
-        content = __builtin_amdgcn_mfma_f64_16x16x4f64(a[u], m, content, 0, 0, 0);
-        unc = __builtin_amdgcn_mfma_f64_16x16x4f64(fabs(a[u]), sd, unc, 0, 0, 0);
+        content = __builtin_amdgcn_mfma_f64_16x16x4f64(a[u], static_cast<double>(bm[u]), content,
+                                                       0, 0, 0);
+        unc = __builtin_amdgcn_mfma_f64_16x16x4f64(fabs(a[u]), static_cast<double>(bs[u]), unc,
+                                                   0, 0, 0);
       }
     }
 #pragma unroll
@@ -633,6 +638,7 @@ __global__ void __launch_bounds__(kThreads) select_tile_kernel(const TileParams 
   put_keys(L, kv, tid, nchunks, wave, lane);
   L.eq[qi * kQRow + lane] = static_cast<double>(aqe);
   L.rq[qi * kQRow + lane] = static_cast<double>(arqe);
+  if (lane < kQRow - 64) L.rq[qi * kQRow + 64 + lane] = 0.0;
   const int t = clamp_pos(decode_index(pw, p.pos_dtype));
   const int ls = t - p.L + 1 > 0 ? t - p.L + 1 : 0;
   if (lane == 0) L.qr[qi].t = t;
@@ -641,16 +647,23 @@ __global__ void __launch_bounds__(kThreads) select_tile_kernel(const TileParams 
 
   float kmax = staged_kmax(L);
   const int ntiles = T >> 4;
-  for (int tt = wave; tt < ntiles; tt += kQ) {
-    const int row = tt * 16 + c16;
-    const uint4 b0 = *reinterpret_cast<const uint4*>(L.keys + key_chunk_offset(row, g4));
-    const uint4 b1 = *reinterpret_cast<const uint4*>(L.keys + key_chunk_offset(row, 4 + g4));
-    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    acc = mfma_bf16(a0, b0, acc);
-    acc = mfma_bf16(a1, b1, acc);
-    *reinterpret_cast<float4*>(L.sc + row * kSQ + 4 * g4) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  // Waves [0, hw) compute the head scores (a chain of LDS round trips and
+  // float64 MFMAs), the other waves score the key tiles meanwhile.
+  const int hw = min(p.H * ((p.NB + 15) >> 4), 8);
+  if (wave < hw) {
+    head_scores(p, L, 0, wave, hw, lane);
+  } else {
+    for (int tt = wave - hw; tt < ntiles; tt += kQ - hw) {
+      const int row = tt * 16 + c16;
+      const uint4 b0 = *reinterpret_cast<const uint4*>(L.keys + key_chunk_offset(row, g4));
+      const uint4 b1 = *reinterpret_cast<const uint4*>(L.keys + key_chunk_offset(row, 4 + g4));
+      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      acc = mfma_bf16(a0, b0, acc);
+      acc = mfma_bf16(a1, b1, acc);
+      *reinterpret_cast<float4*>(L.sc + row * kSQ + 4 * g4) =
+          make_float4(acc[0], acc[1], acc[2], acc[3]);
+    }
   }
-  head_scores(p, L, 0, wave, lane);
   __syncthreads();  // B1: s~ and the head scores complete
 
   block_picks(p, L, qi, lane, t, ls);
@@ -702,18 +715,22 @@ __global__ void __launch_bounds__(kThreads) select_tile_kernel(const TileParams 
   const uint4 al0 = *reinterpret_cast<const uint4*>(L.frag + kQ * 64 + frag_offset(c16, 8 * g4));
   const uint4 ah1 = *reinterpret_cast<const uint4*>(L.frag + frag_offset(c16, 32 + 8 * g4));
   const uint4 al1 = *reinterpret_cast<const uint4*>(L.frag + kQ * 64 + frag_offset(c16, 32 + 8 * g4));
-  for (int tt = wave; tt < ntiles; tt += kQ) {
-    const int row = tt * 16 + c16;
-    const uint4 b0 = *reinterpret_cast<const uint4*>(L.keys + key_chunk_offset(row, g4));
-    const uint4 b1 = *reinterpret_cast<const uint4*>(L.keys + key_chunk_offset(row, 4 + g4));
-    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    acc = mfma_bf16(ah0, b0, acc);
-    acc = mfma_bf16(al0, b0, acc);
-    acc = mfma_bf16(ah1, b1, acc);
-    acc = mfma_bf16(al1, b1, acc);
-    *reinterpret_cast<float4*>(L.sc + row * kSQ + 4 * g4) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  if (wave < hw) {
+    head_scores(p, L, 1, wave, hw, lane);
+  } else {
+    for (int tt = wave - hw; tt < ntiles; tt += kQ - hw) {
+      const int row = tt * 16 + c16;
+      const uint4 b0 = *reinterpret_cast<const uint4*>(L.keys + key_chunk_offset(row, g4));
+      const uint4 b1 = *reinterpret_cast<const uint4*>(L.keys + key_chunk_offset(row, 4 + g4));
+      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      acc = mfma_bf16(ah0, b0, acc);
+      acc = mfma_bf16(al0, b0, acc);
+      acc = mfma_bf16(ah1, b1, acc);
+      acc = mfma_bf16(al1, b1, acc);
+      *reinterpret_cast<float4*>(L.sc + row * kSQ + 4 * g4) =
+          make_float4(acc[0], acc[1], acc[2], acc[3]);
+    }
   }
-  head_scores(p, L, 1, wave, lane);
   __syncthreads();  // B4: s~ and the head scores complete
 
   block_picks(p, L, qi, lane, t, ls);
