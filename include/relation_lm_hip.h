@@ -333,6 +333,22 @@ hipError_t rlm_relation_reduce_fused_seq(
     const rlm_tensor* norm_weight, const rlm_tensor* norm_bias, const rlm_tensor* positions,
     double norm_eps, const rlm_tensor* out, hipStream_t stream);
 
+/*
+ * Whether rlm_relation_reduce_fused_seq takes these operands (no reference
+ * counterpart: the capability query behind relation_lm::relation_reduce_fused_seq,
+ * which runs the unfused relation_hidden_cached_seq -> relation_linear ->
+ * relation_norm_reduce_seq chain for every other shape, e.g. the reference's
+ * fp32 D = 576 cases of tests/test_relation_reduce_gpu.py:163-200).  Returns 1
+ * for bf16 caches and weights, 1 <= K <= 16, R in {32,64,128}, H a multiple of
+ * 128, D in {128, 256, 384, 512} and 16-byte aligned operand_cache,
+ * product_weight and second_weight; 0 otherwise.  Reads descriptors only.
+ */
+int rlm_relation_reduce_fused_seq_fits(const rlm_tensor* expanded_cache,
+                                       const rlm_tensor* operand_cache,
+                                       const rlm_tensor* partner_index,
+                                       const rlm_tensor* product_weight,
+                                       const rlm_tensor* second_weight);
+
 /* ------------------------------------------------------------------------
  * Router cache (decode producer of the selection's block statistics)
  * ---------------------------------------------------------------------- */

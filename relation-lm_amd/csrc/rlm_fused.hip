@@ -662,6 +662,28 @@ hipError_t launch_fused(const FusedParams& p, hipStream_t stream) {
 
 using namespace rlm;
 
+extern "C" int rlm_relation_reduce_fused_seq_fits(const rlm_tensor* expanded_cache,
+                                                  const rlm_tensor* operand_cache,
+                                                  const rlm_tensor* partner_index,
+                                                  const rlm_tensor* product_weight,
+                                                  const rlm_tensor* second_weight) {
+  for (const rlm_tensor* t : {expanded_cache, operand_cache, partner_index, product_weight,
+                              second_weight})
+    if (t == nullptr) return 0;
+  if (operand_cache->ndim != 3 || expanded_cache->ndim != 3 || partner_index->ndim != 3 ||
+      product_weight->ndim != 2 || second_weight->ndim != 2)
+    return 0;
+  for (const rlm_tensor* t : {expanded_cache, operand_cache, product_weight, second_weight})
+    if (t->dtype != RLM_BF16) return 0;
+  const int64_t R = operand_cache->shape[2], H = product_weight->shape[0];
+  const int64_t D = second_weight->shape[0], K = partner_index->shape[2];
+  if (K < 1 || K > 16 || !(R == 32 || R == 64 || R == 128) || H <= 0 || H % kHC != 0) return 0;
+  if (!(D == 128 || D == 256 || D == 384 || D == 512)) return 0;
+  for (const rlm_tensor* t : {operand_cache, product_weight, second_weight})
+    if ((reinterpret_cast<uintptr_t>(t->data) & 15u) != 0) return 0;
+  return 1;
+}
+
 extern "C" hipError_t rlm_relation_reduce_fused_seq(
     const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
     const rlm_tensor* anchor_index, const rlm_tensor* partner_index,

@@ -557,6 +557,10 @@ std::tuple<at::Tensor, at::Tensor> relation_linear_norm_reduce_output(
   return {context, final};
 }
 
+at::Tensor relation_linear(const at::Tensor& input, const at::Tensor& weight,
+                           const c10::optional<at::Tensor>& bias,
+                           c10::optional<at::ScalarType> out_dtype);
+
 at::Tensor relation_reduce_fused_seq(const at::Tensor& expanded_cache,
                                      const at::Tensor& operand_cache,
                                      const at::Tensor& anchor_index,
@@ -574,6 +578,23 @@ at::Tensor relation_reduce_fused_seq(const at::Tensor& expanded_cache,
            &second_weight, &second_bias, &partner_scores, &norm_weight, &norm_bias, &positions});
   TORCH_CHECK(partner_index.dim() == 3 && second_weight.dim() == 2, op,
               ": partner_index must be [B,Tq,K] and second_weight [D,H]");
+  {
+    const rlm_tensor e = desc(expanded_cache, "expanded_cache");
+    const rlm_tensor o = desc(operand_cache, "operand_cache");
+    const rlm_tensor pi = desc(partner_index, "partner_index");
+    const rlm_tensor wm = desc(product_weight, "product_weight");
+    const rlm_tensor w2 = desc(second_weight, "second_weight");
+    if (!rlm_relation_reduce_fused_seq_fits(&e, &o, &pi, &wm, &w2)) {
+      // Shapes or dtypes the fused kernel does not take (fp32, d_model 576, ...):
+      // the same result from the three-op chain it fuses, every step on HIP.
+      const at::Tensor hidden = relation_hidden_cached_seq(expanded_cache, operand_cache,
+                                                           anchor_index, partner_index,
+                                                           product_weight);
+      const at::Tensor raw = relation_linear(hidden, second_weight, second_bias, at::kFloat);
+      return relation_norm_reduce_seq(raw, partner_scores, norm_weight, norm_bias, positions,
+                                      norm_eps);
+    }
+  }
   at::Tensor out = at::empty({partner_index.size(0), partner_index.size(1), second_weight.size(0)},
                              f32(operand_cache));
   rlm_tensor d[12] = {desc(expanded_cache, "expanded_cache"), desc(operand_cache, "operand_cache"),

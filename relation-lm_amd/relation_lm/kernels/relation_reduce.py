@@ -249,6 +249,9 @@ def relation_reduce_fused_seq(
     second_weight, second_bias), ...)`` (the reference's three-call sequence,
     benchmarks/benchmark_relation_reduce.py:55-64) with bf16 caches and weights: the
     hidden is rounded to bf16 before the second linear, as the unfused bf16 linear does.
+    Operands the fused kernel does not take (fp32, d_model outside {128, 256, 384,
+    512}, K > 16, ...) run that three-op chain on HIP instead, so every shape the
+    reference's ops accept goes through this op.
     """
     return torch.ops.relation_lm.relation_reduce_fused_seq(
         expanded_cache, operand_cache, anchor_index, partner_index, product_weight,

@@ -53,7 +53,7 @@ def lib():
 
 def declared_functions():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:hipError_t|const char\*)\s+(rlm_\w+)\s*\(", text,
+    return sorted(set(re.findall(r"^\s*(?:hipError_t|const char\*|int)\s+(rlm_\w+)\s*\(", text,
                                  flags=re.M)))
 
 
@@ -69,6 +69,29 @@ def test_library_exports_every_declared_symbol(lib):
     missing = [name for name in declared_functions() if not hasattr(lib, name)]
     assert not missing, missing
     assert b"gfx950" in lib.rlm_version()
+
+
+def test_fused_reduce_fits_predicate(lib):
+    """rlm_relation_reduce_fused_seq_fits reads descriptors only: 1 for the shapes
+    the fused kernel takes, 0 for those the op runs as the three-op chain."""
+    base = {"expanded": tensor([2, 64, 1024], RLM_BF16), "operand": tensor([2, 64, 64], RLM_BF16),
+            "partner": tensor([2, 8, 8], RLM_I32), "wm": tensor([512, 64], RLM_BF16),
+            "w2": tensor([512, 512], RLM_BF16)}
+
+    def fits(**override):
+        d = {**base, **override}
+        return lib.rlm_relation_reduce_fused_seq_fits(
+            *(ctypes.byref(d[k]) for k in ("expanded", "operand", "partner", "wm", "w2")))
+
+    assert fits() == 1
+    assert fits(partner=tensor([2, 8, 5], RLM_I64)) == 1
+    assert fits(w2=tensor([576, 512], RLM_BF16)) == 0                    # d_model 576
+    assert fits(operand=tensor([2, 64, 64], RLM_F32)) == 0               # fp32 operands
+    assert fits(w2=tensor([512, 512], RLM_F32)) == 0
+    assert fits(partner=tensor([2, 8, 17], RLM_I32)) == 0                # K > 16
+    assert fits(wm=tensor([500, 64], RLM_BF16)) == 0                     # H % 128 != 0
+    assert fits(operand=tensor([2, 64, 48], RLM_BF16)) == 0              # R not 32/64/128
+    assert fits(w2=tensor([512, 512], RLM_BF16, data=0x1008)) == 0       # misaligned
 
 
 def _select_packed_args(b=2, t=64, e=64, nb=8, k=4, **override):

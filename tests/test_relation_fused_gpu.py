@@ -141,24 +141,59 @@ def test_fused_batched_positions_and_ragged_rows(device):
     assert abs_err(host(fused), host(unfused)) <= TIGHT_ABS
 
 
-def test_fused_rejects_unsupported_shapes(device):
-    cfg = CONFIGS["cfg3"]  # d_model 576 is outside the fused kernel's register budget
-    red = reduce_inputs(RelationConfig(**{**cfg.__dict__, "batch": 1}), device=device)
+def test_fused_op_runs_the_chain_outside_the_kernel_bf16(device):
+    """cfg3's d_model 576 is outside the fused kernel's register budget: the op
+    runs the unfused three-op chain and still matches the oracle chain."""
+    cfg = RelationConfig(**{**CONFIGS["cfg3"].__dict__, "batch": 2})
+    red = reduce_inputs(cfg, device=device)
     expanded = relation_linear(red["operand_cache"], red["expanded_weight"], red["expanded_bias"])
-    anchor = torch.zeros(1, 4, dtype=torch.int32, device=device)
-    partner = torch.zeros(1, 4, 8, dtype=torch.int32, device=device)
-    scores = torch.zeros(1, 4, 8, device=device)
-    with pytest.raises(RuntimeError, match="d_model"):
-        relation_reduce_fused_seq(expanded, red["operand_cache"], anchor, partner,
-                                  red["product_weight"], red["second_weight"],
-                                  red["second_bias"], scores, red["norm_weight"],
-                                  red["norm_bias"], torch.arange(4, device=device), 1e-5)
-    with pytest.raises(RuntimeError, match="bfloat16"):
-        relation_reduce_fused_seq(expanded.float(), red["operand_cache"].float(), anchor,
-                                  partner, red["product_weight"].float(),
-                                  red["second_weight"].float(), red["second_bias"], scores,
-                                  red["norm_weight"], red["norm_bias"],
-                                  torch.arange(4, device=device), 1e-5)
+    anchor, partner, scores, pos = indices_and_scores(2, 40, cfg.context, cfg.k_out, seed=13)
+    fused = run_fused(red, expanded, anchor, partner, scores, pos, device)
+    unfused = run_unfused(red, expanded, anchor, partner, scores, pos, device)
+    torch.cuda.synchronize()
+    assert fused.shape == (2, 40, 576)
+    assert torch.equal(fused, unfused)
+    expected = oracle_chain(red, expanded, host(anchor), host(partner), host(scores),
+                            np.arange(40))
+    assert abs_err(host(fused), expected) <= TIGHT_ABS
+
+
+def rel_err(got, expected):
+    got = np.asarray(got, np.float64)
+    expected = np.asarray(expected, np.float64)
+    return float(np.abs(got - expected).max() / max(np.abs(expected).max(), 1e-30))
+
+
+@pytest.mark.parametrize("k_out", [5, 6, 7])
+def test_fused_op_reference_shapes_fp32(device, k_out):
+    """The reference's fp32 d_model 576 / hidden 2304 reduce with K = 5, 6, 7
+    (tests/test_relation_reduce_gpu.py:163-200 of the reference) through
+    relation_reduce_fused_seq: fp32 operands run the three-op chain on HIP;
+    float64 oracle chain (no bf16 rounding) at 1e-5 relative."""
+    g = torch.Generator().manual_seed(20261130 + k_out)
+    batch, context, queries, rdim, hdim, dmodel = 2, 64, 24, 128, 2304, 576
+    operand = torch.randn(batch, context, rdim, generator=g)
+    expanded = torch.randn(batch, context, 2 * hdim, generator=g) * 0.5
+    product_weight = torch.randn(hdim, rdim, generator=g) * 0.05
+    second_weight = torch.randn(dmodel, hdim, generator=g) * 0.02
+    second_bias = torch.randn(dmodel, generator=g) * 0.01
+    norm_weight = torch.randn(dmodel, generator=g) * 0.05 + 1.0
+    norm_bias = torch.randn(dmodel, generator=g) * 0.01
+    anchor, partner, scores, pos = indices_and_scores(batch, queries, context, k_out,
+                                                      seed=70 + k_out)
+    got = relation_reduce_fused_seq(expanded.to(device), operand.to(device), anchor.to(device),
+                                    partner.to(device), product_weight.to(device),
+                                    second_weight.to(device), second_bias.to(device),
+                                    scores.to(device), norm_weight.to(device),
+                                    norm_bias.to(device), pos.to(device), 1e-5)
+    torch.cuda.synchronize()
+    assert got.shape == (batch, queries, dmodel) and got.dtype == torch.float32
+    hidden = ored.relation_hidden_cached_seq(host(expanded), host(operand), host(anchor),
+                                             host(partner), host(product_weight))
+    raw = ored.linear(hidden, host(second_weight), host(second_bias))
+    expected = ored.relation_norm_reduce_seq(raw, host(scores), host(norm_weight),
+                                             host(norm_bias), host(pos), 1e-5)
+    assert rel_err(host(got), expected) <= 1e-5
 
 
 def test_cfg4_fused_reduce(device):
