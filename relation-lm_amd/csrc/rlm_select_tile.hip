@@ -291,45 +291,91 @@ __device__ void head_scores(const TileParams& p, const Lds& L, int side, int wav
   }
 }
 
-// Log-sum-exp over heads (relation_select.py:97-106) of the wave's query, one
-// lane per (block, head) with a block's heads in consecutive lanes, and the
-// TOP picks by rank: block j is pick rank(j) = #{k : key_k > key_j} with key
-// (score, lower block first) -- the reference's sequential argmax with ties to
-// the lowest block (:229-242).  Picks past the last block are block 0, invalid.
-__device__ void block_picks(const TileParams& p, const Lds& L, int qi, int lane, int t, int ls) {
-  QRec& R = L.qr[qi];
-  uint64_t* row = L.blk + qi * p.NB;
-  const int pairs = p.NB * p.H;
-  for (int base = 0; base < pairs; base += kWave) {
-    const int pr = base + lane;
-    const bool live = pr < pairs;
-    const int j = (live ? pr : 0) >> p.H_log2;
-    const int h = pr & (p.H - 1);
-    const double v = live ? L.sh[(h * kQ + qi) * p.NB + j] : 0.0;
-    const double m = group_max_f64(v, p.H);
-    const double sum = group_sum_f64(exp(v - m), p.H);
-    if (live && h == 0) {
-      const double lse = m + log(sum);
-      const int end = (j + 1) * p.BS - 1;
-      const bool eligible = end <= t && (!p.strict || end < ls);
-      row[j] = select_key(eligible ? static_cast<float>(lse) : -INFINITY, static_cast<uint32_t>(j));
+// Block picks of all 16 queries, one lane per (query, block): pair g = 16 NB
+// pairs in query order on waves [0, NB / 4) (NB % 4 == 0).
+//   block_keys: the log-sum-exp over the H heads (relation_select.py:97-106)
+//     of the per-head scores, summed as the pairwise tree ((e0 + e1) + (e2 +
+//     e3)) + ..., and the 64-bit selection key (score, lower block first) of
+//     an eligible block, -inf otherwise, into blk[q][j];
+//   block_ranks: pick rank(j) = #{k : key_k > key_j} among the query's NB
+//     keys -- the reference's sequential argmax with ties to the lowest block
+//     (:229-242) -- into the query's candidate table.
+// Each query's wave clears its table first (picks past the last block are
+// block 0, invalid) and sets the local-window entry.
+template <int HL>
+__device__ __forceinline__ void block_keys(const TileParams& p, const Lds& L, int g) {
+  constexpr int H = 1 << HL;
+  const int q = g / p.NB;
+  const int j = g - q * p.NB;
+  double v[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) v[h] = L.sh[(h * kQ + q) * p.NB + j];
+  const int t = L.qr[q].t;
+  double m = v[0];
+#pragma unroll
+  for (int h = 1; h < H; ++h) m = fmax(m, v[h]);
+  double e[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) e[h] = exp(v[h] - m);
+#pragma unroll
+  for (int w = 1; w < H; w *= 2)
+#pragma unroll
+    for (int h = 0; h < H; h += 2 * w) e[h] += e[h + w];
+  const double lse = m + log(e[0]);
+  const int ls = t - p.L + 1 > 0 ? t - p.L + 1 : 0;
+  const int end = (j + 1) * p.BS - 1;
+  const bool eligible = end <= t && (!p.strict || end < ls);
+  L.blk[g] = select_key(eligible ? static_cast<float>(lse) : -INFINITY, static_cast<uint32_t>(j));
+}
+
+__device__ __forceinline__ void block_ranks(const TileParams& p, const Lds& L, int g) {
+  const int q = g / p.NB;
+  const int j = g - q * p.NB;
+  const uint64_t* row = L.blk + q * p.NB;
+  const uint64_t kj = row[j];
+  int rank = 0;
+  for (int k = 0; k < p.NB; k += 2) {
+    const uint4 o = *reinterpret_cast<const uint4*>(row + k);
+    rank += ((static_cast<uint64_t>(o.y) << 32) | o.x) > kj;
+    rank += ((static_cast<uint64_t>(o.w) << 32) | o.z) > kj;
+  }
+  if (rank < p.TOP) {
+    const int t = L.qr[q].t;
+    const int ls = t - p.L + 1 > 0 ? t - p.L + 1 : 0;
+    L.qr[q].ent[1 + rank] =
+        make_int2(j << p.BS_log2, key_score(kj) > -1.0e30f ? min(t + 1, ls) : 0);
+  }
+}
+
+// The picks phase of one stream, between two workgroup barriers: keys, then
+// (once every key of a query is written) ranks.
+__device__ __forceinline__ void block_picks(const TileParams& p, const Lds& L, int wave, int lane) {
+  const int g = wave * kWave + lane;
+  const bool mine = g < kQ * p.NB;  // whole waves: 16 NB is a multiple of 64
+  if (mine) {
+    switch (p.H_log2) {
+      case 0: block_keys<0>(p, L, g); break;
+      case 1: block_keys<1>(p, L, g); break;
+      case 2: block_keys<2>(p, L, g); break;
+      default: block_keys<3>(p, L, g); break;
     }
   }
+  // A query's keys sit in one wave when NB divides 64, else they may span two.
+  if (kWave % p.NB != 0) {
+    __syncthreads();
+  } else {
+    wave_sync();
+  }
+  if (mine) block_ranks(p, L, g);
+}
+
+// Clears the wave's query's candidate table: the local window (positions
+// t - L + 1 .. t) and TOP invalid picks.
+__device__ __forceinline__ void clear_table(const TileParams& p, const Lds& L, int qi, int lane,
+                                            int t) {
+  QRec& R = L.qr[qi];
   if (lane < p.TOP) R.ent[1 + lane] = make_int2(0, 0);
   if (lane == kWave - 1) R.ent[0] = make_int2(t - p.L + 1, t + 1);
-  wave_sync();
-  for (int j = lane; j < p.NB; j += kWave) {
-    const uint64_t kj = row[j];
-    int rank = 0;
-    for (int k = 0; k < p.NB; k += 2) {
-      const uint4 o = *reinterpret_cast<const uint4*>(row + k);
-      rank += ((static_cast<uint64_t>(o.y) << 32) | o.x) > kj;
-      rank += ((static_cast<uint64_t>(o.w) << 32) | o.z) > kj;
-    }
-    if (rank < p.TOP)
-      R.ent[1 + rank] = make_int2(j << p.BS_log2, key_score(kj) > -1.0e30f ? min(t + 1, ls) : 0);
-  }
-  wave_sync();
 }
 
 // Candidate-table entry and offset of candidate lane c (relation_select.py:
@@ -642,6 +688,7 @@ __global__ void __launch_bounds__(kThreads) select_tile_kernel(const TileParams 
   const int t = clamp_pos(decode_index(pw, p.pos_dtype));
   const int ls = t - p.L + 1 > 0 ? t - p.L + 1 : 0;
   if (lane == 0) L.qr[qi].t = t;
+  clear_table(p, L, qi, lane, t);
   float qn1 = wave_sum_f32(fabsf(aqe)) * (1.0f + 1.0f / 1024.0f);  // covers fp32 rounding
   __syncthreads();  // B0
 
@@ -666,9 +713,11 @@ __global__ void __launch_bounds__(kThreads) select_tile_kernel(const TileParams 
   }
   __syncthreads();  // B1: s~ and the head scores complete
 
-  block_picks(p, L, qi, lane, t, ls);
+  block_picks(p, L, wave, lane);
+  __syncthreads();  // every query's picks are in its candidate table
   const int anchor = exact_select<true>(p, L, qi, lane, t, ls, -1, L.eq + qi * kQRow, qn1, kmax,
                                         active, qrow);
+  clear_table(p, L, qi, lane, t);
 
   // ---- Partner side.  The anchor's cached row and the partner keys are
   //      loaded together; the keys replace the anchor's once every wave is
@@ -733,7 +782,8 @@ __global__ void __launch_bounds__(kThreads) select_tile_kernel(const TileParams 
   }
   __syncthreads();  // B4: s~ and the head scores complete
 
-  block_picks(p, L, qi, lane, t, ls);
+  block_picks(p, L, wave, lane);
+  __syncthreads();  // every query's picks are in its candidate table
   exact_select<false>(p, L, qi, lane, t, ls, anchor, L.eq + qi * kQRow, qn1, kmax, active, qrow);
 }
 
