@@ -14,7 +14,10 @@ multi-anchor selection (local window plus the top blocks of a block router,
   relation MLP Linear -> GELU     relation_lm::relation_hidden_cached_seq_out
     (factorized: operand cache, expanded cache = [W_a+W_d; W_p-W_d] op + [b; 0];
     stored in bf16 when the second Linear is bf16)
-  relation MLP second Linear      relation_lm::relation_linear
+  relation MLP second Linear      torch.addmm(out_dtype=float32): a plain bias GEMM,
+    on the ROCm BLAS (hipBLASLt) for 16-bit weights -- measured 1.8x the
+    hand-written tile GEMM at cfg5's [98304, 3072] x [3072, 768] --
+    relation_lm::relation_linear otherwise
   LayerNorm, partner softmax,     relation_lm::multi_relation_reduce_seq
     slot mix, residual gate
   final_norm (stack)              relation_lm::layer_norm
@@ -46,6 +49,23 @@ from relation_lm.kernels.relation_reduce import factor_relation_first_layer
 
 ops = torch.ops.relation_lm
 
+
+
+def _second_linear(rows: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
+    """fp32 ``rows @ weight.T + bias`` of the relation MLP's second Linear (the
+    reference's plain ``nn.Linear``, multi_relation_blocks.py:47-52).
+
+    With 16-bit weights this is a plain bias GEMM and runs on the ROCm BLAS
+    (``addmm`` with an fp32 output: hipBLASLt, bias in its epilogue); fp32 weights
+    take ``relation_linear``'s fp32 kernel."""
+    if weight.dtype not in (torch.bfloat16, torch.float16) or rows.dtype != weight.dtype:
+        return ops.relation_linear(rows, weight, bias, torch.float32)
+    flat = rows.reshape(-1, rows.shape[-1])
+    if bias is None:
+        out = torch.mm(flat, weight.t(), out_dtype=torch.float32)
+    else:
+        out = torch.addmm(bias.float(), flat, weight.t(), out_dtype=torch.float32)
+    return out.view(*rows.shape[:-1], weight.shape[0])
 
 @dataclass
 class MultiRelationBlockConfig:
@@ -213,7 +233,7 @@ class MultiAnchorRelationBlock(nn.Module):
                 sel["anchor"][b:b + 1].reshape(1, length * h),
                 sel["partner"][b:b + 1].reshape(1, length * h, k_count), sel["product_weight"],
                 rows)
-            raw = ops.relation_linear(rows, mlp[2].weight, mlp[2].bias, torch.float32)
+            raw = _second_linear(rows, mlp[2].weight, mlp[2].bias)
             outputs.append(ops.multi_relation_reduce_seq(
                 raw.view(1, length, h, k_count, d), sel["partner_score"][b:b + 1], mlp[3].weight,
                 mlp[3].bias, self.slot_mix_logits, self.residual_gate, hidden[b:b + 1],
