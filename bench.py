@@ -152,11 +152,9 @@ def main() -> int:
     import torch
 
     from relation_lm.kernels.relation_reduce import (
-        relation_hidden_cache_update,
         relation_hidden_cached,
         relation_hidden_cached_seq,
         relation_linear,
-        relation_linear_out,
         relation_norm_reduce,
         relation_linear_norm_reduce_output,
         relation_norm_reduce_seq,
@@ -164,14 +162,12 @@ def main() -> int:
     )
     from relation_lm.kernels.relation_select import (
         multi_relation_select_seq,
-        relation_select_packed,
+        relation_select_packed_expand_row,
         relation_select_packed_seq,
     )
     from relation_lm.inference import pack_sparse_cache_projection_weights
     from relation_lm.kernels.ring import (
-        relation_hidden_cache_update_ring,
         relation_hidden_cached_ring,
-        relation_select_packed_ring,
     )
     from relation_lm.workloads import (
         CONFIGS,
@@ -215,8 +211,6 @@ def main() -> int:
         ring_position: decode at that absolute position over ring-buffer caches of
         the cfg3 length (the *_ring ops; rows written at position mod length)."""
         ring = ring_position is not None
-        select_op = relation_select_packed_ring if ring else relation_select_packed
-        update_op = relation_hidden_cache_update_ring if ring else relation_hidden_cache_update
         cached_op = relation_hidden_cached_ring if ring else relation_hidden_cached
         decode = {}
         for batch in (1, 8):
@@ -254,15 +248,12 @@ def main() -> int:
                     dsel["partner_block_mean"], dsel["partner_block_std"],
                     rc["anchor_conv_weight"], rc["partner_conv_weight"], dcfg.block_size,
                     ring=ring)
-                a_, s_, p_, ps_ = select_op(*dargs)
-                if batch == 1:
-                    hid = update_op(
-                        dexp, dred["operand_cache"], a_, p_, dred["anchor_weight"],
-                        dred["partner_weight"], dred["product_weight"], dred["first_bias"], position)
-                else:  # separate update: the row is written straight into the cache
-                    relation_linear_out(dred["operand_cache"][:, t], dred["expanded_weight"],
-                                        dred["expanded_bias"], dexp[:, t])
-                    hid = cached_op(dexp, dred["operand_cache"], a_, p_, dred["product_weight"])
+                # selection, with the token's expanded-cache row projected by extra
+                # workgroups of the same launch; then the cached hidden (B=1 and B=8)
+                a_, s_, p_, ps_ = relation_select_packed_expand_row(
+                    *dargs, dred["operand_cache"], dred["expanded_weight"],
+                    dred["expanded_bias"], dexp, ring)
+                hid = cached_op(dexp, dred["operand_cache"], a_, p_, dred["product_weight"])
                 # second linear (split over the hidden dim) and norm-reduce with the
                 # output-head preparation as its epilogue, the partials summed there
                 return relation_linear_norm_reduce_output(

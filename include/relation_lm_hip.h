@@ -107,6 +107,37 @@ hipError_t rlm_relation_select_packed_seq(
     const rlm_tensor* out_partner_score, hipStream_t stream);
 
 /*
+ * rlm_relation_select_packed (decode form) plus the token's expanded-cache row:
+ * no reference op.  Replaces, in one launch, relation_select_packed
+ * (relation_select.py:311-382) and the reference decode's row projection
+ * (docs/benchmarks.md:80-81: "separate cuBLAS cache projection" for B > 1; the
+ * fresh row relation_hidden_cache_update writes, relation_reduce.py:215-251,
+ * for B == 1): for every batch row b,
+ *   expanded_cache[b, r] = expanded_weight . operand_cache[b, r] + expanded_bias,
+ * r = position (ring != 0: position mod T), in bf16 with fp32 sums; nothing is
+ * written when the position is outside a linear cache.  The selection is the
+ * same as rlm_relation_select_packed(_ring).  operand_cache [B,T,R] bf16
+ * (R in {32,64,96,128}), expanded_weight [N,R] bf16 (N % 16 == 0),
+ * expanded_bias [N] or NULL, expanded_cache [B,T,N] bf16.  Where the decode
+ * selection kernel applies, the row is projected by extra workgroups of its
+ * launch, beside the B selection workgroups; otherwise by a launch of its own.
+ */
+hipError_t rlm_relation_select_packed_expand_row(
+    const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
+    const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
+    const rlm_tensor* anchor_block_std, const rlm_tensor* anchor_gamma,
+    const rlm_tensor* anchor_bias, const rlm_tensor* partner_base,
+    const rlm_tensor* partner_anchor_cache, const rlm_tensor* partner_keys,
+    const rlm_tensor* partner_block_mean, const rlm_tensor* partner_block_std,
+    const rlm_tensor* partner_gamma, const rlm_tensor* partner_bias,
+    const rlm_tensor* position, int64_t local_window, int64_t top_blocks,
+    int64_t k_out, int32_t strict_valid, const rlm_tensor* operand_cache,
+    const rlm_tensor* expanded_weight, const rlm_tensor* expanded_bias,
+    const rlm_tensor* expanded_cache, int32_t ring, const rlm_tensor* out_anchor,
+    const rlm_tensor* out_anchor_score, const rlm_tensor* out_partner,
+    const rlm_tensor* out_partner_score, hipStream_t stream);
+
+/*
  * Routed multi-anchor selection: no reference kernel.  The reference has only
  * the dense form, MultiAnchorRelationBlock._select_distinct_anchors and
  * forward's partner selection (src/relation_lm/models/multi_relation_blocks.py:69-147);

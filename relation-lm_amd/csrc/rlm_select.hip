@@ -1494,6 +1494,65 @@ bool decode_params(const SelectParams& p, const Geometry& g, int act, int stat,
   return select_decode_layout(dp);
 }
 
+// The decode step's expanded-cache row, requested with the selection: for
+// every batch row b, expanded_cache[b, row] = expanded_weight . operand_cache[b,
+// row] + expanded_bias, row = position (linear caches) or position mod T (ring).
+struct RowArgs {
+  const rlm_tensor* operand;  // [B, T, R] bf16
+  const rlm_tensor* weight;   // [N, R] bf16
+  const rlm_tensor* bias;     // [N] or null
+  const rlm_tensor* cache;    // [B, T, N] bf16, row written
+};
+
+hipError_t fill_expand_row(const RowArgs& a, const Geometry& g, const rlm_tensor* position,
+                           bool ring, ExpandRowParams& x) {
+  RLM_TRY(check_tensor(a.operand, "operand_cache", 3));
+  RLM_TRY(check_dtype_is(a.operand, "operand_cache", RLM_BF16));
+  RLM_TRY(check_dim(a.operand, "operand_cache", 0, g.B));
+  RLM_TRY(check_dim(a.operand, "operand_cache", 1, g.T));
+  const int64_t R = a.operand->shape[2];
+  RLM_REQUIRE(R >= 32 && R <= 128 && R % 32 == 0,
+              "operand_cache: the expanded row needs a relation dim of 32, 64, 96 or 128, got %lld",
+              (long long)R);
+  RLM_TRY(check_tensor(a.weight, "expanded_weight", 2));
+  RLM_TRY(check_dtype_is(a.weight, "expanded_weight", RLM_BF16));
+  RLM_TRY(check_dim(a.weight, "expanded_weight", 1, R));
+  const int64_t N = a.weight->shape[0];
+  RLM_REQUIRE(N >= 16 && N % 16 == 0,
+              "expanded_weight: output width must be a positive multiple of 16, got %lld",
+              (long long)N);
+  if (a.bias != nullptr) {
+    RLM_TRY(check_tensor(a.bias, "expanded_bias", 1));
+    RLM_TRY(check_dtype_float(a.bias, "expanded_bias"));
+    RLM_TRY(check_dim(a.bias, "expanded_bias", 0, N));
+  }
+  RLM_TRY(check_tensor(a.cache, "expanded_cache", 3));
+  RLM_TRY(check_dtype_is(a.cache, "expanded_cache", RLM_BF16));
+  RLM_TRY(check_dim(a.cache, "expanded_cache", 0, g.B));
+  RLM_TRY(check_dim(a.cache, "expanded_cache", 1, g.T));
+  RLM_TRY(check_dim(a.cache, "expanded_cache", 2, N));
+  for (const rlm_tensor* t : {a.operand, a.weight, a.cache})
+    RLM_TRY(aligned16(t, "expanded-row tensors"));
+  const int64_t op_bytes = g.B * g.T * R * 2, w_bytes = N * R * 2;
+  RLM_REQUIRE(op_bytes < (int64_t(1) << 31) && w_bytes < (int64_t(1) << 31),
+              "operand_cache / expanded_weight: at most 2 GiB each");
+  x.op = static_cast<const bf16*>(a.operand->data);
+  x.w = static_cast<const bf16*>(a.weight->data);
+  x.bias = a.bias != nullptr ? a.bias->data : nullptr;
+  x.bias_dtype = a.bias != nullptr ? a.bias->dtype : RLM_F32;
+  x.cache = static_cast<bf16*>(a.cache->data);
+  x.pos = position->data;
+  x.pos_dtype = position->dtype;
+  x.B = g.B;
+  x.T = g.T;
+  x.KS = static_cast<int>(R / 32);
+  x.N = static_cast<int>(N);
+  x.ring = ring ? 1 : 0;
+  x.op_bytes = static_cast<uint32_t>(op_bytes);
+  x.w_bytes = static_cast<uint32_t>(w_bytes);
+  return hipSuccess;
+}
+
 hipError_t select_packed_impl(
     bool seq, bool ring, const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
     const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
@@ -1504,7 +1563,8 @@ hipError_t select_packed_impl(
     const rlm_tensor* partner_gamma, const rlm_tensor* partner_bias, const rlm_tensor* position,
     int64_t local_window, int64_t top_blocks, int64_t k_out, int32_t strict_valid,
     const rlm_tensor* out_anchor, const rlm_tensor* out_anchor_score,
-    const rlm_tensor* out_partner, const rlm_tensor* out_partner_score, hipStream_t stream) {
+    const rlm_tensor* out_partner, const rlm_tensor* out_partner_score, hipStream_t stream,
+    const RowArgs* xrow = nullptr) {
   clear_error();
   const int qd = seq ? 3 : 2;  // rank of query-side tensors
   RLM_TRY(check_tensor(anchor_query, "anchor_query", qd));
@@ -1559,6 +1619,12 @@ hipError_t select_packed_impl(
   RLM_TRY(check_position(position, "position", g, seq, p));
   RLM_TRY(check_outputs(out_anchor, out_anchor_score, "anchor", g, seq, -1));
   RLM_TRY(check_outputs(out_partner, out_partner_score, "partner", g, seq, k_out));
+  ExpandRowParams xr{};
+  if (xrow != nullptr) {
+    RLM_REQUIRE(!seq, "the expanded-cache row is computed with the decode form only");
+    const hipError_t xe = fill_expand_row(*xrow, g, position, ring, xr);
+    if (xe != hipSuccess) return xe;
+  }
   hipError_t err = finish_params(p, g, local_window, top_blocks, k_out, strict_valid,
                                  act == RLM_F32 ? 4 : 2);
   if (err != hipSuccess) return err;
@@ -1601,11 +1667,19 @@ hipError_t select_packed_impl(
     if (decode_params(p, g, act, stat, position, anchor_query, anchor_router_query, partner_base,
                       partner_anchor_cache, anchor_keys, partner_keys, anchor_block_mean,
                       anchor_block_std, anchor_gamma, anchor_bias, partner_block_mean,
-                      partner_block_std, partner_gamma, partner_bias, dp))
+                      partner_block_std, partner_gamma, partner_bias, dp)) {
+      if (xrow != nullptr) {
+        // The expanded row on workgroups beside the B selection workgroups.
+        dp.x = xr;
+        dp.xgroups = (xr.N + kExpandCols - 1) / kExpandCols;
+      }
       return select_decode_launch(dp, act, stat, ring, stream);
+    }
   }
-  if (ring) return launch_select<kPacked, true>(p, act, stat, stream);
-  return launch_select<kPacked>(p, act, stat, stream);
+  const hipError_t se = ring ? launch_select<kPacked, true>(p, act, stat, stream)
+                             : launch_select<kPacked>(p, act, stat, stream);
+  if (se != hipSuccess || xrow == nullptr) return se;
+  return expand_row_launch(xr, stream);
 }
 
 bool check_slot_rows(const rlm_tensor* t, const char* name, int64_t d0, int64_t d1, int64_t S,
@@ -1870,6 +1944,28 @@ extern "C" hipError_t rlm_relation_select_packed_seq(
                             partner_block_std, partner_gamma, partner_bias, positions,
                             local_window, top_blocks, k_out, strict_valid, out_anchor,
                             out_anchor_score, out_partner, out_partner_score, stream);
+}
+
+extern "C" hipError_t rlm_relation_select_packed_expand_row(
+    const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
+    const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
+    const rlm_tensor* anchor_block_std, const rlm_tensor* anchor_gamma,
+    const rlm_tensor* anchor_bias, const rlm_tensor* partner_base,
+    const rlm_tensor* partner_anchor_cache, const rlm_tensor* partner_keys,
+    const rlm_tensor* partner_block_mean, const rlm_tensor* partner_block_std,
+    const rlm_tensor* partner_gamma, const rlm_tensor* partner_bias, const rlm_tensor* position,
+    int64_t local_window, int64_t top_blocks, int64_t k_out, int32_t strict_valid,
+    const rlm_tensor* operand_cache, const rlm_tensor* expanded_weight,
+    const rlm_tensor* expanded_bias, const rlm_tensor* expanded_cache, int32_t ring,
+    const rlm_tensor* out_anchor, const rlm_tensor* out_anchor_score,
+    const rlm_tensor* out_partner, const rlm_tensor* out_partner_score, hipStream_t stream) {
+  const RowArgs x{operand_cache, expanded_weight, expanded_bias, expanded_cache};
+  return select_packed_impl(false, ring != 0, anchor_query, anchor_keys, anchor_router_query,
+                            anchor_block_mean, anchor_block_std, anchor_gamma, anchor_bias,
+                            partner_base, partner_anchor_cache, partner_keys, partner_block_mean,
+                            partner_block_std, partner_gamma, partner_bias, position,
+                            local_window, top_blocks, k_out, strict_valid, out_anchor,
+                            out_anchor_score, out_partner, out_partner_score, stream, &x);
 }
 
 extern "C" hipError_t rlm_relation_select_packed_ring(

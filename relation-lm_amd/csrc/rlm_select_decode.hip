@@ -26,6 +26,7 @@
 //     both use wave maxima that stay in VALU (DPP and row swaps).
 #include "rlm_common.hpp"
 #include "rlm_select_decode.hpp"
+#include "rlm_tile_util.hpp"
 
 namespace rlm {
 namespace {
@@ -109,9 +110,80 @@ struct Shared {
   int* sel;                // [TOP] picked blocks, then [TOP] validity flags
 };
 
+// Columns [kExpandCols * grp, + kExpandCols) of the token's expanded-cache row
+// for every batch row: wave w takes two 16-column tiles, lane (r16, g) batch
+// row b0 + r16 and k-pieces 8g .. 8g + 7 of each 32-wide k-step.  The sums are
+// v_mfma_f32_16x16x32_bf16 with the weight rows as A, k-steps in order from
+// zero, the bias added in fp32 and one bf16 rounding (relation_linear's
+// smallk_kernel order for the same tile).  Every load of a row tile is issued
+// before the first product.
+__device__ void expand_row_group(const ExpandRowParams& x, int grp, int tid) {
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int64_t t = index_at(x.pos, x.pos_dtype, 0);
+  if (t < 0 || (!x.ring && t >= x.T)) return;  // no row to write (uniform)
+  const int64_t row = x.ring ? (t & (x.T - 1)) : t;
+  const uint32_t R = 32u * static_cast<uint32_t>(x.KS);
+  const uint32_t N = static_cast<uint32_t>(x.N);
+  const rsrc_t opr = make_rsrc(x.op, x.op_bytes);
+  const rsrc_t wr = make_rsrc(x.w, x.w_bytes);
+  const bool is32 = x.bias_dtype == RLM_F32;
+  const bool has_bias = x.bias != nullptr;
+  const rsrc_t br = make_rsrc(x.bias, N * (is32 ? 4u : 2u));
+  for (int64_t b0 = 0; b0 < x.B; b0 += 16) {
+    const int64_t b = b0 + r16;
+    const bool bv = b < x.B;
+    const uint32_t orow = static_cast<uint32_t>((bv ? b : 0) * x.T + row);
+    uint4 af[4], wf[2][4], bq[2];
+    uint2 bh[2];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      af[s] = buf_load_b128(opr, bv && s < x.KS ? (orow * R + 32u * s + 8u * g) * 2u : kNoOffset);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t n0 = static_cast<uint32_t>(grp * kExpandCols + wave * 32 + j * 16);
+      const bool live = n0 < N;
+      const uint32_t n = n0 + r16;  // weight row of the A operand
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        wf[j][s] = buf_load_b128(wr, live && s < x.KS ? (n * R + 32u * s + 8u * g) * 2u : kNoOffset);
+      const uint32_t nc = n0 + 4u * g;  // this lane's output columns
+      bq[j] = buf_load_b128(br, live && has_bias && is32 ? 4u * nc : kNoOffset);
+      bh[j] = buf_load_b64(br, live && has_bias && !is32 ? 2u * nc : kNoOffset);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t n0 = static_cast<uint32_t>(grp * kExpandCols + wave * 32 + j * 16);
+      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        if (s < x.KS) acc = mfma_bf16(wf[j][s], af[s], acc);
+      const uint32_t w16[4] = {bh[j].x & 0xffffu, bh[j].x >> 16, bh[j].y & 0xffffu, bh[j].y >> 16};
+      const uint32_t w32[4] = {bq[j].x, bq[j].y, bq[j].z, bq[j].w};
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] = acc[e] + decode_float(FloatWords{w32[e], w16[e]}, x.bias_dtype);
+      // Lane (r16, g) holds batch row b, columns n0 + 4g .. + 3.
+      if (bv && n0 < N)
+        *reinterpret_cast<uint2*>(x.cache + (static_cast<size_t>(b) * x.T + row) * N + n0 + 4 * g) =
+            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) expand_row_kernel(const ExpandRowParams x) {
+  expand_row_group(x, static_cast<int>(blockIdx.x), static_cast<int>(threadIdx.x));
+}
+
 template <typename TA, typename TS, bool RING>
 __global__ void __launch_bounds__(kThreads) select_decode_kernel(const DecodeParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
+  if (blockIdx.x >= p.B) {  // workgroup-uniform: the expanded-row workgroups
+    expand_row_group(p.x, static_cast<int>(blockIdx.x - p.B), static_cast<int>(threadIdx.x));
+    return;
+  }
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int64_t b = blockIdx.x;
@@ -481,7 +553,7 @@ bool select_decode_layout(DecodeParams& p) {
 hipError_t select_decode_launch(const DecodeParams& p, int act_dtype, int stat_dtype, bool ring,
                                 hipStream_t stream) {
   if (p.B == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>(p.B));
+  const dim3 grid(static_cast<unsigned>(p.B + p.xgroups));
   const size_t lds = static_cast<size_t>(p.lds_total);
 #define RLM_DECODE_CASE(TA_ID, TA, TS_ID, TS, RING)                                           \
   if (act_dtype == TA_ID && stat_dtype == TS_ID && ring == RING) {                          \
@@ -508,6 +580,14 @@ hipError_t select_decode_launch(const DecodeParams& p, int act_dtype, int stat_d
 #undef RLM_DECODE_CASE
   set_error("relation_select: unsupported dtype combination for the decode kernel");
   return hipErrorInvalidValue;
+}
+
+hipError_t expand_row_launch(const ExpandRowParams& x, hipStream_t stream) {
+  const int groups = (x.N + kExpandCols - 1) / kExpandCols;
+  if (x.B == 0 || groups == 0) return hipSuccess;
+  hipLaunchKernelGGL(expand_row_kernel, dim3(static_cast<unsigned>(groups)), dim3(kThreads), 0,
+                     stream, x);
+  return launch_status("relation_select (expanded row)");
 }
 
 }  // namespace rlm

@@ -116,3 +116,50 @@ def multi_relation_select_seq(
         anchor_gamma, anchor_bias, partner_base, partner_anchor_cache, partner_keys,
         partner_block_mean, partner_block_std, partner_gamma, partner_bias, positions,
         local_window, top_blocks, k_out, strict_valid)
+
+
+def relation_select_packed_expand_row(
+    anchor_query: Tensor,
+    anchor_keys: Tensor,
+    anchor_router_query: Tensor,
+    anchor_block_mean: Tensor,
+    anchor_block_std: Tensor,
+    anchor_gamma: Tensor,
+    anchor_bias: Tensor,
+    partner_base: Tensor,
+    partner_anchor_cache: Tensor,
+    partner_keys: Tensor,
+    partner_block_mean: Tensor,
+    partner_block_std: Tensor,
+    partner_gamma: Tensor,
+    partner_bias: Tensor,
+    position: Tensor,
+    local_window: int,
+    top_blocks: int,
+    k_out: int,
+    strict_valid: bool,
+    operand_cache: Tensor,
+    expanded_weight: Tensor,
+    expanded_bias: Tensor | None,
+    expanded_cache: Tensor,
+    ring: bool = False,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Decode-form ``relation_select_packed`` (``ring``: ``relation_select_packed_ring``)
+    that also writes the token's expanded-cache row in place:
+    ``expanded_cache[:, r] = F.linear(operand_cache[:, r], expanded_weight, expanded_bias)``
+    with r the position (ring: position mod T), read on the device.
+
+    The reference decode builds that row with a separate BLAS projection for B > 1
+    (docs/benchmarks.md:80-81) or inside ``relation_hidden_cache_update`` for B == 1
+    (relation_reduce.py:215-251); afterwards ``relation_hidden_cached`` serves both.
+    The selection launch runs one workgroup per batch row on a few CUs, so the row
+    is projected by extra workgroups of the same launch on CUs that would idle.
+    bf16 caches and weights, relation dim 32..128, width a multiple of 16.
+    """
+    return torch.ops.relation_lm.relation_select_packed_expand_row(
+        anchor_query, anchor_keys, anchor_router_query, anchor_block_mean, anchor_block_std,
+        anchor_gamma, anchor_bias, partner_base, partner_anchor_cache, partner_keys,
+        partner_block_mean, partner_block_std, partner_gamma, partner_bias, position,
+        local_window, top_blocks, k_out, strict_valid, operand_cache, expanded_weight,
+        expanded_bias, expanded_cache, ring)
+

@@ -171,6 +171,11 @@ def op_cases(device):
     cases.append(("relation_select_packed", ops.relation_select_packed.default, dec_args))
     cases.append(("relation_select_packed_seq", ops.relation_select_packed_seq.default,
                   seq_args))
+    xcache = relation_linear(red["operand_cache"], red["expanded_weight"], red["expanded_bias"])
+    cases.append(("relation_select_packed_expand_row",
+                  ops.relation_select_packed_expand_row.default,
+                  dec_args + (red["operand_cache"], red["expanded_weight"], red["expanded_bias"],
+                              xcache, False)))
     ring_pos = torch.tensor(3 * t + 17, device=device)
     cases.append(("relation_select_packed_ring", ops.relation_select_packed_ring.default,
                   dec_args[:14] + (ring_pos,) + dec_args[15:]))
@@ -287,7 +292,7 @@ def op_cases(device):
 
 
 OP_NAMES = ("relation_select_packed", "relation_select_packed_seq",
-            "relation_select_packed_ring", "anchor_select", "partner_topk",
+            "relation_select_packed_expand_row", "relation_select_packed_ring", "anchor_select", "partner_topk",
             "multi_relation_select_seq", "relation_hidden_cached", "relation_hidden_cached_seq",
             "relation_hidden_cached_seq_out",
             "relation_hidden_cached_ring", "relation_hidden_cache_update",
