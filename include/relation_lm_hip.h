@@ -552,12 +552,15 @@ hipError_t rlm_linear(const rlm_tensor* input, const rlm_tensor* weight,
  *   S*K <= 64; D a multiple of 4, at most 2048.
  * Outputs: out [B,Tq,D] in hidden's dtype = hidden + sigmoid(gate) * context;
  *          context f32 [B,Tq,D] (the block's relation_context), or NULL.
+ * raw_bias [D] or NULL: added to every raw row as it is loaded (fp32), so
+ * the second Linear that produces raw may run without its bias.
  */
 hipError_t rlm_multi_relation_reduce_seq(
     const rlm_tensor* raw, const rlm_tensor* partner_scores, const rlm_tensor* norm_weight,
     const rlm_tensor* norm_bias, const rlm_tensor* slot_mix_logits,
     const rlm_tensor* residual_gate, const rlm_tensor* hidden, const rlm_tensor* positions,
-    double norm_eps, const rlm_tensor* out, const rlm_tensor* context, hipStream_t stream);
+    double norm_eps, const rlm_tensor* out, const rlm_tensor* context,
+    const rlm_tensor* raw_bias, hipStream_t stream);
 
 /*
  * Replaces nn.LayerNorm over the last dimension: the block's input_norm and

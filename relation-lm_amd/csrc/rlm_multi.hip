@@ -64,6 +64,8 @@ struct MultiReduceParams {
   float eps;
   void* out;                // [Q, D], hidden's dtype
   float* context;           // [Q, D] fp32 or null
+  const void* rb;           // [D] bias added to every raw row as it is loaded, or null
+  int rb_dtype;
 };
 
 // Row weight of lane l = (slot l / K, partner l % K), 0 for l >= S*K:
@@ -114,17 +116,20 @@ __global__ void __launch_bounds__(256) multi_reduce_kernel(const MultiReducePara
   const float score = p.scores[q * SK + (lane < SK ? lane : 0)];
   const TR* raw = static_cast<const TR*>(p.raw) + q * SK * static_cast<int64_t>(p.D);
   const TH* hid = static_cast<const TH*>(p.hidden) + q * static_cast<int64_t>(p.D);
-  F4Words gw[G], bw[G];
+  F4Words gw[G], bw[G], rbw[G];
   float4 h4[G];
+  const bool has_rb = p.rb != nullptr;  // uniform
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int g = lane + kWave * i;
     const int gs = g < groups ? g : 0;
     gw[i] = f4_issue(p.w, p.w_dtype, gs);
     bw[i] = f4_issue(p.b, p.b_dtype, gs);
+    rbw[i] = f4_issue(has_rb ? p.rb : p.b, has_rb ? p.rb_dtype : p.b_dtype, gs);
     h4[i] = load4(hid + 4 * gs);
   }
   float4 x[RB][G];
+  // raw row + the second Linear's bias (fp32 adds, as the GEMM epilogue would).
   auto load_batch = [&](int r0) {
 #pragma unroll
     for (int rr = 0; rr < RB; ++rr)
@@ -133,7 +138,8 @@ __global__ void __launch_bounds__(256) multi_reduce_kernel(const MultiReducePara
         const int g = lane + kWave * i;
         const bool in = r0 + rr < SK && g < groups;
         const float4 v = load4(raw + static_cast<int64_t>(in ? r0 + rr : 0) * p.D + 4 * (in ? g : 0));
-        x[rr][i] = in ? v : f4_zero();
+        const float4 c = has_rb ? f4_decode(rbw[i], p.rb_dtype) : f4_zero();
+        x[rr][i] = in ? make_float4(v.x + c.x, v.y + c.y, v.z + c.z, v.w + c.w) : f4_zero();
       }
   };
   load_batch(0);
@@ -341,7 +347,8 @@ extern "C" hipError_t rlm_multi_relation_reduce_seq(
     const rlm_tensor* raw, const rlm_tensor* partner_scores, const rlm_tensor* norm_weight,
     const rlm_tensor* norm_bias, const rlm_tensor* slot_mix_logits,
     const rlm_tensor* residual_gate, const rlm_tensor* hidden, const rlm_tensor* positions,
-    double norm_eps, const rlm_tensor* out, const rlm_tensor* context, hipStream_t stream) {
+    double norm_eps, const rlm_tensor* out, const rlm_tensor* context, const rlm_tensor* raw_bias,
+    hipStream_t stream) {
   clear_error();
   RLM_TRY(check_tensor(partner_scores, "partner_scores", 4));
   RLM_TRY(check_dtype_is(partner_scores, "partner_scores", RLM_F32));
@@ -420,6 +427,11 @@ extern "C" hipError_t rlm_multi_relation_reduce_seq(
   p.pos_dtype = positions->dtype;
   p.eps = static_cast<float>(norm_eps);
   p.out = out->data;
+  if (raw_bias != nullptr) {
+    RLM_TRY(check_vector(raw_bias, "raw_bias", D));
+    p.rb = raw_bias->data;
+    p.rb_dtype = raw_bias->dtype;
+  }
   if (p.Q == 0) return hipSuccess;
   const int groups = static_cast<int>((D / 4 + kWave - 1) / kWave);
   if (groups <= 1) return launch_multi_reduce<1>(p, raw->dtype, hidden->dtype, stream);

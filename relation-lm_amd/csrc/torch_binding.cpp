@@ -850,17 +850,20 @@ at::Tensor multi_relation_reduce_seq(const at::Tensor& raw, const at::Tensor& pa
                                     const at::Tensor& norm_weight, const at::Tensor& norm_bias,
                                     const at::Tensor& slot_mix_logits,
                                     const at::Tensor& residual_gate, const at::Tensor& hidden,
-                                    const at::Tensor& positions, double norm_eps) {
+                                    const at::Tensor& positions, double norm_eps,
+                                    const c10::optional<at::Tensor>& raw_bias) {
   const char* op = "relation_lm::multi_relation_reduce_seq";
+  const at::Tensor rb = raw_bias.has_value() ? *raw_bias : at::Tensor();
   c10::DeviceGuard guard(raw.device());
   hipStream_t stream = device_stream(op, {&raw, &partner_scores, &norm_weight, &norm_bias,
-                                          &slot_mix_logits, &residual_gate, &hidden, &positions});
+                                          &slot_mix_logits, &residual_gate, &hidden, &positions,
+                                          &rb});
   TORCH_CHECK(raw.dim() == 5 && partner_scores.dim() == 4, op,
               ": raw must be [B,Tq,S,K,D] and partner_scores [B,Tq,S,K]");
   const at::Tensor rows = raw.reshape({raw.size(0), raw.size(1), raw.size(2) * raw.size(3),
                                        raw.size(4)});
   at::Tensor out = at::empty_like(hidden, hidden.options().memory_format(at::MemoryFormat::Contiguous));
-  rlm_tensor d[9] = {desc(rows, "raw"),
+  rlm_tensor d[10] = {desc(rows, "raw"),
                      desc(partner_scores, "partner_scores"),
                      desc(norm_weight, "norm_weight"),
                      desc(norm_bias, "norm_bias"),
@@ -868,9 +871,12 @@ at::Tensor multi_relation_reduce_seq(const at::Tensor& raw, const at::Tensor& pa
                      desc(residual_gate, "residual_gate"),
                      desc(hidden, "hidden"),
                      desc(positions, "positions"),
-                     desc(out, "out")};
+                     desc(out, "out"),
+                     rlm_tensor{}};
+  if (rb.defined()) d[9] = desc(rb, "raw_bias");
   check(rlm_multi_relation_reduce_seq(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7],
-                                      norm_eps, &d[8], nullptr, stream),
+                                      norm_eps, &d[8], nullptr, rb.defined() ? &d[9] : nullptr,
+                                      stream),
         op);
   return out;
 }
@@ -1014,7 +1020,7 @@ TORCH_LIBRARY(relation_lm, m) {
   m.def(
       "multi_relation_reduce_seq(Tensor raw, Tensor partner_scores, Tensor norm_weight, Tensor "
       "norm_bias, Tensor slot_mix_logits, Tensor residual_gate, Tensor hidden, Tensor positions, "
-      "float norm_eps) -> Tensor");
+      "float norm_eps, Tensor? raw_bias=None) -> Tensor");
   m.def("layer_norm(Tensor input, Tensor weight, Tensor bias, float eps) -> Tensor");
   // Norm-reduce with the last-token output preparation as its epilogue
   // (roadmap item of the reference, README.md:150-151; relation_lm.py:203-206).

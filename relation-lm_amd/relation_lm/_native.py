@@ -132,7 +132,7 @@ def _register_fakes() -> None:
 
     @torch.library.register_fake("relation_lm::multi_relation_reduce_seq")
     def _(raw, partner_scores, norm_weight, norm_bias, slot_mix_logits, residual_gate, hidden,
-          positions, norm_eps):
+          positions, norm_eps, raw_bias=None):
         return torch.empty_like(hidden, memory_format=torch.contiguous_format)
 
     def fake_norm_output(raw, partner_scores, norm_weight, norm_bias, position, norm_eps, query,

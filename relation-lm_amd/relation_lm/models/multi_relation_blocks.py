@@ -14,10 +14,10 @@ multi-anchor selection (local window plus the top blocks of a block router,
   relation MLP Linear -> GELU     relation_lm::relation_hidden_cached_seq_out
     (factorized: operand cache, expanded cache = [W_a+W_d; W_p-W_d] op + [b; 0];
     stored in bf16 when the second Linear is bf16)
-  relation MLP second Linear      torch.addmm(out_dtype=float32): a plain bias GEMM,
-    on the ROCm BLAS (hipBLASLt) for 16-bit weights -- measured 1.8x the
-    hand-written tile GEMM at cfg5's [98304, 3072] x [3072, 768] --
-    relation_lm::relation_linear otherwise
+  relation MLP second Linear      torch.mm(out_dtype=float32): a plain GEMM on the
+    ROCm BLAS (hipBLASLt) for 16-bit weights -- measured 1.8x the hand-written
+    tile GEMM at cfg5's [98304, 3072] x [3072, 768] -- its bias added by the
+    slot reduce as it loads the rows; relation_lm::relation_linear otherwise
   LayerNorm, partner softmax,     relation_lm::multi_relation_reduce_seq
     slot mix, residual gate
   final_norm (stack)              relation_lm::layer_norm
@@ -51,21 +51,20 @@ ops = torch.ops.relation_lm
 
 
 
-def _second_linear(rows: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
-    """fp32 ``rows @ weight.T + bias`` of the relation MLP's second Linear (the
-    reference's plain ``nn.Linear``, multi_relation_blocks.py:47-52).
+def _second_linear(rows: Tensor, weight: Tensor, bias: Tensor | None) -> tuple[Tensor, Tensor | None]:
+    """fp32 ``rows @ weight.T`` of the relation MLP's second Linear (the reference's
+    plain ``nn.Linear``, multi_relation_blocks.py:47-52) and the bias still to add.
 
-    With 16-bit weights this is a plain bias GEMM and runs on the ROCm BLAS
-    (``addmm`` with an fp32 output: hipBLASLt, bias in its epilogue); fp32 weights
-    take ``relation_linear``'s fp32 kernel."""
+    With 16-bit weights this is a plain GEMM on the ROCm BLAS (``mm`` with an fp32
+    output: hipBLASLt) and the bias is returned for the slot reduce to add as it
+    loads the rows (a bias in ``addmm`` costs a copy of the whole output first);
+    fp32 weights take ``relation_linear``'s fp32 kernel with the bias."""
     if weight.dtype not in (torch.bfloat16, torch.float16) or rows.dtype != weight.dtype:
-        return ops.relation_linear(rows, weight, bias, torch.float32)
+        return ops.relation_linear(rows, weight, bias, torch.float32), None
     flat = rows.reshape(-1, rows.shape[-1])
-    if bias is None:
-        out = torch.mm(flat, weight.t(), out_dtype=torch.float32)
-    else:
-        out = torch.addmm(bias.float(), flat, weight.t(), out_dtype=torch.float32)
-    return out.view(*rows.shape[:-1], weight.shape[0])
+    out = torch.mm(flat, weight.t(), out_dtype=torch.float32)
+    return out.view(*rows.shape[:-1], weight.shape[0]), bias
+
 
 @dataclass
 class MultiRelationBlockConfig:
@@ -233,11 +232,11 @@ class MultiAnchorRelationBlock(nn.Module):
                 sel["anchor"][b:b + 1].reshape(1, length * h),
                 sel["partner"][b:b + 1].reshape(1, length * h, k_count), sel["product_weight"],
                 rows)
-            raw = _second_linear(rows, mlp[2].weight, mlp[2].bias)
+            raw, raw_bias = _second_linear(rows, mlp[2].weight, mlp[2].bias)
             outputs.append(ops.multi_relation_reduce_seq(
                 raw.view(1, length, h, k_count, d), sel["partner_score"][b:b + 1], mlp[3].weight,
                 mlp[3].bias, self.slot_mix_logits, self.residual_gate, hidden[b:b + 1],
-                sel["positions"], mlp[3].eps))
+                sel["positions"], mlp[3].eps, raw_bias))
         return outputs[0] if batch == 1 else torch.cat(outputs, dim=0)
 
     def forward(self, hidden: Tensor, memory: Tensor) -> tuple[Tensor, dict[str, Tensor]]:

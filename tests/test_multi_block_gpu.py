@@ -77,6 +77,26 @@ def test_multi_reduce_op(device, shape, raw_dtype, hid_dtype, pos2d):
         assert (np.abs(got - expected) <= ulp + 1e-5).all()
 
 
+@pytest.mark.parametrize("bias_dtype", [torch.float32, torch.bfloat16])
+def test_multi_reduce_raw_bias(device, bias_dtype):
+    # raw_bias is added (fp32) to every raw row as the rows are loaded: the
+    # result equals the op on raw + bias bit for bit.
+    g = torch.Generator().manual_seed(77)
+    b, tq, s, k, d = 2, 9, 4, 6, 768
+    raw = torch.randn(b, tq, s, k, d, generator=g)
+    scores = torch.randn(b, tq, s, k, generator=g)
+    rb = (0.5 * torch.randn(d, generator=g)).to(bias_dtype)
+    w = 1 + 0.1 * torch.randn(d, generator=g)
+    nb = 0.1 * torch.randn(d, generator=g)
+    args = [t.to(device) for t in (scores, w, nb, torch.randn(s, generator=g), torch.tensor(0.3),
+                                   torch.randn(b, tq, d, generator=g).to(torch.bfloat16),
+                                   torch.arange(tq))]
+    got = ops.multi_relation_reduce_seq(raw.to(device), *args, 1e-5, rb.to(device))
+    ref = ops.multi_relation_reduce_seq((raw + rb.float()).to(device), *args, 1e-5)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+
+
 @pytest.mark.parametrize("shape,dtype", [((3, 5, 768), torch.float32), ((3, 5, 768), torch.bfloat16),
                                          ((7, 64), torch.float32), ((2, 3, 4, 2048), torch.bfloat16),
                                          ((11, 12), torch.float32)])
