@@ -129,7 +129,6 @@ __global__ void __launch_bounds__(256) multi_reduce_kernel(const MultiReducePara
     h4[i] = load4(hid + 4 * gs);
   }
   float4 x[RB][G];
-  // raw row + the second Linear's bias (fp32 adds, as the GEMM epilogue would).
   auto load_batch = [&](int r0) {
 #pragma unroll
     for (int rr = 0; rr < RB; ++rr)
@@ -138,11 +137,28 @@ __global__ void __launch_bounds__(256) multi_reduce_kernel(const MultiReducePara
         const int g = lane + kWave * i;
         const bool in = r0 + rr < SK && g < groups;
         const float4 v = load4(raw + static_cast<int64_t>(in ? r0 + rr : 0) * p.D + 4 * (in ? g : 0));
-        const float4 c = has_rb ? f4_decode(rbw[i], p.rb_dtype) : f4_zero();
-        x[rr][i] = in ? make_float4(v.x + c.x, v.y + c.y, v.z + c.z, v.w + c.w) : f4_zero();
+        x[rr][i] = in ? v : f4_zero();
       }
   };
   load_batch(0);
+  // The second Linear's bias, decoded once and added to each raw row before its
+  // statistics (fp32 adds, as the GEMM epilogue would).  Zero without a bias and
+  // on lanes past the row, whose row values must stay zero for the row sums.
+  float4 rb4[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i)
+    rb4[i] = has_rb && lane + kWave * i < groups ? f4_decode(rbw[i], p.rb_dtype) : f4_zero();
+  auto add_bias = [&]() {
+#pragma unroll
+    for (int rr = 0; rr < RB; ++rr)
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        x[rr][i].x += rb4[i].x;
+        x[rr][i].y += rb4[i].y;
+        x[rr][i].z += rb4[i].z;
+        x[rr][i].w += rb4[i].w;
+      }
+  };
   const float weight = row_weight(p, score, t, lane);
   const float inv_d = 1.0f / static_cast<float>(p.D);
   float4 acc[G];
@@ -151,6 +167,7 @@ __global__ void __launch_bounds__(256) multi_reduce_kernel(const MultiReducePara
   float wsum = 0.0f;
   for (int r0 = 0; r0 < SK; r0 += RB) {
     if (r0 > 0) load_batch(r0);
+    if (has_rb) add_bias();  // uniform
 #pragma unroll
     for (int rr = 0; rr < RB; ++rr) {
       if (r0 + rr >= SK) break;

@@ -78,11 +78,13 @@ def test_multi_reduce_op(device, shape, raw_dtype, hid_dtype, pos2d):
 
 
 @pytest.mark.parametrize("bias_dtype", [torch.float32, torch.bfloat16])
-def test_multi_reduce_raw_bias(device, bias_dtype):
+@pytest.mark.parametrize("d", [768, 200])
+def test_multi_reduce_raw_bias(device, bias_dtype, d):
     # raw_bias is added (fp32) to every raw row as the rows are loaded: the
-    # result equals the op on raw + bias bit for bit.
+    # result equals the op on raw + bias bit for bit.  d = 200 leaves lanes of
+    # the last column group past the row (they must stay zero).
     g = torch.Generator().manual_seed(77)
-    b, tq, s, k, d = 2, 9, 4, 6, 768
+    b, tq, s, k = 2, 9, 4, 6
     raw = torch.randn(b, tq, s, k, d, generator=g)
     scores = torch.randn(b, tq, s, k, generator=g)
     rb = (0.5 * torch.randn(d, generator=g)).to(bias_dtype)
