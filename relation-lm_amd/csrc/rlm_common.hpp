@@ -121,6 +121,32 @@ __device__ __forceinline__ uint16_t buf_load_b16(rsrc_t r, uint32_t off) {
 __device__ __forceinline__ void buf_store_f32(float v, rsrc_t r, uint32_t off) {
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
 }
+// 16 bytes per lane from global memory straight into LDS: lane i's bytes land
+// at lds_addr + 16*i (lds_addr wave-uniform, an LDS byte address).  Issued as
+// inline assembly so that the compiler does not follow it with a full
+// vmcnt(0) before the next LDS access; the caller waits (s_waitcnt vmcnt +
+// barrier) before the data is read.  The LDS base travels in M0, passed as an
+// operand bound to that register ("{m0}"), so the compiler writes M0 itself
+// and knows it holds this value.
+__device__ __forceinline__ void lds_dma16(rsrc_t r, uint32_t lds_addr, uint32_t voff) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(r), "{m0}"(lds_addr)
+               : "memory");
+}
+// The same with a wave-uniform byte offset added to every lane's (soff, an SGPR).
+__device__ __forceinline__ void lds_dma16(rsrc_t r, uint32_t lds_addr, uint32_t voff,
+                                          uint32_t soff) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(r), "s"(soff), "{m0}"(lds_addr)
+               : "memory");
+}
+// s_waitcnt immediate that waits until at most n vector-memory operations of
+// this wave are outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14),
+// leaving the export and LDS counters untouched.
+constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
 // A wave-uniform condition that the compiler must treat as lane-varying.
 // Selects on a uniform condition may be turned into a branch with the loads
 // that feed one side sunk into it (each branch join then waits for its

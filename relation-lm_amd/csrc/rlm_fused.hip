@@ -150,19 +150,6 @@ __device__ __forceinline__ u16x8 lds_frag(const unsigned char* p) {
 
 __device__ __forceinline__ u16x8 as_frag(uint4 v) { return __builtin_bit_cast(u16x8, v); }
 
-// 16 bytes per lane from global memory straight into LDS: lane i's bytes land
-// at lds_addr + 16*i.  Issued as inline assembly so that the compiler does not
-// follow it with a full vmcnt(0) before the next LDS access; the caller waits
-// (s_waitcnt vmcnt(0) + barrier) before the tile is read.  The LDS base of the
-// transfer travels in M0, passed as an operand bound to that register ("{m0}"),
-// so the compiler writes M0 itself and knows it holds this value.
-__device__ __forceinline__ void lds_dma16(rsrc_t r, uint32_t lds_addr, uint32_t voff) {
-  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds"
-               :
-               : "v"(voff), "s"(r), "{m0}"(lds_addr)
-               : "memory");
-}
-
 // Weight p_k of partner k in its query's mixture, from the query's K scores
 // and position t: softmax over the active partners (rank < k_limit, score >
 // -1e30; inactive scores -1e4), renormalised by max(sum, 1e-9) --

@@ -8,7 +8,14 @@
 // A may be fp32 (the relation hidden); it is rounded to the weight type while
 // it is staged, so the MFMA sees the same operand a bf16 F.linear would.
 //
-//   tile_kernel   (M > 64)   BMxBN workgroup tile (128x128 or 64x128), four
+//   dma_tile_kernel (M > 64, A of the weight's 16-bit type, K % 64 == 0)
+//                 256x256 workgroup tiles of eight waves (128x128 of four
+//                 waves, two workgroups per CU, for problems under one tile
+//                 per CU) on v_mfma_f32_32x32x16; A and W k-slices of 64 go
+//                 from global memory straight into LDS (two stages), the
+//                 output is restaged through LDS into whole row segments.
+//   tile_kernel   (M > 64, the other cases: fp32 A, K % 64 != 0)
+//                 BMxBN workgroup tile (128x128 or 64x128), four
 //                 waves in 2x2, each a (BM/2)x(BN/2) grid of 16x16 MFMA tiles.
 //                 A and W k-slices of 32 are double-buffered in LDS: the
 //                 global loads of slice k+1 are in flight while slice k runs
@@ -634,8 +641,314 @@ __global__ void __launch_bounds__(256) f32_tile_kernel(const GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// 16-bit A and W, large M, K % BK == 0: macro tiles fed by LDS DMA
+// ---------------------------------------------------------------------------
+//
+// A workgroup of WM x WN waves owns a BM x BN output tile; each wave a
+// (BM/WM) x (BN/WN) grid of 32x32 blocks on v_mfma_f32_32x32x16_{bf16,f16}.
+// k advances in BK-wide slices (32 or 64).  A slice's A and W rows go from
+// global memory straight into LDS (lds_dma16: no VGPRs, no LDS write
+// instructions) into one of NS stages; the DMA of slice s + NS is issued as
+// soon as every wave has read slice s, so a DMA has NS - 1 slices of matrix
+// work to land (global-memory latency under load is a few thousand cycles,
+// one 256x256x32 slice about a thousand).  Within a slice the fragments of
+// the next 16-wide k-group are read while the current group's MFMAs run, and
+// the barrier that publishes the next slice sits before the slice's last
+// MFMA group, so its first fragment reads overlap matrix work too.
+//
+// LDS tile rows are BK*2 bytes; 16-byte piece q of row r is stored at piece
+// q ^ swz(r): the 16 rows a fragment read serves together land on 16 distinct
+// 16-byte bank groups, whether the LDS serves 8 or 16 lanes of a 16-byte read
+// per cycle.  A DMA instruction writes 64 consecutive 16-byte pieces, so the
+// swizzle is applied on the global side: each lane fetches the piece that
+// belongs at its LDS position.
+//
+// The product is computed transposed, out^T = W . A^T, so that a lane holds
+// four consecutive columns of one output row (16-byte fp32 stores).
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <typename W>
+__device__ __forceinline__ f32x16 mfma32(const u16x8& a, const u16x8& b, const f32x16& c);
+template <>
+__device__ __forceinline__ f32x16 mfma32<bf16>(const u16x8& a, const u16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x16 mfma32<f16>(const u16x8& a, const u16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Piece swizzle of tile row r (only r % 16 matters) for BK-wide rows.
+template <int BK>
+__device__ __forceinline__ int dma_swz(int r) {
+  if constexpr (BK == 64) return (r & 7) ^ ((r >> 3) & 1);   // 8 pieces per row
+  else return ((r >> 1) & 3) ^ ((r >> 3) & 1);              // 4 pieces per row
+}
+
+// NS stages of the A and W tiles, then the tile's BN bias columns (fp32).
+constexpr int kDmaSliceK = 64;  // k-slice of the production configurations
+
+template <int BM, int BN, int NS, int BK>
+constexpr size_t dma_lds_bytes() {
+  return static_cast<size_t>(NS) * (BM + BN) * BK * 2 + BN * 4;
+}
+
+// Epilogue of the DMA tile kernels.  Lane holds out[m][n .. n+3] of block
+// (j, i) for m = m0 + wm0 + 32i + (lane & 31), n = n0 + wn0 + 32j + 8q +
+// 4 (lane >> 5), q = 0..3 (acc elements 4q .. 4q+3); the bias of the tile's
+// columns comes from LDS (bias_lds[c] = bias[n0 + c], zero past N or without
+// a bias).  Each wave restages one 32-row block at a time in its own LDS
+// region (rows padded by 16 bytes) and writes it back as whole 16-byte pieces
+// of consecutive columns, so a store instruction covers two or more complete
+// row segments instead of 32 rows x 32 bytes.  The caller has passed a
+// barrier after the last LDS read of the main loop.
+template <typename TO, int TMB, int TNB>
+__device__ __forceinline__ void dma_epilogue(const GemmParams& p, const f32x16 (&acc)[TNB][TMB],
+                                             const float* bias_lds, unsigned char* stage,
+                                             int64_t m0, int64_t n0, int wm0, int wn0, int lane) {
+  constexpr int kSz = static_cast<int>(sizeof(TO));
+  constexpr int WC = 32 * TNB;                 // columns of the wave's block
+  constexpr int RS = WC * kSz + 16;            // staged row stride (bytes)
+  constexpr int kPiecesRow = WC * kSz / 16;    // 16-byte pieces per staged row
+  constexpr int kVec = 16 / kSz;               // outputs per piece
+  static_assert((32 * kPiecesRow) % kWave == 0, "whole store rounds");
+  float4 bv[TNB][4];
+#pragma unroll
+  for (int j = 0; j < TNB; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      bv[j][q] = *reinterpret_cast<const float4*>(bias_lds + wn0 + 32 * j + 8 * q + 4 * (lane >> 5));
+  TO* out = static_cast<TO*>(p.out);
+#pragma unroll
+  for (int i = 0; i < TMB; ++i) {
+#pragma unroll
+    for (int j = 0; j < TNB; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        put4<TO>(reinterpret_cast<TO*>(stage + (lane & 31) * RS +
+                                       (32 * j + 8 * q + 4 * (lane >> 5)) * kSz),
+                 acc[j][i][4 * q] + bv[j][q].x, acc[j][i][4 * q + 1] + bv[j][q].y,
+                 acc[j][i][4 * q + 2] + bv[j][q].z, acc[j][i][4 * q + 3] + bv[j][q].w);
+    wave_sync();
+#pragma unroll
+    for (int t = 0; t < 32 * kPiecesRow / kWave; ++t) {
+      const int piece = t * kWave + lane;
+      const int row = piece / kPiecesRow, col = (piece % kPiecesRow) * kVec;
+      const int64_t m = m0 + wm0 + 32 * i + row;
+      const int64_t n = n0 + wn0 + col;
+      const uint4 v = *reinterpret_cast<const uint4*>(stage + row * RS + col * kSz);
+      if (m < p.M) {
+        TO* dst = out + m * p.ldo + n;
+        if (n + kVec <= p.N) {
+          *reinterpret_cast<uint4*>(dst) = v;
+        } else {
+          const TO* e = reinterpret_cast<const TO*>(&v);
+#pragma unroll
+          for (int k = 0; k < kVec; ++k)
+            if (n + k < p.N) dst[k] = e[k];
+        }
+      }
+    }
+    wave_sync();
+  }
+}
+
+// Bytes of one wave's epilogue staging region.
+template <typename TO, int TNB>
+constexpr int dma_stage_region() {
+  return 32 * (32 * TNB * static_cast<int>(sizeof(TO)) + 16);
+}
+
+// Bias of tile columns n0 .. n0 + BN - 1 into LDS (threads t < BN, one column
+// each); the caller's next barrier publishes it.
+template <int BN>
+__device__ __forceinline__ void dma_stage_bias(const GemmParams& p, float* bias_lds, int64_t n0) {
+  const int t = threadIdx.x;
+  if (t < BN) {
+    const int64_t n = n0 + t;
+    bias_lds[t] = (p.bias != nullptr && n < p.N) ? load_any_f(p.bias, p.bias_dtype, n) : 0.0f;
+  }
+}
+
+template <typename W, typename TO, int BM, int BN, int WM, int WN, int NS, int BK>
+__global__ void __launch_bounds__(WM * WN * kWave) dma_tile_kernel(const GemmParams p) {
+  constexpr int kWaves = WM * WN;
+  constexpr int TMB = BM / WM / 32;         // 32-row blocks of A per wave
+  constexpr int TNB = BN / WN / 32;         // 32-row blocks of W per wave
+  constexpr int KK = BK / 16;               // MFMA k-groups per slice
+  constexpr int RB = BK * 2;                // bytes per LDS tile row
+  constexpr int PR = BK / 8;                // 16-byte pieces per row
+  constexpr int RPI = kWave / PR;           // rows per DMA instruction
+  constexpr int kStage = (BM + BN) * RB;
+  constexpr int kLoadsA = BM / RPI / kWaves;  // DMA instructions per wave per slice
+  constexpr int kLoadsB = BN / RPI / kWaves;
+  constexpr int L = kLoadsA + kLoadsB;
+  static_assert(BK == 32 || BK == 64, "32- or 64-wide k-slices");
+  static_assert(BM % (RPI * kWaves) == 0 && BN % (RPI * kWaves) == 0, "whole DMA row groups per wave");
+  static_assert(NS >= 2 && (NS - 1) * L <= 63, "stages within the vmcnt range");
+  static_assert(KK % 2 == 0, "fragment double buffer alternates within a slice");
+  static_assert(WM * WN * kWave >= BN, "one thread per bias column");
+  static_assert(kWaves * dma_stage_region<TO, TNB>() <= NS * kStage, "epilogue staging fits the stages");
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  const int64_t tiles_n = (p.N + BN - 1) / BN;
+  const int64_t tiles = tiles_n * ((p.M + BM - 1) / BM);
+  const int64_t tile = xcd_tile(blockIdx.x, tiles);
+  const int64_t m0 = (tile / tiles_n) * BM;
+  const int64_t n0 = (tile % tiles_n) * BN;
+
+  // Descriptors based at the tile's first row; their sizes end with the
+  // matrices' last elements (clipped below 2 GiB: the host checks that a
+  // tile's rows lie within that), so rows past M or N read zeros.
+  const int64_t a_left = ((p.M - 1 - m0) * p.lda + p.K) * 2;
+  const int64_t w_left = (p.N - n0) * p.K * 2;
+  const rsrc_t ar = make_rsrc(static_cast<const unsigned char*>(p.a) + m0 * p.lda * 2,
+                              static_cast<uint32_t>(a_left < 0x7fffffff ? a_left : 0x7fffffff));
+  const rsrc_t wr = make_rsrc(static_cast<const unsigned char*>(p.w) + n0 * p.K * 2,
+                              static_cast<uint32_t>(w_left < 0x7fffffff ? w_left : 0x7fffffff));
+  const uint32_t a_row_bytes = static_cast<uint32_t>(p.lda * 2);
+  const uint32_t w_row_bytes = static_cast<uint32_t>(p.K * 2);
+
+  // DMA lane roles: row (lane / PR) of a RPI-row group, LDS piece (lane % PR).
+  // The group's row offset modulo 16 is 0 or 8 (h, for 8-row groups).
+  const int sub = lane / PR, pc = lane % PR;
+  uint32_t a_off[2], w_off[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t q = static_cast<uint32_t>(pc ^ dma_swz<BK>(8 * h + sub)) << 4;
+    a_off[h] = sub * a_row_bytes + q;
+    w_off[h] = sub * w_row_bytes + q;
+  }
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
+  auto issue = [&](int stage, int slice) {
+    const uint32_t st = lds0 + stage * kStage;
+    const uint32_t kb = static_cast<uint32_t>(slice) * RB;
+#pragma unroll
+    for (int j = 0; j < kLoadsA; ++j) {
+      const int g = wave * kLoadsA + j;
+      lds_dma16(ar, st + g * RPI * RB, a_off[(g * RPI / 8) & 1], kb + g * RPI * a_row_bytes);
+    }
+#pragma unroll
+    for (int j = 0; j < kLoadsB; ++j) {
+      const int g = wave * kLoadsB + j;
+      lds_dma16(wr, st + (BM + g * RPI) * RB, w_off[(g * RPI / 8) & 1], kb + g * RPI * w_row_bytes);
+    }
+  };
+
+  // Fragment roles: row (lane & 31) of a 32-row block, k-half (lane >> 5).
+  const int wm0 = (wave / WN) * (BM / WM);
+  const int wn0 = (wave % WN) * (BN / WN);
+  const int swz = dma_swz<BK>(lane & 15);
+  int frag_off[KK];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) frag_off[kk] = (lane & 31) * RB + (((2 * kk + (lane >> 5)) ^ swz) << 4);
+
+  u16x8 fa[2][TMB], fw[2][TNB];
+  auto read_frags = [&](int buf, int stage, int kk) {
+    const unsigned char* st = smem + stage * kStage;
+#pragma unroll
+    for (int i = 0; i < TMB; ++i)
+      fa[buf][i] = *reinterpret_cast<const u16x8*>(st + (wm0 + 32 * i) * RB + frag_off[kk]);
+#pragma unroll
+    for (int j = 0; j < TNB; ++j)
+      fw[buf][j] = *reinterpret_cast<const u16x8*>(st + (BM + wn0 + 32 * j) * RB + frag_off[kk]);
+  };
+
+  f32x16 acc[TNB][TMB];
+#pragma unroll
+  for (int j = 0; j < TNB; ++j)
+#pragma unroll
+    for (int i = 0; i < TMB; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[j][i][e] = 0.0f;
+
+  const int slices = static_cast<int>(p.K / BK);
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    if (s < slices) issue(s, s);
+  float* bias_lds = reinterpret_cast<float*>(smem + NS * kStage);
+  dma_stage_bias<BN>(p, bias_lds, n0);
+  if (slices >= NS) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 1) * L));
+  } else {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  }
+  __syncthreads();
+  read_frags(0, 0, 0);
+  int stage = 0;
+  for (int s = 0; s < slices; ++s) {
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      if (kk + 1 < KK) {
+        read_frags((kk + 1) & 1, stage, kk + 1);
+      } else if (s + 1 < slices) {
+        // Slice s + 1 has landed once this wave's DMAs up to it are done
+        // and every wave has passed the barrier; after the barrier no wave
+        // reads slice s again, so its stage takes slice s + NS.
+        if (s + NS - 1 < slices) {
+          __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * L));
+        } else {
+          __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        }
+        __syncthreads();
+        if (s + NS < slices) issue(stage, s + NS);
+        stage = stage + 1 == NS ? 0 : stage + 1;
+        read_frags(0, stage, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < TNB; ++j)
+#pragma unroll
+        for (int i = 0; i < TMB; ++i) acc[j][i] = mfma32<W>(fw[kk & 1][j], fa[kk & 1][i], acc[j][i]);
+    }
+  }
+
+  __syncthreads();  // every wave has read its last fragments: the stages are free
+  dma_epilogue<TO, TMB, TNB>(p, acc, bias_lds, smem + wave * dma_stage_region<TO, TNB>(), m0, n0,
+                             wm0, wn0, lane);
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+
+// The DMA tile kernel at one configuration: LDS above 64 KiB is a
+// per-process function attribute, set on first use.
+template <typename W, typename TO, int BM, int BN, int WM, int WN, int NS, int BK>
+hipError_t launch_dma(const GemmParams& p, hipStream_t s) {
+  constexpr size_t lds = dma_lds_bytes<BM, BN, NS, BK>();
+  auto kernel = &dma_tile_kernel<W, TO, BM, BN, WM, WN, NS, BK>;
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+      static_cast<int>(lds));
+  if (attr != hipSuccess) {
+    set_error("linear: cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(attr));
+    return attr;
+  }
+  const int64_t tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(tiles)), dim3(WM * WN * kWave), lds, s, p);
+  return launch_status("linear");
+}
+
+// Whether the DMA tile kernel takes this problem: 16-bit A of the weight's
+// type, whole 64-wide k-slices, 16-byte aligned rows of A, W and out, and a
+// tile's rows of A and W within the 2 GiB its descriptors address.
+template <typename TA, typename W, typename TO>
+bool dma_fits(const GemmParams& p) {
+  if constexpr (!__is_same(TA, W)) {
+    return false;
+  } else {
+    constexpr int64_t kLimit = int64_t(1) << 31;
+    return p.K % kDmaSliceK == 0 && p.lda % 8 == 0 &&
+           (p.ldo * static_cast<int64_t>(sizeof(TO))) % 16 == 0 &&
+           (reinterpret_cast<uintptr_t>(p.out) & 15u) == 0 && 256 * p.lda * 2 < kLimit &&
+           256 * p.K * 2 < kLimit;
+  }
+}
 
 template <typename TA, typename W, typename TO>
 hipError_t launch_typed(const GemmParams& p, hipStream_t s) {
@@ -704,6 +1017,13 @@ hipError_t launch_typed(const GemmParams& p, hipStream_t s) {
       }
     }
     return launch_status("linear");
+  }
+  if (dma_fits<TA, W, TO>(p)) {
+    // 256x256 tiles (eight waves of 128x64) once they fill the chip; 128x128
+    // (four waves, two workgroups per CU) below that.
+    if (((p.M + 255) / 256) * ((p.N + 255) / 256) >= 256)
+      return launch_dma<W, TO, 256, 256, 2, 4, 2, kDmaSliceK>(p, s);
+    return launch_dma<W, TO, 128, 128, 2, 2, 2, kDmaSliceK>(p, s);
   }
   if (big >= 256) {
     hipLaunchKernelGGL((tile_kernel<TA, W, TO, 128, 128>), dim3(static_cast<unsigned>(big)),

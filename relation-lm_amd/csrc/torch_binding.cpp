@@ -881,6 +881,46 @@ at::Tensor multi_relation_reduce_seq(const at::Tensor& raw, const at::Tensor& pa
   return out;
 }
 
+// multi_relation_reduce_seq into caller tensors: out (hidden's shape and
+// dtype; a batch-row slice of a larger output) and, when given, the fp32
+// relation context.
+void multi_relation_reduce_seq_out(const at::Tensor& raw, const at::Tensor& partner_scores,
+                                   const at::Tensor& norm_weight, const at::Tensor& norm_bias,
+                                   const at::Tensor& slot_mix_logits,
+                                   const at::Tensor& residual_gate, const at::Tensor& hidden,
+                                   const at::Tensor& positions, double norm_eps,
+                                   const c10::optional<at::Tensor>& raw_bias, at::Tensor& out,
+                                   const c10::optional<at::Tensor>& context) {
+  const char* op = "relation_lm::multi_relation_reduce_seq_out";
+  const at::Tensor rb = raw_bias.has_value() ? *raw_bias : at::Tensor();
+  const at::Tensor ctx = context.has_value() ? *context : at::Tensor();
+  c10::DeviceGuard guard(raw.device());
+  hipStream_t stream = device_stream(op, {&raw, &partner_scores, &norm_weight, &norm_bias,
+                                          &slot_mix_logits, &residual_gate, &hidden, &positions,
+                                          &rb, &out, &ctx});
+  TORCH_CHECK(raw.dim() == 5 && partner_scores.dim() == 4, op,
+              ": raw must be [B,Tq,S,K,D] and partner_scores [B,Tq,S,K]");
+  const at::Tensor rows = raw.reshape({raw.size(0), raw.size(1), raw.size(2) * raw.size(3),
+                                       raw.size(4)});
+  rlm_tensor d[11] = {desc(rows, "raw"),
+                      desc(partner_scores, "partner_scores"),
+                      desc(norm_weight, "norm_weight"),
+                      desc(norm_bias, "norm_bias"),
+                      desc(slot_mix_logits, "slot_mix_logits"),
+                      desc(residual_gate, "residual_gate"),
+                      desc(hidden, "hidden"),
+                      desc(positions, "positions"),
+                      desc(out, "out"),
+                      rlm_tensor{},
+                      rlm_tensor{}};
+  if (ctx.defined()) d[9] = desc(ctx, "context");
+  if (rb.defined()) d[10] = desc(rb, "raw_bias");
+  check(rlm_multi_relation_reduce_seq(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7],
+                                      norm_eps, &d[8], ctx.defined() ? &d[9] : nullptr,
+                                      rb.defined() ? &d[10] : nullptr, stream),
+        op);
+}
+
 at::Tensor layer_norm(const at::Tensor& input, const at::Tensor& weight, const at::Tensor& bias,
                       double eps) {
   const char* op = "relation_lm::layer_norm";
@@ -1021,6 +1061,11 @@ TORCH_LIBRARY(relation_lm, m) {
       "multi_relation_reduce_seq(Tensor raw, Tensor partner_scores, Tensor norm_weight, Tensor "
       "norm_bias, Tensor slot_mix_logits, Tensor residual_gate, Tensor hidden, Tensor positions, "
       "float norm_eps, Tensor? raw_bias=None) -> Tensor");
+  m.def(
+      "multi_relation_reduce_seq_out(Tensor raw, Tensor partner_scores, Tensor norm_weight, "
+      "Tensor norm_bias, Tensor slot_mix_logits, Tensor residual_gate, Tensor hidden, Tensor "
+      "positions, float norm_eps, Tensor? raw_bias, Tensor(a!) out, Tensor(b!)? context=None) "
+      "-> ()");
   m.def("layer_norm(Tensor input, Tensor weight, Tensor bias, float eps) -> Tensor");
   // Norm-reduce with the last-token output preparation as its epilogue
   // (roadmap item of the reference, README.md:150-151; relation_lm.py:203-206).
@@ -1071,6 +1116,7 @@ TORCH_LIBRARY_IMPL(relation_lm, CUDA, m) {
   m.impl("relation_linear_out", TORCH_FN(relation_linear_out));
   m.impl("relation_hidden_cached_seq_out", TORCH_FN(relation_hidden_cached_seq_out));
   m.impl("multi_relation_reduce_seq", TORCH_FN(multi_relation_reduce_seq));
+  m.impl("multi_relation_reduce_seq_out", TORCH_FN(multi_relation_reduce_seq_out));
   m.impl("layer_norm", TORCH_FN(layer_norm));
   m.impl("relation_norm_reduce_output", TORCH_FN(relation_norm_reduce_output));
   m.impl("relation_norm_reduce_output_seq", TORCH_FN(relation_norm_reduce_output_seq));

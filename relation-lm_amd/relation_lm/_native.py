@@ -135,6 +135,11 @@ def _register_fakes() -> None:
           positions, norm_eps, raw_bias=None):
         return torch.empty_like(hidden, memory_format=torch.contiguous_format)
 
+    @torch.library.register_fake("relation_lm::multi_relation_reduce_seq_out")
+    def _(raw, partner_scores, norm_weight, norm_bias, slot_mix_logits, residual_gate, hidden,
+          positions, norm_eps, raw_bias, out, context=None):
+        return None
+
     def fake_norm_output(raw, partner_scores, norm_weight, norm_bias, position, norm_eps, query,
                          mix_logit, output_weight, output_bias, output_eps):
         shape = tuple(raw.shape[:-2]) + (raw.shape[-1],)

@@ -14,10 +14,8 @@ multi-anchor selection (local window plus the top blocks of a block router,
   relation MLP Linear -> GELU     relation_lm::relation_hidden_cached_seq_out
     (factorized: operand cache, expanded cache = [W_a+W_d; W_p-W_d] op + [b; 0];
     stored in bf16 when the second Linear is bf16)
-  relation MLP second Linear      torch.mm(out_dtype=float32): a plain GEMM on the
-    ROCm BLAS (hipBLASLt) for 16-bit weights -- measured 1.8x the hand-written
-    tile GEMM at cfg5's [98304, 3072] x [3072, 768] -- its bias added by the
-    slot reduce as it loads the rows; relation_lm::relation_linear otherwise
+  relation MLP second Linear      relation_lm::relation_linear (the MFMA DMA-tile GEMM,
+    bias in its epilogue, fp32 output)
   LayerNorm, partner softmax,     relation_lm::multi_relation_reduce_seq
     slot mix, residual gate
   final_norm (stack)              relation_lm::layer_norm
@@ -48,22 +46,6 @@ from relation_lm import _native  # noqa: F401  (registers torch.ops.relation_lm)
 from relation_lm.kernels.relation_reduce import factor_relation_first_layer
 
 ops = torch.ops.relation_lm
-
-
-
-def _second_linear(rows: Tensor, weight: Tensor, bias: Tensor | None) -> tuple[Tensor, Tensor | None]:
-    """fp32 ``rows @ weight.T`` of the relation MLP's second Linear (the reference's
-    plain ``nn.Linear``, multi_relation_blocks.py:47-52) and the bias still to add.
-
-    With 16-bit weights this is a plain GEMM on the ROCm BLAS (``mm`` with an fp32
-    output: hipBLASLt) and the bias is returned for the slot reduce to add as it
-    loads the rows (a bias in ``addmm`` costs a copy of the whole output first);
-    fp32 weights take ``relation_linear``'s fp32 kernel with the bias."""
-    if weight.dtype not in (torch.bfloat16, torch.float16) or rows.dtype != weight.dtype:
-        return ops.relation_linear(rows, weight, bias, torch.float32), None
-    flat = rows.reshape(-1, rows.shape[-1])
-    out = torch.mm(flat, weight.t(), out_dtype=torch.float32)
-    return out.view(*rows.shape[:-1], weight.shape[0]), bias
 
 
 @dataclass
@@ -210,14 +192,14 @@ class MultiAnchorRelationBlock(nn.Module):
                 "partner_score": partner_score, "operand_cache": mem["operand_cache"],
                 "expanded_cache": mem["expanded_cache"], "product_weight": packed["product_weight"]}
 
-    def relate(self, hidden: Tensor, sel: dict) -> Tensor:
+    def relate(self, hidden: Tensor, sel: dict, context: Tensor | None = None) -> Tensor:
         """The relation MLP over every (query, slot, partner) row of the selection,
-        the partner and slot mixing, and the residual gate."""
+        the partner and slot mixing, and the residual gate.  ``context`` (fp32,
+        hidden's shape), when given, receives the block's relation context."""
         cfg = self.cfg
         batch, length, d = hidden.shape
         h, k_count = cfg.anchors_per_block, cfg.partners_per_anchor
         mlp = self.relation_mlp
-        outputs = []
         # The MLP hidden in the second Linear's operand dtype: a bf16 Linear
         # rounds an fp32 hidden to bf16 before its products, so storing bf16
         # gives the same result at half the bytes.  One batch row at a time:
@@ -226,18 +208,22 @@ class MultiAnchorRelationBlock(nn.Module):
         hid_dtype = torch.bfloat16 if mlp[2].weight.dtype == torch.bfloat16 else torch.float32
         rows = torch.empty((1, length * h, k_count, mlp[2].weight.shape[1]), dtype=hid_dtype,
                            device=hidden.device)
+        output = torch.empty_like(hidden, memory_format=torch.contiguous_format)
         for b in range(batch):
             ops.relation_hidden_cached_seq_out(
                 sel["expanded_cache"][b:b + 1], sel["operand_cache"][b:b + 1],
                 sel["anchor"][b:b + 1].reshape(1, length * h),
                 sel["partner"][b:b + 1].reshape(1, length * h, k_count), sel["product_weight"],
                 rows)
-            raw, raw_bias = _second_linear(rows, mlp[2].weight, mlp[2].bias)
-            outputs.append(ops.multi_relation_reduce_seq(
+            # The second Linear with its bias, fp32 output (the LayerNorm that
+            # follows reads the rows unrounded).
+            raw = ops.relation_linear(rows, mlp[2].weight, mlp[2].bias, torch.float32)
+            ops.multi_relation_reduce_seq_out(
                 raw.view(1, length, h, k_count, d), sel["partner_score"][b:b + 1], mlp[3].weight,
                 mlp[3].bias, self.slot_mix_logits, self.residual_gate, hidden[b:b + 1],
-                sel["positions"], mlp[3].eps, raw_bias))
-        return outputs[0] if batch == 1 else torch.cat(outputs, dim=0)
+                sel["positions"], mlp[3].eps, None, output[b:b + 1],
+                None if context is None else context[b:b + 1])
+        return output
 
     def forward(self, hidden: Tensor, memory: Tensor) -> tuple[Tensor, dict[str, Tensor]]:
         sel = self.select(hidden, memory)

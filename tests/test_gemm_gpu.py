@@ -1,0 +1,81 @@
+"""GPU parity of relation_lm::relation_linear on its large-M 16-bit path (the
+LDS-DMA tile GEMM: 256x256 tiles when the problem fills the chip, 128x128
+otherwise) against a float64 product of the same 16-bit operands.
+
+The relation MLP's second Linear of the multi-anchor block (cfg5:
+[98304, 3072] x [3072, 768], bf16) and the reference's second linear G3
+(benchmark_relation_reduce.py:63) run here.  Shapes cover both tile sizes,
+edges in M and N, a row-strided input, fp16 weights, fp32 and bf16 outputs
+and the bias in the epilogue.  fp32 outputs: within fp32 accumulation of the
+exact products (1e-5 of sum |a w|); 16-bit outputs: that plus half an ulp of
+the output type.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+ops = torch.ops.relation_lm
+
+
+def reference(a, w, bias):
+    a64, w64 = a.double().cpu(), w.double().cpu()
+    out = a64 @ w64.T
+    mag = a64.abs() @ w64.abs().T
+    if bias is not None:
+        out = out + bias.double().cpu()
+        mag = mag + bias.double().cpu().abs()
+    return out.numpy(), mag.numpy()
+
+
+def check(got, a, w, bias):
+    exp, mag = reference(a, w, bias)
+    g = got.double().cpu().numpy()
+    tol = 1e-5 * mag + 1e-6
+    if got.dtype != torch.float32:
+        bits = 8 if got.dtype == torch.bfloat16 else 11
+        tol = tol + np.exp2(np.floor(np.log2(np.maximum(np.abs(exp), 1e-30))) - bits)
+    bad = np.abs(g - exp) > tol
+    assert not bad.any(), (int(bad.sum()), float(np.abs(g - exp).max()))
+
+
+CASES = [
+    # (M, N, K, weight dtype, out dtype, bias, input row padding)
+    (32768, 512, 512, torch.bfloat16, torch.float32, True, 0),    # 256x256 tiles (A8 shape)
+    (32768, 512, 512, torch.bfloat16, torch.bfloat16, False, 0),
+    (16384, 768, 768, torch.bfloat16, torch.bfloat16, True, 0),   # 256x256 tiles, cfg5 projection
+    (1000, 300, 192, torch.bfloat16, torch.float32, True, 0),     # 128x128, edges in M and N
+    (4100, 264, 320, torch.bfloat16, torch.float32, False, 64),   # edges, row-strided input
+    (3000, 512, 256, torch.float16, torch.float32, True, 0),      # fp16 weights
+    (2048, 768, 3072, torch.bfloat16, torch.float32, True, 0),    # cfg5 second-Linear widths
+]
+
+
+@pytest.mark.parametrize("m,n,k,wdt,odt,with_bias,pad", CASES)
+def test_relation_linear_dma_path(device, m, n, k, wdt, odt, with_bias, pad):
+    g = torch.Generator().manual_seed(m + n + k)
+    base = torch.randn(m, k + pad, generator=g).to(wdt)
+    a = base[:, :k]
+    w = (torch.randn(n, k, generator=g) / np.sqrt(k)).to(wdt)
+    bias = (0.5 * torch.randn(n, generator=g)).to(wdt) if with_bias else None
+    print(f"relation_linear M={m} N={n} K={k} {wdt} -> {odt} bias={with_bias} pad={pad}",
+          flush=True)
+    a_dev = base.to(device)[:, :k]
+    got = ops.relation_linear(a_dev, w.to(device), None if bias is None else bias.to(device), odt)
+    torch.cuda.synchronize()
+    assert got.shape == (m, n) and got.dtype == odt
+    check(got, a, w, bias)
+
+
+def test_relation_linear_dma_repeat_identical(device):
+    # Same inputs, same bits: no atomics or order-dependent accumulation.
+    g = torch.Generator().manual_seed(5)
+    a = torch.randn(8192, 1024, generator=g).to(torch.bfloat16).to(device)
+    w = (torch.randn(768, 1024, generator=g) / 32).to(torch.bfloat16).to(device)
+    b = torch.randn(768, generator=g).to(device)
+    first = ops.relation_linear(a, w, b, torch.float32)
+    second = ops.relation_linear(a, w, b, torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(first, second)

@@ -10,7 +10,9 @@
   (bit-exact) and its relation / mixing steps against the factorized path
   oracle (relate_rows) on the block's own caches;
 * one layer and the 4-layer stack at the full cfg5 shape (B=4, T=4096, d=768,
-  4 slots x K=6, block 64, local 128, top 8, bf16), checked on sampled queries.
+  4 slots x K=6, block 64, local 128, top 8, bf16): selection bit-exact and the
+  fp32 relation context within 5e-3 of the oracle on 256 sampled queries per
+  layer, and on every query of one batch row for one layer.
 """
 from __future__ import annotations
 
@@ -260,11 +262,47 @@ def cfg5_inputs(device, seed=20261205):
     return hidden, memory
 
 
-def sample_rows(seed, batch=4, length=4096, per_row=16):
+def sample_rows(seed, batch=4, length=4096, per_row=64):
     rng = np.random.default_rng(seed)
     fixed = np.array([0, 1, 2, 3, 127, 128, length - 1])[:per_row]
     t = np.concatenate([fixed, rng.integers(0, length, size=per_row - len(fixed))])
     return np.repeat(np.arange(batch), per_row), np.tile(t, batch)
+
+
+CONTEXT_ABS = 2e-2     # bf16 bar of the relation state
+CONTEXT_TIGHT = 5e-3   # observed margin of the fp32-accumulated path
+
+
+def check_cfg5_layer(block, x, memory, rows_b, rows_t):
+    """One cfg5 layer: the block's fp32 relation context and bf16 output on the
+    sampled queries against the oracles (selection bit-exact, context within
+    CONTEXT_TIGHT, output within the context bound plus the bf16 rounding of
+    the output).  Returns the layer's output."""
+    sel = block.select(x, memory)
+    context = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    y = block.relate(x, sel, context)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all() and torch.isfinite(context).all()
+    check_layer_on_rows(block, x, memory, sel, y, rows_b, rows_t, "bfloat16", 0.03)
+    mlp = block.relation_mlp
+    _, expected = omb.relate_rows(
+        host(sel["expanded_cache"]), host(sel["operand_cache"]), host(sel["product_weight"]),
+        host(mlp[2].weight), host(mlp[2].bias), host(mlp[3].weight), host(mlp[3].bias),
+        host(block.slot_mix_logits), float(block.residual_gate.detach()),
+        host(x[rows_b, rows_t]), rows_b, rows_t, host(sel["anchor"][rows_b, rows_t]),
+        host(sel["partner"][rows_b, rows_t]), host(sel["partner_score"][rows_b, rows_t]),
+        mlp[3].eps, "bfloat16")
+    err = np.abs(host(context[rows_b, rows_t]) - expected)
+    assert err.max() <= CONTEXT_ABS, err.max()
+    assert err.max() <= CONTEXT_TIGHT, err.max()
+    # out = bf16(hidden + sigmoid(gate) * context): the context error plus one
+    # bf16 rounding of the output value.
+    gate = 1.0 / (1.0 + np.exp(-float(block.residual_gate.detach())))
+    exp_out = host(x[rows_b, rows_t]).astype(np.float64) + gate * expected
+    half_ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(exp_out), 1e-30))) - 8)
+    out_err = np.abs(host(y[rows_b, rows_t]) - exp_out)
+    assert (out_err <= half_ulp + gate * CONTEXT_TIGHT + 1e-6).all(), float(out_err.max())
+    return y
 
 
 def test_cfg5_one_layer(device):
@@ -274,15 +312,29 @@ def test_cfg5_one_layer(device):
     randomize(block, 11)
     block = block.to(device=device, dtype=torch.bfloat16)
     x, memory = cfg5_inputs(device)
-    print("cfg5 one layer: select", flush=True)
-    with torch.no_grad():
-        sel = block.select(x, memory)
-        print("cfg5 one layer: relate", flush=True)
-        y = block.relate(x, sel)
-    torch.cuda.synchronize()
-    assert torch.isfinite(y.float()).all()
     rows_b, rows_t = sample_rows(1)
-    check_layer_on_rows(block, x, memory, sel, y, rows_b, rows_t, "bfloat16", 0.03)
+    print("cfg5 one layer: 256 sampled queries", flush=True)
+    with torch.no_grad():
+        check_cfg5_layer(block, x, memory, rows_b, rows_t)
+        # The whole of batch row 0 (4096 queries): context against the oracle.
+        sel = block.select(x, memory)
+        context = torch.empty(x.shape, dtype=torch.float32, device=device)
+        block.relate(x, sel, context)
+    torch.cuda.synchronize()
+    mlp = block.relation_mlp
+    rb, rt = np.zeros(4096, dtype=np.int64), np.arange(4096)
+    print("cfg5 one layer: every query of batch row 0", flush=True)
+    for lo in range(0, 4096, 1024):
+        sl = slice(lo, lo + 1024)
+        _, expected = omb.relate_rows(
+            host(sel["expanded_cache"]), host(sel["operand_cache"]), host(sel["product_weight"]),
+            host(mlp[2].weight), host(mlp[2].bias), host(mlp[3].weight), host(mlp[3].bias),
+            host(block.slot_mix_logits), float(block.residual_gate.detach()),
+            host(x[rb[sl], rt[sl]]), rb[sl], rt[sl], host(sel["anchor"][0, sl]),
+            host(sel["partner"][0, sl]), host(sel["partner_score"][0, sl]), mlp[3].eps,
+            "bfloat16")
+        err = np.abs(host(context[0, sl]) - expected).max()
+        assert err <= CONTEXT_TIGHT, (lo, err)
 
 
 def test_cfg5_stack(device):
@@ -300,10 +352,7 @@ def test_cfg5_stack(device):
         h = x
         for i, block in enumerate(stack.blocks):
             print(f"cfg5 stack: layer {i}", flush=True)
-            sel = block.select(h, memory)
-            y = block.relate(h, sel)
-            check_layer_on_rows(block, h, memory, sel, y, rows_b, rows_t, "bfloat16", 0.03)
-            h = y
+            h = check_cfg5_layer(block, h, memory, rows_b, rows_t)
     final = stack.final_norm
     expected = omb.layer_norm(host(h[rows_b, rows_t]), host(final.weight), host(final.bias),
                               final.eps)
