@@ -12,6 +12,9 @@ graph in which the selection runs on a second stream beside the projection
 (checked bit-equal to the eager step) -- and `value` is the faster one's
 queries per second, with every input resident in HBM.
 
+Before the first timed window the serial step runs for at least SETTLE_S
+seconds (reported as `settle`).
+
 Also reported:
   * every schedule's time (forked graph, serial eager, serial graph);
   * the same step through the reference's unfused op sequence
@@ -23,7 +26,11 @@ Also reported:
     cache-row writes, select, reduce, output-head preparation) at B=1 and B=8,
     eager and replayed from a HIP graph; the same step at position 4095 over 512-row ring-buffer caches;
   * routed multi-anchor selection at cfg5 (B=4, T=4096, 4 anchor slots x K=6,
-    block 64, local 128, top 8): one layer's selection over all 16384 queries;
+    block 64, local 128, top 8): one layer's selection over all 16384 queries,
+    and the 4-layer RelationBlockStack;
+  * the reference's published microbenchmark policy (context 512, block 8,
+    local 16, top 2, K 8, fp32): relation_select_packed, the two-op path and
+    the packed projection at B=1 and B=8, beside the reference's figures;
   * the CPU baseline: the path restated in eager fp32 torch (oracle/eager.py),
     timed on all of this host's affinity threads at cfg1, cfg2 and the cfg3
     decode step.
@@ -47,6 +54,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 CALIBRATION_BYTES = 256 << 20  # plain copy whose counter readings scale FETCH/WRITE_SIZE
 RING_POSITION = 4095            # decode position of the ring-buffer step (512-row caches)
 MALL_BYTES = 256 * 2**20        # MI355X last-level (Infinity) cache
+SETTLE_S = 3.0                  # seconds of headline steps before the first timed window
 CPU_WARMUP = 3                  # CPU baseline: warm-up calls per shape
 CPU_SAMPLES = 9                 # CPU baseline: timed calls per shape (median)
 # Kernel-name prefixes (as rocprofv3 reports them) of the timed kernels.
@@ -73,6 +81,9 @@ def parse_args():
                     help="run only the timed chain (for profiler runs)")
     ap.add_argument("--decode-only", action="store_true",
                     help="time only the cfg3 decode step (B=1 and B=8) and exit")
+    ap.add_argument("--policy-only", action="store_true",
+                    help="time only the reference's published routing policy (block 8, local 16, "
+                         "top 2, K 8, fp32)")
     ap.add_argument("--multi-only", action="store_true",
                     help="time only the cfg5 routed multi-anchor selection and exit")
     ap.add_argument("--reduce-only", action="store_true",
@@ -152,36 +163,28 @@ def main() -> int:
     import torch
 
     from relation_lm.kernels.relation_reduce import (
-        relation_hidden_cached,
         relation_hidden_cached_seq,
         relation_linear,
-        relation_norm_reduce,
-        relation_linear_norm_reduce_output,
         relation_norm_reduce_seq,
         relation_reduce_fused_seq,
     )
     from relation_lm.kernels.relation_select import (
         multi_relation_select_seq,
-        relation_select_packed_expand_row,
         relation_select_packed_seq,
-    )
-    from relation_lm.inference import pack_sparse_cache_projection_weights
-    from relation_lm.kernels.ring import (
-        relation_hidden_cached_ring,
     )
     from relation_lm.workloads import (
         CONFIGS,
         MULTI_CONFIGS,
         RelationConfig,
         causal_partner_indices,
+        decode_state,
         multi_select_args,
         multi_selection_inputs,
-        packed_projection_inputs,
         reduce_inputs,
-        router_cache_inputs,
         select_args,
         selection_inputs,
     )
+    from relation_lm.workloads import decode_step as workload_decode_step
 
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
@@ -210,56 +213,16 @@ def main() -> int:
 
         ring_position: decode at that absolute position over ring-buffer caches of
         the cfg3 length (the *_ring ops; rows written at position mod length)."""
-        ring = ring_position is not None
-        cached_op = relation_hidden_cached_ring if ring else relation_hidden_cached
         decode = {}
         for batch in (1, 8):
             dcfg = RelationConfig(**{**CONFIGS["cfg3"].__dict__, "batch": batch})
-            dsel = selection_inputs(dcfg, queries=1, device=device)
-            dred = reduce_inputs(dcfg, device=device)
-            dexp = relation_linear(dred["operand_cache"], dred["expanded_weight"],
-                                   dred["expanded_bias"])
-            memory, weights = packed_projection_inputs(dcfg, device=device)
-            projection = pack_sparse_cache_projection_weights(weights)
-            rc = router_cache_inputs(dcfg, device=device)
-            if ring:
-                dsel["position"] = torch.tensor(ring_position, dtype=torch.int64, device=device)
-            dargs = select_args(dsel, dcfg)
-            t = (ring_position if ring else dcfg.context - 1) % dcfg.context  # cache row
-            position = dsel["position"]
-            # Output-head preparation inputs (relation_lm.py:203-206): the token's
-            # query stream, the relation mix logit and output_norm.
-            gq = torch.Generator().manual_seed(dcfg.seed + 3)
-            head = {"query": torch.randn(batch, dcfg.d_model, generator=gq).to(device, dcfg.dtype),
-                    "mix": torch.tensor(-1.0, device=device),
-                    "weight": (1 + 0.1 * torch.randn(dcfg.d_model, generator=gq)).to(device, dcfg.dtype),
-                    "bias": (0.1 * torch.randn(dcfg.d_model, generator=gq)).to(device, dcfg.dtype)}
+            state = decode_state(dcfg, device=device, position=ring_position)
 
-            def decode_step(dsel=dsel, dred=dred, dexp=dexp, memory=memory, projection=projection,
-                            dargs=dargs, t=t, position=position, batch=batch, rc=rc, dcfg=dcfg,
-                            head=head):
-                # projection + the token's key / operand / partner-anchor cache rows, with
-                # the router cache update folded in (one launch)
-                projection.project_into_routed(
-                    memory, dsel["anchor_keys"], dsel["partner_keys"], dred["operand_cache"],
-                    dsel["partner_anchor_cache"], position, rc["anchor_raw_cache"],
-                    rc["partner_raw_cache"], rc["anchor_conv_cache"], rc["partner_conv_cache"],
-                    dsel["anchor_block_mean"], dsel["anchor_block_std"],
-                    dsel["partner_block_mean"], dsel["partner_block_std"],
-                    rc["anchor_conv_weight"], rc["partner_conv_weight"], dcfg.block_size,
-                    ring=ring)
-                # selection, with the token's expanded-cache row projected by extra
-                # workgroups of the same launch; then the cached hidden (B=1 and B=8)
-                a_, s_, p_, ps_ = relation_select_packed_expand_row(
-                    *dargs, dred["operand_cache"], dred["expanded_weight"],
-                    dred["expanded_bias"], dexp, ring)
-                hid = cached_op(dexp, dred["operand_cache"], a_, p_, dred["product_weight"])
-                # second linear (split over the hidden dim) and norm-reduce with the
-                # output-head preparation as its epilogue, the partials summed there
-                return relation_linear_norm_reduce_output(
-                    hid, dred["second_weight"], dred["second_bias"], ps_, dred["norm_weight"],
-                    dred["norm_bias"], position, 1e-5, head["query"], head["mix"],
-                    head["weight"], head["bias"], 1e-5)[1]
+            def decode_step(state=state, dcfg=dcfg):
+                # projection + cache rows + router update; selection with the
+                # token's expanded-cache row; cached hidden; split-K second
+                # linear and norm-reduce with the output-head preparation
+                return workload_decode_step(state, dcfg)[-1]
 
             for _ in range(20):
                 decode_step()
@@ -410,6 +373,105 @@ def main() -> int:
             "algorithmic_bytes": nbytes,
         }
 
+    def run_published_policy(repeats=100, samples=9):
+        """The only routing policy the reference publishes numbers for
+        (benchmarks/benchmark_relation_select.py:14-57, results in
+        benchmarks/results/relation_select_microbenchmark.json; packed projection:
+        benchmarks/benchmark_packed_cache.py:13-47, packed_cache_microbenchmark.json):
+        context 512, block 8 (64 blocks), local 16, top 2, K 8, fp32 inputs with
+        the reference's distributions (randn, std = rand; projection weights
+        0.02 randn), B=1 and B=8.  Each figure is the median of `samples`
+        windows of `repeats` eager calls (event-timed), after 50 warm-up calls.
+        The reference's numbers are from an unnamed NVIDIA GPU."""
+        from relation_lm.inference import pack_sparse_cache_projection_weights
+        from relation_lm.kernels.relation_select import relation_select_packed
+        from relation_lm.kernels.triton_select import anchor_select, partner_topk
+
+        reference_ms = {
+            "B1": {"relation_select_packed": 0.14487551689147948, "two_op": 0.34379776000976564,
+                   "packed_projection": 0.03127978642781575},
+            "B8": {"relation_select_packed": 0.14664704322814942, "two_op": 0.3483852767944336,
+                   "packed_projection": 0.03799040158589681},
+        }
+
+        def median_ms(fn):
+            for _ in range(50):
+                fn()
+            torch.cuda.synchronize()
+            marks = [torch.cuda.Event(enable_timing=True) for _ in range(samples + 1)]
+            marks[0].record()
+            for i in range(samples):
+                for _ in range(repeats):
+                    fn()
+                marks[i + 1].record()
+            torch.cuda.synchronize()
+            return statistics.median(marks[i].elapsed_time(marks[i + 1]) / repeats
+                                     for i in range(samples))
+
+        out = {"policy": "context 512, block 8, local 16, top 2, K 8, fp32 (the reference's "
+                         "published microbenchmark policy)",
+               "reference_hardware": "unnamed NVIDIA GPU (reference's committed results)"}
+        for batch in (1, 8):
+            g = torch.Generator().manual_seed(17)
+            ctx, blocks = 512, 64
+            r = lambda *shape: torch.randn(*shape, generator=g)
+            u = lambda *shape: torch.rand(*shape, generator=g)
+            inp = {"aq": r(batch, 64), "ak": r(batch, ctx, 64), "arq": r(batch, 64),
+                   "am": r(batch, blocks, 4, 16), "as": u(batch, blocks, 4, 16), "ag": r(4),
+                   "ab": r(4, 16), "pb": r(batch, 128), "pc": r(batch, ctx, 128),
+                   "pk": r(batch, ctx, 64), "pm": r(batch, blocks, 4, 16),
+                   "ps": u(batch, blocks, 4, 16), "pg": r(4), "pbias": r(4, 16)}
+            inp = {k: v.to(device) for k, v in inp.items()}
+            position = torch.tensor(ctx - 1, dtype=torch.int64, device=device)
+
+            def packed(inp=inp, position=position):
+                return relation_select_packed(
+                    inp["aq"], inp["ak"], inp["arq"], inp["am"], inp["as"], inp["ag"], inp["ab"],
+                    inp["pb"], inp["pc"], inp["pk"], inp["pm"], inp["ps"], inp["pg"],
+                    inp["pbias"], position, 16, 2, 8, False)
+
+            def two_op(inp=inp, position=position):
+                anchor, anchor_score = anchor_select(inp["aq"], inp["ak"], inp["arq"], inp["am"],
+                                                     inp["as"], inp["ag"], inp["ab"], position,
+                                                     16, 2, False)
+                rows = torch.arange(anchor.size(0), device=anchor.device)
+                contribution = inp["pc"][rows, anchor.long()]
+                exact = inp["pb"][:, :64] + contribution[:, :64]
+                router = inp["pb"][:, 64:] + contribution[:, 64:]
+                partner, partner_score = partner_topk(
+                    exact.contiguous(), inp["pk"], router.contiguous(), inp["pm"], inp["ps"],
+                    inp["pg"], inp["pbias"], position, anchor, 16, 2, 8, False)
+                return anchor, anchor_score, partner, partner_score
+
+            ref, got = two_op(), packed()
+            torch.cuda.synchronize()
+            index_equal = bool(torch.equal(ref[0], got[0]) and torch.equal(ref[2], got[2]))
+            gp = torch.Generator().manual_seed(20260822)
+            memory = torch.randn(batch, 576, generator=gp).to(device)
+            weights = [(torch.randn(w, 576, generator=gp) * 0.02).to(device)
+                       for w in (64, 64, 128, 128, 64, 64)]
+            projection = pack_sparse_cache_projection_weights(weights)
+            packed_ms = median_ms(packed)
+            two_ms = median_ms(two_op)
+            proj_ms = median_ms(lambda projection=projection, memory=memory:
+                                projection.project(memory))
+            refs = reference_ms[f"B{batch}"]
+            out[f"B{batch}"] = {
+                "relation_select_packed_ms": round(packed_ms, 5),
+                "two_op_ms": round(two_ms, 5),
+                "packed_projection_ms": round(proj_ms, 5),
+                "index_equal_packed_vs_two_op": index_equal,
+                "reference_ms": refs,
+                "speedup_vs_reference": {
+                    "relation_select_packed": round(refs["relation_select_packed"] / packed_ms, 2),
+                    "two_op": round(refs["two_op"] / two_ms, 2),
+                    "packed_projection": round(refs["packed_projection"] / proj_ms, 2)},
+            }
+        return out
+
+    if args.policy_only:
+        print(json.dumps({"published_policy": run_published_policy()}), flush=True)
+        return 0
     if args.multi_only:
         print(json.dumps({"multi_anchor_select": run_multi()}), flush=True)
         return 0
@@ -525,7 +587,18 @@ def main() -> int:
         torch.cuda.synchronize()
         return start.elapsed_time(end) / count
 
-    timed(step, args.steps)  # settles clocks and caches before the schedules are measured
+    # Warm-up floor: the serial step for at least SETTLE_S seconds (and at least
+    # `warmup` steps) before any window is timed, so that short driver runs
+    # (--steps 20 --warmup 5) measure settled clocks too.
+    settle_start = time.perf_counter()
+    settle_steps = 0
+    while settle_steps < args.warmup or time.perf_counter() - settle_start < SETTLE_S:
+        step()
+        settle_steps += 1
+        if settle_steps % 256 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    settle_s = time.perf_counter() - settle_start
     ms_unfused = timed(step_unfused, args.steps)
 
     def capture(fn):
@@ -667,6 +740,7 @@ def main() -> int:
     ring_decode = run_decode(RING_POSITION)
     multi = run_multi()
     reduce4 = run_reduce_cfg4()
+    policy = run_published_policy()
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -695,6 +769,8 @@ def main() -> int:
         "rooflines": rooflines,
         "per_kernel_in_step_us": {k: round(v, 2) for k, v in in_step_us.items()},
         "per_kernel_us": {k: round(v, 2) for k, v in per_kernel_us.items()},
+        "settle": {"seconds": round(settle_s, 2), "steps": settle_steps,
+                   "floor_s": SETTLE_S},
         "schedule": schedules[chosen][0],
         "schedules_ms_per_step": {"forked_graph": round(ms_forked_graph, 5),
                                   "serial_eager": round(ms_serial, 5),
@@ -721,6 +797,7 @@ def main() -> int:
         "ring_decode_step_us": {"position": RING_POSITION, "cache_rows": 512, **ring_decode},
         "multi_anchor_select": multi,
         "fused_reduce_cfg4": reduce4,
+        "published_policy": policy,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

@@ -274,3 +274,76 @@ def causal_partner_indices(cfg: RelationConfig, seed: int):
     partner[:, 0, :] = 0 - cfg.local_window + 1
     scores[:, 0, :] = -torch.inf
     return anchor.int(), partner.int(), scores, pos
+
+
+def decode_state(cfg: RelationConfig, *, device: torch.device | str, position: int | None = None,
+                 seed: int | None = None) -> dict:
+    """State of the cfg3 decode step: selection inputs (query side for one token,
+    caches and block statistics), reduce inputs with the expanded cache, the
+    packed 576->512 projection and a memory row, the router state of both
+    streams and the output-head preparation inputs (the token's query stream,
+    the relation mix logit, output_norm; relation_lm.py:203-206).
+
+    ``position`` (default: the last cache row) is the token's absolute
+    position; past the cache length the step runs on ring-buffer caches."""
+    from relation_lm.inference import pack_sparse_cache_projection_weights
+    from relation_lm.kernels.relation_reduce import relation_linear
+
+    st = {"sel": selection_inputs(cfg, queries=1, device=device, seed=seed),
+          "red": reduce_inputs(cfg, device=device, seed=seed),
+          "router": router_cache_inputs(cfg, device=device, seed=seed)}
+    st["expanded_cache"] = relation_linear(st["red"]["operand_cache"],
+                                           st["red"]["expanded_weight"],
+                                           st["red"]["expanded_bias"])
+    memory, weights = packed_projection_inputs(cfg, device=device, seed=seed)
+    st["memory"] = memory
+    st["projection"] = pack_sparse_cache_projection_weights(weights)
+    t = cfg.context - 1 if position is None else int(position)
+    st["sel"]["position"] = torch.tensor(t, dtype=torch.int64, device=device)
+    st["ring"] = t >= cfg.context
+    g = _gen((cfg.seed if seed is None else seed) + 3)
+    st["head"] = {"query": _randn(g, cfg.batch, cfg.d_model, dtype=cfg.dtype).to(device),
+                  "mix": torch.tensor(-1.0, device=device),
+                  "weight": (1 + _randn(g, cfg.d_model, scale=0.1)).to(device, cfg.dtype),
+                  "bias": _randn(g, cfg.d_model, scale=0.1, dtype=cfg.dtype).to(device)}
+    return st
+
+
+def decode_step(st: dict, cfg: RelationConfig) -> tuple:
+    """One decode step on ``decode_state`` tensors, the launch sequence the
+    benchmark times:
+      1. packed projection of the memory row, writing the token's rows of the
+         anchor / partner key, operand and partner-anchor caches, with the
+         router cache update of both streams folded in (one launch);
+      2. relation_select_packed with the token's expanded-cache row projected by
+         extra workgroups of the same launch;
+      3. the cached relation hidden (relation_hidden_cached);
+      4. the second linear split over the hidden dim and the norm-reduce with the
+         output-head preparation as its epilogue.
+    The caches are updated in place at the state's position (ring: mod T).
+    Returns (anchor, anchor_score, partner, partner_score, context, final)."""
+    from relation_lm.kernels.relation_reduce import (
+        relation_hidden_cached,
+        relation_linear_norm_reduce_output,
+    )
+    from relation_lm.kernels.relation_select import relation_select_packed_expand_row
+    from relation_lm.kernels.ring import relation_hidden_cached_ring
+
+    sel, red, rc, head = st["sel"], st["red"], st["router"], st["head"]
+    ring, position, expanded = st["ring"], sel["position"], st["expanded_cache"]
+    st["projection"].project_into_routed(
+        st["memory"], sel["anchor_keys"], sel["partner_keys"], red["operand_cache"],
+        sel["partner_anchor_cache"], position, rc["anchor_raw_cache"], rc["partner_raw_cache"],
+        rc["anchor_conv_cache"], rc["partner_conv_cache"], sel["anchor_block_mean"],
+        sel["anchor_block_std"], sel["partner_block_mean"], sel["partner_block_std"],
+        rc["anchor_conv_weight"], rc["partner_conv_weight"], cfg.block_size, ring=ring)
+    a, s, p, ps = relation_select_packed_expand_row(
+        *select_args(sel, cfg), red["operand_cache"], red["expanded_weight"],
+        red["expanded_bias"], expanded, ring)
+    cached = relation_hidden_cached_ring if ring else relation_hidden_cached
+    hidden = cached(expanded, red["operand_cache"], a, p, red["product_weight"])
+    context, final = relation_linear_norm_reduce_output(
+        hidden, red["second_weight"], red["second_bias"], ps, red["norm_weight"],
+        red["norm_bias"], position, 1e-5, head["query"], head["mix"], head["weight"],
+        head["bias"], 1e-5)
+    return a, s, p, ps, context, final
