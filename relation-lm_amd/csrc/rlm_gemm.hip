@@ -36,7 +36,8 @@
 //                 tiles meet once in LDS.
 //
 // fp32 weights: f32_tile_kernel, 64x64 tiles on v_mfma_f32_16x16x4f32 (fp32
-// operands, fp32 accumulation), so fp32 mode never passes through reduced
+// operands, fp32 accumulation), and f32_skinny_kernel (M <= 64: fp32 FMA dot
+// products split over a wave), so fp32 mode never passes through reduced
 // precision.
 #include "rlm_common.hpp"
 
@@ -578,6 +579,79 @@ __global__ void __launch_bounds__(kSkinnyWaves * kWave) skinny_kernel(const Gemm
 }
 
 // ---------------------------------------------------------------------------
+// fp32 weights, M <= 64 (decode)
+// ---------------------------------------------------------------------------
+
+constexpr int kF32SkinnyCols = 2;    // output columns per wave
+constexpr int kF32SkinnyRows = 8;    // rows of A per workgroup (grid.y)
+constexpr int kF32SkinnyPieces = 3;  // 4-element pieces per lane per pass (768 of K)
+
+// One wave per pair of output columns, four waves per workgroup, eight rows
+// of A per workgroup.  The lanes split K in 16-byte pieces; every load of a
+// pass (both W rows, the A rows) is issued before the first product, through
+// range-checked buffer loads (pieces past K, rows past M or N read zero, so
+// there is no branch), then each of the 8 x 2 dot products is summed over the
+// wave and lane 2r + c writes output (m0 + r, n0 + c).  fp32 FMA throughout:
+// the fp32 path never passes through reduced precision.
+template <typename TO>
+__global__ void __launch_bounds__(256) f32_skinny_kernel(const GemmParams p) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kF32SkinnyCols;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kF32SkinnyRows;
+  const rsrc_t ar = make_rsrc(p.a, p.a_bytes);
+  const rsrc_t wr = make_rsrc(p.w, p.w_bytes);
+  float acc[kF32SkinnyRows][kF32SkinnyCols];
+#pragma unroll
+  for (int r = 0; r < kF32SkinnyRows; ++r)
+#pragma unroll
+    for (int c = 0; c < kF32SkinnyCols; ++c) acc[r][c] = 0.0f;
+  for (int64_t k0 = 0; k0 < p.K; k0 += kWave * 4 * kF32SkinnyPieces) {
+    uint4 wv[kF32SkinnyCols][kF32SkinnyPieces], av[kF32SkinnyRows][kF32SkinnyPieces];
+#pragma unroll
+    for (int j = 0; j < kF32SkinnyPieces; ++j) {
+      const int64_t k = k0 + (j * kWave + lane) * 4;
+#pragma unroll
+      for (int c = 0; c < kF32SkinnyCols; ++c) {
+        const int64_t n = n0 + c;
+        wv[c][j] = buf_load_b128(wr, n < p.N && k < p.K ? static_cast<uint32_t>((n * p.K + k) * 4)
+                                                        : kNoOffset);
+      }
+#pragma unroll
+      for (int r = 0; r < kF32SkinnyRows; ++r) {
+        const int64_t m = m0 + r;
+        av[r][j] = buf_load_b128(ar, m < p.M && k < p.K ? static_cast<uint32_t>((m * p.lda + k) * 4)
+                                                        : kNoOffset);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kF32SkinnyPieces; ++j)
+#pragma unroll
+      for (int r = 0; r < kF32SkinnyRows; ++r)
+#pragma unroll
+        for (int c = 0; c < kF32SkinnyCols; ++c) {
+          float s = acc[r][c];
+          s = fmaf(__uint_as_float(av[r][j].x), __uint_as_float(wv[c][j].x), s);
+          s = fmaf(__uint_as_float(av[r][j].y), __uint_as_float(wv[c][j].y), s);
+          s = fmaf(__uint_as_float(av[r][j].z), __uint_as_float(wv[c][j].z), s);
+          acc[r][c] = fmaf(__uint_as_float(av[r][j].w), __uint_as_float(wv[c][j].w), s);
+        }
+  }
+  TO* out = static_cast<TO*>(p.out);
+#pragma unroll
+  for (int r = 0; r < kF32SkinnyRows; ++r)
+#pragma unroll
+    for (int c = 0; c < kF32SkinnyCols; ++c) {
+      const float sum = wave_sum_f32(acc[r][c]);
+      const int64_t m = m0 + r, n = n0 + c;
+      if (lane == r * kF32SkinnyCols + c && m < p.M && n < p.N) {
+        const float bv = p.bias ? load_any_f(p.bias, p.bias_dtype, n) : 0.0f;
+        out[m * p.ldo + n] = from_f32<TO>(sum + bv);
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // fp32 weights (fp32 MFMA, K steps of 4 per instruction)
 // ---------------------------------------------------------------------------
 
@@ -1102,6 +1176,19 @@ hipError_t linear_impl(const rlm_tensor* input, const rlm_tensor* weight, const 
   if (weight->dtype == RLM_F32) {
     RLM_REQUIRE(input->dtype == RLM_F32, "%s: fp32 weights need fp32 input (got %s)", what,
                 dtype_name(input->dtype));
+    if (M <= kSkinnyM && p.a_bytes != 0 && K % 4 == 0 && p.lda % 4 == 0 &&
+        (reinterpret_cast<uintptr_t>(input->data) & 15u) == 0 &&
+        (reinterpret_cast<uintptr_t>(weight->data) & 15u) == 0) {
+      const dim3 grid(static_cast<unsigned>((N + 4 * kF32SkinnyCols - 1) / (4 * kF32SkinnyCols)),
+                      static_cast<unsigned>((M + kF32SkinnyRows - 1) / kF32SkinnyRows));
+      if (out->dtype == RLM_F32)
+        hipLaunchKernelGGL((f32_skinny_kernel<float>), grid, dim3(256), 0, stream, p);
+      else if (out->dtype == RLM_BF16)
+        hipLaunchKernelGGL((f32_skinny_kernel<bf16>), grid, dim3(256), 0, stream, p);
+      else
+        hipLaunchKernelGGL((f32_skinny_kernel<f16>), grid, dim3(256), 0, stream, p);
+      return launch_status(what);
+    }
     const dim3 grid(static_cast<unsigned>(((M + 63) / 64) * ((N + 63) / 64)));
     if (out->dtype == RLM_F32)
       hipLaunchKernelGGL((f32_tile_kernel<float>), grid, dim3(256), 0, stream, p);

@@ -79,3 +79,37 @@ def test_relation_linear_dma_repeat_identical(device):
     second = ops.relation_linear(a, w, b, torch.float32)
     torch.cuda.synchronize()
     assert torch.equal(first, second)
+
+
+@pytest.mark.parametrize("m,n,k,with_bias", [(1, 512, 576, False), (8, 512, 576, True),
+                                             (3, 37, 100, True), (17, 300, 1000, False),
+                                             (64, 130, 2308, True)])
+def test_relation_linear_fp32_skinny(device, m, n, k, with_bias):
+    # fp32 weights, M <= 64: the fp32 FMA skinny kernel (decode shapes, the
+    # reference's fp32 packed-projection benchmark at B=1 / B=8).
+    g = torch.Generator().manual_seed(m * 7 + n + k)
+    a = torch.randn(m, k, generator=g)
+    w = torch.randn(n, k, generator=g) * 0.02
+    bias = torch.randn(n, generator=g) if with_bias else None
+    print(f"relation_linear fp32 M={m} N={n} K={k} bias={with_bias}", flush=True)
+    got = ops.relation_linear(a.to(device), w.to(device),
+                              None if bias is None else bias.to(device))
+    torch.cuda.synchronize()
+    assert got.dtype == torch.float32
+    check(got, a, w, bias)
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_packed_projection_fp32(device, batch):
+    # The reference's packed-cache benchmark inputs: fp32 memory [B, 576] and
+    # six fp32 weights (benchmarks/benchmark_packed_cache.py:36-47).
+    from relation_lm.inference import pack_sparse_cache_projection_weights
+
+    g = torch.Generator().manual_seed(20260822 + batch)
+    memory = torch.randn(batch, 576, generator=g)
+    weights = [torch.randn(wd, 576, generator=g) * 0.02 for wd in (64, 64, 128, 128, 64, 64)]
+    proj = pack_sparse_cache_projection_weights([x.to(device) for x in weights])
+    parts = proj.project(memory.to(device))
+    torch.cuda.synchronize()
+    for got, wt in zip(parts, weights):
+        check(got, memory, wt, None)
