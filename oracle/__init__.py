@@ -14,6 +14,11 @@ Modules
   router   -- DistilledBlockRouter.block_statistics / _scores restated
   dense    -- RelationLexLM.relation_context and MultiAnchorRelationBlock
               selection restated (dense O(T^2) forms used as special cases)
+  dense_block -- the reference's MultiAnchorRelationBlock module structure in
+              dense torch (float64), the independent check of the routed block
+  multi_block -- the multi-anchor block after selection (relation MLP, slot
+              reduce, stack) restated in numpy
+  eager    -- the whole path in eager fp32 torch (the CPU baseline of bench.py)
 
 Numerics contract shared with the kernels (the reference computes in fp32 with
 Triton's reduction order, which no CPU code can reproduce bit for bit):

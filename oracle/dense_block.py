@@ -1,7 +1,7 @@
 """The reference's MultiAnchorRelationBlock structure as a dense torch module
-(src/relation_lm/models/multi_relation_blocks.py:21-187): test-only, the
-independent formulation the oracle and the routed HIP block are checked
-against (dense causal selection: iterative distinct-anchor argmax with
+(src/relation_lm/models/multi_relation_blocks.py:21-187) -- TEST
+INFRASTRUCTURE ONLY (see oracle/__init__.py): the independent formulation the
+oracle and the routed HIP block are checked against (dense causal selection: iterative distinct-anchor argmax with
 F.one_hot masks, torch.topk over the all-anchor-masked partner scores)."""
 from __future__ import annotations
 

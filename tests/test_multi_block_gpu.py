@@ -3,7 +3,7 @@
 * relation_lm::multi_relation_reduce_seq / layer_norm / block_statistics against
   oracle/multi_block.py (float64) on random inputs, fp32 and bf16;
 * the routed HIP block against the reference block's dense structure
-  (tests/dense_block.py, float64 CPU) where routing keeps every causal position
+  (oracle/dense_block.py, float64 CPU) where routing keeps every causal position
   (T <= local window): same anchors and partner sets, same output within fp32
   rounding;
 * with routing active, the block's selection against the selection oracle
@@ -24,7 +24,7 @@ from oracle import multi_block as omb
 from oracle import select as osel
 from relation_lm.models import MultiRelationBlockConfig, RelationBlockStack
 from relation_lm.models.multi_relation_blocks import MultiAnchorRelationBlock
-from tests.dense_block import DenseBlock
+from oracle.dense_block import DenseBlock
 
 pytestmark = pytest.mark.gpu
 ops = torch.ops.relation_lm

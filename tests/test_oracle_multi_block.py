@@ -16,7 +16,7 @@ import torch
 from torch import nn
 
 from oracle import multi_block as omb
-from tests.dense_block import DenseBlock
+from oracle.dense_block import DenseBlock
 
 
 def params_of(block: DenseBlock) -> dict:
