@@ -57,6 +57,29 @@ __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return f32_to_bf16(v);
 template <>
 __device__ __forceinline__ f16 from_f32<f16>(float v) { return static_cast<f16>(v); }
 
+// The two bf16 halves of a 32-bit word as floats.
+__device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+
+// Four consecutive outputs of one row, converted to TO and written with one
+// store (16 bytes for fp32, 8 bytes for 16-bit types).
+template <typename TO>
+__device__ __forceinline__ void put4(TO* dst, float v0, float v1, float v2, float v3) {
+  if constexpr (sizeof(TO) == 4) {
+    *reinterpret_cast<float4*>(dst) = make_float4(v0, v1, v2, v3);
+  } else if constexpr (__is_same(TO, bf16)) {
+    *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
+  } else {
+    const f16 h[4] = {static_cast<f16>(v0), static_cast<f16>(v1), static_cast<f16>(v2),
+                      static_cast<f16>(v3)};
+    *reinterpret_cast<uint2*>(dst) =
+        make_uint2(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h[0])) |
+                       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h[1])) << 16),
+                   static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h[2])) |
+                       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h[3])) << 16));
+  }
+}
+
 // Four consecutive elements starting at p (p aligned to 4 elements).
 __device__ __forceinline__ float4 load4(const float* p) {
   return *reinterpret_cast<const float4*>(p);

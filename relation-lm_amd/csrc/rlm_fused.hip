@@ -172,8 +172,6 @@ __device__ float row_weight(const float (&sc)[16], int64_t t, uint32_t K, uint32
   return mine / fmaxf(total, 1.0e-9f);
 }
 
-__device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
 
 // Streams rows [chunk*128, chunk*128+128) of W_m into an LDS tile of 128 rows
 // x R bf16.  16-byte piece q of row n is stored at piece q ^ (n % (R/8)) so

@@ -290,19 +290,6 @@ __device__ __forceinline__ uint4 load8_buf(rsrc_t r, uint32_t elem, bool valid) 
   }
 }
 
-// Four consecutive outputs of one row, packed for one LDS write.
-template <typename TO>
-__device__ __forceinline__ void put4(TO* dst, float v0, float v1, float v2, float v3) {
-  if constexpr (sizeof(TO) == 4) {
-    *reinterpret_cast<float4*>(dst) = make_float4(v0, v1, v2, v3);
-  } else if constexpr (__is_same(TO, bf16)) {
-    *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
-  } else {
-    *reinterpret_cast<uint2*>(dst) =
-        make_uint2(pack2(to_bits<f16>(v0), to_bits<f16>(v1)), pack2(to_bits<f16>(v2), to_bits<f16>(v3)));
-  }
-}
-
 // LDS of smallk_kernel: the workgroup's A and W tiles, 128 rows x K 16-bit
 // elements each, 16-byte piece q of row r stored at piece q ^ (r % SW) (SW
 // the largest of 16, 8, 4 dividing K/8) so that the rows of an MFMA fragment

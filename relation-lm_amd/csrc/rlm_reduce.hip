@@ -65,20 +65,22 @@ struct HiddenParams {
 // Per-row bookkeeping of a workgroup's 64 (query, partner) rows, in LDS.
 // Offsets are byte offsets into the caches; kNoOffset marks an index outside
 // [0, T) (the row then gathers zeros) or a padding row past the end.
-struct RowTable {
-  int32_t b[kRows];      // batch row
-  int32_t a[kRows];      // anchor index (-1 if out of range)
-  int32_t p[kRows];      // partner index (-1 if out of range)
-  uint32_t op_a[kRows];  // operand row of the anchor (kNoOffset unless both indices are valid)
-  uint32_t op_p[kRows];  // operand row of the partner (same validity)
-  uint32_t x_a[kRows];   // anchor half of the anchor's expanded row
-  uint32_t x_p[kRows];   // partner half of the partner's expanded row
+template <int NR>
+struct RowTableN {
+  int32_t b[NR];      // batch row
+  int32_t a[NR];      // anchor index (-1 if out of range)
+  int32_t p[NR];      // partner index (-1 if out of range)
+  uint32_t op_a[NR];  // operand row of the anchor (kNoOffset unless both indices are valid)
+  uint32_t op_p[NR];  // operand row of the partner (same validity)
+  uint32_t x_a[NR];   // anchor half of the anchor's expanded row
+  uint32_t x_p[NR];   // partner half of the partner's expanded row
 };
+using RowTable = RowTableN<kRows>;
 
-template <typename T>
-__device__ __forceinline__ void load_rows(const HiddenParams& p, int64_t r0, RowTable& rt) {
+template <typename T, int NR = kRows>
+__device__ __forceinline__ void load_rows(const HiddenParams& p, int64_t r0, RowTableN<NR>& rt) {
   const int tid = threadIdx.x;
-  if (tid < kRows) {
+  if (tid < NR) {
     const int64_t row = r0 + tid;
     // Unconditional loads (padding rows read row 0, the position a stand-in
     // when there is none), decoded by selects: one round trip.
@@ -438,6 +440,230 @@ __global__ void __launch_bounds__(256) hidden_bf16_kernel(const HiddenParams p) 
 #pragma unroll
     for (int j = 0; j < TN; ++j)
       store_hidden(p, outr, acc[i][j], xs[i][j], r0, wr + i * 16, n0 + wc + j * 16 + r16, lane);
+}
+
+// bf16 caches, sequence form with many rows: a workgroup of four waves owns
+// 64 rows and walks every 256-column tile of the hidden dimension, so the
+// rows' indices and operand products are read and formed once per row tile.
+//   set-up  the row table, then the rows' exact operand products op[a] *
+//           op[p] (fp32, split into hi + lo bf16 as hidden_bf16_kernel does)
+//           into LDS;
+//   per column tile (wave w: columns n0 + 64w .. + 63)
+//     - hidden^T = W_m . P^T on v_mfma_f32_32x32x16_bf16 (hi and lo; W_m
+//       fragments straight from L2 in operand layout, loaded during the
+//       second half of the previous column tile's epilogue);
+//     - the fp32 sums are restaged through the wave's own LDS region one
+//       32-row block at a time and read back row-contiguous: a lane takes
+//       eight consecutive columns of one row, adds the expanded-cache halves
+//       X[a, n..n+7] and X[p, H+n..H+n+7] (16-byte gathers, eight lanes per
+//       128-byte row segment, issued one column tile ahead), applies GELU and
+//       stores 8 outputs.
+// Several workgroups share a CU, so one's load round trips overlap another's
+// GELU and matrix work.  LDS rows of the products are R*2 bytes, 16-byte
+// piece q of row r stored at piece q ^ swz(r) (conflict-free fragment reads).
+constexpr int kTileRows = 64;
+constexpr int kTileCols = 256;
+constexpr int kTileThreads = 256;
+constexpr int kStageRow = 64 * 4 + 16;                 // staged fp32 row stride (bytes)
+constexpr int kStageBytes = 32 * kStageRow;            // one wave's 32-row block
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int PR>
+__device__ __forceinline__ int tile_swz(int r) {
+  if constexpr (PR == 16) return r & 15;
+  else return (r & 7) ^ ((r >> 3) & 1);
+}
+
+// LDS: the hi / lo product tiles, the four waves' staging, the row table.
+template <int R>
+constexpr int hidden_tile_stage_offset() {
+  return 2 * kTileRows * R * 2;
+}
+template <int R>
+constexpr int hidden_tile_table_offset() {
+  return hidden_tile_stage_offset<R>() + 4 * kStageBytes;
+}
+template <int R>
+constexpr size_t hidden_tile_lds_bytes() {
+  return static_cast<size_t>(hidden_tile_table_offset<R>()) + sizeof(RowTableN<kTileRows>);
+}
+
+// Eight consecutive outputs of one row.
+template <typename TO>
+__device__ __forceinline__ void put8(TO* dst, const float (&v)[8]) {
+  if constexpr (sizeof(TO) == 4) {
+    reinterpret_cast<float4*>(dst)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(dst)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+    *reinterpret_cast<uint4*>(dst) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+  }
+}
+
+template <typename TO, int R>
+__global__ void __launch_bounds__(kTileThreads, 2) hidden_tile_kernel(const HiddenParams p) {
+  constexpr int PR = R / 8;                              // 16-byte pieces per LDS row
+  constexpr int RB = R * 2;                              // bytes per LDS row
+  constexpr int KK = R / 16;                             // MFMA k-steps
+  constexpr int kPieces = kTileRows * PR / kTileThreads; // product pieces per thread
+  static_assert(R == 64 || R == 128, "relation dim 64 or 128");
+  static_assert(__is_same(TO, float) || __is_same(TO, bf16), "fp32 or bf16 hidden");
+  extern __shared__ __align__(16) unsigned char smem[];
+  unsigned char* p_hi = smem;
+  unsigned char* p_lo = smem + kTileRows * RB;
+  auto& rt = *reinterpret_cast<RowTableN<kTileRows>*>(smem + hidden_tile_table_offset<R>());
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int64_t row_tiles = (p.rows + kTileRows - 1) / kTileRows;
+  // Row tiles of neighbouring queries run on one XCD (one L2 for their gathers).
+  const int64_t r0 = xcd_tile(blockIdx.x, row_tiles) * kTileRows;
+  const int col_tiles = (p.H + kTileCols - 1) / kTileCols;
+  const rsrc_t xr = make_rsrc(p.expanded, p.expanded_bytes);
+  const rsrc_t opr = make_rsrc(p.operand, p.operand_bytes);
+  const rsrc_t wr = make_rsrc(p.wm, p.wm_bytes);
+  unsigned char* stage = smem + hidden_tile_stage_offset<R>() + wave * kStageBytes;
+  TO* out = reinterpret_cast<TO*>(p.out);
+
+  // W_m fragments of column tile ct: block j of 32 hidden columns, k-step kk --
+  // row n0 + 64 wave + 32j + (lane & 31), k = 16kk + 8 (lane >> 5) .. +7
+  // (rows past H read zero).
+  u16x8 fw[2][KK];
+  auto load_w = [&](int ct) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = ct * kTileCols + wave * 64 + 32 * j + (lane & 31);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk)
+        fw[j][kk] = __builtin_bit_cast(
+            u16x8, buf_load_b128(wr, n < p.H ? static_cast<uint32_t>(n * RB + 32 * kk + 16 * (lane >> 5))
+                                             : kNoOffset));
+    }
+  };
+
+  // Set-up: row table, then the products (every load of a thread issued first).
+  load_rows<bf16, kTileRows>(p, r0, rt);
+  __syncthreads();
+  {
+    uint4 va[kPieces], vp[kPieces];
+#pragma unroll
+    for (int c = 0; c < kPieces; ++c) {
+      const int piece = c * kTileThreads + tid;
+      const int row = piece / PR, q = piece % PR;
+      va[c] = buf_load_b128(opr, rt.op_a[row] + 16u * q);
+      vp[c] = buf_load_b128(opr, rt.op_p[row] + 16u * q);
+    }
+    load_w(0);
+#pragma unroll
+    for (int c = 0; c < kPieces; ++c) {
+      const int piece = c * kTileThreads + tid;
+      const int row = piece / PR, q = piece % PR;
+      const uint32_t wa[4] = {va[c].x, va[c].y, va[c].z, va[c].w};
+      const uint32_t wp[4] = {vp[c].x, vp[c].y, vp[c].z, vp[c].w};
+      uint32_t h[4], l[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x0 = bf16_lo(wp[e]) * bf16_lo(wa[e]);
+        const float x1 = bf16_hi(wp[e]) * bf16_hi(wa[e]);
+        h[e] = pack_bf16x2(x0, x1);
+        l[e] = pack_bf16x2(x0 - bf16_lo(h[e]), x1 - bf16_hi(h[e]));
+      }
+      const int at = row * RB + ((q ^ tile_swz<PR>(row)) << 4);
+      *reinterpret_cast<uint4*>(p_hi + at) = make_uint4(h[0], h[1], h[2], h[3]);
+      *reinterpret_cast<uint4*>(p_lo + at) = make_uint4(l[0], l[1], l[2], l[3]);
+    }
+  }
+  __syncthreads();
+  const int swz = tile_swz<PR>(lane & 15);
+
+  // Row-contiguous roles of the epilogue: piece t of block i is row
+  // 32i + 8t + (lane >> 3), columns 8 (lane & 7) .. +7 of the wave's 64.
+  const int c8 = 8 * (lane & 7);
+  uint4 xa[2][4], xp[2][4];
+  auto load_x = [&](int ct, int i) {
+    const int n = ct * kTileCols + wave * 64 + c8;
+    const bool in = n < p.H;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int m = 32 * i + 8 * t + (lane >> 3);
+      xa[i][t] = buf_load_b128(xr, in ? rt.x_a[m] + 2u * n : kNoOffset);
+      xp[i][t] = buf_load_b128(xr, in ? rt.x_p[m] + 2u * n : kNoOffset);
+    }
+  };
+  load_x(0, 0);
+  load_x(0, 1);
+
+  for (int ct = 0; ct < col_tiles; ++ct) {
+    const int wn0 = ct * kTileCols + wave * 64;
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[j][i][e] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const int off = (lane & 31) * RB + (((2 * kk + (lane >> 5)) ^ swz) << 4);
+      u16x8 fh[2], fl[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        fh[i] = *reinterpret_cast<const u16x8*>(p_hi + 32 * i * RB + off);
+        fl[i] = *reinterpret_cast<const u16x8*>(p_lo + 32 * i * RB + off);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8, fw[j][kk]), __builtin_bit_cast(bf16x8, fh[i]), acc[j][i], 0, 0, 0);
+          acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8, fw[j][kk]), __builtin_bit_cast(bf16x8, fl[i]), acc[j][i], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      // The next tile's W_m fragments once block 0's accumulators are free.
+      if (i == 1 && ct + 1 < col_tiles) load_w(ct + 1);
+      // acc block i: lane holds row (lane & 31), columns 32j + 8q + 4 (lane >> 5) .. +3.
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<float4*>(stage + (lane & 31) * kStageRow + (32 * j + 8 * q + 4 * (lane >> 5)) * 4) =
+              make_float4(acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2],
+                          acc[j][i][4 * q + 3]);
+      wave_sync();
+      // Wave-uniform: whole pieces inside the output, or the edge path.
+      const bool full = r0 + 32 * i + 32 <= p.rows && wn0 + 64 <= p.H;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int row = 8 * t + (lane >> 3);
+        const float4 s0 = *reinterpret_cast<const float4*>(stage + row * kStageRow + c8 * 4);
+        const float4 s1 = *reinterpret_cast<const float4*>(stage + row * kStageRow + c8 * 4 + 16);
+        const uint32_t a[4] = {xa[i][t].x, xa[i][t].y, xa[i][t].z, xa[i][t].w};
+        const uint32_t b[4] = {xp[i][t].x, xp[i][t].y, xp[i][t].z, xp[i][t].w};
+        const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[2 * e] = gelu_erf(sv[2 * e] + (bf16_lo(a[e]) + bf16_lo(b[e])));
+          v[2 * e + 1] = gelu_erf(sv[2 * e + 1] + (bf16_hi(a[e]) + bf16_hi(b[e])));
+        }
+        const int64_t m = r0 + 32 * i + row;
+        if (full) {
+          put8<TO>(out + m * p.H + wn0 + c8, v);
+        } else if (m < p.rows) {
+          for (int k = 0; k < 8; ++k)
+            if (wn0 + c8 + k < p.H) out[m * p.H + wn0 + c8 + k] = from_f32<TO>(v[k]);
+        }
+      }
+      wave_sync();
+      if (ct + 1 < col_tiles) load_x(ct + 1, i);
+    }
+  }
 }
 
 // fp32 / fp16 caches: fp32 products on v_mfma_f32_16x16x4f32.  64 hidden
@@ -1077,8 +1303,37 @@ hipError_t launch_hidden(HiddenParams& p, int dtype, bool update, hipStream_t st
   const unsigned row_tiles = static_cast<unsigned>((p.rows + kRows - 1) / kRows);
   RLM_REQUIRE(row_tiles <= 65535u * 1024u, "too many relation rows");
   if (dtype == RLM_BF16) {
-    // 128-column tiles when there are enough rows to fill the chip, else 64
-    // (always 64 in the update form, whose fresh rows live in LDS too).
+    // Sequence form with many rows, relation dim 64 or 128: a 64-row tile of
+    // four waves per workgroup over every column (the same arithmetic for
+    // fp32 and bf16 outputs).  Otherwise 128-column tiles when there are enough rows
+    // to fill the chip, else 64 (always 64 in the update form, whose fresh
+    // rows live in LDS too).
+    if (!update && p.rows >= 4096 && (p.R == 128 || p.R == 64) && p.H % 8 == 0 &&
+        (reinterpret_cast<uintptr_t>(p.out) & 15u) == 0) {
+      const int64_t tiles = (p.rows + kTileRows - 1) / kTileRows;
+      RLM_REQUIRE(tiles <= 0x7fffffff, "too many relation rows");
+#define RLM_TILE_CASE(TO, R)                                                                    \
+  {                                                                                             \
+    constexpr size_t lds = hidden_tile_lds_bytes<R>();                                          \
+    static const hipError_t attr = hipFuncSetAttribute(                                         \
+        reinterpret_cast<const void*>(&hidden_tile_kernel<TO, R>),                              \
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));                     \
+    if (attr != hipSuccess) {                                                                   \
+      set_error("relation_hidden: cannot reserve %zu bytes of LDS: %s", lds,                   \
+                hipGetErrorString(attr));                                                       \
+      return attr;                                                                              \
+    }                                                                                           \
+    hipLaunchKernelGGL((hidden_tile_kernel<TO, R>), dim3(static_cast<unsigned>(tiles)),         \
+                       dim3(kTileThreads), lds, stream, p);                                     \
+  }
+      if (p.out_bf16) {
+        if (p.R == 128) RLM_TILE_CASE(bf16, 128) else RLM_TILE_CASE(bf16, 64)
+      } else {
+        if (p.R == 128) RLM_TILE_CASE(float, 128) else RLM_TILE_CASE(float, 64)
+      }
+#undef RLM_TILE_CASE
+      return launch_status("relation_hidden");
+    }
     if (update) {
       const dim3 grid(static_cast<unsigned>((p.H + 63) / 64), row_tiles);
       hipLaunchKernelGGL((hidden_bf16_kernel<true, 64>), grid, dim3(256), 0, stream, p);

@@ -510,3 +510,44 @@ def test_hidden_seq_out_bf16_feeds_the_linear_unchanged(device, hidden_dim, rela
     assert torch.equal(h32b, h32)
     assert torch.equal(h16, h32.to(torch.bfloat16))
     assert torch.equal(raw16, raw32)
+
+
+@pytest.mark.parametrize("b,t,tq,k,r,h,out_dtype", [
+    (2, 256, 256, 8, 128, 768, torch.float32),    # 4096 rows, a partial column tile
+    (1, 512, 600, 7, 64, 520, torch.bfloat16),    # 4200 rows (partial row tile), R = 64
+    (1, 512, 600, 7, 64, 520, torch.float32),
+    (1, 4096, 1024, 6, 128, 3072, torch.bfloat16),  # the multi-anchor block's widths
+])
+def test_hidden_seq_tile_path(device, b, t, tq, k, r, h, out_dtype):
+    """relation_hidden_cached_seq(_out) with many rows (the 128 x 256 tile kernel)
+    against the float64 oracle: fp32 within 1e-5 relative, bf16 within that
+    plus one rounding of the element.  Some partner indices are out of
+    range (the selection's negative sentinel, and past the cache), which read
+    as zero rows."""
+    from relation_lm.kernels.relation_reduce import relation_hidden_cached_seq_out
+    g = torch.Generator().manual_seed(b * 1000 + tq + k + r + h)
+    operand = torch.randn(b, t, r, generator=g).to(torch.bfloat16)
+    expanded = torch.randn(b, t, 2 * h, generator=g).to(torch.bfloat16)
+    wm = (torch.randn(h, r, generator=g) * r ** -0.5).to(torch.bfloat16)
+    anchor = torch.randint(0, t, (b, tq), generator=g)
+    partner = torch.randint(0, t, (b, tq, k), generator=g)
+    partner[:, ::17, 0] = -3          # sentinel of an exhausted partner slot
+    partner[:, 5::23, 1] = t + 2      # past the cache
+    print(f"hidden tile path B={b} Tq={tq} K={k} R={r} H={h} {out_dtype}", flush=True)
+    out = torch.empty(b, tq, k, h, dtype=out_dtype, device=device)
+    relation_hidden_cached_seq_out(expanded.to(device), operand.to(device), anchor.to(device),
+                                   partner.to(device), wm.to(device), out)
+    torch.cuda.synchronize()
+    exp = ored.relation_hidden_cached_seq(host(expanded), host(operand), host(anchor),
+                                          host(partner), host(wm))
+    got = host(out)
+    # fp32: the relative bound; bf16: one rounding of the element on top of it
+    # (the fp32 floor covers the GELU tail, where outputs of ~1e-7 carry the
+    # erf approximation's absolute error).
+    bound = FP32_REL * np.abs(exp).max()
+    if out_dtype != torch.float32:
+        bound = bound + np.exp2(np.floor(np.log2(np.maximum(np.abs(exp), 1e-30))) - 7)
+    excess = np.abs(got - exp) - bound
+    worst = np.unravel_index(np.argmax(excess), excess.shape)
+    assert excess[worst] <= 0, (worst, float(got[worst]), float(exp[worst]),
+                                int((excess > 0).sum()))
