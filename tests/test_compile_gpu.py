@@ -284,6 +284,11 @@ def op_cases(device):
                   (raw_multi, scores_multi, red["norm_weight"], red["norm_bias"],
                    torch.zeros(slots, device=device), torch.tensor(-1.5, device=device),
                    query_seq, positions, 1e-5)))
+    cases.append(("multi_relation_reduce_seq_out", ops.multi_relation_reduce_seq_out.default,
+                  (raw_multi, scores_multi, red["norm_weight"], red["norm_bias"],
+                   torch.zeros(slots, device=device), torch.tensor(-1.5, device=device),
+                   query_seq, positions, 1e-5, None, torch.empty_like(query_seq),
+                   torch.empty(query_seq.shape, device=device, dtype=torch.float32))))
     cases.append(("layer_norm", ops.layer_norm.default,
                   (query_seq, red["norm_weight"], red["norm_bias"], 1e-5)))
     keys = torch.randn(b, t, 64, generator=g).to(device, torch.bfloat16)
@@ -302,7 +307,8 @@ OP_NAMES = ("relation_select_packed", "relation_select_packed_seq",
             "packed_projection_to_caches", "packed_projection_router_update",
             "relation_linear", "relation_linear_out",
             "relation_norm_reduce_output", "relation_norm_reduce_output_seq",
-            "relation_linear_norm_reduce_output", "multi_relation_reduce_seq", "layer_norm", "block_statistics")
+            "relation_linear_norm_reduce_output", "multi_relation_reduce_seq",
+            "multi_relation_reduce_seq_out", "layer_norm", "block_statistics")
 
 
 def test_opcheck_every_registered_op(device):
