@@ -295,7 +295,9 @@ __device__ __forceinline__ float gelu_erf(float x) {
   y = fmaf(y, t, 0.5f * 0.254829592f);
   y *= t;
   const float e = __builtin_amdgcn_exp2f(x * (x * (-0.5f * 1.44269504088896340736f)));
-  return fmaf(-a, y * e, fmaxf(x, 0.0f));
+  // max(x, 0) on the bit pattern: one integer max, where fmaxf would first
+  // quiet a possible signalling NaN (x is usually a matrix-core result).
+  return fmaf(-a, y * e, __int_as_float(max(__float_as_int(x), 0)));
 }
 
 // Renumbers workgroup `i` of `count` so that each XCD (the hardware deals

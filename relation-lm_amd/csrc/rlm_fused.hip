@@ -32,10 +32,10 @@
 //            hidden fragments from LDS one fragment ahead, and the raw
 //            accumulators stay in registers for the whole kernel.  The
 //            transposed product leaves one slot's columns in a lane.
-// Epilogue: + b2; LayerNorm moments per slot (in-lane sums, the two wave
-// halves, then the D-direction waves merged in LDS); partner weights and the
-// sum over a query's partners (in-lane over row tiles, then DPP / permlane
-// across the lanes of the query); 16-byte buffer stores.
+// Epilogue (the accumulators start at b2): LayerNorm moments per slot (in-lane
+// sums, the two wave halves, then the D-direction waves merged in LDS); partner
+// weights and the sum over a query's partners (in-lane over row tiles, then DPP
+// / permlane across the lanes of the query); 16-byte buffer stores.
 #include "rlm_common.hpp"
 
 namespace rlm {
@@ -362,14 +362,9 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
       w[j] = as_frag(buf_load_b128(w2r, w2_lane + (32u * j * H + chunk * kHC + 16 * s) * 2u));
   };
 
-  // raw[j][i][4ii + jj] = raw^T[d = d0 + 32j + 8ii + 4h + jj][slot 32(RTW rg + i) + n32].
+  // raw[j][i][4ii + jj] = raw^T[d = d0 + 32j + 8ii + 4h + jj][slot 32(RTW rg + i) + n32],
+  // started at b2[d] once the set-up has put b2 in LDS.
   f32x16 raw[DTW][RTW];
-#pragma unroll
-  for (int j = 0; j < DTW; ++j)
-#pragma unroll
-    for (int i = 0; i < RTW; ++i)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) raw[j][i][e] = 0.0f;
 
   const unsigned char* my_gat = smem + kOffGather + lslot * kGatherRowBytes;
   // Constant A operand [I16 | I16]: lane (r16, g) holds row r16, k = 8g..8g+7,
@@ -377,6 +372,7 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
   u16x8 ident;
 #pragma unroll
   for (int k = 0; k < 8; ++k) ident[k] = (8 * (g & 1) + k == r16) ? 0x3F80 : 0;
+  asm volatile("" : "+v"(ident));  // kept in four registers, not rebuilt in every chunk
   unsigned char* my_hid = hid + lslot * (2 * kLd) + 8 * g;
   // B operand of phase 2: hidden slot 32(RTW rg + i) + n32, k = 16s + 8h.
   const unsigned char* brow = hid + (32 * RTW * rg + n32) * (2 * kLd) + 16 * h;
@@ -384,6 +380,19 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
   const int nchunks = H / kHC;
   __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this lane's W_m and gather pieces of chunk 0 are in LDS
   __syncthreads();
+#pragma unroll
+  for (int j = 0; j < DTW; ++j)
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const float4 b4 = *reinterpret_cast<const float4*>(cst + d0 + 32 * j + 8 * ii + 4 * h);
+#pragma unroll
+      for (int i = 0; i < RTW; ++i) {
+        raw[j][i][4 * ii + 0] = b4.x;
+        raw[j][i][4 * ii + 1] = b4.y;
+        raw[j][i][4 * ii + 2] = b4.z;
+        raw[j][i][4 * ii + 3] = b4.w;
+      }
+    }
 
   for (int c = 0; c < nchunks; ++c) {
     // W2 fragments of this chunk's phase 2, k-step by k-step.  The first
@@ -467,20 +476,7 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
   }
 
   // ---- Epilogue.  A lane holds, for each of its RTW slots, 16*DTW of the
-  // wave's 32*DTW columns; the other 16*DTW are in lane ^ 32.
-#pragma unroll
-  for (int j = 0; j < DTW; ++j)
-#pragma unroll
-    for (int ii = 0; ii < 4; ++ii) {
-      const float4 b4 = *reinterpret_cast<const float4*>(cst + d0 + 32 * j + 8 * ii + 4 * h);
-#pragma unroll
-      for (int i = 0; i < RTW; ++i) {
-        raw[j][i][4 * ii + 0] += b4.x;
-        raw[j][i][4 * ii + 1] += b4.y;
-        raw[j][i][4 * ii + 2] += b4.z;
-        raw[j][i][4 * ii + 3] += b4.w;
-      }
-    }
+  // wave's 32*DTW columns; the other 16*DTW are in lane ^ 32.  b2 is already in.
   // Row moments.  Each wave takes the mean and centred sum of squares of its
   // 32*DTW columns of each of its slots (in-lane sums, then the two halves of
   // the wave); threads 0..127 merge the DG waves of the slot's row group (Chan,
