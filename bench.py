@@ -184,6 +184,7 @@ def main() -> int:
         select_args,
         selection_inputs,
     )
+    from relation_lm.workloads import ONE_ROUND_WORKGROUPS
     from relation_lm.workloads import decode_step as workload_decode_step
 
     device = torch.device("cuda", 0)
@@ -220,8 +221,8 @@ def main() -> int:
 
             def decode_step(state=state, dcfg=dcfg):
                 # projection + cache rows + router update; selection with the
-                # token's expanded-cache row; cached hidden; split-K second
-                # linear and norm-reduce with the output-head preparation
+                # token's expanded-cache row; the relation tail (cached hidden,
+                # second linear, norm-reduce with the output-head preparation)
                 return workload_decode_step(state, dcfg)[-1]
 
             for _ in range(20):
@@ -240,7 +241,21 @@ def main() -> int:
                 graph.replay()
             torch.cuda.synchronize()
             graph_us = windowed_us(graph.replay, args.decode_steps)
-            decode[f"B{batch}"] = {"eager_us": round(eager_us, 2), "graph_us": round(graph_us, 2)}
+            # Four steps per replay: the host's per-replay launch cost (about the
+            # GPU time of one step once the step is three launches) paid once per
+            # four steps; the GPU work per step is the same.
+            graph4 = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph4):
+                for _ in range(4):
+                    decode_step()
+            for _ in range(5):
+                graph4.replay()
+            torch.cuda.synchronize()
+            graph4_us = windowed_us(graph4.replay, max(10, args.decode_steps // 4)) / 4
+            one_launch_tail = batch * (dcfg.hidden_dim // 64) <= ONE_ROUND_WORKGROUPS
+            decode[f"B{batch}"] = {"eager_us": round(eager_us, 2), "graph_us": round(graph_us, 2),
+                                   "graph_x4_us": round(graph4_us, 2),
+                                   "launches": 3 if one_launch_tail else 5}
 
         return decode
 

@@ -330,6 +330,58 @@ hipError_t rlm_relation_linear_norm_reduce_output_noalloc(
     const rlm_tensor* out_context, const rlm_tensor* out_final, hipStream_t stream);
 
 /*
+ * The decode step's relation tail in one launch (no single reference op: the
+ * reference calls relation_hidden_cached, src/relation_lm/kernels/
+ * relation_reduce.py:149-183, then F.linear and relation_norm_reduce,
+ * relation_reduce.py:420-450, benchmarks/benchmark_relation_reduce.py:55-64,
+ * and prepares the output head, models/relation_lm.py:203-206): the result of
+ *   hidden = rlm_relation_hidden_cached(_ring)(...)       (fp32, [B,K,H])
+ *   rlm_relation_linear_norm_reduce_output(hidden, ...)
+ * with the hidden rounded to bf16 for the second linear (as that op's 16-bit
+ * path does) and the linear's fp32 sums in another order: equal to fp32
+ * rounding of the raw rows, not bit for bit.
+ *   expanded_cache [B,T,2H], operand_cache [B,T,R], product_weight [H,R],
+ *   second_weight [D,H] (all bf16), anchor_index [B], partner_index [B,K]
+ *   (int32/int64), second_bias/norm_weight/norm_bias/output_weight/
+ *   output_bias [D], partner_scores f32 [B,K], position 0-d, query [B,D],
+ *   mix_logit 0-d; ring != 0: ring-buffer caches (T a power of two, index i
+ *   in row i mod T), as rlm_relation_hidden_cached_ring.
+ *   workspace: fp32 [n] and counters: int32 [m] with n, m from
+ *   rlm_relation_hidden_linear_norm_reduce_output_workspace.  The counters
+ *   must be zero before the first call and are zero again when each call
+ *   ends; calls that overlap on one device must use different counters.
+ *   out_context f32 [B,D], out_final [B,D] in the query's dtype.
+ * Shapes: R in {64, 128}, H a multiple of 64 up to 3072, 1 <= K <= 8,
+ * D a multiple of 4 up to 768 (rlm_relation_hidden_linear_norm_reduce_output_fits
+ * says whether given tensors qualify; other shapes fail with
+ * hipErrorInvalidValue and run the two ops above).
+ */
+hipError_t rlm_relation_hidden_linear_norm_reduce_output(
+    const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
+    const rlm_tensor* anchor_index, const rlm_tensor* partner_index,
+    const rlm_tensor* product_weight, const rlm_tensor* second_weight,
+    const rlm_tensor* second_bias, const rlm_tensor* partner_scores,
+    const rlm_tensor* norm_weight, const rlm_tensor* norm_bias, const rlm_tensor* position,
+    double norm_eps, const rlm_tensor* query, const rlm_tensor* mix_logit,
+    const rlm_tensor* output_weight, const rlm_tensor* output_bias, double output_eps,
+    int32_t ring, const rlm_tensor* workspace, const rlm_tensor* counters,
+    const rlm_tensor* out_context, const rlm_tensor* out_final, hipStream_t stream);
+
+/* Workspace sizes of rlm_relation_hidden_linear_norm_reduce_output for B
+ * queries of K partners, hidden dim H (a multiple of 64) and d_model D:
+ * *workspace_floats fp32 elements and *counters int32 elements. */
+hipError_t rlm_relation_hidden_linear_norm_reduce_output_workspace(
+    int64_t batch, int64_t partners, int64_t hidden_dim, int64_t d_model,
+    int64_t* workspace_floats, int64_t* counters);
+
+/* 1 if rlm_relation_hidden_linear_norm_reduce_output takes these tensors
+ * (dtypes, shapes, alignment), else 0. */
+int rlm_relation_hidden_linear_norm_reduce_output_fits(
+    const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
+    const rlm_tensor* partner_index, const rlm_tensor* product_weight,
+    const rlm_tensor* second_weight);
+
+/*
  * Sequence form of rlm_relation_norm_reduce_output: raw [B,Tq,K,D],
  * partner_scores [B,Tq,K], positions [Tq] or [B,Tq], query [B,Tq,D];
  * out_context f32 [B,Tq,D], out_final [B,Tq,D].

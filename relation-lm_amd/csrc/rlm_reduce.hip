@@ -30,6 +30,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kRows = 64;   // (query, partner) rows per workgroup
 constexpr int kRC16 = 128;  // relation-dim chunk staged in LDS, 16-bit path
@@ -779,7 +780,7 @@ struct NormParams {
   // Raw rows given as split-K partial products (the per-query kernel only):
   // raw = sum_z parts[z] + b2, the splits added in order.
   const float* parts;   // [nparts][Q*K][D] fp32
-  int nparts;
+  int nparts;           // 1 .. the kernel's NP
   const void* b2;       // [D]
   int b2_dtype;
 };
@@ -1018,16 +1019,21 @@ __device__ __forceinline__ float4 chunk4_decode(const Chunk4& v, int dtype) {
 }
 
 // NP > 0: the raw rows are the sum of NP split-K partial products plus b2.
-template <int RPW, int GI, int NP>
-__global__ void __launch_bounds__(kQWaves * kWave) __attribute__((amdgpu_waves_per_eu(1, 1)))
-norm_reduce_query_kernel(const NormParams p) {
+// Query q on threads 0 .. 4*64-1 of the workgroup (any further waves of the
+// workgroup must have exited: the barriers below count the threads that remain).
+// Cache policy of a device-coherent access (SC1): what agent-scope atomic loads and
+// stores use, so data another workgroup (on any XCD) publishes this way is read
+// without stale cache lines, with no whole-cache writeback or invalidation.
+constexpr int kCpolDevice = 16;
+
+template <int RPW, int GI, int NP, bool COHERENT = false>
+__device__ __forceinline__ void norm_query(const NormParams& p, int64_t q) {
   __shared__ float4 par[5][kQMaxD / 4];         // w, b, query, ow, ob as fp32
   __shared__ float4 part[kQWaves][kQMaxD / 4];  // each wave's sum_k p_k xhat_k
   __shared__ float red[2][kQWaves];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int64_t q = blockIdx.x;
   const int64_t b = q / p.Tq;
   const int64_t tq = q - b * p.Tq;
   const int groups = p.D >> 2;
@@ -1053,7 +1059,7 @@ norm_reduce_query_kernel(const NormParams p) {
     // partial of the wave's rows is loaded before any is added, so the
     // partials cost one memory round trip.
     const uint32_t pstride = static_cast<uint32_t>(p.Q * p.K * p.D) * 4u;  // bytes per split
-    const rsrc_t prs = make_rsrc(p.parts, pstride * static_cast<uint32_t>(NP));
+    const rsrc_t prs = make_rsrc(p.parts, pstride * static_cast<uint32_t>(p.nparts));
     const uint32_t qoff = static_cast<uint32_t>(q * p.K * p.D) * 4u;
     F4Words bw[GI];
 #pragma unroll
@@ -1072,7 +1078,11 @@ norm_reduce_query_kernel(const NormParams p) {
         // Lanes past the row and rows past K read nothing.
         const uint32_t off = qoff + static_cast<uint32_t>((in ? k : 0) * p.D + 4 * (in ? g : 0)) * 4u;
 #pragma unroll
-        for (int z = 0; z < NP; ++z) w[r][i][z] = buf_load_b128(prs, in ? off + z * pstride : kNoOffset);
+        for (int z = 0; z < NP; ++z)
+          w[r][i][z] = __builtin_bit_cast(
+              uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                         prs, in && z < p.nparts ? off + z * pstride : kNoOffset, 0,
+                         COHERENT ? kCpolDevice : 0));
       }
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
@@ -1085,10 +1095,11 @@ norm_reduce_query_kernel(const NormParams p) {
                                __uint_as_float(w[r][i][0].z), __uint_as_float(w[r][i][0].w));
 #pragma unroll
         for (int z = 1; z < NP; ++z) {
-          v.x += __uint_as_float(w[r][i][z].x);
-          v.y += __uint_as_float(w[r][i][z].y);
-          v.z += __uint_as_float(w[r][i][z].z);
-          v.w += __uint_as_float(w[r][i][z].w);
+          const bool use = z < p.nparts;  // at most NP partial products, nparts of them given
+          v.x = use ? v.x + __uint_as_float(w[r][i][z].x) : v.x;
+          v.y = use ? v.y + __uint_as_float(w[r][i][z].y) : v.y;
+          v.z = use ? v.z + __uint_as_float(w[r][i][z].z) : v.z;
+          v.w = use ? v.w + __uint_as_float(w[r][i][z].w) : v.w;
         }
         const float4 b4 = f4_decode(bw[i], p.b2_dtype);
         x[r][i] = in ? make_float4(v.x + b4.x, v.y + b4.y, v.z + b4.z, v.w + b4.w)
@@ -1211,6 +1222,289 @@ norm_reduce_query_kernel(const NormParams p) {
                make_float4(fmaf(dy.x * yrstd, w4.x, b4.x), fmaf(dy.y * yrstd, w4.y, b4.y),
                            fmaf(dy.z * yrstd, w4.z, b4.z), fmaf(dy.w * yrstd, w4.w, b4.w)));
   }
+}
+
+template <int RPW, int GI, int NP>
+__global__ void __launch_bounds__(kQWaves * kWave) __attribute__((amdgpu_waves_per_eu(1, 1)))
+norm_reduce_query_kernel(const NormParams p) {
+  norm_query<RPW, GI, NP>(p, blockIdx.x);
+}
+
+// ---------------------------------------------------------------------------
+// Decode relation tail in one launch: relation hidden -> second linear ->
+// norm-reduce with the output-head preparation, for a few queries (one per
+// batch row) of K <= 16 partner rows each.
+//
+// Workgroup (s, q) owns hidden columns [64 s, 64 s + 64) of query q's K rows:
+//   1. hidden^T[64 x 16 rows] = W_m[slice] . P^T on v_mfma_f32_16x16x32_bf16
+//      (P = op[a] * op[p], exact in fp32, as an exact hi + lo bf16 pair), plus
+//      the expanded-cache halves X[a, n] + X[p, H + n], erf-GELU, rounded to
+//      bf16 (the operand the two-launch linear sees) into LDS; waves 0..3, one
+//      16-column tile each.  Invalid indices gather zero rows, as
+//      relation_hidden_cached(_ring) does.
+//   2. partial^T[D x 16 rows] = W2[:, slice] . hidden^T over the slice's 64
+//      columns (all 8 waves, 16-row tiles of D; the W2 fragments are loaded at
+//      entry), stored fp32 to partials[s][q K + k][:].
+//   3. The slices are counted in groups of `spg`: each workgroup stores its
+//      partials with device-coherent (SC1) stores, waits for their
+//      acknowledgement and adds one to its group's counter with a vector
+//      atomic; the workgroup that brings the count to the group's size reads
+//      them back with device-coherent loads (no whole-L2 writeback or
+//      invalidation, which every workgroup would otherwise pay) and sums the
+//      group's partials in slice order into gsum[group], then
+//      counts on the query's counter; the last group's workgroup runs the
+//      per-query norm-reduce and output head (norm_query) on the group sums
+//      plus b2, in group order.  Every sum has a fixed order: the result does
+//      not depend on which workgroup arrives last.  Nothing waits for another
+//      workgroup; the last arrival of each level does the next step.  Each
+//      counter is reset to zero by that last arrival, so the next launch (and a
+//      graph replay) starts from zero.
+// ---------------------------------------------------------------------------
+constexpr int kDecSlice = 64;                  // hidden columns per workgroup
+constexpr int kDecWaves = 8;
+constexpr int kDecThreads = kDecWaves * kWave;
+constexpr int kDecMaxK = 8;                    // partner rows per query (rows of one 16-row tile)
+constexpr int kDecMaxD = 768;                  // d_model: norm_query with RPW <= 2, GI <= 3
+constexpr int kDecMaxDT = 6;                   // 16-row tiles of D per wave (D <= 768)
+constexpr int kDecMaxSpg = 12;                 // slices per group
+constexpr int kDecGroups = kMaxParts;          // groups per query (norm_query's NP)
+constexpr int kDecHidLd = kDecSlice + 8;       // bf16 per hidden row in LDS (conflict-free b128)
+constexpr int kDecSumBatch = 3;                // float4 elements per thread per level-1 round
+
+struct DecodeParams {
+  NormParams n;            // level 2: parts = gsum, nparts = groups, b2, output head
+  int64_t T;               // cache rows
+  int B, K, R, H, D;
+  int S, G, spg;           // slices, groups, slices per group
+  int ring;                // ring caches: index i lives in row i mod T, any i < 2^31
+  const void* expanded;    // [B,T,2H] bf16
+  const void* operand;     // [B,T,R] bf16
+  const void* anchor;      // [B]
+  const void* partner;     // [B,K]
+  int index_dtype_a, index_dtype_p;
+  const void* wm;          // [H,R] bf16
+  const void* w2;          // [D,H] bf16
+  float* partials;         // [S][B*K][D]
+  float* gsum;             // [G][B*K][D]
+  uint32_t* counters;      // [B*G] group counters, then [B] query counters
+  uint32_t expanded_bytes, operand_bytes, wm_bytes, w2_bytes, partials_bytes, gsum_bytes;
+};
+
+template <int KS, int RPW, int GI>
+__global__ void __launch_bounds__(kDecThreads) decode_relation_kernel(const DecodeParams p) {
+  __shared__ __align__(16) uint16_t hid[16][kDecHidLd];
+  __shared__ int last;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int s = blockIdx.x, q = blockIdx.y;
+  const int h0 = s * kDecSlice;
+  const uint32_t H = static_cast<uint32_t>(p.H), R = static_cast<uint32_t>(p.R);
+  const rsrc_t wmr = make_rsrc(p.wm, p.wm_bytes);
+  const rsrc_t w2r = make_rsrc(p.w2, p.w2_bytes);
+  const rsrc_t xr = make_rsrc(p.expanded, p.expanded_bytes);
+  const rsrc_t opr = make_rsrc(p.operand, p.operand_bytes);
+
+  // ---- Loads that need no index, all issued at entry.  W2 fragments of this
+  // wave's D tiles (A operand: row d = 16 dt + r16, k = 32 ks + 8 g of the slice).
+  u16x8 w2f[kDecMaxDT][2];
+#pragma unroll
+  for (int i = 0; i < kDecMaxDT; ++i) {
+    const int d = (wave + kDecWaves * i) * 16 + r16;
+    const bool in = d < p.D;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      w2f[i][ks] = __builtin_bit_cast(
+          u16x8, buf_load_b128(w2r, in ? (static_cast<uint32_t>(d) * H + h0 + 32 * ks + 8 * g) * 2u
+                                       : kNoOffset));
+  }
+  // W_m fragments of the hidden tile of waves 0..3: columns h0 + 16 wave + r16.
+  const bool hw = wave < 4;
+  u16x8 wmf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    wmf[ks] = __builtin_bit_cast(
+        u16x8, buf_load_b128(wmr, hw ? ((h0 + 16u * wave + r16) * R + 32 * ks + 8 * g) * 2u
+                                     : kNoOffset));
+  // Row m = r16 of the tile is partner m of query q (m < K).
+  const bool live = r16 < p.K;
+  const int64_t ai = index_at(p.anchor, p.index_dtype_a, q);
+  const int64_t pi = index_at(p.partner, p.index_dtype_p, static_cast<int64_t>(q) * p.K + (live ? r16 : 0));
+  const int64_t hi_idx = p.ring ? (int64_t(1) << 31) : p.T;
+  const int32_t a = (ai >= 0 && ai < hi_idx) ? static_cast<int32_t>(ai) : -1;
+  const int32_t pp = (live && pi >= 0 && pi < hi_idx) ? static_cast<int32_t>(pi) : -1;
+  const uint32_t mask = p.ring ? static_cast<uint32_t>(p.T - 1) : 0xffffffffu;
+  const uint32_t base = static_cast<uint32_t>(q) * static_cast<uint32_t>(p.T);
+  const uint32_t ra = base + (static_cast<uint32_t>(a) & mask);
+  const uint32_t rp = base + (static_cast<uint32_t>(pp) & mask);
+  const bool both = a >= 0 && pp >= 0;
+
+  // ---- 1. Hidden tile (waves 0..3).
+  if (hw) {
+    uint4 va[KS], vp[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      va[ks] = buf_load_b128(opr, both ? (ra * R + 32 * ks + 8 * g) * 2u : kNoOffset);
+      vp[ks] = buf_load_b128(opr, both ? (rp * R + 32 * ks + 8 * g) * 2u : kNoOffset);
+    }
+    const uint32_t col = h0 + 16u * wave + 4u * g;
+    const uint2 xa = buf_load_b64(xr, (live && a >= 0) ? (ra * 2u * H + col) * 2u : kNoOffset);
+    const uint2 xp = buf_load_b64(xr, pp >= 0 ? (rp * 2u * H + H + col) * 2u : kNoOffset);
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const uint32_t wa[4] = {va[ks].x, va[ks].y, va[ks].z, va[ks].w};
+      const uint32_t wp[4] = {vp[ks].x, vp[ks].y, vp[ks].z, vp[ks].w};
+      uint32_t h[4], l[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float x0 = bf16_lo(wp[k]) * bf16_lo(wa[k]);  // exact: 8-bit x 8-bit significands
+        const float x1 = bf16_hi(wp[k]) * bf16_hi(wa[k]);
+        h[k] = pack_bf16x2(x0, x1);
+        l[k] = pack_bf16x2(x0 - bf16_lo(h[k]), x1 - bf16_hi(h[k]));
+      }
+      const uint4 hv = make_uint4(h[0], h[1], h[2], h[3]), lv = make_uint4(l[0], l[1], l[2], l[3]);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wmf[ks]),
+                                                    __builtin_bit_cast(bf16x8, hv), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wmf[ks]),
+                                                    __builtin_bit_cast(bf16x8, lv), acc, 0, 0, 0);
+    }
+    // acc[e] = hidden^T[column col + e][row r16].
+    const float xs[4] = {bf16_lo(xa.x) + bf16_lo(xp.x), bf16_hi(xa.x) + bf16_hi(xp.x),
+                         bf16_lo(xa.y) + bf16_lo(xp.y), bf16_hi(xa.y) + bf16_hi(xp.y)};
+    *reinterpret_cast<uint2*>(&hid[r16][16 * wave + 4 * g]) =
+        make_uint2(pack_bf16x2(gelu_erf(acc[0] + xs[0]), gelu_erf(acc[1] + xs[1])),
+                   pack_bf16x2(gelu_erf(acc[2] + xs[2]), gelu_erf(acc[3] + xs[3])));
+  }
+  __syncthreads();
+
+  // ---- 2. Partial products of the slice: partial^T[d][row] over 64 columns.
+  const int BK = p.B * p.K;
+  const rsrc_t pr = make_rsrc(p.partials, p.partials_bytes);
+  {
+    u16x8 hb[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) hb[ks] = *reinterpret_cast<const u16x8*>(&hid[r16][32 * ks + 8 * g]);
+    const uint32_t row_off = (static_cast<uint32_t>(s) * BK + static_cast<uint32_t>(q) * p.K + r16) *
+                             static_cast<uint32_t>(p.D);
+#pragma unroll
+    for (int i = 0; i < kDecMaxDT; ++i) {
+      const int d0 = (wave + kDecWaves * i) * 16;
+      if (d0 >= p.D) break;  // uniform
+      f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w2f[i][ks]),
+                                                      __builtin_bit_cast(bf16x8, hb[ks]), acc, 0, 0, 0);
+      // acc[e] = partial^T[d0 + 4 g + e][row r16]; D % 4 == 0.
+      const int d = d0 + 4 * g;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), pr,
+                                             (live && d < p.D) ? (row_off + d) * 4u : kNoOffset,
+                                             0, kCpolDevice);
+    }
+  }
+
+  // ---- 3a. Group count: the group's last workgroup sums its partials.
+  const int grp = s / p.spg;
+  const int s_lo = grp * p.spg;
+  const int n_grp = min(p.S - s_lo, p.spg);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partials are acknowledged
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t* ctr = p.counters + q * p.G + grp;
+    last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           static_cast<uint32_t>(n_grp - 1);
+  }
+  __syncthreads();
+  if (!last) return;  // uniform
+  if (tid == 0) __hip_atomic_store(p.counters + q * p.G + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  {
+    const rsrc_t gr = make_rsrc(p.gsum, p.gsum_bytes);
+    const uint32_t n4 = static_cast<uint32_t>(p.K * p.D / 4);       // float4 of the query's rows
+    const uint32_t q4 = static_cast<uint32_t>(q) * n4;               // the query's first float4
+    const uint32_t split4 = static_cast<uint32_t>(BK * p.D / 4);     // float4 per slice
+    for (uint32_t e0 = 0; e0 < n4; e0 += kDecThreads * kDecSumBatch) {
+      uint4 v[kDecSumBatch][kDecMaxSpg];
+#pragma unroll
+      for (int u = 0; u < kDecSumBatch; ++u) {
+        const uint32_t e = e0 + tid + kDecThreads * u;
+#pragma unroll
+        for (int z = 0; z < kDecMaxSpg; ++z)
+          v[u][z] = __builtin_bit_cast(
+              uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                         pr, (e < n4 && z < n_grp) ? ((s_lo + z) * split4 + q4 + e) * 16u
+                                                   : kNoOffset,
+                         0, kCpolDevice));
+      }
+#pragma unroll
+      for (int u = 0; u < kDecSumBatch; ++u) {
+        const uint32_t e = e0 + tid + kDecThreads * u;
+        float4 acc = make_float4(__uint_as_float(v[u][0].x), __uint_as_float(v[u][0].y),
+                                 __uint_as_float(v[u][0].z), __uint_as_float(v[u][0].w));
+#pragma unroll
+        for (int z = 1; z < kDecMaxSpg; ++z) {
+          const bool use = z < n_grp;
+          acc.x = use ? acc.x + __uint_as_float(v[u][z].x) : acc.x;
+          acc.y = use ? acc.y + __uint_as_float(v[u][z].y) : acc.y;
+          acc.z = use ? acc.z + __uint_as_float(v[u][z].z) : acc.z;
+          acc.w = use ? acc.w + __uint_as_float(v[u][z].w) : acc.w;
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), gr,
+                                               e < n4 ? (grp * split4 + q4 + e) * 16u : kNoOffset,
+                                               0, kCpolDevice);
+      }
+    }
+  }
+
+  // ---- 3b. Query count: the last group's workgroup runs the norm-reduce.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's group sums are acknowledged
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t* ctr = p.counters + p.B * p.G + q;
+    last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           static_cast<uint32_t>(p.G - 1);
+  }
+  __syncthreads();
+  if (!last) return;  // uniform
+  if (tid == 0) __hip_atomic_store(p.counters + p.B * p.G + q, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (wave >= kQWaves) return;  // norm_query runs on four waves
+  norm_query<RPW, GI, kDecGroups, true>(p.n, q);
+}
+
+// Slices, groups and slices per group for hidden dim H (a multiple of 64).
+struct DecodeShape {
+  int S, G, spg;
+};
+inline DecodeShape decode_shape(int64_t H) {
+  const int S = static_cast<int>(H / kDecSlice);
+  const int G = S < kDecGroups ? S : kDecGroups;
+  return {S, G, G > 0 ? (S + G - 1) / G : 0};
+}
+inline bool decode_fits_shape(int64_t B, int64_t K, int64_t R, int64_t H, int64_t D) {
+  if (!(R == 64 || R == 128) || H <= 0 || H % kDecSlice != 0) return false;
+  return B >= 1 && B <= 65535 && K >= 1 && K <= kDecMaxK && D >= 4 && D % 4 == 0 &&
+         D <= kDecMaxD && decode_shape(H).spg <= kDecMaxSpg;
+}
+
+template <int KS, int RPW>
+hipError_t launch_decode_rpw(const DecodeParams& p, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(p.S), static_cast<unsigned>(p.B));
+  const int gi = (p.D / 4 + kWave - 1) / kWave;
+  if (gi <= 1)
+    hipLaunchKernelGGL((decode_relation_kernel<KS, RPW, 1>), grid, dim3(kDecThreads), 0, stream, p);
+  else if (gi <= 2)
+    hipLaunchKernelGGL((decode_relation_kernel<KS, RPW, 2>), grid, dim3(kDecThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((decode_relation_kernel<KS, RPW, 3>), grid, dim3(kDecThreads), 0, stream, p);
+  return launch_status("relation_hidden_linear_norm_reduce_output");
+}
+
+hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
+  const bool one_row = p.K <= kQWaves;  // one partner row per wave in norm_query
+  if (p.R == 128)
+    return one_row ? launch_decode_rpw<4, 1>(p, stream) : launch_decode_rpw<4, 2>(p, stream);
+  return one_row ? launch_decode_rpw<2, 1>(p, stream) : launch_decode_rpw<2, 2>(p, stream);
 }
 
 template <typename TR, int VPL>
@@ -1520,11 +1814,12 @@ struct OutputPrep {
   const rlm_tensor* final = nullptr;
 };
 
-hipError_t norm_impl(bool seq, const rlm_tensor* raw, const rlm_tensor* partner_scores,
-                     const rlm_tensor* norm_weight, const rlm_tensor* norm_bias,
-                     const rlm_tensor* position, double norm_eps, const rlm_tensor* out,
-                     hipStream_t stream, const OutputPrep& prep = OutputPrep()) {
-  clear_error();
+// Checks the norm-reduce arguments and fills the kernel parameters; `raw`
+// only describes the shape when the rows come as partial products (prep.parts).
+hipError_t norm_setup(bool seq, const rlm_tensor* raw, const rlm_tensor* partner_scores,
+                      const rlm_tensor* norm_weight, const rlm_tensor* norm_bias,
+                      const rlm_tensor* position, double norm_eps, const rlm_tensor* out,
+                      const OutputPrep& prep, NormParams& p) {
   const int qd = seq ? 2 : 1;
   RLM_TRY(check_tensor(raw, "raw", qd + 2));
   RLM_TRY(check_dtype_float(raw, "raw"));
@@ -1552,7 +1847,7 @@ hipError_t norm_impl(bool seq, const rlm_tensor* raw, const rlm_tensor* partner_
   RLM_TRY(check_dim(out, "out", 0, B));
   if (seq) RLM_TRY(check_dim(out, "out", 1, Tq));
   RLM_TRY(check_dim(out, "out", qd, D));
-  NormParams p{};
+  p = NormParams{};
   RLM_REQUIRE(position != nullptr && is_index_dtype(position->dtype),
               "position: expected an int32/int64 tensor");
   if (!seq) {
@@ -1645,10 +1940,22 @@ hipError_t norm_impl(bool seq, const rlm_tensor* raw, const rlm_tensor* partner_
     p.nparts = static_cast<int>(prep.parts->shape[0]);
     p.b2 = prep.b2->data;
     p.b2_dtype = prep.b2->dtype;
-    if (p.Q == 0) return hipSuccess;
-    return launch_norm_query(p, stream);
   }
+  return hipSuccess;
+}
+
+hipError_t norm_impl(bool seq, const rlm_tensor* raw, const rlm_tensor* partner_scores,
+                     const rlm_tensor* norm_weight, const rlm_tensor* norm_bias,
+                     const rlm_tensor* position, double norm_eps, const rlm_tensor* out,
+                     hipStream_t stream, const OutputPrep& prep = OutputPrep()) {
+  clear_error();
+  NormParams p;
+  const hipError_t err = norm_setup(seq, raw, partner_scores, norm_weight, norm_bias, position,
+                                    norm_eps, out, prep, p);
+  if (err != hipSuccess) return err;
   if (p.Q == 0) return hipSuccess;
+  if (prep.parts != nullptr) return launch_norm_query(p, stream);
+  const int64_t K = p.K, D = p.D;
   const bool vec_ok = D % 4 == 0 && (reinterpret_cast<uintptr_t>(raw->data) & 15u) == 0 &&
                       (reinterpret_cast<uintptr_t>(norm_weight->data) & 15u) == 0 &&
                       (reinterpret_cast<uintptr_t>(norm_bias->data) & 15u) == 0;
@@ -1896,6 +2203,176 @@ extern "C" hipError_t rlm_relation_norm_reduce_seq(const rlm_tensor* raw,
                                                    const rlm_tensor* out, hipStream_t stream) {
   return norm_impl(true, raw, partner_scores, norm_weight, norm_bias, positions, norm_eps, out,
                    stream);
+}
+
+extern "C" int rlm_relation_hidden_linear_norm_reduce_output_fits(
+    const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
+    const rlm_tensor* partner_index, const rlm_tensor* product_weight,
+    const rlm_tensor* second_weight) {
+  for (const rlm_tensor* t : {expanded_cache, operand_cache, partner_index, product_weight,
+                              second_weight})
+    if (t == nullptr) return 0;
+  if (operand_cache->ndim != 3 || expanded_cache->ndim != 3 || partner_index->ndim != 2 ||
+      product_weight->ndim != 2 || second_weight->ndim != 2)
+    return 0;
+  for (const rlm_tensor* t : {expanded_cache, operand_cache, product_weight, second_weight})
+    if (t->dtype != RLM_BF16) return 0;
+  const int64_t B = operand_cache->shape[0], R = operand_cache->shape[2];
+  const int64_t H = product_weight->shape[0], D = second_weight->shape[0];
+  if (product_weight->shape[1] != R || second_weight->shape[1] != H ||
+      partner_index->shape[0] != B)
+    return 0;
+  for (const rlm_tensor* t : {operand_cache, product_weight, second_weight})
+    if ((reinterpret_cast<uintptr_t>(t->data) & 15u) != 0) return 0;
+  if ((reinterpret_cast<uintptr_t>(expanded_cache->data) & 7u) != 0) return 0;
+  return decode_fits_shape(B, partner_index->shape[1], R, H, D) ? 1 : 0;
+}
+
+extern "C" hipError_t rlm_relation_hidden_linear_norm_reduce_output_workspace(
+    int64_t batch, int64_t partners, int64_t hidden_dim, int64_t d_model,
+    int64_t* workspace_floats, int64_t* counters) {
+  clear_error();
+  RLM_REQUIRE(workspace_floats != nullptr && counters != nullptr, "null output pointer");
+  RLM_REQUIRE(batch >= 0 && partners >= 0 && d_model >= 0 && hidden_dim > 0 &&
+                  hidden_dim % kDecSlice == 0,
+              "relation_hidden_linear_norm_reduce_output: hidden dim must be a positive "
+              "multiple of %d, got %lld", kDecSlice, (long long)hidden_dim);
+  const DecodeShape sh = decode_shape(hidden_dim);
+  *workspace_floats = static_cast<int64_t>(sh.S + sh.G) * batch * partners * d_model;
+  *counters = batch * (sh.G + 1);
+  return hipSuccess;
+}
+
+extern "C" hipError_t rlm_relation_hidden_linear_norm_reduce_output(
+    const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
+    const rlm_tensor* anchor_index, const rlm_tensor* partner_index,
+    const rlm_tensor* product_weight, const rlm_tensor* second_weight,
+    const rlm_tensor* second_bias, const rlm_tensor* partner_scores,
+    const rlm_tensor* norm_weight, const rlm_tensor* norm_bias, const rlm_tensor* position,
+    double norm_eps, const rlm_tensor* query, const rlm_tensor* mix_logit,
+    const rlm_tensor* output_weight, const rlm_tensor* output_bias, double output_eps,
+    int32_t ring, const rlm_tensor* workspace, const rlm_tensor* counters,
+    const rlm_tensor* out_context, const rlm_tensor* out_final, hipStream_t stream) {
+  clear_error();
+  const char* what = "relation_hidden_linear_norm_reduce_output";
+  RLM_TRY(check_tensor(operand_cache, "operand_cache", 3));
+  RLM_TRY(check_tensor(expanded_cache, "expanded_cache", 3));
+  RLM_TRY(check_tensor(product_weight, "product_weight", 2));
+  RLM_TRY(check_tensor(second_weight, "second_weight", 2));
+  for (const rlm_tensor* t : {operand_cache, expanded_cache, product_weight, second_weight})
+    RLM_REQUIRE(t->dtype == RLM_BF16, "%s: caches and weights must be bfloat16", what);
+  const int64_t B = operand_cache->shape[0], T = operand_cache->shape[1];
+  const int64_t R = operand_cache->shape[2], H = product_weight->shape[0];
+  const int64_t D = second_weight->shape[0];
+  RLM_TRY(check_dim(product_weight, "product_weight", 1, R));
+  RLM_TRY(check_dim(expanded_cache, "expanded_cache", 0, B));
+  RLM_TRY(check_dim(expanded_cache, "expanded_cache", 1, T));
+  RLM_TRY(check_dim(expanded_cache, "expanded_cache", 2, 2 * H));
+  RLM_TRY(check_dim(second_weight, "second_weight", 1, H));
+  RLM_TRY(check_tensor(anchor_index, "anchor_index", 1));
+  RLM_TRY(check_tensor(partner_index, "partner_index", 2));
+  RLM_REQUIRE(is_index_dtype(anchor_index->dtype) && is_index_dtype(partner_index->dtype),
+              "anchor_index/partner_index must be int32 or int64");
+  RLM_TRY(check_dim(anchor_index, "anchor_index", 0, B));
+  RLM_TRY(check_dim(partner_index, "partner_index", 0, B));
+  const int64_t K = partner_index->shape[1];
+  RLM_REQUIRE(decode_fits_shape(B, K, R, H, D),
+              "%s: needs relation dim 64 or 128, a hidden dim that is a multiple of %d up to "
+              "%d, 1..%d partners, d_model a multiple of 4 up to %d and 1..65535 queries (got "
+              "R=%lld H=%lld K=%lld D=%lld B=%lld); other shapes run "
+              "relation_hidden_cached + relation_linear_norm_reduce_output",
+              what, kDecSlice, kDecSlice * kDecGroups * kDecMaxSpg, kDecMaxK, kDecMaxD,
+              (long long)R, (long long)H, (long long)K, (long long)D, (long long)B);
+  RLM_REQUIRE(!ring || (T > 0 && (T & (T - 1)) == 0),
+              "ring-buffer caches need a power-of-two cache length, got %lld", (long long)T);
+  constexpr int64_t kMaxBytes = int64_t(1) << 31;
+  RLM_REQUIRE(B * T * 2 * H * 2 < kMaxBytes && B * T * R * 2 < kMaxBytes && D * H * 2 < kMaxBytes,
+              "%s: caches and weights must each be smaller than 2 GiB", what);
+  for (const rlm_tensor* t : {operand_cache, product_weight, second_weight})
+    RLM_REQUIRE((reinterpret_cast<uintptr_t>(t->data) & 15u) == 0,
+                "%s: operand_cache, product_weight and second_weight must be 16-byte aligned", what);
+  RLM_REQUIRE((reinterpret_cast<uintptr_t>(expanded_cache->data) & 7u) == 0,
+              "%s: expanded_cache must be 8-byte aligned", what);
+  const DecodeShape sh = decode_shape(H);
+  const int64_t rows = B * K;
+  RLM_TRY(check_tensor(workspace, "workspace", 1));
+  RLM_TRY(check_dtype_is(workspace, "workspace", RLM_F32));
+  RLM_REQUIRE(workspace->shape[0] >= (sh.S + sh.G) * rows * D,
+              "%s: workspace needs %lld fp32 elements, got %lld", what,
+              (long long)((sh.S + sh.G) * rows * D), (long long)workspace->shape[0]);
+  RLM_REQUIRE((sh.S + sh.G) * rows * D * 4 < kMaxBytes, "%s: workspace over 2 GiB", what);
+  RLM_REQUIRE((reinterpret_cast<uintptr_t>(workspace->data) & 15u) == 0,
+              "%s: workspace must be 16-byte aligned", what);
+  RLM_TRY(check_tensor(counters, "counters", 1));
+  RLM_TRY(check_dtype_is(counters, "counters", RLM_I32));
+  RLM_REQUIRE(counters->shape[0] >= B * (sh.G + 1), "%s: counters needs %lld int32 elements",
+              what, (long long)(B * (sh.G + 1)));
+  RLM_REQUIRE(query != nullptr, "query: missing tensor");
+  RLM_REQUIRE(second_bias != nullptr, "second_bias: missing tensor");
+  float* partials = static_cast<float*>(workspace->data);
+  float* gsum = partials + static_cast<int64_t>(sh.S) * rows * D;
+  // The raw shape [B, K, D] for the norm checks; the values come from the group sums.
+  rlm_tensor raw{};
+  raw.data = gsum;
+  raw.dtype = RLM_F32;
+  raw.ndim = 3;
+  raw.shape[0] = B;
+  raw.shape[1] = K;
+  raw.shape[2] = D;
+  raw.stride[0] = K * D;
+  raw.stride[1] = D;
+  raw.stride[2] = 1;
+  rlm_tensor parts{};
+  parts.data = gsum;
+  parts.dtype = RLM_F32;
+  parts.ndim = 3;
+  parts.shape[0] = sh.G;
+  parts.shape[1] = rows;
+  parts.shape[2] = D;
+  parts.stride[0] = rows * D;
+  parts.stride[1] = D;
+  parts.stride[2] = 1;
+  OutputPrep prep;
+  prep.parts = &parts;
+  prep.b2 = second_bias;
+  prep.query = query;
+  prep.mix_logit = mix_logit;
+  prep.weight = output_weight;
+  prep.bias = output_bias;
+  prep.eps = output_eps;
+  prep.final = out_final;
+  DecodeParams p{};
+  const hipError_t err = norm_setup(false, &raw, partner_scores, norm_weight, norm_bias, position,
+                                    norm_eps, out_context, prep, p.n);
+  if (err != hipSuccess) return err;
+  p.T = T;
+  p.B = static_cast<int>(B);
+  p.K = static_cast<int>(K);
+  p.R = static_cast<int>(R);
+  p.H = static_cast<int>(H);
+  p.D = static_cast<int>(D);
+  p.S = sh.S;
+  p.G = sh.G;
+  p.spg = sh.spg;
+  p.ring = ring ? 1 : 0;
+  p.expanded = expanded_cache->data;
+  p.operand = operand_cache->data;
+  p.anchor = anchor_index->data;
+  p.partner = partner_index->data;
+  p.index_dtype_a = anchor_index->dtype;
+  p.index_dtype_p = partner_index->dtype;
+  p.wm = product_weight->data;
+  p.w2 = second_weight->data;
+  p.partials = partials;
+  p.gsum = gsum;
+  p.counters = static_cast<uint32_t*>(counters->data);
+  p.expanded_bytes = static_cast<uint32_t>(B * T * 2 * H * 2);
+  p.operand_bytes = static_cast<uint32_t>(B * T * R * 2);
+  p.wm_bytes = static_cast<uint32_t>(H * R * 2);
+  p.w2_bytes = static_cast<uint32_t>(D * H * 2);
+  p.partials_bytes = static_cast<uint32_t>(static_cast<int64_t>(sh.S) * rows * D * 4);
+  p.gsum_bytes = static_cast<uint32_t>(static_cast<int64_t>(sh.G) * rows * D * 4);
+  return launch_decode(p, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -23,7 +23,10 @@
 #include <torch/library.h>
 
 #include <initializer_list>
+#include <map>
+#include <mutex>
 #include <tuple>
+#include <utility>
 
 #include "relation_lm_hip.h"
 
@@ -612,6 +615,120 @@ std::tuple<at::Tensor, at::Tensor> relation_linear_norm_reduce_output(
 at::Tensor relation_linear(const at::Tensor& input, const at::Tensor& weight,
                            const c10::optional<at::Tensor>& bias,
                            c10::optional<at::ScalarType> out_dtype);
+// Counters of the one-launch decode tail: int32, zero before a launch and left
+// zero by it (the last workgroup of each level resets its counter).  Each device
+// has one buffer, zeroed once when it is created (outside graph capture), cut
+// into fixed slots; a stream takes a slot at its first call (no kernel, so a
+// capture stream gets one without recording a fill into the graph) and keeps
+// it.  Launches on one stream are ordered, so they never share a counter
+// concurrently.
+constexpr int64_t kCounterSlots = 64;
+constexpr int64_t kCounterSlot = 4096;  // int32 counters per stream: B * (groups + 1)
+
+at::Tensor decode_counters(const char* op, const at::Tensor& like, hipStream_t stream) {
+  static std::mutex mu;
+  static std::map<int, at::Tensor> buffers;
+  static std::map<int, int64_t> used;
+  static std::map<std::pair<int, hipStream_t>, int64_t> slots;
+  std::lock_guard<std::mutex> lock(mu);
+  const int dev = static_cast<int>(like.device().index());
+  auto buf = buffers.find(dev);
+  if (buf == buffers.end()) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    check(hipStreamIsCapturing(stream, &status), op);
+    TORCH_CHECK(status == hipStreamCaptureStatusNone, op,
+                ": the first call on a device must run outside graph capture (it creates and "
+                "zeroes the device's counter buffer)");
+    buf = buffers.emplace(dev, at::zeros({kCounterSlots * kCounterSlot}, i32(like))).first;
+    check(hipStreamSynchronize(stream), op);  // zeroed before any stream uses a slot
+  }
+  const auto key = std::make_pair(dev, stream);
+  auto slot = slots.find(key);
+  if (slot == slots.end()) {
+    TORCH_CHECK(used[dev] < kCounterSlots, op, ": more than ", kCounterSlots,
+                " streams on one device");
+    slot = slots.emplace(key, used[dev]++).first;
+  }
+  return buf->second.narrow(0, slot->second * kCounterSlot, kCounterSlot);
+}
+
+std::tuple<at::Tensor, at::Tensor> relation_hidden_linear_norm_reduce_output(
+    const at::Tensor& expanded_cache, const at::Tensor& operand_cache,
+    const at::Tensor& anchor_index, const at::Tensor& partner_index,
+    const at::Tensor& product_weight, const at::Tensor& second_weight,
+    const at::Tensor& second_bias, const at::Tensor& partner_scores,
+    const at::Tensor& norm_weight, const at::Tensor& norm_bias, const at::Tensor& position,
+    double norm_eps, const at::Tensor& query, const at::Tensor& mix_logit,
+    const at::Tensor& output_weight, const at::Tensor& output_bias, double output_eps,
+    bool ring) {
+  const char* op = "relation_lm::relation_hidden_linear_norm_reduce_output";
+  c10::DeviceGuard guard(operand_cache.device());
+  hipStream_t stream = device_stream(
+      op, {&operand_cache, &expanded_cache, &anchor_index, &partner_index, &product_weight,
+           &second_weight, &second_bias, &partner_scores, &norm_weight, &norm_bias, &position,
+           &query, &mix_logit, &output_weight, &output_bias});
+  TORCH_CHECK(partner_index.dim() == 2 && second_weight.dim() == 2 && product_weight.dim() == 2,
+              op, ": partner_index must be [B,K], product_weight [H,R], second_weight [D,H]");
+  bool fits;
+  {
+    const rlm_tensor e = desc(expanded_cache, "expanded_cache");
+    const rlm_tensor o = desc(operand_cache, "operand_cache");
+    const rlm_tensor pi = desc(partner_index, "partner_index");
+    const rlm_tensor wm = desc(product_weight, "product_weight");
+    const rlm_tensor w2 = desc(second_weight, "second_weight");
+    fits = rlm_relation_hidden_linear_norm_reduce_output_fits(&e, &o, &pi, &wm, &w2) != 0;
+  }
+  const int64_t B = operand_cache.size(0), K = partner_index.size(1);
+  const int64_t H = product_weight.size(0), D = second_weight.size(0);
+  int64_t ws = 0, nctr = 0;
+  if (fits) {
+    check(rlm_relation_hidden_linear_norm_reduce_output_workspace(B, K, H, D, &ws, &nctr), op);
+    fits = nctr <= kCounterSlot;
+  }
+  if (!fits) {
+    // Shapes and dtypes the one-launch kernel does not take (fp32 caches, K > 8,
+    // d_model > 768, more than 819 queries, ...) run the two-op form: the fp32
+    // hidden, then the second linear with the norm-reduce and output head.
+    at::Tensor hidden = ring ? relation_hidden_cached_ring(expanded_cache, operand_cache,
+                                                           anchor_index, partner_index,
+                                                           product_weight)
+                             : relation_hidden_cached(expanded_cache, operand_cache, anchor_index,
+                                                      partner_index, product_weight);
+    return relation_linear_norm_reduce_output(hidden, second_weight, second_bias, partner_scores,
+                                              norm_weight, norm_bias, position, norm_eps, query,
+                                              mix_logit, output_weight, output_bias, output_eps);
+  }
+  at::Tensor workspace = at::empty({std::max<int64_t>(ws, 1)}, f32(operand_cache));
+  at::Tensor counters = decode_counters(op, operand_cache, stream);
+  at::Tensor context = at::empty({B, D}, f32(operand_cache));
+  at::Tensor final = at::empty({B, D}, query.options().memory_format(at::MemoryFormat::Contiguous));
+  rlm_tensor d[21] = {desc(expanded_cache, "expanded_cache"),
+                      desc(operand_cache, "operand_cache"),
+                      desc(anchor_index, "anchor_index"),
+                      desc(partner_index, "partner_index"),
+                      desc(product_weight, "product_weight"),
+                      desc(second_weight, "second_weight"),
+                      desc(second_bias, "second_bias"),
+                      desc(partner_scores, "partner_scores"),
+                      desc(norm_weight, "norm_weight"),
+                      desc(norm_bias, "norm_bias"),
+                      desc(position, "position"),
+                      desc(query, "query"),
+                      desc(mix_logit, "mix_logit"),
+                      desc(output_weight, "output_weight"),
+                      desc(output_bias, "output_bias"),
+                      desc(workspace, "workspace"),
+                      desc(counters, "counters"),
+                      desc(context, "out_context"),
+                      desc(final, "out_final")};
+  check(rlm_relation_hidden_linear_norm_reduce_output(
+            &d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7], &d[8], &d[9], &d[10],
+            norm_eps, &d[11], &d[12], &d[13], &d[14], output_eps, ring ? 1 : 0, &d[15], &d[16],
+            &d[17], &d[18], stream),
+        op);
+  return {context, final};
+}
+
 
 at::Tensor relation_reduce_fused_seq(const at::Tensor& expanded_cache,
                                      const at::Tensor& operand_cache,
@@ -1048,6 +1165,12 @@ TORCH_LIBRARY(relation_lm, m) {
       "position, float norm_eps, Tensor query, Tensor mix_logit, Tensor output_weight, Tensor "
       "output_bias, float output_eps) -> (Tensor, Tensor)");
   m.def(
+      "relation_hidden_linear_norm_reduce_output(Tensor expanded_cache, Tensor operand_cache, "
+      "Tensor anchor_index, Tensor partner_index, Tensor product_weight, Tensor second_weight, "
+      "Tensor second_bias, Tensor partner_scores, Tensor norm_weight, Tensor norm_bias, Tensor "
+      "position, float norm_eps, Tensor query, Tensor mix_logit, Tensor output_weight, Tensor "
+      "output_bias, float output_eps, bool ring=False) -> (Tensor, Tensor)");
+  m.def(
       "relation_linear(Tensor input, Tensor weight, Tensor? bias=None, ScalarType? "
       "out_dtype=None) -> Tensor");
   m.def(
@@ -1112,6 +1235,8 @@ TORCH_LIBRARY_IMPL(relation_lm, CUDA, m) {
   m.impl("packed_projection_to_caches", TORCH_FN(packed_projection_to_caches));
   m.impl("packed_projection_router_update", TORCH_FN(packed_projection_router_update));
   m.impl("relation_linear_norm_reduce_output", TORCH_FN(relation_linear_norm_reduce_output));
+  m.impl("relation_hidden_linear_norm_reduce_output",
+         TORCH_FN(relation_hidden_linear_norm_reduce_output));
   m.impl("relation_linear", TORCH_FN(relation_linear));
   m.impl("relation_linear_out", TORCH_FN(relation_linear_out));
   m.impl("relation_hidden_cached_seq_out", TORCH_FN(relation_hidden_cached_seq_out));

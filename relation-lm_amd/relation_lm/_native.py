@@ -155,6 +155,13 @@ def _register_fakes() -> None:
         shape = (hidden.shape[0], second_weight.shape[0])
         return (hidden.new_empty(shape, dtype=torch.float32), query.new_empty(shape))
 
+    @torch.library.register_fake("relation_lm::relation_hidden_linear_norm_reduce_output")
+    def _(expanded_cache, operand_cache, anchor_index, partner_index, product_weight,
+          second_weight, second_bias, partner_scores, norm_weight, norm_bias, position, norm_eps,
+          query, mix_logit, output_weight, output_bias, output_eps, ring=False):
+        shape = (operand_cache.shape[0], second_weight.shape[0])
+        return (operand_cache.new_empty(shape, dtype=torch.float32), query.new_empty(shape))
+
     @torch.library.register_fake("relation_lm::layer_norm")
     def _(input, weight, bias, eps):
         return torch.empty_like(input, memory_format=torch.contiguous_format)

@@ -229,6 +229,46 @@ def relation_linear_norm_reduce_output(
         float(norm_eps), query, mix_logit, output_weight, output_bias, float(output_eps))
 
 
+def relation_hidden_linear_norm_reduce_output(
+    expanded_cache: Tensor,
+    operand_cache: Tensor,
+    anchor_index: Tensor,
+    partner_index: Tensor,
+    product_weight: Tensor,
+    second_weight: Tensor,
+    second_bias: Tensor,
+    partner_scores: Tensor,
+    norm_weight: Tensor,
+    norm_bias: Tensor,
+    position: Tensor,
+    norm_eps: float,
+    query: Tensor,
+    mix_logit: Tensor,
+    output_weight: Tensor,
+    output_bias: Tensor,
+    output_eps: float,
+    ring: bool = False,
+) -> tuple[Tensor, Tensor]:
+    """The decode step's relation tail: relation_hidden_cached (relation_reduce.py:149-183;
+    ``ring``: the ring-buffer form) followed by relation_linear_norm_reduce_output -- the
+    second linear, relation_norm_reduce (relation_reduce.py:420-450) and the output-head
+    preparation (relation_lm.py:203-206) -- returning (context f32 [B,D], final [B,D]).
+
+    With bf16 caches and weights, relation dim 64 or 128, hidden dim a multiple of 64 up
+    to 3072, at most 8 partners and d_model up to 768 this is one launch: each workgroup
+    forms a 64-column slice of the hidden rows and that slice's partial products of the
+    second linear, and the last workgroups to finish sum the partials (in a fixed order)
+    and run the norm-reduce.  The hidden is rounded to bf16 for the linear, as the
+    two-op form's 16-bit linear does, and the partial sums are added in another order, so
+    the raw rows agree with the two-op form to fp32 rounding.  Other shapes run the two
+    ops (relation_hidden_linear_norm_reduce_output_fits in the C library tells which)."""
+    return torch.ops.relation_lm.relation_hidden_linear_norm_reduce_output(
+        expanded_cache, operand_cache, anchor_index, partner_index, product_weight,
+        second_weight, second_bias, partner_scores, norm_weight, norm_bias, position,
+        float(norm_eps), query, mix_logit, output_weight, output_bias, float(output_eps),
+        bool(ring))
+
+
 def relation_reduce_fused_seq(
     expanded_cache: Tensor,
     operand_cache: Tensor,

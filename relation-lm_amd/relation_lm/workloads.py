@@ -309,6 +309,11 @@ def decode_state(cfg: RelationConfig, *, device: torch.device | str, position: i
     return st
 
 
+# Workgroups the GPU runs in one round (one per CU on MI355X at the one-launch decode
+# tail's size); beyond this the tail's latency chain runs twice.
+ONE_ROUND_WORKGROUPS = 256
+
+
 def decode_step(st: dict, cfg: RelationConfig) -> tuple:
     """One decode step on ``decode_state`` tensors, the launch sequence the
     benchmark times:
@@ -317,13 +322,18 @@ def decode_step(st: dict, cfg: RelationConfig) -> tuple:
          router cache update of both streams folded in (one launch);
       2. relation_select_packed with the token's expanded-cache row projected by
          extra workgroups of the same launch;
-      3. the cached relation hidden (relation_hidden_cached);
-      4. the second linear split over the hidden dim and the norm-reduce with the
-         output-head preparation as its epilogue.
+      3. the relation tail: while its grid (one workgroup per query and 64 hidden
+         columns) fits one round of the chip's 256 CUs, one launch -- the cached
+         relation hidden, the second linear over slices of the hidden dim and the
+         norm-reduce with the output-head preparation
+         (relation_hidden_linear_norm_reduce_output); beyond that (cfg3 at B=8) the
+         two-launch form is faster on MI355X: relation_hidden_cached(_ring), then
+         relation_linear_norm_reduce_output (the split-K linear and the norm-reduce).
     The caches are updated in place at the state's position (ring: mod T).
     Returns (anchor, anchor_score, partner, partner_score, context, final)."""
     from relation_lm.kernels.relation_reduce import (
         relation_hidden_cached,
+        relation_hidden_linear_norm_reduce_output,
         relation_linear_norm_reduce_output,
     )
     from relation_lm.kernels.relation_select import relation_select_packed_expand_row
@@ -340,10 +350,13 @@ def decode_step(st: dict, cfg: RelationConfig) -> tuple:
     a, s, p, ps = relation_select_packed_expand_row(
         *select_args(sel, cfg), red["operand_cache"], red["expanded_weight"],
         red["expanded_bias"], expanded, ring)
-    cached = relation_hidden_cached_ring if ring else relation_hidden_cached
-    hidden = cached(expanded, red["operand_cache"], a, p, red["product_weight"])
-    context, final = relation_linear_norm_reduce_output(
-        hidden, red["second_weight"], red["second_bias"], ps, red["norm_weight"],
-        red["norm_bias"], position, 1e-5, head["query"], head["mix"], head["weight"],
-        head["bias"], 1e-5)
+    tail = (red["second_weight"], red["second_bias"], ps, red["norm_weight"], red["norm_bias"],
+            position, 1e-5, head["query"], head["mix"], head["weight"], head["bias"], 1e-5)
+    if a.shape[0] * (red["product_weight"].shape[0] // 64) <= ONE_ROUND_WORKGROUPS:
+        context, final = relation_hidden_linear_norm_reduce_output(
+            expanded, red["operand_cache"], a, p, red["product_weight"], *tail, ring=ring)
+    else:
+        cached = relation_hidden_cached_ring if ring else relation_hidden_cached
+        hidden = cached(expanded, red["operand_cache"], a, p, red["product_weight"])
+        context, final = relation_linear_norm_reduce_output(hidden, *tail)
     return a, s, p, ps, context, final

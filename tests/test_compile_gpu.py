@@ -277,6 +277,11 @@ def op_cases(device):
                   ops.relation_linear_norm_reduce_output.default,
                   (hidden_dec, red["second_weight"], red["second_bias"], scores_dec,
                    red["norm_weight"], red["norm_bias"], pos, 1e-5, query_dec) + head))
+    cases.append(("relation_hidden_linear_norm_reduce_output",
+                  ops.relation_hidden_linear_norm_reduce_output.default,
+                  (expanded, red["operand_cache"], a_dec, p_dec, wm, red["second_weight"],
+                   red["second_bias"], scores_dec, red["norm_weight"], red["norm_bias"], pos,
+                   1e-5, query_dec) + head + (False,)))
     slots, kk = 2, 3
     raw_multi = torch.randn(b, t, slots, kk, d, generator=g).to(device)
     scores_multi = torch.randn(b, t, slots, kk, generator=g).to(device)
@@ -307,7 +312,8 @@ OP_NAMES = ("relation_select_packed", "relation_select_packed_seq",
             "packed_projection_to_caches", "packed_projection_router_update",
             "relation_linear", "relation_linear_out",
             "relation_norm_reduce_output", "relation_norm_reduce_output_seq",
-            "relation_linear_norm_reduce_output", "multi_relation_reduce_seq",
+            "relation_linear_norm_reduce_output", "relation_hidden_linear_norm_reduce_output",
+            "multi_relation_reduce_seq",
             "multi_relation_reduce_seq_out", "layer_norm", "block_statistics")
 
 
