@@ -18,6 +18,7 @@ TORCH_LIBRARY = os.path.join(LIB_DIR, "_rlm_torch.so")
 C_LIBRARY = os.path.join(LIB_DIR, "librlm_hip.so")
 
 _loaded = False
+_c_library = None
 
 
 def load() -> None:
@@ -33,6 +34,18 @@ def load() -> None:
     torch.ops.load_library(TORCH_LIBRARY)
     _register_fakes()
     _loaded = True
+
+
+def c_library():
+    """The C-ABI library (``ctypes.CDLL``), for the host-only queries it exports."""
+    global _c_library
+    if _c_library is None:
+        load()
+        import ctypes
+
+        _c_library = ctypes.CDLL(C_LIBRARY)
+        _c_library.rlm_last_error.restype = ctypes.c_char_p
+    return _c_library
 
 
 def _register_fakes() -> None:

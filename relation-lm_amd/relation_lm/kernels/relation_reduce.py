@@ -13,6 +13,7 @@ expanded-cache projection and the relation MLP's second linear).
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -267,6 +268,42 @@ def relation_hidden_linear_norm_reduce_output(
         second_weight, second_bias, partner_scores, norm_weight, norm_bias, position,
         float(norm_eps), query, mix_logit, output_weight, output_bias, float(output_eps),
         bool(ring))
+
+
+_DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2, torch.int32: 3,
+               torch.int64: 4}
+
+
+class _TensorDesc(ctypes.Structure):
+    """The C library's ``rlm_tensor`` descriptor (include/relation_lm_hip.h)."""
+
+    _fields_ = [("data", ctypes.c_void_p), ("dtype", ctypes.c_int32), ("ndim", ctypes.c_int32),
+                ("shape", ctypes.c_int64 * 4), ("stride", ctypes.c_int64 * 4)]
+
+
+def _desc(t: Tensor) -> _TensorDesc:
+    if t.dim() > 4 or t.dtype not in _DTYPE_CODE:
+        raise ValueError(f"unsupported tensor for the C library: {t.dtype}, {t.dim()}-d")
+    d = _TensorDesc(t.data_ptr(), _DTYPE_CODE[t.dtype], t.dim())
+    for i, (n, st) in enumerate(zip(t.shape, t.stride())):
+        d.shape[i], d.stride[i] = n, st
+    return d
+
+
+def relation_reduce_fused_seq_fits(
+    expanded_cache: Tensor,
+    operand_cache: Tensor,
+    partner_index: Tensor,
+    product_weight: Tensor,
+    second_weight: Tensor,
+) -> bool:
+    """True when ``relation_reduce_fused_seq`` runs these operands as one fused kernel, False
+    when it runs the three-launch chain instead (fp32, d_model 576, K > 16, ...).  Reads only
+    shapes, dtypes and pointer alignment; launches nothing."""
+    lib = _native.c_library()
+    return bool(lib.rlm_relation_reduce_fused_seq_fits(
+        *(ctypes.byref(_desc(t)) for t in (expanded_cache, operand_cache, partner_index,
+                                           product_weight, second_weight))))
 
 
 def relation_reduce_fused_seq(

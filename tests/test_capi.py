@@ -11,6 +11,7 @@ import os
 import re
 
 import pytest
+import torch
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "relation_lm_hip.h")
@@ -299,3 +300,17 @@ def test_multi_select_fake_shapes():
                 torch.empty(4), torch.empty(4, 16), torch.empty(t, dtype=torch.long)]
         a, sc, p, ps = multi_relation_select_seq(*args, 16, 2, 6, False)
         assert a.shape == (b, t, s) and p.shape == (b, t, s, 6) and ps.dtype == torch.float32
+
+
+def test_fused_reduce_fits_from_python():
+    """relation_reduce_fused_seq_fits (Python) asks the C library's predicate about torch
+    tensors; CPU tensors serve, since it reads only their descriptors."""
+    from relation_lm.kernels.relation_reduce import relation_reduce_fused_seq_fits
+
+    bf = torch.bfloat16
+    e, o = torch.empty(2, 64, 1024, dtype=bf), torch.empty(2, 64, 64, dtype=bf)
+    pi, wm = torch.empty(2, 8, 8, dtype=torch.int32), torch.empty(512, 64, dtype=bf)
+    assert relation_reduce_fused_seq_fits(e, o, pi, wm, torch.empty(512, 512, dtype=bf))
+    assert not relation_reduce_fused_seq_fits(e, o, pi, wm, torch.empty(576, 512, dtype=bf))
+    assert not relation_reduce_fused_seq_fits(e, o.float(), pi, wm,
+                                              torch.empty(512, 512, dtype=bf))
