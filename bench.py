@@ -86,6 +86,8 @@ def parse_args():
                          "top 2, K 8, fp32)")
     ap.add_argument("--multi-only", action="store_true",
                     help="time only the cfg5 routed multi-anchor selection and exit")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="time only the hand-written GEMM on the second-Linear shapes and exit")
     ap.add_argument("--reduce-only", action="store_true",
                     help="time only the cfg4 fused reduce in isolation and exit")
     ap.add_argument("--profile-kernels", type=int, default=0, metavar="N",
@@ -388,6 +390,41 @@ def main() -> int:
             "algorithmic_bytes": nbytes,
         }
 
+    def run_gemm(repeats=20):
+        """The hand-written MFMA GEMM (relation_linear, fp32 output with bias) on the
+        second-Linear shapes of the path: cfg5's relation MLP (one batch row's
+        [T*S*K, 4d] x [d, 4d]^T, bf16) and cfg2's second linear ([Q*K, H] x [D, H]^T,
+        bf16 hidden as the fused reduce sees it, and the unfused chain's fp32 hidden)."""
+        g = torch.Generator(device="cpu").manual_seed(7)
+        shapes = {
+            "cfg5_mlp_second_linear": (98304, 3072, 768, torch.bfloat16),
+            "cfg5_mlp_second_linear_2rows": (196608, 3072, 768, torch.bfloat16),
+            "cfg2_second_linear_bf16": (32768, 512, 512, torch.bfloat16),
+            "cfg2_second_linear_fp32_hidden": (32768, 512, 512, torch.float32),
+        }
+        out = {}
+        for name, (m, k, n, adt) in shapes.items():
+            a = torch.randn(m, k, generator=g).to(device=device, dtype=adt)
+            w = (torch.randn(n, k, generator=g) * k ** -0.5).to(device=device,
+                                                               dtype=torch.bfloat16)
+            bias = torch.randn(n, generator=g).to(device=device, dtype=torch.bfloat16)
+            for _ in range(3):
+                relation_linear(a, w, bias, out_dtype=torch.float32)
+            torch.cuda.synchronize()
+            start.record()
+            for _ in range(repeats):
+                relation_linear(a, w, bias, out_dtype=torch.float32)
+            end.record()
+            torch.cuda.synchronize()
+            us = start.elapsed_time(end) * 1e3 / repeats
+            flops = 2 * m * k * n
+            tf = flops / (us * 1e-6) / 1e12
+            out[name] = {"shape": f"[{m},{k}] x [{n},{k}]^T, A {str(adt)[6:]}, W bf16, fp32 out",
+                         "us": round(us, 2), "tflops": round(tf, 1),
+                         "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+            del a, w, bias
+        return out
+
     def run_published_policy(repeats=100, samples=9):
         """The only routing policy the reference publishes numbers for
         (benchmarks/benchmark_relation_select.py:14-57, results in
@@ -489,6 +526,9 @@ def main() -> int:
         return 0
     if args.multi_only:
         print(json.dumps({"multi_anchor_select": run_multi()}), flush=True)
+        return 0
+    if args.gemm_only:
+        print(json.dumps({"gemm": run_gemm()}), flush=True)
         return 0
     if args.reduce_only:
         print(json.dumps({"fused_reduce_cfg4": run_reduce_cfg4()}), flush=True)
@@ -756,6 +796,7 @@ def main() -> int:
     multi = run_multi()
     reduce4 = run_reduce_cfg4()
     policy = run_published_policy()
+    gemm = run_gemm()
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -813,6 +854,7 @@ def main() -> int:
         "multi_anchor_select": multi,
         "fused_reduce_cfg4": reduce4,
         "published_policy": policy,
+        "gemm": gemm,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

@@ -202,27 +202,35 @@ class MultiAnchorRelationBlock(nn.Module):
         mlp = self.relation_mlp
         # The MLP hidden in the second Linear's operand dtype: a bf16 Linear
         # rounds an fp32 hidden to bf16 before its products, so storing bf16
-        # gives the same result at half the bytes.  One batch row at a time:
-        # the [T*S, K, hidden] hidden of a row stays below the 2 GiB a kernel
-        # addresses.
+        # gives the same result at half the bytes.  A few batch rows at a time:
+        # the [rows, T*S, K, hidden] hidden of a group stays below the 2 GiB a
+        # kernel addresses, and the groups are of equal size so that each
+        # second Linear fills the chip alike.
         hid_dtype = torch.bfloat16 if mlp[2].weight.dtype == torch.bfloat16 else torch.float32
-        rows = torch.empty((1, length * h, k_count, mlp[2].weight.shape[1]), dtype=hid_dtype,
+        width = mlp[2].weight.shape[1]
+        row_bytes = length * h * k_count * width * torch.empty((), dtype=hid_dtype).element_size()
+        most = max(1, min(batch, (2**31 - 1) // row_bytes))
+        group = -(-batch // -(-batch // most))
+        rows = torch.empty((group, length * h, k_count, width), dtype=hid_dtype,
                            device=hidden.device)
         output = torch.empty_like(hidden, memory_format=torch.contiguous_format)
-        for b in range(batch):
+        for b0 in range(0, batch, group):
+            b1 = min(batch, b0 + group)
+            n = b1 - b0
+            part = rows[:n]
             ops.relation_hidden_cached_seq_out(
-                sel["expanded_cache"][b:b + 1], sel["operand_cache"][b:b + 1],
-                sel["anchor"][b:b + 1].reshape(1, length * h),
-                sel["partner"][b:b + 1].reshape(1, length * h, k_count), sel["product_weight"],
-                rows)
+                sel["expanded_cache"][b0:b1], sel["operand_cache"][b0:b1],
+                sel["anchor"][b0:b1].reshape(n, length * h),
+                sel["partner"][b0:b1].reshape(n, length * h, k_count), sel["product_weight"],
+                part)
             # The second Linear with its bias, fp32 output (the LayerNorm that
             # follows reads the rows unrounded).
-            raw = ops.relation_linear(rows, mlp[2].weight, mlp[2].bias, torch.float32)
+            raw = ops.relation_linear(part, mlp[2].weight, mlp[2].bias, torch.float32)
             ops.multi_relation_reduce_seq_out(
-                raw.view(1, length, h, k_count, d), sel["partner_score"][b:b + 1], mlp[3].weight,
-                mlp[3].bias, self.slot_mix_logits, self.residual_gate, hidden[b:b + 1],
-                sel["positions"], mlp[3].eps, None, output[b:b + 1],
-                None if context is None else context[b:b + 1])
+                raw.view(n, length, h, k_count, d), sel["partner_score"][b0:b1], mlp[3].weight,
+                mlp[3].bias, self.slot_mix_logits, self.residual_gate, hidden[b0:b1],
+                sel["positions"], mlp[3].eps, None, output[b0:b1],
+                None if context is None else context[b0:b1])
         return output
 
     def forward(self, hidden: Tensor, memory: Tensor) -> tuple[Tensor, dict[str, Tensor]]:
