@@ -423,7 +423,58 @@ def main() -> int:
                          "us": round(us, 2), "tflops": round(tf, 1),
                          "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
             del a, w, bias
+        out["cfg5_relation_mlp"] = run_relation_mlp(repeats)
         return out
+
+    def run_relation_mlp(repeats=20):
+        """cfg5's relation MLP for one batch row (T=4096, 4 slots x K=6 = 98304 rows,
+        relation dim 128, hidden 3072, d_model 768, bf16): the fused kernel
+        (relation_hidden_linear_seq_out, hidden on chip) against the two launches it
+        replaces (relation_hidden_cached_seq_out into bf16, then relation_linear).
+        Indices uniform over the batch row's 4096 positions."""
+        from relation_lm.kernels.relation_reduce import (mfma_fragments,
+                                                         relation_hidden_cached_seq_out,
+                                                         relation_hidden_linear_seq_out)
+        g = torch.Generator(device="cpu").manual_seed(11)
+        t, q, k, r, h, d = 4096, 4096 * 4, 6, 128, 3072, 768
+        expanded = (torch.randn(1, t, 2 * h, generator=g) * 0.5).to(device, torch.bfloat16)
+        operand = torch.randn(1, t, r, generator=g).to(device, torch.bfloat16)
+        anchor = torch.randint(0, t, (1, q), generator=g).to(device)
+        partner = torch.randint(0, t, (1, q, k), generator=g).to(device)
+        wm = (torch.randn(h, r, generator=g) * r ** -0.5).to(device, torch.bfloat16)
+        w2 = (torch.randn(d, h, generator=g) * h ** -0.5).to(device, torch.bfloat16)
+        raw = torch.empty((1, q, k, d), device=device)
+        hidden = torch.empty((1, q, k, h), device=device, dtype=torch.bfloat16)
+
+        wm_frags, w2_frags = mfma_fragments(wm), mfma_fragments(w2)
+
+        def fused():
+            relation_hidden_linear_seq_out(expanded, operand, anchor, partner, wm_frags, w2_frags,
+                                           raw)
+
+        def two_ops():
+            relation_hidden_cached_seq_out(expanded, operand, anchor, partner, wm, hidden)
+            relation_linear(hidden.view(q * k, h), w2, None, out_dtype=torch.float32)
+
+        res = {}
+        for name, fn in (("fused", fused), ("two_ops", two_ops)):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            start.record()
+            for _ in range(repeats):
+                fn()
+            end.record()
+            torch.cuda.synchronize()
+            res[f"{name}_us"] = round(start.elapsed_time(end) * 1e3 / repeats, 2)
+        rows = q * k
+        flops = 2 * rows * h * (2 * r) + 2 * rows * h * d   # hi/lo product MFMAs + second Linear
+        res.update({"rows": rows, "workload": "cfg5 relation MLP, one batch row: 98304 rows, "
+                    "relation dim 128 -> hidden 3072 (GELU, bf16) -> d_model 768, fp32 out",
+                    "mfma_tflop": round(flops / 1e12, 4),
+                    "fused_tflops": round(flops / (res["fused_us"] * 1e-6) / 1e12, 1)})
+        del expanded, operand, raw, hidden
+        return res
 
     def run_published_policy(repeats=100, samples=9):
         """The only routing policy the reference publishes numbers for

@@ -230,6 +230,48 @@ hipError_t rlm_relation_hidden_cached_seq(
     hipStream_t stream);
 
 /*
+ * The relation MLP of MultiAnchorRelationBlock up to its closing LayerNorm
+ *   (src/relation_lm/models/multi_relation_blocks.py:47-52,163: Linear -> GELU ->
+ * Linear, the first Linear factorized as relation_hidden_cached,
+ * src/relation_lm/kernels/relation_reduce.py:149-183), bias-free, in one
+ * launch:
+ *   out[b,q,k,:] = second_weight . bf16(hidden[b,q,k,:])
+ * with hidden as rlm_relation_hidden_cached_seq; the hidden never reaches
+ * memory.  Bit-identical to rlm_relation_hidden_cached_seq with a bf16 output
+ * followed by rlm_linear with an fp32 output and no bias.
+ *   expanded_cache [B,T,2H], operand_cache [B,T,R] (bf16, 16-byte aligned),
+ *   anchor_index [B,Tq], partner_index [B,Tq,K] (int32/int64);
+ *   product_weight [H/32, R/16, 64, 8] and second_weight [D/32, H/16, 64, 8]:
+ *   the [H,R] and [D,H] bf16 weights in MFMA fragment order
+ *   (rlm_mfma_fragments, done once per weight).
+ * Output: out f32 [B,Tq,K,D].  Shapes: R in {64, 128}, H a multiple of 128,
+ * D in {256, 512, 768} (rlm_relation_hidden_linear_seq_fits says whether given
+ * tensors qualify; other shapes fail with hipErrorInvalidValue).
+ */
+hipError_t rlm_relation_hidden_linear_seq(
+    const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
+    const rlm_tensor* anchor_index, const rlm_tensor* partner_index,
+    const rlm_tensor* product_weight, const rlm_tensor* second_weight,
+    const rlm_tensor* out, hipStream_t stream);
+
+/* 1 if rlm_relation_hidden_linear_seq takes these tensors (dtypes, shapes,
+ * alignment; the weights in fragment order), else 0. */
+int rlm_relation_hidden_linear_seq_fits(const rlm_tensor* expanded_cache,
+                                        const rlm_tensor* operand_cache,
+                                        const rlm_tensor* product_weight,
+                                        const rlm_tensor* second_weight);
+
+/*
+ * MFMA fragment order of a [N,K] bf16/f16 weight (no reference counterpart: a
+ * weight packing step, like the reference's pack_sparse_cache_projection_weights):
+ * out [N/32, K/16, 64, 8], fragment (nb, g) lane l = weight[32 nb + l % 32,
+ * 16 g + 8 (l / 32) .. +7] -- the operand a wave's v_mfma_f32_32x32x16 reads,
+ * contiguous per fragment.  N % 32 == 0, K % 16 == 0, 16-byte aligned.
+ */
+hipError_t rlm_mfma_fragments(const rlm_tensor* weight, const rlm_tensor* out,
+                              hipStream_t stream);
+
+/*
  * Replaces relation_lm::relation_hidden_cache_update
  *   (src/relation_lm/kernels/relation_reduce.py:312-357).
  * Writes expanded_cache[b, position] = [W_a op[t] + b1, W_p op[t]] (the only

@@ -667,6 +667,282 @@ __global__ void __launch_bounds__(kTileThreads, 2) hidden_tile_kernel(const Hidd
   }
 }
 
+// ---------------------------------------------------------------------------
+// Relation MLP, sequence form: the relation hidden and the second Linear in one
+// kernel -- the multi-anchor block's relation MLP Linear -> GELU -> Linear
+// (multi_relation_blocks.py:47-52,163) with its first Linear factorized
+// (relation_hidden_cached, relation_reduce.py:149-183), bias-free:
+//   raw[m, :] = W2 . bf16(GELU(W_m (op[a_m] * op[p_m]) + X[a_m, :H] + X[p_m, H:]))
+// The [rows, H] hidden never reaches memory.  A workgroup of eight waves owns
+// 64 rows and all D output columns and walks the hidden dimension in chunks of
+// 128 columns:
+//   phase 1  wave w forms the 32 x 32 block (rows 32 (w & 1).., chunk columns
+//            32 (w >> 1)..) of the chunk's hidden with hidden_tile_kernel's
+//            arithmetic -- the same MFMA sums over the exact hi / lo product
+//            split, the same fp32 adds of the expanded-cache halves, GELU and
+//            bf16 rounding -- into the LDS hidden tile (two buffers, so the
+//            next chunk's phase 1 needs no barrier against this chunk's
+//            phase 2);
+//   phase 2  raw^T[D x 64] += W2[:, chunk] . hidden^T on 32x32x16 MFMAs, wave w
+//            owning D columns [32 TNB w, 32 TNB (w + 1)), k ascending in
+//            16-wide groups: the accumulation of relation_linear's tile kernel.
+// So raw is bit-identical to relation_hidden_cached_seq (bf16 hidden) followed
+// by relation_linear (fp32 output, no bias).  W_m fragments come from L2 into
+// operand registers one chunk ahead, W2 fragments kMlpW2Ahead k-groups ahead;
+// the expanded-cache halves are gathered one chunk ahead.  The output rows are
+// restaged through LDS and stored as whole 16-byte row pieces.
+constexpr int kMlpRows = 64;
+constexpr int kMlpWaves = 8;
+constexpr int kMlpThreads = kMlpWaves * kWave;
+constexpr int kMlpChunk = 128;                  // hidden columns per chunk
+constexpr int kMlpHidRow = kMlpChunk * 2 + 16;  // LDS hidden row (bytes): conflict-free 16-byte reads
+constexpr int kMlpStageRow = 32 * 4 + 16;       // phase-1 restaged fp32 row (bytes)
+constexpr int kMlpW2Ahead = 2;                  // W2 k-groups loaded ahead of their products
+
+// Both weights arrive in MFMA fragment order (rlm_mfma_fragments): fragment
+// (n-block nb, k-group g) of a [N, K] weight is 64 lanes x 8 consecutive k,
+// lane l holding row 32 nb + (l & 31), k = 16 g + 8 (l >> 5) .. +7, stored
+// as 1 KiB at ((nb * K/16 + g) * 64 + l) * 16 bytes -- so a wave reads a
+// fragment as one contiguous 1 KiB instead of 32 rows of 32 bytes.
+struct MlpParams {
+  HiddenParams h;      // rows, caches, indices and W_m (fragment order; h.out unused)
+  const void* w2;      // second Linear weight [D, H] in fragment order, bf16
+  float* out;          // [rows, D]
+  int D;
+  uint32_t w2_bytes;
+};
+
+// LDS: the hi / lo product tiles, two hidden tiles, the waves' phase-1
+// staging, the row table; after the main loop the output restaging reuses it
+// from the start.
+template <int R>
+constexpr int mlp_hid_offset() {
+  return 2 * kMlpRows * R * 2;
+}
+template <int R>
+constexpr int mlp_stage_offset() {
+  return mlp_hid_offset<R>() + 2 * kMlpRows * kMlpHidRow;
+}
+template <int R>
+constexpr int mlp_table_offset() {
+  return mlp_stage_offset<R>() + kMlpWaves * 32 * kMlpStageRow;
+}
+template <int TNB>
+constexpr int mlp_out_row() {
+  return 32 * TNB * 4 + 16;
+}
+template <int R, int TNB>
+constexpr size_t mlp_lds_bytes() {
+  constexpr size_t main_bytes = mlp_table_offset<R>() + sizeof(RowTableN<kMlpRows>);
+  constexpr size_t out_bytes = static_cast<size_t>(kMlpWaves) * 32 * mlp_out_row<TNB>();
+  return main_bytes > out_bytes ? main_bytes : out_bytes;
+}
+
+template <int R, int TNB>
+__global__ void __launch_bounds__(kMlpThreads) relation_mlp_kernel(const MlpParams mp) {
+  const HiddenParams& p = mp.h;
+  constexpr int PR = R / 8;                               // 16-byte pieces per product row
+  constexpr int RB = R * 2;                               // bytes per product row
+  constexpr int KK = R / 16;                              // phase-1 k-steps
+  constexpr int K2 = kMlpChunk / 16;                      // phase-2 k-groups per chunk
+  constexpr int kPieces = kMlpRows * PR / kMlpThreads;    // product pieces per thread
+  static_assert(R == 64 || R == 128, "relation dim 64 or 128");
+  static_assert(kPieces * kMlpThreads == kMlpRows * PR, "whole product pieces per thread");
+  extern __shared__ __align__(16) unsigned char smem[];
+  unsigned char* p_hi = smem;
+  unsigned char* p_lo = smem + kMlpRows * RB;
+  unsigned char* hid = smem + mlp_hid_offset<R>();
+  auto& rt = *reinterpret_cast<RowTableN<kMlpRows>*>(smem + mlp_table_offset<R>());
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int64_t row_tiles = (p.rows + kMlpRows - 1) / kMlpRows;
+  // Row tiles of neighbouring queries run on one XCD (one L2 for their gathers).
+  const int64_t r0 = xcd_tile(blockIdx.x, row_tiles) * kMlpRows;
+  const int nchunks = p.H / kMlpChunk;
+  const uint32_t H = static_cast<uint32_t>(p.H);
+  const rsrc_t xr = make_rsrc(p.expanded, p.expanded_bytes);
+  const rsrc_t opr = make_rsrc(p.operand, p.operand_bytes);
+  const rsrc_t wr = make_rsrc(p.wm, p.wm_bytes);
+  const rsrc_t w2r = make_rsrc(mp.w2, mp.w2_bytes);
+  unsigned char* stage = smem + mlp_stage_offset<R>() + wave * 32 * kMlpStageRow;
+
+  // Phase-1 roles: row block i1 and column block j1 (32 hidden columns of the
+  // chunk).  W_m fragment kk: rows c*128 + 32 j1 .. +31, k-group kk.
+  const int i1 = wave & 1, j1 = wave >> 1;
+  u16x8 fwm[KK];
+  auto load_wm = [&](int c) {
+    const uint32_t nb = static_cast<uint32_t>(c * (kMlpChunk / 32) + j1);
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      fwm[kk] = __builtin_bit_cast(u16x8, buf_load_b128(wr, ((nb * KK + kk) * kWave + lane) * 16u));
+  };
+  // Row-contiguous roles of the phase-1 epilogue: piece t is row 16t + (lane >> 2)
+  // of the block, columns 8 (lane & 3) .. +7 of its 32.  Rows outside the
+  // caches have kNoOffset bases: their gathers read zeros.
+  const int c8 = 8 * (lane & 3);
+  uint4 xa[2], xp[2];
+  auto load_x = [&](int c) {
+    const uint32_t n = static_cast<uint32_t>(c * kMlpChunk + 32 * j1 + c8);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int m = 32 * i1 + 16 * t + (lane >> 2);
+      xa[t] = buf_load_b128(xr, rt.x_a[m] + 2u * n);
+      xp[t] = buf_load_b128(xr, rt.x_p[m] + 2u * n);
+    }
+  };
+
+  // Set-up: row table, then the products (every load of a thread issued first).
+  load_rows<bf16, kMlpRows>(p, r0, rt);
+  __syncthreads();
+  {
+    uint4 va[kPieces], vp[kPieces];
+#pragma unroll
+    for (int c = 0; c < kPieces; ++c) {
+      const int piece = c * kMlpThreads + tid;
+      const int row = piece / PR, q = piece % PR;
+      va[c] = buf_load_b128(opr, rt.op_a[row] + 16u * q);
+      vp[c] = buf_load_b128(opr, rt.op_p[row] + 16u * q);
+    }
+    load_wm(0);
+    load_x(0);
+#pragma unroll
+    for (int c = 0; c < kPieces; ++c) {
+      const int piece = c * kMlpThreads + tid;
+      const int row = piece / PR, q = piece % PR;
+      const uint32_t wa[4] = {va[c].x, va[c].y, va[c].z, va[c].w};
+      const uint32_t wp[4] = {vp[c].x, vp[c].y, vp[c].z, vp[c].w};
+      uint32_t h[4], l[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x0 = bf16_lo(wp[e]) * bf16_lo(wa[e]);  // exact: 8-bit x 8-bit significands
+        const float x1 = bf16_hi(wp[e]) * bf16_hi(wa[e]);
+        h[e] = pack_bf16x2(x0, x1);
+        l[e] = pack_bf16x2(x0 - bf16_lo(h[e]), x1 - bf16_hi(h[e]));
+      }
+      const int at = row * RB + ((q ^ tile_swz<PR>(row)) << 4);
+      *reinterpret_cast<uint4*>(p_hi + at) = make_uint4(h[0], h[1], h[2], h[3]);
+      *reinterpret_cast<uint4*>(p_lo + at) = make_uint4(l[0], l[1], l[2], l[3]);
+    }
+  }
+  __syncthreads();
+  const int swz = tile_swz<PR>(lane & 15);
+  const int prod_off = (32 * i1 + (lane & 31)) * RB;
+
+  // Phase-2 roles: D columns dw0 .. dw0 + 32 TNB - 1.  W2 fragment j of global
+  // k-group g: n-block TNB w + j, k-group g.
+  const int dw0 = 32 * TNB * wave;
+  const uint32_t kgroups = H / 16u;
+  auto load_w2 = [&](u16x8 (&w)[TNB], int g) {
+#pragma unroll
+    for (int j = 0; j < TNB; ++j)
+      w[j] = __builtin_bit_cast(
+          u16x8, buf_load_b128(w2r, ((static_cast<uint32_t>(TNB * wave + j) * kgroups + g) * kWave +
+                                     lane) * 16u));
+  };
+  // Hidden-tile A fragments: row 32i + (lane & 31), k = 16s + 8 (lane >> 5) of the chunk.
+  const int hid_lane = (lane & 31) * kMlpHidRow + 16 * (lane >> 5);
+
+  f32x16 acc[TNB][2];
+#pragma unroll
+  for (int j = 0; j < TNB; ++j)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[j][i][e] = 0.0f;
+
+  for (int c = 0; c < nchunks; ++c) {
+    unsigned char* hb = hid + (c & 1) * (kMlpRows * kMlpHidRow);
+    // ---- Phase 1: hidden^T block (columns 32 j1.., rows 32 i1..) of chunk c.
+    f32x16 hacc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) hacc[e] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const int off = prod_off + (((2 * kk + (lane >> 5)) ^ swz) << 4);
+      const u16x8 fh = *reinterpret_cast<const u16x8*>(p_hi + off);
+      const u16x8 fl = *reinterpret_cast<const u16x8*>(p_lo + off);
+      hacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fwm[kk]),
+                                                     __builtin_bit_cast(bf16x8, fh), hacc, 0, 0, 0);
+      hacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fwm[kk]),
+                                                     __builtin_bit_cast(bf16x8, fl), hacc, 0, 0, 0);
+    }
+    if (c + 1 < nchunks) load_wm(c + 1);
+    u16x8 wq[K2][TNB];
+#pragma unroll
+    for (int s = 0; s < kMlpW2Ahead; ++s) load_w2(wq[s], c * K2 + s);
+    // hacc: lane holds hidden^T[column 8q + 4 (lane >> 5) + e][row lane & 31].
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<float4*>(stage + (lane & 31) * kMlpStageRow + (8 * q + 4 * (lane >> 5)) * 4) =
+          make_float4(hacc[4 * q], hacc[4 * q + 1], hacc[4 * q + 2], hacc[4 * q + 3]);
+    wave_sync();
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int row = 16 * t + (lane >> 2);
+      const float4 s0 = *reinterpret_cast<const float4*>(stage + row * kMlpStageRow + c8 * 4);
+      const float4 s1 = *reinterpret_cast<const float4*>(stage + row * kMlpStageRow + c8 * 4 + 16);
+      const uint32_t a[4] = {xa[t].x, xa[t].y, xa[t].z, xa[t].w};
+      const uint32_t b[4] = {xp[t].x, xp[t].y, xp[t].z, xp[t].w};
+      const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[2 * e] = gelu_erf(sv[2 * e] + (bf16_lo(a[e]) + bf16_lo(b[e])));
+        v[2 * e + 1] = gelu_erf(sv[2 * e + 1] + (bf16_hi(a[e]) + bf16_hi(b[e])));
+      }
+      put8<bf16>(reinterpret_cast<bf16*>(hb + (32 * i1 + row) * kMlpHidRow + (32 * j1 + c8) * 2), v);
+    }
+    wave_sync();  // the staging is read before the next chunk writes it
+    if (c + 1 < nchunks) load_x(c + 1);
+    __syncthreads();  // hidden chunk c complete
+    // ---- Phase 2: raw^T += W2[:, chunk c] . hidden chunk^T.
+#pragma unroll
+    for (int s = 0; s < K2; ++s) {
+      if (s + kMlpW2Ahead < K2) load_w2(wq[s + kMlpW2Ahead], c * K2 + s + kMlpW2Ahead);
+      u16x8 fa[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        fa[i] = *reinterpret_cast<const u16x8*>(hb + 32 * i * kMlpHidRow + hid_lane + 32 * s);
+#pragma unroll
+      for (int j = 0; j < TNB; ++j)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8, wq[s][j]), __builtin_bit_cast(bf16x8, fa[i]), acc[j][i], 0, 0, 0);
+    }
+  }
+
+  // ---- Output: acc[j][i] holds raw[row 32i + (lane & 31)][columns dw0 + 32j +
+  // 8q + 4 (lane >> 5) .. +3] in element 4q..4q+3.  Each wave restages one
+  // 32-row block at a time and stores whole 16-byte row pieces.
+  __syncthreads();  // every wave is done with the main loop's LDS
+  constexpr int RS = mlp_out_row<TNB>();
+  constexpr int kPiecesRow = 32 * TNB * 4 / 16;
+  unsigned char* ost = smem + wave * 32 * RS;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < TNB; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float4*>(ost + (lane & 31) * RS + (32 * j + 8 * q + 4 * (lane >> 5)) * 4) =
+            make_float4(acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2],
+                        acc[j][i][4 * q + 3]);
+    wave_sync();
+#pragma unroll
+    for (int t = 0; t < 32 * kPiecesRow / kWave; ++t) {
+      const int piece = t * kWave + lane;
+      const int row = piece / kPiecesRow, col = (piece % kPiecesRow) * 4;
+      const int64_t m = r0 + 32 * i + row;
+      const uint4 v = *reinterpret_cast<const uint4*>(ost + row * RS + col * 4);
+      if (m < p.rows) *reinterpret_cast<uint4*>(mp.out + m * mp.D + dw0 + col) = v;
+    }
+    wave_sync();
+  }
+}
+
 // fp32 / fp16 caches: fp32 products on v_mfma_f32_16x16x4f32.  64 hidden
 // columns per workgroup; waves in 2x2, each 32 x 32.
 template <typename T, bool UPDATE>
@@ -2011,6 +2287,199 @@ extern "C" hipError_t rlm_relation_hidden_cached_seq(const rlm_tensor* expanded_
                                product_weight, out, p);
   if (err != hipSuccess) return err;
   return launch_hidden(p, operand_cache->dtype, false, stream);
+}
+
+namespace rlm {
+namespace {
+
+// Shapes relation_mlp_kernel takes: relation dim 64 or 128, a hidden dim that
+// is a positive multiple of 128, d_model 256, 512 or 768 (32 columns per wave
+// times 1..3).
+bool mlp_fits_shape(int64_t R, int64_t H, int64_t D) {
+  return (R == 64 || R == 128) && H > 0 && H % kMlpChunk == 0 && H <= (1 << 20) &&
+         (D == 256 || D == 512 || D == 768);
+}
+
+template <int R, int TNB>
+hipError_t launch_mlp_rt(const MlpParams& mp, hipStream_t stream) {
+  constexpr size_t lds = mlp_lds_bytes<R, TNB>();
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&relation_mlp_kernel<R, TNB>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  if (attr != hipSuccess) {
+    set_error("relation_hidden_linear_seq: cannot reserve %zu bytes of LDS: %s", lds,
+              hipGetErrorString(attr));
+    return attr;
+  }
+  const int64_t tiles = (mp.h.rows + kMlpRows - 1) / kMlpRows;
+  hipLaunchKernelGGL((relation_mlp_kernel<R, TNB>), dim3(static_cast<unsigned>(tiles)),
+                     dim3(kMlpThreads), lds, stream, mp);
+  return launch_status("relation_hidden_linear_seq");
+}
+
+template <int R>
+hipError_t launch_mlp_r(const MlpParams& mp, hipStream_t stream) {
+  if (mp.D == 256) return launch_mlp_rt<R, 1>(mp, stream);
+  if (mp.D == 512) return launch_mlp_rt<R, 2>(mp, stream);
+  return launch_mlp_rt<R, 3>(mp, stream);
+}
+
+}  // namespace
+}  // namespace rlm
+
+// Element (n, k) of a [N, K] weight in MFMA fragment order: fragment
+// (n / 32, k / 16), lane 32 * ((k % 16) / 8) + n % 32, element k % 8.
+__global__ void mfma_fragments_kernel(const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
+                                      int64_t N, int64_t K) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // one 16-byte piece
+  if (i >= N * K / 8) return;
+  const int64_t lane = i & 63, frag = i >> 6;
+  const int64_t kg = K / 16;
+  const int64_t nb = frag / kg, g = frag - nb * kg;
+  const int64_t n = 32 * nb + (lane & 31), k = 16 * g + 8 * (lane >> 5);
+  *reinterpret_cast<uint4*>(out + 8 * i) = *reinterpret_cast<const uint4*>(w + n * K + k);
+}
+
+extern "C" hipError_t rlm_mfma_fragments(const rlm_tensor* weight, const rlm_tensor* out,
+                                         hipStream_t stream) {
+  using namespace rlm;
+  clear_error();
+  RLM_TRY(check_tensor(weight, "weight", 2));
+  RLM_TRY(check_tensor(out, "out", 4));
+  RLM_REQUIRE(weight->dtype == RLM_BF16 || weight->dtype == RLM_F16,
+              "mfma_fragments: weight must be bfloat16 or float16");
+  RLM_TRY(check_dtype_is(out, "out", weight->dtype));
+  const int64_t N = weight->shape[0], K = weight->shape[1];
+  RLM_REQUIRE(N % 32 == 0 && K % 16 == 0,
+              "mfma_fragments: weight rows must be a multiple of 32 and columns of 16, got [%lld, %lld]",
+              (long long)N, (long long)K);
+  RLM_TRY(check_dim(out, "out", 0, N / 32));
+  RLM_TRY(check_dim(out, "out", 1, K / 16));
+  RLM_TRY(check_dim(out, "out", 2, 64));
+  RLM_TRY(check_dim(out, "out", 3, 8));
+  RLM_REQUIRE((reinterpret_cast<uintptr_t>(weight->data) & 15u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(out->data) & 15u) == 0,
+              "mfma_fragments: weight and out must be 16-byte aligned");
+  const int64_t pieces = N * K / 8;
+  if (pieces == 0) return hipSuccess;
+  hipLaunchKernelGGL(mfma_fragments_kernel, dim3(static_cast<unsigned>((pieces + 255) / 256)),
+                     dim3(256), 0, stream, static_cast<const uint16_t*>(weight->data),
+                     static_cast<uint16_t*>(out->data), N, K);
+  return launch_status("mfma_fragments");
+}
+
+namespace rlm {
+namespace {
+// A [N/32, K/16, 64, 8] weight in fragment order of an [N, K] weight: N and K.
+bool frag_dims(const rlm_tensor* t, int64_t& N, int64_t& K) {
+  if (t == nullptr || t->ndim != 4 || t->shape[2] != 64 || t->shape[3] != 8) return false;
+  N = t->shape[0] * 32;
+  K = t->shape[1] * 16;
+  return true;
+}
+}  // namespace
+}  // namespace rlm
+
+extern "C" int rlm_relation_hidden_linear_seq_fits(const rlm_tensor* expanded_cache,
+                                                   const rlm_tensor* operand_cache,
+                                                   const rlm_tensor* product_weight,
+                                                   const rlm_tensor* second_weight) {
+  using namespace rlm;
+  for (const rlm_tensor* t : {expanded_cache, operand_cache, product_weight, second_weight})
+    if (t == nullptr || t->dtype != RLM_BF16) return 0;
+  if (operand_cache->ndim != 3 || expanded_cache->ndim != 3) return 0;
+  int64_t H, R, D, H2;
+  if (!frag_dims(product_weight, H, R) || !frag_dims(second_weight, D, H2)) return 0;
+  if (R != operand_cache->shape[2] || H2 != H || expanded_cache->shape[2] != 2 * H) return 0;
+  for (const rlm_tensor* t : {operand_cache, product_weight, second_weight, expanded_cache})
+    if ((reinterpret_cast<uintptr_t>(t->data) & 15u) != 0) return 0;
+  return mlp_fits_shape(R, H, D) ? 1 : 0;
+}
+
+extern "C" hipError_t rlm_relation_hidden_linear_seq(
+    const rlm_tensor* expanded_cache, const rlm_tensor* operand_cache,
+    const rlm_tensor* anchor_index, const rlm_tensor* partner_index,
+    const rlm_tensor* product_weight, const rlm_tensor* second_weight, const rlm_tensor* out,
+    hipStream_t stream) {
+  using namespace rlm;
+  clear_error();
+  const char* what = "relation_hidden_linear_seq";
+  RLM_TRY(check_tensor(operand_cache, "operand_cache", 3));
+  RLM_TRY(check_tensor(expanded_cache, "expanded_cache", 3));
+  RLM_TRY(check_tensor(product_weight, "product_weight", 4));
+  RLM_TRY(check_tensor(second_weight, "second_weight", 4));
+  for (const rlm_tensor* t : {operand_cache, expanded_cache, product_weight, second_weight})
+    RLM_REQUIRE(t->dtype == RLM_BF16, "%s: caches and weights must be bfloat16", what);
+  int64_t H, Rw, D, H2;
+  RLM_REQUIRE(frag_dims(product_weight, H, Rw) && frag_dims(second_weight, D, H2),
+              "%s: product_weight and second_weight must be in MFMA fragment order "
+              "[N/32, K/16, 64, 8] (rlm_mfma_fragments)", what);
+  const int64_t B = operand_cache->shape[0], T = operand_cache->shape[1];
+  const int64_t R = operand_cache->shape[2];
+  RLM_REQUIRE(Rw == R, "%s: product_weight is for relation dim %lld, the operand cache has %lld",
+              what, (long long)Rw, (long long)R);
+  RLM_REQUIRE(H2 == H, "%s: second_weight is for hidden dim %lld, product_weight has %lld", what,
+              (long long)H2, (long long)H);
+  RLM_TRY(check_dim(expanded_cache, "expanded_cache", 0, B));
+  RLM_TRY(check_dim(expanded_cache, "expanded_cache", 1, T));
+  RLM_TRY(check_dim(expanded_cache, "expanded_cache", 2, 2 * H));
+  RLM_TRY(check_tensor(anchor_index, "anchor_index", 2));
+  RLM_TRY(check_tensor(partner_index, "partner_index", 3));
+  RLM_REQUIRE(is_index_dtype(anchor_index->dtype) && is_index_dtype(partner_index->dtype),
+              "anchor_index/partner_index must be int32 or int64");
+  RLM_TRY(check_dim(anchor_index, "anchor_index", 0, B));
+  RLM_TRY(check_dim(partner_index, "partner_index", 0, B));
+  const int64_t Tq = anchor_index->shape[1];
+  RLM_TRY(check_dim(partner_index, "partner_index", 1, Tq));
+  const int64_t K = partner_index->shape[2];
+  RLM_REQUIRE(mlp_fits_shape(R, H, D),
+              "%s: needs relation dim 64 or 128, a hidden dim that is a multiple of %d and "
+              "d_model 256, 512 or 768 (got R=%lld H=%lld D=%lld); other shapes run "
+              "relation_hidden_cached_seq + relation_linear",
+              what, kMlpChunk, (long long)R, (long long)H, (long long)D);
+  constexpr int64_t kMaxBytes = int64_t(1) << 31;
+  RLM_REQUIRE(B * T * 2 * H * 2 < kMaxBytes && B * T * R * 2 < kMaxBytes && H * R * 2 < kMaxBytes &&
+                  D * H * 2 < kMaxBytes,
+              "%s: caches and weights must each be smaller than 2 GiB", what);
+  for (const rlm_tensor* t : {operand_cache, product_weight, second_weight, expanded_cache})
+    RLM_REQUIRE((reinterpret_cast<uintptr_t>(t->data) & 15u) == 0,
+                "%s: caches and weights must be 16-byte aligned", what);
+  RLM_TRY(check_tensor(out, "out", 4));
+  RLM_TRY(check_dtype_is(out, "out", RLM_F32));
+  RLM_TRY(check_dim(out, "out", 0, B));
+  RLM_TRY(check_dim(out, "out", 1, Tq));
+  RLM_TRY(check_dim(out, "out", 2, K));
+  RLM_TRY(check_dim(out, "out", 3, D));
+  RLM_REQUIRE((reinterpret_cast<uintptr_t>(out->data) & 15u) == 0, "%s: out must be 16-byte aligned",
+              what);
+  const int64_t rows = B * Tq * K;
+  RLM_REQUIRE((rows + kMlpRows - 1) / kMlpRows <= 0x7fffffff, "%s: too many relation rows", what);
+  if (rows == 0) return hipSuccess;
+  MlpParams mp{};
+  HiddenParams& p = mp.h;
+  p.B = B;
+  p.Tq = Tq;
+  p.T = T;
+  p.R = static_cast<int>(R);
+  p.H = static_cast<int>(H);
+  p.K = static_cast<int>(K);
+  p.rows = rows;
+  p.expanded = expanded_cache->data;
+  p.expanded_out = expanded_cache->data;
+  p.operand = operand_cache->data;
+  p.anchor = anchor_index->data;
+  p.partner = partner_index->data;
+  p.index_dtype_a = anchor_index->dtype;
+  p.index_dtype_p = partner_index->dtype;
+  p.wm = product_weight->data;
+  p.expanded_bytes = static_cast<uint32_t>(B * T * 2 * H * 2);
+  p.operand_bytes = static_cast<uint32_t>(B * T * R * 2);
+  p.wm_bytes = static_cast<uint32_t>(H * R * 2);
+  mp.w2 = second_weight->data;
+  mp.w2_bytes = static_cast<uint32_t>(D * H * 2);
+  mp.out = static_cast<float*>(out->data);
+  mp.D = static_cast<int>(D);
+  return R == 128 ? launch_mlp_r<128>(mp, stream) : launch_mlp_r<64>(mp, stream);
 }
 
 namespace rlm {

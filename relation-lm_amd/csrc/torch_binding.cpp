@@ -399,6 +399,39 @@ void relation_hidden_cached_seq_out(const at::Tensor& expanded_cache,
   check(rlm_relation_hidden_cached_seq(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], stream), op);
 }
 
+void relation_hidden_linear_seq_out(const at::Tensor& expanded_cache,
+                                    const at::Tensor& operand_cache,
+                                    const at::Tensor& anchor_index,
+                                    const at::Tensor& partner_index,
+                                    const at::Tensor& product_weight,
+                                    const at::Tensor& second_weight, at::Tensor& out) {
+  const char* op = "relation_lm::relation_hidden_linear_seq_out";
+  c10::DeviceGuard guard(operand_cache.device());
+  hipStream_t stream =
+      device_stream(op, {&operand_cache, &expanded_cache, &anchor_index, &partner_index,
+                         &product_weight, &second_weight, &out});
+  TORCH_CHECK(out.is_contiguous(), op, ": out must be contiguous");
+  rlm_tensor d[7] = {desc(expanded_cache, "expanded_cache"), desc(operand_cache, "operand_cache"),
+                     desc(anchor_index, "anchor_index"),     desc(partner_index, "partner_index"),
+                     desc(product_weight, "product_weight"), desc(second_weight, "second_weight"),
+                     desc(out, "out")};
+  check(rlm_relation_hidden_linear_seq(&d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], stream),
+        op);
+}
+
+at::Tensor mfma_fragments(const at::Tensor& weight) {
+  const char* op = "relation_lm::mfma_fragments";
+  c10::DeviceGuard guard(weight.device());
+  hipStream_t stream = device_stream(op, {&weight});
+  TORCH_CHECK(weight.dim() == 2, op, ": weight must be 2-d");
+  TORCH_CHECK(weight.size(0) % 32 == 0 && weight.size(1) % 16 == 0, op,
+              ": weight rows must be a multiple of 32 and columns of 16");
+  at::Tensor out = at::empty({weight.size(0) / 32, weight.size(1) / 16, 64, 8}, weight.options());
+  rlm_tensor d[2] = {desc(weight, "weight"), desc(out, "out")};
+  check(rlm_mfma_fragments(&d[0], &d[1], stream), op);
+  return out;
+}
+
 at::Tensor hidden_update_common(bool ring, at::Tensor& expanded_cache,
                                 const at::Tensor& operand_cache, const at::Tensor& anchor_index,
                                 const at::Tensor& partner_index, const at::Tensor& anchor_weight,
@@ -1178,6 +1211,13 @@ TORCH_LIBRARY(relation_lm, m) {
   m.def(
       "relation_hidden_cached_seq_out(Tensor expanded_cache, Tensor operand_cache, Tensor "
       "anchor_index, Tensor partner_index, Tensor product_weight, Tensor(a!) out) -> ()");
+  // The relation MLP's hidden and bias-free second Linear in one launch (the
+  // reference runs nn.Linear -> GELU -> nn.Linear, multi_relation_blocks.py:47-52).
+  m.def(
+      "relation_hidden_linear_seq_out(Tensor expanded_cache, Tensor operand_cache, Tensor "
+      "anchor_index, Tensor partner_index, Tensor product_weight, Tensor second_weight, "
+      "Tensor(a!) out) -> ()");
+  m.def("mfma_fragments(Tensor weight) -> Tensor");
   // Multi-anchor relation block (no reference op: the reference runs these in
   // eager torch inside MultiAnchorRelationBlock / DistilledBlockRouter).
   m.def(
@@ -1240,6 +1280,8 @@ TORCH_LIBRARY_IMPL(relation_lm, CUDA, m) {
   m.impl("relation_linear", TORCH_FN(relation_linear));
   m.impl("relation_linear_out", TORCH_FN(relation_linear_out));
   m.impl("relation_hidden_cached_seq_out", TORCH_FN(relation_hidden_cached_seq_out));
+  m.impl("relation_hidden_linear_seq_out", TORCH_FN(relation_hidden_linear_seq_out));
+  m.impl("mfma_fragments", TORCH_FN(mfma_fragments));
   m.impl("multi_relation_reduce_seq", TORCH_FN(multi_relation_reduce_seq));
   m.impl("multi_relation_reduce_seq_out", TORCH_FN(multi_relation_reduce_seq_out));
   m.impl("layer_norm", TORCH_FN(layer_norm));

@@ -143,6 +143,15 @@ def _register_fakes() -> None:
     def _(expanded_cache, operand_cache, anchor_index, partner_index, product_weight, out):
         return None
 
+    @torch.library.register_fake("relation_lm::mfma_fragments")
+    def _(weight):
+        return weight.new_empty((weight.shape[0] // 32, weight.shape[1] // 16, 64, 8))
+
+    @torch.library.register_fake("relation_lm::relation_hidden_linear_seq_out")
+    def _(expanded_cache, operand_cache, anchor_index, partner_index, product_weight,
+          second_weight, out):
+        return None
+
     @torch.library.register_fake("relation_lm::multi_relation_reduce_seq")
     def _(raw, partner_scores, norm_weight, norm_bias, slot_mix_logits, residual_gate, hidden,
           positions, norm_eps, raw_bias=None):

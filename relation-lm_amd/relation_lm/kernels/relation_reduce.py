@@ -115,6 +115,52 @@ def relation_hidden_cached_seq_out(
         expanded_cache, operand_cache, anchor_index, partner_index, product_weight, out)
 
 
+def mfma_fragments(weight: Tensor) -> Tensor:
+    """A [N, K] bf16 / f16 weight in MFMA fragment order, [N/32, K/16, 64, 8]: fragment
+    (nb, g) holds, for lane l, ``weight[32 nb + l % 32, 16 g + 8 (l // 32) : +8]`` -- what a
+    wave's 32x32x16 matrix instruction reads, contiguous per fragment.  A packing step
+    run once per weight (N % 32 == 0, K % 16 == 0)."""
+    return torch.ops.relation_lm.mfma_fragments(weight)
+
+
+def relation_hidden_linear_seq_fits(
+    expanded_cache: Tensor,
+    operand_cache: Tensor,
+    product_weight: Tensor,
+    second_weight: Tensor,
+) -> bool:
+    """True when ``relation_hidden_linear_seq_out`` takes these operands (bf16 caches and
+    weights, the weights in fragment order, relation dim 64 or 128, hidden dim a multiple
+    of 128, d_model 256, 512 or 768, 16-byte aligned).  Reads only shapes, dtypes and
+    pointer alignment."""
+    lib = _native.c_library()
+    return bool(lib.rlm_relation_hidden_linear_seq_fits(
+        *(ctypes.byref(_desc(t)) for t in (expanded_cache, operand_cache, product_weight,
+                                           second_weight))))
+
+
+def relation_hidden_linear_seq_out(
+    expanded_cache: Tensor,
+    operand_cache: Tensor,
+    anchor_index: Tensor,
+    partner_index: Tensor,
+    product_weight: Tensor,
+    second_weight: Tensor,
+    out: Tensor,
+) -> None:
+    """The relation MLP's hidden and bias-free second Linear in one launch, into ``out``
+    f32 [B,Tq,K,D]: ``second_weight . bf16(hidden)`` with the hidden of
+    ``relation_hidden_cached_seq`` (multi_relation_blocks.py:47-52,163 of the reference:
+    Linear -> GELU -> Linear, the first Linear factorized).  ``product_weight`` [H, R] and
+    ``second_weight`` [D, H] come in fragment order (``mfma_fragments``).  The hidden never
+    reaches memory; the result is bit-identical to ``relation_hidden_cached_seq_out`` into
+    a bf16 buffer followed by ``relation_linear(..., None, torch.float32)``.  Shapes outside
+    ``relation_hidden_linear_seq_fits`` raise."""
+    torch.ops.relation_lm.relation_hidden_linear_seq_out(
+        expanded_cache, operand_cache, anchor_index, partner_index, product_weight,
+        second_weight, out)
+
+
 def relation_hidden_cache_update(
     expanded_cache: Tensor,
     operand_cache: Tensor,

@@ -11,13 +11,15 @@ multi-anchor selection (local window plus the top blocks of a block router,
   projections of hidden / memory  relation_lm::relation_linear (MFMA)
   router block statistics         relation_lm::block_statistics
   distinct anchors, partners      relation_lm::multi_relation_select_seq
-  relation MLP Linear -> GELU     relation_lm::relation_hidden_cached_seq_out
-    (factorized: operand cache, expanded cache = [W_a+W_d; W_p-W_d] op + [b; 0];
-    stored in bf16 when the second Linear is bf16)
-  relation MLP second Linear      relation_lm::relation_linear (the MFMA DMA-tile GEMM,
-    bias in its epilogue, fp32 output)
-  LayerNorm, partner softmax,     relation_lm::multi_relation_reduce_seq
-    slot mix, residual gate
+  relation MLP Linear -> GELU     relation_lm::relation_hidden_linear_seq_out: one
+    -> Linear (bias-free)           kernel (factorized first Linear: operand cache,
+                                    expanded cache = [W_a+W_d; W_p-W_d] op + [b; 0];
+                                    the bf16 hidden stays on chip; fp32 output)
+    other shapes                    relation_lm::relation_hidden_cached_seq_out, then
+                                    relation_lm::relation_linear (MFMA DMA-tile GEMM)
+  second Linear's bias, LayerNorm, relation_lm::multi_relation_reduce_seq
+    partner softmax, slot mix,
+    residual gate
   final_norm (stack)              relation_lm::layer_norm
 
 When the sequence is no longer than the local window every causal position is
@@ -43,7 +45,8 @@ import torch
 from torch import Tensor, nn
 
 from relation_lm import _native  # noqa: F401  (registers torch.ops.relation_lm)
-from relation_lm.kernels.relation_reduce import factor_relation_first_layer
+from relation_lm.kernels.relation_reduce import (factor_relation_first_layer, mfma_fragments,
+                                                 relation_hidden_linear_seq_fits)
 
 ops = torch.ops.relation_lm
 
@@ -129,6 +132,14 @@ class MultiAnchorRelationBlock(nn.Module):
                 "expanded_bias": factors.expanded_bias,
                 "product_weight": factors.product_weight,
             }
+            # The relation MLP's product and second-Linear weights in MFMA fragment
+            # order, for the one-launch relation MLP (bf16 on the GPU only).
+            wm, w2 = factors.product_weight, mlp[2].weight
+            if (wm.is_cuda and wm.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16
+                    and wm.shape[0] % 32 == 0 and wm.shape[1] % 16 == 0
+                    and w2.shape[0] % 32 == 0 and w2.shape[1] % 16 == 0):
+                self._packed["product_weight_frags"] = mfma_fragments(wm.contiguous())
+                self._packed["second_weight_frags"] = mfma_fragments(w2.contiguous())
         self._packed_key = key
         return self._packed
 
@@ -190,7 +201,9 @@ class MultiAnchorRelationBlock(nn.Module):
         return {"select_args": args, "positions": positions, "normalized": normalized,
                 "anchor": anchor, "anchor_score": anchor_score, "partner": partner,
                 "partner_score": partner_score, "operand_cache": mem["operand_cache"],
-                "expanded_cache": mem["expanded_cache"], "product_weight": packed["product_weight"]}
+                "expanded_cache": mem["expanded_cache"], "product_weight": packed["product_weight"],
+                "product_weight_frags": packed.get("product_weight_frags"),
+                "second_weight_frags": packed.get("second_weight_frags")}
 
     def relate(self, hidden: Tensor, sel: dict, context: Tensor | None = None) -> Tensor:
         """The relation MLP over every (query, slot, partner) row of the selection,
@@ -200,6 +213,35 @@ class MultiAnchorRelationBlock(nn.Module):
         batch, length, d = hidden.shape
         h, k_count = cfg.anchors_per_block, cfg.partners_per_anchor
         mlp = self.relation_mlp
+        output = torch.empty_like(hidden, memory_format=torch.contiguous_format)
+        wm_frags, w2_frags = sel.get("product_weight_frags"), sel.get("second_weight_frags")
+        if wm_frags is not None and relation_hidden_linear_seq_fits(
+                sel["expanded_cache"], sel["operand_cache"], wm_frags, w2_frags):
+            # The hidden and the bias-free second Linear in one launch (the
+            # hidden never reaches memory); the second Linear's bias joins the
+            # rows as the slot reduce loads them.  Equal groups of batch rows,
+            # each group's fp32 rows below the 2 GiB a kernel addresses.
+            raw_bytes = length * h * k_count * d * 4
+            most = max(1, min(batch, (2**31 - 1) // raw_bytes))
+            group = -(-batch // -(-batch // most))
+            raw = torch.empty((group, length * h, k_count, d), dtype=torch.float32,
+                              device=hidden.device)
+            for b0 in range(0, batch, group):
+                b1 = min(batch, b0 + group)
+                n = b1 - b0
+                part = raw[:n]
+                ops.relation_hidden_linear_seq_out(
+                    sel["expanded_cache"][b0:b1], sel["operand_cache"][b0:b1],
+                    sel["anchor"][b0:b1].reshape(n, length * h),
+                    sel["partner"][b0:b1].reshape(n, length * h, k_count), wm_frags, w2_frags,
+                    part)
+                ops.multi_relation_reduce_seq_out(
+                    part.view(n, length, h, k_count, d), sel["partner_score"][b0:b1],
+                    mlp[3].weight, mlp[3].bias, self.slot_mix_logits, self.residual_gate,
+                    hidden[b0:b1], sel["positions"], mlp[3].eps, mlp[2].bias, output[b0:b1],
+                    None if context is None else context[b0:b1])
+            return output
+        # Other shapes: the hidden, then the second Linear.
         # The MLP hidden in the second Linear's operand dtype: a bf16 Linear
         # rounds an fp32 hidden to bf16 before its products, so storing bf16
         # gives the same result at half the bytes.  A few batch rows at a time:
@@ -213,7 +255,6 @@ class MultiAnchorRelationBlock(nn.Module):
         group = -(-batch // -(-batch // most))
         rows = torch.empty((group, length * h, k_count, width), dtype=hid_dtype,
                            device=hidden.device)
-        output = torch.empty_like(hidden, memory_format=torch.contiguous_format)
         for b0 in range(0, batch, group):
             b1 = min(batch, b0 + group)
             n = b1 - b0

@@ -95,6 +95,47 @@ def test_fused_reduce_fits_predicate(lib):
     assert fits(w2=tensor([512, 512], RLM_BF16, data=0x1008)) == 0       # misaligned
 
 
+def test_relation_mlp_fits_and_validation(lib):
+    """rlm_relation_hidden_linear_seq_fits reads descriptors only; the entry point rejects
+    shapes the kernel does not take before launching anything."""
+    base = {"expanded": tensor([2, 64, 6144], RLM_BF16), "operand": tensor([2, 64, 128], RLM_BF16),
+            "wm": tensor([96, 8, 64, 8], RLM_BF16), "w2": tensor([24, 192, 64, 8], RLM_BF16)}
+
+    def fits(**override):
+        d = {**base, **override}
+        return lib.rlm_relation_hidden_linear_seq_fits(
+            *(ctypes.byref(d[k]) for k in ("expanded", "operand", "wm", "w2")))
+
+    assert fits() == 1
+    assert fits(w2=tensor([16, 192, 64, 8], RLM_BF16)) == 1              # d_model 512
+    assert fits(w2=tensor([18, 192, 64, 8], RLM_BF16)) == 0              # d_model 576
+    assert fits(w2=tensor([768, 3072], RLM_BF16)) == 0                   # not fragment order
+    assert fits(w2=tensor([24, 192, 64, 8], RLM_F32)) == 0               # fp32 weight
+    assert fits(operand=tensor([2, 64, 96], RLM_BF16),
+                wm=tensor([96, 6, 64, 8], RLM_BF16)) == 0                # R not 64/128
+    assert fits(wm=tensor([94, 8, 64, 8], RLM_BF16), w2=tensor([24, 188, 64, 8], RLM_BF16),
+                expanded=tensor([2, 64, 6016], RLM_BF16)) == 0           # H % 128 != 0
+    assert fits(w2=tensor([24, 192, 64, 8], RLM_BF16, data=0x1008)) == 0  # misaligned
+
+    anchor, partner = tensor([2, 16], RLM_I64), tensor([2, 16, 3], RLM_I64)
+    out = tensor([2, 16, 3, 576])
+    rc = lib.rlm_relation_hidden_linear_seq(
+        ctypes.byref(base["expanded"]), ctypes.byref(base["operand"]), ctypes.byref(anchor),
+        ctypes.byref(partner), ctypes.byref(base["wm"]),
+        ctypes.byref(tensor([18, 192, 64, 8], RLM_BF16)), ctypes.byref(out), None)
+    assert rc == HIP_ERROR_INVALID_VALUE
+    assert b"d_model 256, 512 or 768" in lib.rlm_last_error()
+    rc = lib.rlm_mfma_fragments(ctypes.byref(tensor([48, 40], RLM_BF16)),
+                                ctypes.byref(tensor([1, 2, 64, 8], RLM_BF16)), None)
+    assert rc == HIP_ERROR_INVALID_VALUE                                 # 48 rows: not 32k
+    assert b"multiple of 32" in lib.rlm_last_error()
+    rc = lib.rlm_relation_hidden_linear_seq(
+        ctypes.byref(base["expanded"]), ctypes.byref(base["operand"]), ctypes.byref(anchor),
+        ctypes.byref(partner), ctypes.byref(base["wm"]), ctypes.byref(base["w2"]),
+        ctypes.byref(tensor([2, 16, 3, 768], RLM_BF16)), None)
+    assert rc == HIP_ERROR_INVALID_VALUE                                 # bf16 out
+
+
 def _select_packed_args(b=2, t=64, e=64, nb=8, k=4, **override):
     d = {
         "anchor_query": tensor([b, e]), "anchor_keys": tensor([b, t, e]),

@@ -215,6 +215,11 @@ def op_cases(device):
                           dtype=torch.bfloat16)
     cases.append(("relation_hidden_cached_seq_out", ops.relation_hidden_cached_seq_out.default,
                   (expanded, red["operand_cache"], a_seq, p_seq, wm, hid_out)))
+    mlp_out = torch.empty(tuple(p_seq.shape) + (red["second_weight"].shape[0],), device=device)
+    cases.append(("relation_hidden_linear_seq_out", ops.relation_hidden_linear_seq_out.default,
+                  (expanded, red["operand_cache"], a_seq, p_seq, ops.mfma_fragments(wm),
+                   ops.mfma_fragments(red["second_weight"]), mlp_out)))
+    cases.append(("mfma_fragments", ops.mfma_fragments.default, (red["second_weight"],)))
     cases.append(("relation_hidden_cached_ring", ops.relation_hidden_cached_ring.default,
                   (expanded, red["operand_cache"], a_dec + 2 * t, p_dec + 2 * t, wm)))
     update = (red["anchor_weight"], red["partner_weight"], wm, red["first_bias"])
@@ -304,7 +309,7 @@ def op_cases(device):
 OP_NAMES = ("relation_select_packed", "relation_select_packed_seq",
             "relation_select_packed_expand_row", "relation_select_packed_ring", "anchor_select", "partner_topk",
             "multi_relation_select_seq", "relation_hidden_cached", "relation_hidden_cached_seq",
-            "relation_hidden_cached_seq_out",
+            "relation_hidden_cached_seq_out", "relation_hidden_linear_seq_out", "mfma_fragments",
             "relation_hidden_cached_ring", "relation_hidden_cache_update",
             "relation_hidden_cache_update_ring", "relation_norm_reduce",
             "relation_norm_reduce_seq", "relation_reduce_fused_seq", "router_cache_update",

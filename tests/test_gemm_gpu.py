@@ -16,6 +16,8 @@ import numpy as np
 import pytest
 import torch
 
+from relation_lm import _native  # noqa: F401  (registers torch.ops.relation_lm)
+
 pytestmark = pytest.mark.gpu
 ops = torch.ops.relation_lm
 
