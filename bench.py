@@ -165,6 +165,7 @@ def main() -> int:
     import torch
 
     from relation_lm.kernels.relation_reduce import (
+        mfma_fragments,
         relation_hidden_cached_seq,
         relation_linear,
         relation_norm_reduce_seq,
@@ -350,10 +351,11 @@ def main() -> int:
         rexp = relation_linear(rred["operand_cache"], rred["expanded_weight"],
                                rred["expanded_bias"])
         ra, rp, rs, rpos = (x.to(device) for x in causal_partner_indices(rcfg, seed=41))
+        rw2 = mfma_fragments(rred["second_weight"])   # packed once, like the model's weights
 
         def fused_once():
             return relation_reduce_fused_seq(rexp, rred["operand_cache"], ra, rp,
-                                             rred["product_weight"], rred["second_weight"],
+                                             rred["product_weight"], rw2,
                                              rred["second_bias"], rs, rred["norm_weight"],
                                              rred["norm_bias"], rpos, 1e-5)
 
@@ -614,9 +616,14 @@ def main() -> int:
         return relation_norm_reduce_seq(raw, ps, red["norm_weight"], red["norm_bias"], positions,
                                         1e-5)
 
+    # The second Linear's weight in MFMA fragment order, packed once (a weight
+    # layout, like the reference's packed sparse-cache weights): the fused kernel
+    # then reads each weight fragment as one contiguous 1 KiB, same result bits.
+    second_frags = mfma_fragments(red["second_weight"])
+
     def run_fused(expanded, a, p, ps):
         return relation_reduce_fused_seq(expanded, operand, a, p, red["product_weight"],
-                                         red["second_weight"], red["second_bias"], ps,
+                                         second_frags, red["second_bias"], ps,
                                          red["norm_weight"], red["norm_bias"], positions, 1e-5)
 
     def step():
@@ -762,6 +769,8 @@ def main() -> int:
     n_rot = max(2, -(-2 * MALL_BYTES // set_bytes))
     rot_sets = [({k: v.clone() for k, v in sel.items()}, {k: v.clone() for k, v in red.items()})
                 for _ in range(n_rot)]
+    for _, rr in rot_sets:
+        rr["second_frags"] = mfma_fragments(rr["second_weight"])
     rot_state = {"i": 0}
 
     def step_rotated():
@@ -770,7 +779,7 @@ def main() -> int:
         rexp = relation_linear(rr["operand_cache"], rr["expanded_weight"], rr["expanded_bias"])
         ra, _, rp, rps = relation_select_packed_seq(*select_args(rs, cfg))
         return relation_reduce_fused_seq(rexp, rr["operand_cache"], ra, rp, rr["product_weight"],
-                                         rr["second_weight"], rr["second_bias"], rps,
+                                         rr["second_frags"], rr["second_bias"], rps,
                                          rr["norm_weight"], rr["norm_bias"], rs["positions"], 1e-5)
 
     for _ in range(2 * n_rot):

@@ -444,10 +444,12 @@ hipError_t rlm_relation_norm_reduce_output_seq(
  *   h_k = GELU(W_m (op[a]*op[p_k]) + X[a,0:H] + X[p_k,H:2H]) rounded to bf16,
  *   p = the active-K softmax of relation_norm_reduce.
  *   expanded_cache [B,T,2H], operand_cache [B,T,R], product_weight [H,R],
- *   second_weight [D,H] (all bf16), second_bias [D], partner_scores f32
- *   [B,Tq,K], norm_weight/norm_bias [D], anchor_index [B,Tq], partner_index
- *   [B,Tq,K], positions [Tq] or [B,Tq].  1 <= K <= 16, R in {32,64,128},
- *   H a multiple of 128, D in {128, 256, 384, 512}.
+ *   second_weight [D,H] or the same weight in MFMA fragment order
+ *   [D/32,H/16,64,8] (rlm_mfma_fragments, done once: each fragment load is then
+ *   one contiguous 1 KiB; same result bit for bit) (all bf16), second_bias [D],
+ *   partner_scores f32 [B,Tq,K], norm_weight/norm_bias [D], anchor_index
+ *   [B,Tq], partner_index [B,Tq,K], positions [Tq] or [B,Tq].  1 <= K <= 16,
+ *   R in {32,64,128}, H a multiple of 128, D in {128, 256, 384, 512}.
  * Output: out f32 [B,Tq,D].
  */
 hipError_t rlm_relation_reduce_fused_seq(

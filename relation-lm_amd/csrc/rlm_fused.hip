@@ -213,9 +213,9 @@ __device__ __forceinline__ void dma_gather_chunk(rsrc_t xr, uint32_t tile,
               src[i] == kNoOffset ? kNoOffset : src[i] + chunk * kHC * 2u);
 }
 
-template <int DT, int KS1>
+template <int DT, int KS1, bool FRAG>
 __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParams p) {
-  // DT = D / 128; KS1 = R / 32.
+  // DT = D / 128; KS1 = R / 32; FRAG: W2 in MFMA fragment order (rlm_mfma_fragments).
   extern __shared__ __align__(16) unsigned char smem[];
   unsigned char* hid = smem + kOffHid;                            // [kRows][kLd] bf16
   float* wts = reinterpret_cast<float*>(smem + kOffF32);           // [kRows]
@@ -351,15 +351,19 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
   }
 
   // W2 fragments (A operand of phase 2): rows d0 + 32j + n32 of W2, k = chunk*128
-  // + 16s + 8h (8 bf16 per lane).
+  // + 16s + 8h (8 bf16 per lane).  In fragment order the wave reads each
+  // fragment as one contiguous 1 KiB (fragment (n-block, k-group) at
+  // ((nb * H/16 + g) * 64 + lane) * 16 bytes); row-major, 32 rows of 32 bytes.
   const int dg = wave % DG, rg = wave / DG;
   const int d0 = dg * DTW * 32;
   const int n32 = lane & 31, h = lane >> 5;
-  const uint32_t w2_lane = (static_cast<uint32_t>(d0 + n32) * H + 8 * h) * 2u;
+  const uint32_t w2_lane = FRAG ? ((static_cast<uint32_t>(d0 / 32) * (H / 16)) * kWave + lane) * 16u
+                                : (static_cast<uint32_t>(d0 + n32) * H + 8 * h) * 2u;
   auto load_w2 = [&](u16x8 (&w)[DTW], int chunk, int s) {
+    const uint32_t kg = FRAG ? static_cast<uint32_t>(chunk * (kHC / 16) + s) * 1024u
+                             : static_cast<uint32_t>(chunk * kHC + 16 * s) * 2u;
 #pragma unroll
-    for (int j = 0; j < DTW; ++j)
-      w[j] = as_frag(buf_load_b128(w2r, w2_lane + (32u * j * H + chunk * kHC + 16 * s) * 2u));
+    for (int j = 0; j < DTW; ++j) w[j] = as_frag(buf_load_b128(w2r, w2_lane + 64u * j * H + kg));
   };
 
   // raw[j][i][4ii + jj] = raw^T[d = d0 + 32j + 8ii + 4h + jj][slot 32(RTW rg + i) + n32],
@@ -619,13 +623,13 @@ __global__ void __launch_bounds__(kThreads) fused_reduce_kernel(const FusedParam
   }
 }
 
-template <int DT, int KS1>
+template <int DT, int KS1, bool FRAG>
 hipError_t launch_fused(const FusedParams& p, hipStream_t stream) {
   const dim3 grid((p.rows + kRows - 1) / kRows);
   static bool attr_set = false;  // the LDS opt-in is a per-process function attribute
   if (!attr_set) {
     const hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&fused_reduce_kernel<DT, KS1>),
+        reinterpret_cast<const void*>(&fused_reduce_kernel<DT, KS1, FRAG>),
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsBytes));
     if (e != hipSuccess) {
       set_error("relation_reduce_fused: cannot reserve %zu bytes of LDS: %s", kLdsBytes,
@@ -634,7 +638,8 @@ hipError_t launch_fused(const FusedParams& p, hipStream_t stream) {
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((fused_reduce_kernel<DT, KS1>), grid, dim3(kThreads), kLdsBytes, stream, p);
+  hipLaunchKernelGGL((fused_reduce_kernel<DT, KS1, FRAG>), grid, dim3(kThreads), kLdsBytes, stream,
+                     p);
   return launch_status("relation_reduce_fused");
 }
 
@@ -642,6 +647,24 @@ hipError_t launch_fused(const FusedParams& p, hipStream_t stream) {
 }  // namespace rlm
 
 using namespace rlm;
+
+namespace {
+// second_weight as [D, H] (row-major) or in MFMA fragment order [D/32, H/16, 64, 8]:
+// D and H; false for any other shape.
+bool second_weight_dims(const rlm_tensor* w, int64_t& D, int64_t& H) {
+  if (w->ndim == 2) {
+    D = w->shape[0];
+    H = w->shape[1];
+    return true;
+  }
+  if (w->ndim == 4 && w->shape[2] == 64 && w->shape[3] == 8) {
+    D = w->shape[0] * 32;
+    H = w->shape[1] * 16;
+    return true;
+  }
+  return false;
+}
+}  // namespace
 
 extern "C" int rlm_relation_reduce_fused_seq_fits(const rlm_tensor* expanded_cache,
                                                   const rlm_tensor* operand_cache,
@@ -652,12 +675,14 @@ extern "C" int rlm_relation_reduce_fused_seq_fits(const rlm_tensor* expanded_cac
                               second_weight})
     if (t == nullptr) return 0;
   if (operand_cache->ndim != 3 || expanded_cache->ndim != 3 || partner_index->ndim != 3 ||
-      product_weight->ndim != 2 || second_weight->ndim != 2)
+      product_weight->ndim != 2)
     return 0;
   for (const rlm_tensor* t : {expanded_cache, operand_cache, product_weight, second_weight})
     if (t->dtype != RLM_BF16) return 0;
   const int64_t R = operand_cache->shape[2], H = product_weight->shape[0];
-  const int64_t D = second_weight->shape[0], K = partner_index->shape[2];
+  int64_t D, H2;
+  if (!second_weight_dims(second_weight, D, H2) || H2 != H) return 0;
+  const int64_t K = partner_index->shape[2];
   if (K < 1 || K > 16 || !(R == 32 || R == 64 || R == 128) || H <= 0 || H % kHC != 0) return 0;
   if (!(D == 128 || D == 256 || D == 384 || D == 512)) return 0;
   for (const rlm_tensor* t : {operand_cache, product_weight, second_weight})
@@ -676,19 +701,24 @@ extern "C" hipError_t rlm_relation_reduce_fused_seq(
   RLM_TRY(check_tensor(operand_cache, "operand_cache", 3));
   RLM_TRY(check_tensor(expanded_cache, "expanded_cache", 3));
   RLM_TRY(check_tensor(product_weight, "product_weight", 2));
-  RLM_TRY(check_tensor(second_weight, "second_weight", 2));
+  RLM_REQUIRE(second_weight != nullptr, "second_weight: missing tensor");
+  const bool frag = second_weight->ndim == 4;
+  RLM_TRY(check_tensor(second_weight, "second_weight", frag ? 4 : 2));
   RLM_TRY(check_dtype_is(operand_cache, "operand_cache", RLM_BF16));
   RLM_TRY(check_dtype_is(expanded_cache, "expanded_cache", RLM_BF16));
   RLM_TRY(check_dtype_is(product_weight, "product_weight", RLM_BF16));
   RLM_TRY(check_dtype_is(second_weight, "second_weight", RLM_BF16));
   const int64_t B = operand_cache->shape[0], T = operand_cache->shape[1];
   const int64_t R = operand_cache->shape[2], H = product_weight->shape[0];
-  const int64_t D = second_weight->shape[0];
+  int64_t D, H2;
+  RLM_REQUIRE(second_weight_dims(second_weight, D, H2),
+              "second_weight must be [D, H] or in MFMA fragment order [D/32, H/16, 64, 8]");
   RLM_TRY(check_dim(product_weight, "product_weight", 1, R));
   RLM_TRY(check_dim(expanded_cache, "expanded_cache", 0, B));
   RLM_TRY(check_dim(expanded_cache, "expanded_cache", 1, T));
   RLM_TRY(check_dim(expanded_cache, "expanded_cache", 2, 2 * H));
-  RLM_TRY(check_dim(second_weight, "second_weight", 1, H));
+  RLM_REQUIRE(H2 == H, "second_weight is for hidden dim %lld, product_weight has %lld",
+              (long long)H2, (long long)H);
   RLM_TRY(check_tensor(anchor_index, "anchor_index", 2));
   RLM_TRY(check_tensor(partner_index, "partner_index", 3));
   RLM_REQUIRE(is_index_dtype(anchor_index->dtype) && is_index_dtype(partner_index->dtype),
@@ -785,17 +815,20 @@ extern "C" hipError_t rlm_relation_reduce_fused_seq(
   p.w2_bytes = static_cast<uint32_t>(D * H * 2);
   if (p.rows == 0) return hipSuccess;
   const int ks1 = static_cast<int>(R / 32);
-#define RLM_FUSED_CASE(DT)                                          \
-  if (D == 128 * DT) {                                              \
-    if (ks1 == 1) return launch_fused<DT, 1>(p, stream);            \
-    if (ks1 == 2) return launch_fused<DT, 2>(p, stream);            \
-    return launch_fused<DT, 4>(p, stream);                          \
+#define RLM_FUSED_KS(DT, KS)                                                      \
+  return frag ? launch_fused<DT, KS, true>(p, stream) : launch_fused<DT, KS, false>(p, stream);
+#define RLM_FUSED_CASE(DT)           \
+  if (D == 128 * DT) {               \
+    if (ks1 == 1) RLM_FUSED_KS(DT, 1) \
+    if (ks1 == 2) RLM_FUSED_KS(DT, 2) \
+    RLM_FUSED_KS(DT, 4)              \
   }
   RLM_FUSED_CASE(1)
   RLM_FUSED_CASE(2)
   RLM_FUSED_CASE(3)
   RLM_FUSED_CASE(4)
 #undef RLM_FUSED_CASE
+#undef RLM_FUSED_KS
   set_error("fused relation reduce supports d_model in {128, 256, 384, 512} (a wave keeps "
             "[128, d_model/8] accumulators in registers), got %lld; use the unfused "
             "relation_hidden_cached_seq / relation_linear / relation_norm_reduce_seq chain",

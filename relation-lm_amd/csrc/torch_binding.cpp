@@ -778,8 +778,11 @@ at::Tensor relation_reduce_fused_seq(const at::Tensor& expanded_cache,
   hipStream_t stream = device_stream(
       op, {&operand_cache, &expanded_cache, &anchor_index, &partner_index, &product_weight,
            &second_weight, &second_bias, &partner_scores, &norm_weight, &norm_bias, &positions});
-  TORCH_CHECK(partner_index.dim() == 3 && second_weight.dim() == 2, op,
-              ": partner_index must be [B,Tq,K] and second_weight [D,H]");
+  const bool frag = second_weight.dim() == 4;
+  TORCH_CHECK(partner_index.dim() == 3 && (second_weight.dim() == 2 || frag), op,
+              ": partner_index must be [B,Tq,K] and second_weight [D,H] or in MFMA fragment "
+              "order [D/32,H/16,64,8]");
+  const int64_t d_model = frag ? second_weight.size(0) * 32 : second_weight.size(0);
   {
     const rlm_tensor e = desc(expanded_cache, "expanded_cache");
     const rlm_tensor o = desc(operand_cache, "operand_cache");
@@ -787,6 +790,9 @@ at::Tensor relation_reduce_fused_seq(const at::Tensor& expanded_cache,
     const rlm_tensor wm = desc(product_weight, "product_weight");
     const rlm_tensor w2 = desc(second_weight, "second_weight");
     if (!rlm_relation_reduce_fused_seq_fits(&e, &o, &pi, &wm, &w2)) {
+      TORCH_CHECK(!frag, op, ": a second_weight in fragment order needs the fused kernel's "
+                  "shapes (bf16, d_model 128/256/384/512, K <= 16, relation dim 32/64/128); "
+                  "pass the [D,H] weight for other shapes");
       // Shapes or dtypes the fused kernel does not take (fp32, d_model 576, ...):
       // the same result from the three-op chain it fuses, every step on HIP.
       const at::Tensor hidden = relation_hidden_cached_seq(expanded_cache, operand_cache,
@@ -797,7 +803,7 @@ at::Tensor relation_reduce_fused_seq(const at::Tensor& expanded_cache,
                                       norm_eps);
     }
   }
-  at::Tensor out = at::empty({partner_index.size(0), partner_index.size(1), second_weight.size(0)},
+  at::Tensor out = at::empty({partner_index.size(0), partner_index.size(1), d_model},
                              f32(operand_cache));
   rlm_tensor d[12] = {desc(expanded_cache, "expanded_cache"), desc(operand_cache, "operand_cache"),
                       desc(anchor_index, "anchor_index"), desc(partner_index, "partner_index"),

@@ -112,7 +112,8 @@ def _register_fakes() -> None:
     @torch.library.register_fake("relation_lm::relation_reduce_fused_seq")
     def _(expanded_cache, operand_cache, anchor_index, partner_index, product_weight,
           second_weight, *rest):
-        return operand_cache.new_empty(tuple(partner_index.shape[:2]) + (second_weight.shape[0],),
+        d_model = second_weight.shape[0] * (32 if second_weight.dim() == 4 else 1)
+        return operand_cache.new_empty(tuple(partner_index.shape[:2]) + (d_model,),
                                        dtype=torch.float32)
 
     @torch.library.register_fake("relation_lm::packed_projection_to_caches")

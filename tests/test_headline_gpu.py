@@ -22,7 +22,8 @@ import torch
 
 from oracle import reduce as ored
 from oracle import select as osel
-from relation_lm.kernels.relation_reduce import relation_linear, relation_reduce_fused_seq
+from relation_lm.kernels.relation_reduce import (mfma_fragments, relation_linear,
+                                                 relation_reduce_fused_seq)
 from relation_lm.kernels.relation_select import relation_select_packed_seq
 from relation_lm.workloads import (
     CONFIGS,
@@ -83,7 +84,7 @@ def test_cfg2_headline_step_every_query(device):
     expanded = relation_linear(red["operand_cache"], red["expanded_weight"], red["expanded_bias"])
     a, s, p, ps = relation_select_packed_seq(*select_args(sel, cfg))
     ctx = relation_reduce_fused_seq(expanded, red["operand_cache"], a, p, red["product_weight"],
-                                    red["second_weight"], red["second_bias"], ps,
+                                    mfma_fragments(red["second_weight"]), red["second_bias"], ps,
                                     red["norm_weight"], red["norm_bias"], positions, 1e-5)
     torch.cuda.synchronize()
 
@@ -113,7 +114,8 @@ def test_cfg4_fused_reduce_every_query(device):
     expanded = relation_linear(red["operand_cache"], red["expanded_weight"], red["expanded_bias"])
     ctx = relation_reduce_fused_seq(expanded, red["operand_cache"], anchor.to(device),
                                     partner.to(device), red["product_weight"],
-                                    red["second_weight"], red["second_bias"], scores.to(device),
+                                    mfma_fragments(red["second_weight"]), red["second_bias"],
+                                    scores.to(device),
                                     red["norm_weight"], red["norm_bias"], pos.to(device), 1e-5)
     torch.cuda.synchronize()
     expected = oracle_reduce_chain(host(expanded).astype(np.float64), red, host(anchor),

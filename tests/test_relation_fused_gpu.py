@@ -18,6 +18,7 @@ import torch
 
 from oracle import reduce as ored
 from relation_lm.kernels.relation_reduce import (
+    mfma_fragments,
     relation_hidden_cached_seq,
     relation_linear,
     relation_norm_reduce_seq,
@@ -139,6 +140,42 @@ def test_fused_batched_positions_and_ragged_rows(device):
     torch.cuda.synchronize()
     assert fused.shape == (3, 37, 512)
     assert abs_err(host(fused), host(unfused)) <= TIGHT_ABS
+
+
+@pytest.mark.parametrize("d_model,relation_dim,k_out", [(512, 128, 8), (384, 64, 5),
+                                                        (256, 32, 16), (128, 128, 1)])
+def test_fragment_order_second_weight_same_bits(device, d_model, relation_dim, k_out):
+    """second_weight in MFMA fragment order (mfma_fragments) reads the same fragments from
+    contiguous memory: the output equals the [D, H] weight's bit for bit."""
+    cfg = RelationConfig("frag", 2, 96, d_model, 32, 64, 2, k_out, torch.bfloat16,
+                         relation_dim=relation_dim, hidden_dim=256, seed=99 + d_model)
+    red = reduce_inputs(cfg, device=device)
+    expanded = relation_linear(red["operand_cache"], red["expanded_weight"], red["expanded_bias"])
+    anchor, partner, scores, pos = indices_and_scores(2, 96, 96, k_out, seed=17)
+    plain = run_fused(red, expanded, anchor, partner, scores, pos, device)
+    frag = relation_reduce_fused_seq(expanded, red["operand_cache"], anchor.to(device),
+                                     partner.to(device), red["product_weight"],
+                                     mfma_fragments(red["second_weight"]), red["second_bias"],
+                                     scores.to(device), red["norm_weight"], red["norm_bias"],
+                                     pos.to(device), 1e-5)
+    torch.cuda.synchronize()
+    assert frag.shape == plain.shape
+    assert torch.equal(frag, plain)
+
+
+def test_fragment_order_outside_the_kernel_raises(device):
+    # d_model 576: the three-op chain needs the [D, H] weight.
+    cfg = RelationConfig("frag", 1, 64, 576, 32, 64, 2, 4, torch.bfloat16, relation_dim=128,
+                         hidden_dim=256, seed=5)
+    red = reduce_inputs(cfg, device=device)
+    expanded = relation_linear(red["operand_cache"], red["expanded_weight"], red["expanded_bias"])
+    anchor, partner, scores, pos = indices_and_scores(1, 64, 64, 4, seed=2)
+    with pytest.raises(RuntimeError, match="fragment order needs the fused kernel"):
+        relation_reduce_fused_seq(expanded, red["operand_cache"], anchor.to(device),
+                                  partner.to(device), red["product_weight"],
+                                  mfma_fragments(red["second_weight"]), red["second_bias"],
+                                  scores.to(device), red["norm_weight"], red["norm_bias"],
+                                  pos.to(device), 1e-5)
 
 
 def test_fused_op_runs_the_chain_outside_the_kernel_bf16(device):
