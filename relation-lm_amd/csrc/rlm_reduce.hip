@@ -852,27 +852,20 @@ __global__ void __launch_bounds__(kMlpThreads) relation_mlp_kernel(const MlpPara
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[j][i][e] = 0.0f;
 
-  for (int c = 0; c < nchunks; ++c) {
-    unsigned char* hb = hid + (c & 1) * (kMlpRows * kMlpHidRow);
-    // ---- Phase 1: hidden^T block (columns 32 j1.., rows 32 i1..) of chunk c.
-    f32x16 hacc;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) hacc[e] = 0.0f;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      const int off = prod_off + (((2 * kk + (lane >> 5)) ^ swz) << 4);
-      const u16x8 fh = *reinterpret_cast<const u16x8*>(p_hi + off);
-      const u16x8 fl = *reinterpret_cast<const u16x8*>(p_lo + off);
-      hacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fwm[kk]),
-                                                     __builtin_bit_cast(bf16x8, fh), hacc, 0, 0, 0);
-      hacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fwm[kk]),
-                                                     __builtin_bit_cast(bf16x8, fl), hacc, 0, 0, 0);
-    }
-    if (c + 1 < nchunks) load_wm(c + 1);
-    u16x8 wq[K2][TNB];
-#pragma unroll
-    for (int s = 0; s < kMlpW2Ahead; ++s) load_w2(wq[s], c * K2 + s);
-    // hacc: lane holds hidden^T[column 8q + 4 (lane >> 5) + e][row lane & 31].
+  // Phase 1 of a chunk, one k-step: hidden^T block (columns 32 j1.., rows
+  // 32 i1..) += W_m fragment kk . product fragments (hi, then lo).
+  auto p1_step = [&](f32x16& hacc, int kk) {
+    const int off = prod_off + (((2 * kk + (lane >> 5)) ^ swz) << 4);
+    const u16x8 fh = *reinterpret_cast<const u16x8*>(p_hi + off);
+    const u16x8 fl = *reinterpret_cast<const u16x8*>(p_lo + off);
+    hacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fwm[kk]),
+                                                   __builtin_bit_cast(bf16x8, fh), hacc, 0, 0, 0);
+    hacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fwm[kk]),
+                                                   __builtin_bit_cast(bf16x8, fl), hacc, 0, 0, 0);
+  };
+  // Its epilogue: + expanded-cache halves (xa / xp), GELU, bf16 into hidden
+  // buffer hb.  hacc: lane holds hidden^T[column 8q + 4 (lane >> 5) + e][row lane & 31].
+  auto p1_epilogue = [&](const f32x16& hacc, unsigned char* hb) {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       *reinterpret_cast<float4*>(stage + (lane & 31) * kMlpStageRow + (8 * q + 4 * (lane >> 5)) * 4) =
@@ -894,10 +887,36 @@ __global__ void __launch_bounds__(kMlpThreads) relation_mlp_kernel(const MlpPara
       }
       put8<bf16>(reinterpret_cast<bf16*>(hb + (32 * i1 + row) * kMlpHidRow + (32 * j1 + c8) * 2), v);
     }
-    wave_sync();  // the staging is read before the next chunk writes it
-    if (c + 1 < nchunks) load_x(c + 1);
-    __syncthreads();  // hidden chunk c complete
-    // ---- Phase 2: raw^T += W2[:, chunk c] . hidden chunk^T.
+    wave_sync();  // the staging is read before it is written again
+  };
+
+  // Prologue: chunk 0's hidden, then the first W2 k-groups of chunk 0.
+  u16x8 wq[K2][TNB];
+  {
+    f32x16 hacc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) hacc[e] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) p1_step(hacc, kk);
+    if (nchunks > 1) load_wm(1);
+#pragma unroll
+    for (int s = 0; s < kMlpW2Ahead; ++s) load_w2(wq[s], s);
+    p1_epilogue(hacc, hid);
+    if (nchunks > 1) load_x(1);
+  }
+  __syncthreads();  // hidden chunk 0 complete
+
+  // Iteration c: phase 2 of chunk c with phase 1's matrix work for chunk c + 1
+  // interleaved (one k-step per k-group: independent of phase 2, it fills the
+  // matrix pipeline around phase 2's products), then chunk c + 1's epilogue into
+  // the other hidden buffer.  The last iteration's phase-1 products are
+  // discarded (no branch in the k-loop).
+  for (int c = 0; c < nchunks; ++c) {
+    unsigned char* hb = hid + (c & 1) * (kMlpRows * kMlpHidRow);
+    unsigned char* hn = hid + ((c + 1) & 1) * (kMlpRows * kMlpHidRow);
+    f32x16 hacc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) hacc[e] = 0.0f;
 #pragma unroll
     for (int s = 0; s < K2; ++s) {
       if (s + kMlpW2Ahead < K2) load_w2(wq[s + kMlpW2Ahead], c * K2 + s + kMlpW2Ahead);
@@ -911,7 +930,16 @@ __global__ void __launch_bounds__(kMlpThreads) relation_mlp_kernel(const MlpPara
         for (int i = 0; i < 2; ++i)
           acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
               __builtin_bit_cast(bf16x8, wq[s][j]), __builtin_bit_cast(bf16x8, fa[i]), acc[j][i], 0, 0, 0);
+      if (s < KK) p1_step(hacc, s);
     }
+    if (c + 1 < nchunks) {  // uniform
+      if (c + 2 < nchunks) load_wm(c + 2);
+#pragma unroll
+      for (int s = 0; s < kMlpW2Ahead; ++s) load_w2(wq[s], (c + 1) * K2 + s);
+      p1_epilogue(hacc, hn);
+      if (c + 2 < nchunks) load_x(c + 2);
+    }
+    __syncthreads();  // phase 2 of chunk c read; hidden chunk c + 1 complete
   }
 
   // ---- Output: acc[j][i] holds raw[row 32i + (lane & 31)][columns dw0 + 32j +
