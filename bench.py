@@ -62,7 +62,7 @@ KERNEL_SYMBOLS = {
     "expanded_projection": "smallk_kernel<rlm::bf16, rlm::bf16, rlm::bf16",
     "relation_select": "select_tile_kernel<",
     "relation_reduce_fused": "fused_reduce_kernel<",
-    "relation_hidden": "hidden_bf16_kernel<",
+    "relation_hidden": "hidden_tile_kernel<",
     "second_linear": "tile_kernel<float, rlm::bf16, float",
     "norm_reduce": "norm_reduce_vec_kernel<",
     "multi_anchor_select": "multi_tile_kernel<",
