@@ -310,7 +310,9 @@ __device__ __forceinline__ uint64_t member_key(const MultiTileParams& p, const M
 #pragma unroll 1
   for (int ch = 0; ch < 2; ++ch) {
     const int chunk = 2 * sub + ch;
-    const uint32_t w[4] = {kv[ch].x, kv[ch].y, kv[ch].z, kv[ch].w};
+    // A select, not kv[ch]: a runtime index would put the array in scratch memory.
+    const uint4 kc = ch == 0 ? kv[0] : kv[1];
+    const uint32_t w[4] = {kc.x, kc.y, kc.z, kc.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const double2 q2 = *reinterpret_cast<const double2*>(qrow + 8 * chunk + 2 * e);
@@ -369,9 +371,12 @@ __device__ int exact_select(const MultiTileParams& p, const MLds& L, int qi, int
   const MRec& R = L.qr[qi];
   const int t = R.t, ls = R.ls;
   const int nex = R.nact;
+  // The query's taken anchors, wave-uniform (scalar registers); slots past nex
+  // hold -1, which no valid candidate position equals.
   int excl[kMultiTileMaxSlots];
 #pragma unroll
-  for (int x = 0; x < kMultiTileMaxSlots; ++x) excl[x] = x < nex ? R.taken[x] : -1;
+  for (int x = 0; x < kMultiTileMaxSlots; ++x)
+    excl[x] = __builtin_amdgcn_readfirstlane(x < nex ? R.taken[x] : -1);
   const int K = ANCHOR ? 1 : p.K;
   const float* sc = L.sc + qi * sc_row(p.CAP);
   // Candidate lane c: valid, not excluded, and its approximate score.  The
@@ -381,11 +386,9 @@ __device__ int exact_select(const MultiTileParams& p, const MLds& L, int qi, int
     const int pk = R.pick[!local && c < p.CAP ? (c - p.L) >> p.BS_log2 : 0];
     const int pos = local ? t - p.L + 1 + c : pk * p.BS + ((c - p.L) & (p.BS - 1));
     v = c < p.CAP && pos <= t && pos < p.T && (local ? pos >= 0 : (pk >= 0 && pos < ls));
+    // Every slot compared (no early exit): the array stays in registers.
 #pragma unroll
-    for (int x = 0; x < kMultiTileMaxSlots; ++x) {
-      if (x >= nex) break;  // uniform
-      v = v && pos != excl[x];
-    }
+    for (int x = 0; x < kMultiTileMaxSlots; ++x) v = v && pos != excl[x];
     return sc[c < p.CAP ? c : p.CAP];
   };
   float lm = -INFINITY;
