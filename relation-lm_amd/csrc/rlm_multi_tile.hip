@@ -64,9 +64,12 @@ struct MRec {
 
 struct MLds {
   float* stats;       // [mean, std][NB][kMStatRow] fp32 of the current side
-  float* sc;          // [16][sc_row(CAP)]: s~ of each query's candidate lanes, entry CAP
-                      // a trash slot for branch-free stores (aliases sh)
-  double* sh;         // [H][16][NB]: per-head block scores
+  // Region q (q_bytes from sc) belongs to query q: first its per-head block
+  // scores sh [H][NB] (float64), then, from its block picks on, its candidate
+  // list sc: s~ of each candidate lane, -inf for lanes that are not a candidate
+  // or are excluded, entry CAP a trash slot for branch-free stores.
+  float* sc;
+  double* sh;
   uint64_t* blk;      // [16][NB]: block selection keys
   signed char* rank;  // [16][NB]: pick rank of block j, -1 if not a valid pick
   double* rq;         // [16][kMQRow]: router query, float64
@@ -199,7 +202,7 @@ __device__ void head_scores(const MultiTileParams& p, const MLds& L, int side, i
         const double c = content[r] + sp[h] * unc[r];
         v = c * p.head_scale + bias[h * p.RB + bucket];
       }
-      if (j < p.NB) L.sh[(h * kMQ + q) * p.NB + j] = v;
+      if (j < p.NB) L.sh[q * (p.q_bytes >> 3) + h * p.NB + j] = v;
     }
   }
 }
@@ -219,13 +222,13 @@ __device__ void block_picks(const MultiTileParams& p, const MLds& L, int qi, int
     // time: s0..s2 hold the pending left halves of the tree (H a power of two).
     const int j = lane;
     const bool live = j < p.NB;
-    const double* shj = L.sh + qi * p.NB + (live ? j : 0);
+    const double* shj = L.sh + qi * (p.q_bytes >> 3) + (live ? j : 0);
     double m = -INFINITY;
-    for (int h = 0; h < p.H; ++h) m = fmax(m, shj[h * kMQ * p.NB]);
+    for (int h = 0; h < p.H; ++h) m = fmax(m, shj[h * p.NB]);
     double s0 = 0.0, s1 = 0.0, s2 = 0.0, sum = 0.0;
 #pragma unroll 1
     for (int h = 0; h < p.H; ++h) {
-      double x = exp(shj[h * kMQ * p.NB] - m);
+      double x = exp(shj[h * p.NB] - m);
       if (h & 1) {
         x = s0 + x;
         if (h & 2) {
@@ -267,6 +270,17 @@ __device__ void block_picks(const MultiTileParams& p, const MLds& L, int qi, int
   const uint64_t picks = __builtin_amdgcn_ballot_w64(valid);
   if (lane == 0) R.picks = picks;
   wave_sync();
+}
+
+// Query qi's candidate list to -inf (the tile walk then files every candidate
+// of the routing; a lane it does not file is not a candidate).  The list takes
+// over the region of the query's per-head block scores, which only this wave's
+// block_picks reads.
+__device__ __forceinline__ void clear_list(const MultiTileParams& p, const MLds& L, int qi,
+                                           int lane) {
+  float4* row = reinterpret_cast<float4*>(L.sc + qi * (p.q_bytes >> 2));
+  const float4 ninf = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+  for (int i = lane; i < (p.q_bytes >> 4); i += kWave) row[i] = ninf;
 }
 
 // Position and validity of candidate lane c (relation_select.py:244-284):
@@ -370,34 +384,39 @@ __device__ int exact_select(const MultiTileParams& p, const MLds& L, int qi, int
                             int s, int64_t orow) {
   const MRec& R = L.qr[qi];
   const int t = R.t, ls = R.ls;
-  const int nex = R.nact;
-  // The query's taken anchors, wave-uniform (scalar registers); slots past nex
-  // hold -1, which no valid candidate position equals.
-  int excl[kMultiTileMaxSlots];
-#pragma unroll
-  for (int x = 0; x < kMultiTileMaxSlots; ++x)
-    excl[x] = __builtin_amdgcn_readfirstlane(x < nex ? R.taken[x] : -1);
   const int K = ANCHOR ? 1 : p.K;
-  const float* sc = L.sc + qi * sc_row(p.CAP);
-  // Candidate lane c: valid, not excluded, and its approximate score.  The
-  // passes below stream over the lanes (nothing per candidate is held).
-  auto candidate_score = [&](int c, bool& v) {
-    const bool local = c < p.L;
-    const int pk = R.pick[!local && c < p.CAP ? (c - p.L) >> p.BS_log2 : 0];
-    const int pos = local ? t - p.L + 1 + c : pk * p.BS + ((c - p.L) & (p.BS - 1));
-    v = c < p.CAP && pos <= t && pos < p.T && (local ? pos >= 0 : (pk >= 0 && pos < ls));
-    // Every slot compared (no early exit): the array stays in registers.
-#pragma unroll
-    for (int x = 0; x < kMultiTileMaxSlots; ++x) v = v && pos != excl[x];
-    return sc[c < p.CAP ? c : p.CAP];
+  float* sc = L.sc + qi * (p.q_bytes >> 2);
+  // The query's anchors so far are not candidates: lane x < nact puts -inf in
+  // the lane of anchor x, if it is a candidate of this routing (local window,
+  // else its block's pick).  Anchors are at most t.
+  if (lane < R.nact) {
+    const int pos = R.taken[lane];
+    int c = -1;
+    if (pos >= ls) {
+      c = pos - (t - p.L + 1);
+    } else {
+      const int r = L.rank[qi * p.NB + (pos >> p.BS_log2)];
+      if (r >= 0) c = p.L + r * p.BS + (pos & (p.BS - 1));
+    }
+    if (c >= 0) sc[c] = -INFINITY;
+  }
+  wave_sync();
+  // The list in quads: lane l reads candidates 256 j + 4 l + e (e < 4); those
+  // past CAP (the trash slot, padding) read -inf.
+  const int nquad = (p.CAP + 255) >> 8;
+  auto quad = [&](int j, float (&x)[4]) {
+    const int c = 256 * j + 4 * lane;
+    const float4 v = *reinterpret_cast<const float4*>(sc + (c < p.CAP ? c : 0));
+    x[0] = c < p.CAP ? v.x : -INFINITY;
+    x[1] = c + 1 < p.CAP ? v.y : -INFINITY;
+    x[2] = c + 2 < p.CAP ? v.z : -INFINITY;
+    x[3] = c + 3 < p.CAP ? v.w : -INFINITY;
   };
   float lm = -INFINITY;
-  uint32_t vmask = 0;  // bit i: candidate lane + 64 i is valid
-  for (int c0 = 0, i = 0; c0 < p.CAP; c0 += kWave, ++i) {
-    bool v;
-    const float x = candidate_score(c0 + lane, v);
-    lm = v ? fmaxf(lm, x) : lm;
-    vmask |= v ? 1u << i : 0u;
+  for (int j = 0; j < nquad; ++j) {
+    float x[4];
+    quad(j, x);
+    lm = fmaxf(fmaxf(lm, fmaxf(x[0], x[1])), fmaxf(x[2], x[3]));
   }
   // theta: a lower bound of the k-th largest approximate score.
   float theta;
@@ -418,22 +437,35 @@ __device__ int exact_select(const MultiTileParams& p, const MLds& L, int qi, int
   }
   const float eps = kErrScale * qn1 * kmax;
   const float thr = theta - (2.0f * eps + kErrAbs);
-  // Members (valid candidates with s~ >= thr) numbered in candidate order;
-  // those of window [lo, lo + 64) go to the list (others to its trash entry).
+  // Members (candidates with s~ >= thr) numbered in candidate order; those of
+  // window [lo, lo + 64) go to the list (others to its trash entry).
   uint64_t* list = L.list + qi * kMListRow;
   auto list_members = [&](int lo) {
     int n = 0;
-    for (int c0 = 0, i = 0; c0 < p.CAP; c0 += kWave, ++i) {
-      const int c = c0 + lane;
-      const float x = sc[c < p.CAP ? c : p.CAP];
-      const bool mem = ((vmask >> i) & 1u) && x > -INFINITY && x >= thr;
-      const uint64_t bal = __builtin_amdgcn_ballot_w64(mem);
-      const int mi = n + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
-                             static_cast<uint32_t>(bal >> 32),
-                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u)));
-      list[mem && mi >= lo && mi < lo + kMListCap ? mi - lo : kMListCap] =
-          static_cast<uint64_t>(c0 + lane);
-      n += __builtin_popcountll(bal);
+    for (int j = 0; j < nquad; ++j) {
+      float x[4];
+      quad(j, x);
+      bool mem[4];
+      uint64_t bal[4];
+      int mi = n, tot = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        mem[e] = x[e] > -INFINITY && x[e] >= thr;
+        bal[e] = __builtin_amdgcn_ballot_w64(mem[e]);
+        mi += static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+            static_cast<uint32_t>(bal[e] >> 32),
+            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal[e]), 0u)));
+        tot += __builtin_popcountll(bal[e]);
+      }
+      // mi: members in the lanes below; then this lane's, in e order.
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (bal[e] != 0)  // uniform
+          list[mem[e] && mi >= lo && mi < lo + kMListCap ? mi - lo : kMListCap] =
+              static_cast<uint64_t>(256 * j + 4 * lane + e);
+        mi += mem[e];
+      }
+      n += tot;
     }
     return n;
   };
@@ -553,7 +585,7 @@ __device__ uint32_t score_tiles(const MultiTileParams& p, const MLds& L, rsrc_t 
   const int tq = R.on ? R.t : -1;  // no candidates when the routing is off
   const int lq = R.ls;
   const signed char* rank = L.rank + c16 * p.NB;
-  float* sc = L.sc + c16 * sc_row(p.CAP);
+  float* sc = L.sc + c16 * (p.q_bytes >> 2);
   u16x2_t km = {0, 0};
   const int ntiles = (u.hi + 16) >> 4;
   // kTB tiles per round: every key load of the round is issued before the
@@ -652,7 +684,10 @@ __global__ void __launch_bounds__(kMThreads) multi_tile_kernel(const MultiTilePa
   __syncthreads();
   head_scores(p, L, 0, wave, lane);
   __syncthreads();
-  for (int h = 0; h < kMQ / kMWaves; ++h) block_picks(p, L, wave + kMWaves * h, lane);
+  for (int h = 0; h < kMQ / kMWaves; ++h) {
+    block_picks(p, L, wave + kMWaves * h, lane);
+    clear_list(p, L, wave + kMWaves * h, lane);  // the anchor slots share one candidate set
+  }
   __syncthreads();
 
   // ---- Anchor slots: distinct argmaxes over the one candidate set. ----
@@ -715,7 +750,10 @@ __global__ void __launch_bounds__(kMThreads) multi_tile_kernel(const MultiTilePa
     __syncthreads();  // query rows, statistics; previous slot's lists done
     head_scores(p, L, 1, wave, lane);
     __syncthreads();
-    for (int h = 0; h < kMQ / kMWaves; ++h) block_picks(p, L, wave + kMWaves * h, lane);
+    for (int h = 0; h < kMQ / kMWaves; ++h) {
+      block_picks(p, L, wave + kMWaves * h, lane);
+      clear_list(p, L, wave + kMWaves * h, lane);
+    }
     __syncthreads();
     uint4 ah0, al0, ah1, al1;
     {
@@ -760,9 +798,11 @@ bool multi_tile_layout(MultiTileParams& p) {
     return o;
   };
   p.off_stats = take(2 * p.NB * kMStatRow * 4);
-  const int sc_bytes = kMQ * sc_row(p.CAP) * 4;
-  const int sh_bytes = p.H * kMQ * p.NB * 8;
-  p.off_sc = take(sc_bytes > sh_bytes ? sc_bytes : sh_bytes);  // per-head scores alias the lists
+  // Per query: its per-head block scores, then its candidate list.
+  const int sc_bytes = sc_row(p.CAP) * 4;
+  const int sh_bytes = p.H * p.NB * 8;
+  p.q_bytes = ((sc_bytes > sh_bytes ? sc_bytes : sh_bytes) + 15) & ~15;
+  p.off_sc = take(kMQ * p.q_bytes);
   p.off_blk = take(kMQ * p.NB * 8);
   p.off_rank = take(kMQ * p.NB);
   p.off_rq = take(kMQ * kMQRow * 8);

@@ -46,6 +46,8 @@ struct MultiTileParams {
   int tiles;  // workgroups per batch row
   int off_stats, off_sc, off_blk, off_rank, off_rq, off_eq, off_list, off_top, off_qrec,
       off_bias, off_sp, off_kmax, lds_total;
+  int q_bytes;  // LDS bytes per query of the region that holds its per-head block
+                // scores, then its candidate score list
 };
 
 // Fills the LDS layout; false when it exceeds one CU's 160 KiB.
