@@ -70,7 +70,6 @@ struct MLds {
   // or are excluded, entry CAP a trash slot for branch-free stores.
   float* sc;
   double* sh;
-  uint64_t* blk;      // [16][NB]: block selection keys
   signed char* rank;  // [16][NB]: pick rank of block j, -1 if not a valid pick
   double* rq;         // [16][kMQRow]: router query, float64
   double* eq;         // [16][kMQRow]: exact query, float64
@@ -90,7 +89,6 @@ __device__ __forceinline__ MLds carve(const MultiTileParams& p, unsigned char* s
   s.stats = reinterpret_cast<float*>(smem + p.off_stats);
   s.sc = reinterpret_cast<float*>(smem + p.off_sc);
   s.sh = reinterpret_cast<double*>(smem + p.off_sc);
-  s.blk = reinterpret_cast<uint64_t*>(smem + p.off_blk);
   s.rank = reinterpret_cast<signed char*>(smem + p.off_rank);
   s.rq = reinterpret_cast<double*>(smem + p.off_rq);
   s.eq = reinterpret_cast<double*>(smem + p.off_eq);
@@ -215,13 +213,13 @@ __device__ void head_scores(const MultiTileParams& p, const MLds& L, int side, i
 __device__ void block_picks(const MultiTileParams& p, const MLds& L, int qi, int lane) {
   MRec& R = L.qr[qi];
   const int t = R.t, ls = R.ls;
-  uint64_t* row = L.blk + qi * p.NB;
+  const int j = lane;
+  const bool live = j < p.NB;
+  uint64_t kj = 0;  // lane j's block key; 0 (below every block's key) past the blocks
   {
     // Lane j: block j's heads, summed pairwise (((h0 + h1) + (h2 + h3)) + ...),
     // the order of a lane-group tree reduction over the heads.  One exp at a
     // time: s0..s2 hold the pending left halves of the tree (H a power of two).
-    const int j = lane;
-    const bool live = j < p.NB;
     const double* shj = L.sh + qi * (p.q_bytes >> 3) + (live ? j : 0);
     double m = -INFINITY;
     for (int h = 0; h < p.H; ++h) m = fmax(m, shj[h * p.NB]);
@@ -247,25 +245,37 @@ __device__ void block_picks(const MultiTileParams& p, const MLds& L, int qi, int
       const double lse = m + log(sum);
       const int end = (j + 1) * p.BS - 1;
       const bool eligible = end <= t && (!p.strict || end < ls);
-      row[j] = select_key(eligible ? static_cast<float>(lse) : -INFINITY, static_cast<uint32_t>(j));
+      kj = select_key(eligible ? static_cast<float>(lse) : -INFINITY, static_cast<uint32_t>(j));
     }
   }
   if (lane < p.TOP) R.pick[lane] = -1;
-  wave_sync();
-  const int j = lane;
-  const bool live = j < p.NB;
-  const uint64_t kj = live ? row[j] : 0;
-  int rank = kWave;
-  if (live) {
-    rank = 0;
-    for (int k = 0; k < p.NB; k += 2) {
-      const uint4 o = *reinterpret_cast<const uint4*>(row + k);
-      rank += ((static_cast<uint64_t>(o.y) << 32) | o.x) > kj;
-      rank += ((static_cast<uint64_t>(o.w) << 32) | o.z) > kj;
-    }
+  // The TOP largest keys.  T: the TOP-th largest score half over the blocks
+  // (0 when there are fewer than TOP blocks), bit by bit from the top; then
+  // every block scoring above T and the lowest blocks scoring T.
+  const uint32_t sk = static_cast<uint32_t>(kj >> 32);
+  uint32_t T = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = T | (1u << bit);
+    if (__builtin_popcountll(__builtin_amdgcn_ballot_w64(live && sk >= cand)) >= p.TOP) T = cand;
   }
-  const bool valid = live && rank < p.TOP && key_score(kj) > -1.0e30f && R.on != 0;
-  if (live && rank < p.TOP) R.pick[rank] = key_score(kj) > -1.0e30f ? j : -1;
+  const uint64_t at_t = __builtin_amdgcn_ballot_w64(live && sk == T);
+  const int above = __builtin_popcountll(__builtin_amdgcn_ballot_w64(live && sk > T));
+  const int below_t = static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+      static_cast<uint32_t>(at_t >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(at_t), 0u)));
+  const bool sel = live && (sk > T || (sk == T && below_t < p.TOP - above));
+  // Pick rank of a selected block: #{k : key_k > key_j}; every such k is
+  // selected, so the selected keys (read lane by lane) are all it compares.
+  int rank = 0;
+  for (uint64_t rest = __builtin_amdgcn_ballot_w64(sel); rest != 0; rest &= rest - 1) {
+    const int k = static_cast<int>(__builtin_ctzll(rest));
+    const uint64_t kk =
+        (static_cast<uint64_t>(__builtin_amdgcn_readlane(static_cast<int>(kj >> 32), k)) << 32) |
+        static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(kj), k));
+    rank += kk > kj;
+  }
+  wave_sync();  // the pick slots are cleared
+  const bool valid = sel && key_score(kj) > -1.0e30f && R.on != 0;
+  if (sel) R.pick[rank] = key_score(kj) > -1.0e30f ? j : -1;
   if (live) L.rank[qi * p.NB + j] = static_cast<signed char>(valid ? rank : -1);
   const uint64_t picks = __builtin_amdgcn_ballot_w64(valid);
   if (lane == 0) R.picks = picks;
@@ -547,27 +557,41 @@ __device__ int exact_select(const MultiTileParams& p, const MLds& L, int qi, int
 
 // The union of the workgroup's candidate rows for the current routing: the
 // local windows [min ls, max t] and the valid picked blocks of every query
-// whose routing is on.  Returns the number of 16-row tiles to walk.
+// whose routing is on.  Lane l reads query l % 16's record and DPP row steps
+// combine the 16 (every row holds the same copies); wave-uniform result.
 struct Union {
   int lo, hi;
   uint64_t picks;
 };
-__device__ __forceinline__ Union candidate_union(const MultiTileParams& p, const MLds& L) {
-  Union u{1 << 30, -1, 0};
-#pragma unroll
-  for (int q = 0; q < kMQ; ++q) {
-    const MRec& R = L.qr[q];
-    if (R.on) {
-      u.lo = min(u.lo, R.ls);
-      u.hi = max(u.hi, R.t);
-      u.picks |= R.picks;
-    }
-  }
-  u.hi = min(u.hi, static_cast<int>(p.T) - 1);
+template <int CTRL>
+__device__ __forceinline__ void union_step(uint32_t& nlo, uint32_t& hi1, uint32_t& plo,
+                                           uint32_t& phi) {
+  nlo = umax32(nlo, dpp_u32<CTRL>(nlo));
+  hi1 = umax32(hi1, dpp_u32<CTRL>(hi1));
+  plo |= dpp_u32<CTRL>(plo);
+  phi |= dpp_u32<CTRL>(phi);
+}
+__device__ __forceinline__ Union candidate_union(const MultiTileParams& p, const MLds& L,
+                                                 int lane) {
+  const MRec& R = L.qr[lane & 15];
+  const bool on = R.on != 0;
+  uint32_t nlo = ~static_cast<uint32_t>(on ? R.ls : 1 << 30);  // max of ~ls: min of ls
+  uint32_t hi1 = on ? static_cast<uint32_t>(R.t + 1) : 0u;
+  uint32_t plo = on ? static_cast<uint32_t>(R.picks) : 0u;
+  uint32_t phi = on ? static_cast<uint32_t>(R.picks >> 32) : 0u;
+  union_step<kDppXor1>(nlo, hi1, plo, phi);
+  union_step<kDppXor2>(nlo, hi1, plo, phi);
+  union_step<kDppHalfMirror>(nlo, hi1, plo, phi);
+  union_step<kDppMirror>(nlo, hi1, plo, phi);
+  Union u;
+  u.lo = static_cast<int>(~__builtin_amdgcn_readfirstlane(nlo));
+  u.hi = min(static_cast<int>(__builtin_amdgcn_readfirstlane(hi1)) - 1, static_cast<int>(p.T) - 1);
+  u.picks = (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(phi)) << 32) |
+            __builtin_amdgcn_readfirstlane(plo);
   return u;
 }
 
-// Scores every candidate tile of the union against the 16 queries and files
+// Scores every candidate tile of the union `u` against the 16 queries and files
 // each score under its candidate lane of each query.  The product is
 // D[position][query] = keys (A, row lane%16) x queries (B, column lane%16):
 // lane l holds positions 4 (l/16) .. +3 of the tile for query l%16, so it
@@ -577,9 +601,8 @@ __device__ __forceinline__ Union candidate_union(const MultiTileParams& p, const
 template <bool PAIR>
 __device__ uint32_t score_tiles(const MultiTileParams& p, const MLds& L, rsrc_t keys, int64_t b,
                                 int s, const uint4& ah0, const uint4& al0, const uint4& ah1,
-                                const uint4& al1, int wave, int lane) {
+                                const uint4& al1, const Union& u, int wave, int lane) {
   const int c16 = lane & 15, g4 = lane >> 4;
-  const Union u = candidate_union(p, L);
   // The query this lane files scores for.
   const MRec& R = L.qr[c16];
   const int tq = R.on ? R.t : -1;  // no candidates when the routing is off
@@ -689,6 +712,7 @@ __global__ void __launch_bounds__(kMThreads) multi_tile_kernel(const MultiTilePa
     clear_list(p, L, wave + kMWaves * h, lane);  // the anchor slots share one candidate set
   }
   __syncthreads();
+  const Union anchor_union = candidate_union(p, L, lane);
 
   // ---- Anchor slots: distinct argmaxes over the one candidate set. ----
   for (int s = 0; s < p.S; ++s) {
@@ -702,7 +726,7 @@ __global__ void __launch_bounds__(kMThreads) multi_tile_kernel(const MultiTilePa
     const bf16* arow = p.aq + (frag_row * p.S + s) * 64;
     const uint4 a0 = *reinterpret_cast<const uint4*>(arow + 8 * g4);
     const uint4 a1 = *reinterpret_cast<const uint4*>(arow + 32 + 8 * g4);
-    const uint32_t kb = score_tiles<false>(p, L, akeys, b, s, a0, a0, a1, a1, wave, lane);
+    const uint32_t kb = score_tiles<false>(p, L, akeys, b, s, a0, a0, a1, a1, anchor_union, wave, lane);
     if (lane == 0) L.kmax[wave] = kb;
     __syncthreads();
     const float kmax = routing_kmax(L);
@@ -766,7 +790,8 @@ __global__ void __launch_bounds__(kMThreads) multi_tile_kernel(const MultiTilePa
       for (int e = 0; e < 8; ++e) x[e] = static_cast<float>(src[32 + 8 * g4 + e]);
       split_hi_lo(x, ah1, al1);
     }
-    const uint32_t kb = score_tiles<true>(p, L, pkeys, b, s, ah0, al0, ah1, al1, wave, lane);
+    const uint32_t kb = score_tiles<true>(p, L, pkeys, b, s, ah0, al0, ah1, al1, candidate_union(p, L, lane),
+                                         wave, lane);
     if (lane == 0) L.kmax[wave] = kb;
     __syncthreads();
     const float kmax = routing_kmax(L);
@@ -803,7 +828,6 @@ bool multi_tile_layout(MultiTileParams& p) {
   const int sh_bytes = p.H * p.NB * 8;
   p.q_bytes = ((sc_bytes > sh_bytes ? sc_bytes : sh_bytes) + 15) & ~15;
   p.off_sc = take(kMQ * p.q_bytes);
-  p.off_blk = take(kMQ * p.NB * 8);
   p.off_rank = take(kMQ * p.NB);
   p.off_rq = take(kMQ * kMQRow * 8);
   p.off_eq = take(kMQ * kMQRow * 8);

@@ -68,10 +68,10 @@ def test_block_sizes_and_counts(device, context, block):
 
 
 @pytest.mark.parametrize("local,top,k", [(16, 1, 1), (64, 15, 16), (200, 2, 3), (256, 12, 6),
-                                         (8, 0, 4)])
+                                         (8, 0, 4), (37, 3, 6), (255, 1, 5)])
 def test_routing_parameters(device, local, top, k):
     # (64, 15) and (256, 12) at block 64 are the 1024-candidate limit; top 0 routes the
-    # local window only.
+    # local window only; (37, 3) and (255, 1) end the candidate list inside a quad.
     cfg = cfg_of(context=1024, block_size=64, local_window=local, top_blocks=top, k_out=k,
                  slots=min(4, local))
     check(multi_selection_inputs(cfg, seed=local * 100 + top), cfg, device,
