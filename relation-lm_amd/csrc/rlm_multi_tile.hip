@@ -611,26 +611,49 @@ __device__ uint32_t score_tiles(const MultiTileParams& p, const MLds& L, rsrc_t 
   float* sc = L.sc + c16 * (p.q_bytes >> 2);
   u16x2_t km = {0, 0};
   const int ntiles = (u.hi + 16) >> 4;
-  // kTB tiles per round: every key load of the round is issued before the
-  // first product (a tile outside the union reads nothing and files nothing).
-  constexpr int kTB = 2;
-  for (int t0 = wave; t0 < ntiles; t0 += kMWaves * kTB) {
-    uint4 b0[kTB], b1[kTB];
-    bool rel[kTB];
-#pragma unroll
-    for (int v = 0; v < kTB; ++v) {
-      const int tt = t0 + kMWaves * v;
+  // The union's tiles numbered in position order, 64 tiles per group; tile
+  // number i goes to wave i % 16, so every wave walks its share of the union
+  // only.  next_tile() returns this wave's next tile (wave-uniform), -1 at the end.
+  const int ngroups = (ntiles + 63) >> 6;
+  int grp = -1, base = 0;
+  uint64_t mine = 0;
+  auto next_tile = [&]() -> int {
+    while (mine == 0) {
+      if (grp + 1 >= ngroups) return -1;
+      ++grp;
+      const int tt = 64 * grp + lane;
       const int p0 = tt * 16;
-      rel[v] = tt < ntiles &&
-               ((p0 + 15 >= u.lo && p0 <= u.hi) || ((u.picks >> (p0 >> p.BS_log2)) & 1u));
-      const uint32_t off = rel[v] ? key_off(p, b, p0 + c16, s) + 16u * g4 : kNoOffset;
-      b0[v] = buf_load_b128(keys, off);
-      b1[v] = buf_load_b128(keys, rel[v] ? off + 64u : kNoOffset);
+      const bool rel = tt < ntiles && ((p0 + 15 >= u.lo && p0 <= u.hi) ||
+                                       ((u.picks >> ((p0 >> p.BS_log2) & 63)) & 1u));
+      const uint64_t in_union = __builtin_amdgcn_ballot_w64(rel);
+      const int idx = base + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                 static_cast<uint32_t>(in_union >> 32),
+                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(in_union), 0u)));
+      mine = __builtin_amdgcn_ballot_w64(rel && (idx & (kMWaves - 1)) == wave);
+      base += __builtin_popcountll(in_union);
     }
+    const int k = static_cast<int>(__builtin_ctzll(mine));
+    mine &= mine - 1;
+    return 64 * grp + k;
+  };
+  // kTB tiles per round: every key load of the round is issued before the
+  // first product.
+  constexpr int kTB = 2;
+  for (bool more = true; more;) {
+    int tl[kTB];
+    uint4 b0[kTB], b1[kTB];
 #pragma unroll
     for (int v = 0; v < kTB; ++v) {
-      if (!rel[v]) continue;  // uniform
-      const int p0 = (t0 + kMWaves * v) * 16;
+      tl[v] = (v == 0 || tl[v - 1] >= 0) ? next_tile() : -1;
+      const uint32_t off = tl[v] >= 0 ? key_off(p, b, tl[v] * 16 + c16, s) + 16u * g4 : kNoOffset;
+      b0[v] = buf_load_b128(keys, off);
+      b1[v] = buf_load_b128(keys, tl[v] >= 0 ? off + 64u : kNoOffset);
+    }
+    more = tl[kTB - 1] >= 0;
+#pragma unroll
+    for (int v = 0; v < kTB; ++v) {
+      if (tl[v] < 0) break;  // uniform
+      const int p0 = tl[v] * 16;
       km = absmax8(b1[v], absmax8(b0[v], km));
       f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
       acc = mfma_bf16(b0[v], ah0, acc);
