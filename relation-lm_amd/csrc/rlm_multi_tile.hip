@@ -79,6 +79,7 @@ struct MLds {
   double* bias;       // [2 sides][H*RB]
   double* sp;         // [2 sides][16]
   uint32_t* kmax;     // [kMWaves] per-wave max |key| bits
+  bf16* aq;           // [16][S][64]: the queries' anchor query rows, staged once
 };
 
 // Floats per query row of the s~ lists: CAP candidates and a trash slot, 16-byte rows.
@@ -98,6 +99,7 @@ __device__ __forceinline__ MLds carve(const MultiTileParams& p, unsigned char* s
   s.bias = reinterpret_cast<double*>(smem + p.off_bias);
   s.sp = reinterpret_cast<double*>(smem + p.off_sp);
   s.kmax = reinterpret_cast<uint32_t*>(smem + p.off_kmax);
+  s.aq = reinterpret_cast<bf16*>(smem + p.off_aq);
   return s;
 }
 
@@ -218,29 +220,20 @@ __device__ void block_picks(const MultiTileParams& p, const MLds& L, int qi, int
   uint64_t kj = 0;  // lane j's block key; 0 (below every block's key) past the blocks
   {
     // Lane j: block j's heads, summed pairwise (((h0 + h1) + (h2 + h3)) + ...),
-    // the order of a lane-group tree reduction over the heads.  One exp at a
-    // time: s0..s2 hold the pending left halves of the tree (H a power of two).
+    // the order of a lane-group tree reduction over the heads (H a power of
+    // two <= 8).  Four independent exps at a time.
     const double* shj = L.sh + qi * (p.q_bytes >> 3) + (live ? j : 0);
     double m = -INFINITY;
     for (int h = 0; h < p.H; ++h) m = fmax(m, shj[h * p.NB]);
-    double s0 = 0.0, s1 = 0.0, s2 = 0.0, sum = 0.0;
-#pragma unroll 1
-    for (int h = 0; h < p.H; ++h) {
-      double x = exp(shj[h * p.NB] - m);
-      if (h & 1) {
-        x = s0 + x;
-        if (h & 2) {
-          x = s1 + x;
-          if (h & 4) x = s2 + x;
-          else s2 = x;
-        } else {
-          s1 = x;
-        }
-      } else {
-        s0 = x;
-      }
-      sum = x;
-    }
+    auto group4 = [&](int h0) {  // heads h0 .. h0 + 3 (those < H), tree-summed
+      double x[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = exp(shj[(h0 + e < p.H ? h0 + e : h0) * p.NB] - m);
+      const double s01 = p.H >= 2 ? x[0] + x[1] : x[0];
+      return p.H >= 4 ? s01 + (x[2] + x[3]) : s01;
+    };
+    double sum = group4(0);
+    if (p.H == 8) sum = sum + group4(4);
     if (live) {
       const double lse = m + log(sum);
       const int end = (j + 1) * p.BS - 1;
@@ -695,7 +688,6 @@ __global__ void __launch_bounds__(kMThreads) multi_tile_kernel(const MultiTilePa
   const int64_t wg = xcd_tile(blockIdx.x, gridDim.x);
   const int64_t b = wg / p.tiles;
   const int64_t tq0 = (wg - b * p.tiles) * kMQ;
-  const int64_t frag_row = b * p.Tq + (tq0 + c16 < p.Tq ? tq0 + c16 : tq0);  // A fragment query
   const rsrc_t akeys = make_rsrc(p.akeys, p.key_bytes);
   const rsrc_t pkeys = make_rsrc(p.pkeys, p.key_bytes);
   // Query qi = wave + kMWaves h of the workgroup: its row and whether it exists.
@@ -710,6 +702,18 @@ __global__ void __launch_bounds__(kMThreads) multi_tile_kernel(const MultiTilePa
   // ---- Anchor routing: positions, router queries, statistics. ----
   stage_side_stats<TS>(p, L, 0, b, tid);
   stage_router_consts(p, L, tid);
+  {
+    // Every slot's anchor query row of the 16 queries (S 128-byte rows per
+    // query, contiguous), 16 bytes per thread.
+    const int per = p.S * 8;
+    for (int i = tid; i < kMQ * per; i += kMThreads) {
+      const int qi = i / per;
+      bool active;
+      const int64_t qrow = query_row(qi, active);
+      reinterpret_cast<uint4*>(L.aq + qi * p.S * 64)[i - qi * per] =
+          reinterpret_cast<const uint4*>(p.aq + qrow * p.S * 64)[i - qi * per];
+    }
+  }
 #pragma unroll
   for (int h = 0; h < kMQ / kMWaves; ++h) {
     const int qi = wave + kMWaves * h;
@@ -742,11 +746,9 @@ __global__ void __launch_bounds__(kMThreads) multi_tile_kernel(const MultiTilePa
     if (s > 0) __syncthreads();  // every wave is done with the previous slot's scores
     for (int h = 0; h < kMQ / kMWaves; ++h) {
       const int qi = wave + kMWaves * h;
-      bool active;
-      const int64_t qrow = query_row(qi, active);
-      L.eq[qi * kMQRow + lane] = static_cast<double>(to_f32(p.aq[(qrow * p.S + s) * 64 + lane]));
+      L.eq[qi * kMQRow + lane] = static_cast<double>(to_f32(L.aq[(qi * p.S + s) * 64 + lane]));
     }
-    const bf16* arow = p.aq + (frag_row * p.S + s) * 64;
+    const bf16* arow = L.aq + (c16 * p.S + s) * 64;
     const uint4 a0 = *reinterpret_cast<const uint4*>(arow + 8 * g4);
     const uint4 a1 = *reinterpret_cast<const uint4*>(arow + 32 + 8 * g4);
     const uint32_t kb = score_tiles<false>(p, L, akeys, b, s, a0, a0, a1, a1, anchor_union, wave, lane);
@@ -860,6 +862,7 @@ bool multi_tile_layout(MultiTileParams& p) {
   p.off_bias = take(2 * p.H * p.RB * 8);
   p.off_sp = take(2 * 16 * 8);
   p.off_kmax = take(kMWaves * 4);
+  p.off_aq = take(kMQ * p.S * 64 * 2);
   p.lds_total = off;
   return off <= 160 * 1024;
 }

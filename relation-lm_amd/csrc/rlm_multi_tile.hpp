@@ -45,7 +45,7 @@ struct MultiTileParams {
   float* out_partner_score;
   int tiles;  // workgroups per batch row
   int off_stats, off_sc, off_rank, off_rq, off_eq, off_list, off_top, off_qrec,
-      off_bias, off_sp, off_kmax, lds_total;
+      off_bias, off_sp, off_kmax, off_aq, lds_total;
   int q_bytes;  // LDS bytes per query of the region that holds its per-head block
                 // scores, then its candidate score list
 };
