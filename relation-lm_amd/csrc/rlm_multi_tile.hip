@@ -685,9 +685,13 @@ __global__ void __launch_bounds__(kMThreads) multi_tile_kernel(const MultiTilePa
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
   const int c16 = lane & 15, g4 = lane >> 4;
-  const int64_t wg = xcd_tile(blockIdx.x, gridDim.x);
-  const int64_t b = wg / p.tiles;
-  const int64_t tq0 = (wg - b * p.tiles) * kMQ;
+  // Block i takes the i-th most expensive query tile (later positions route
+  // more candidates): batch rows interleaved, positions descending.  Blocks go
+  // to the 8 XCDs in turn, so every XCD gets the same mix of positions, the
+  // costliest tiles start first, and with 4 or 8 batch rows each XCD reads one
+  // row's keys.
+  const int64_t b = static_cast<int64_t>(blockIdx.x) % p.B;
+  const int64_t tq0 = (p.tiles - 1 - static_cast<int64_t>(blockIdx.x) / p.B) * kMQ;
   const rsrc_t akeys = make_rsrc(p.akeys, p.key_bytes);
   const rsrc_t pkeys = make_rsrc(p.pkeys, p.key_bytes);
   // Query qi = wave + kMWaves h of the workgroup: its row and whether it exists.
