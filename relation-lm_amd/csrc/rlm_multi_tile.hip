@@ -67,7 +67,8 @@ struct MLds {
   // Region q (q_bytes from sc) belongs to query q: first its per-head block
   // scores sh [H][NB] (float64), then, from its block picks on, its candidate
   // list sc: s~ of each candidate lane, -inf for lanes that are not a candidate
-  // or are excluded, entry CAP a trash slot for branch-free stores.
+  // or are excluded and for the padding up to a multiple of 256 lanes, then a
+  // trash slot for branch-free stores (list_trash).
   float* sc;
   double* sh;
   signed char* rank;  // [16][NB]: pick rank of block j, -1 if not a valid pick
@@ -82,8 +83,11 @@ struct MLds {
   bf16* aq;           // [16][S][64]: the queries' anchor query rows, staged once
 };
 
-// Floats per query row of the s~ lists: CAP candidates and a trash slot, 16-byte rows.
-__host__ __device__ __forceinline__ int sc_row(int cap) { return (cap + 4) & ~3; }
+// The s~ list of a query: CAP candidate lanes padded to a multiple of 256
+// (read four lanes per thread, 256 at a time, with no bound checks), then the
+// trash slot; 16-byte rows.
+__host__ __device__ __forceinline__ int list_trash(int cap) { return (cap + 255) & ~255; }
+__host__ __device__ __forceinline__ int list_floats(int cap) { return list_trash(cap) + 4; }
 
 __device__ __forceinline__ MLds carve(const MultiTileParams& p, unsigned char* smem) {
   MLds s;
@@ -243,13 +247,14 @@ __device__ void block_picks(const MultiTileParams& p, const MLds& L, int qi, int
   }
   if (lane < p.TOP) R.pick[lane] = -1;
   // The TOP largest keys.  T: the TOP-th largest score half over the blocks
-  // (0 when there are fewer than TOP blocks), bit by bit from the top; then
-  // every block scoring above T and the lowest blocks scoring T.
+  // (0 when there are fewer than TOP blocks), bit by bit from the top (a lane
+  // past the blocks holds 0, below every threshold tried); then every block
+  // scoring above T and the lowest blocks scoring T.
   const uint32_t sk = static_cast<uint32_t>(kj >> 32);
   uint32_t T = 0;
   for (int bit = 31; bit >= 0; --bit) {
     const uint32_t cand = T | (1u << bit);
-    if (__builtin_popcountll(__builtin_amdgcn_ballot_w64(live && sk >= cand)) >= p.TOP) T = cand;
+    if (__builtin_popcountll(__builtin_amdgcn_ballot_w64(sk >= cand)) >= p.TOP) T = cand;
   }
   const uint64_t at_t = __builtin_amdgcn_ballot_w64(live && sk == T);
   const int above = __builtin_popcountll(__builtin_amdgcn_ballot_w64(live && sk > T));
@@ -257,14 +262,21 @@ __device__ void block_picks(const MultiTileParams& p, const MLds& L, int qi, int
       static_cast<uint32_t>(at_t >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(at_t), 0u)));
   const bool sel = live && (sk > T || (sk == T && below_t < p.TOP - above));
   // Pick rank of a selected block: #{k : key_k > key_j}; every such k is
-  // selected, so the selected keys (read lane by lane) are all it compares.
+  // selected, so it counts among the selected keys, gathered in the query's
+  // (still unused) member list.
+  const uint64_t selm = __builtin_amdgcn_ballot_w64(sel);
+  const int nsel = __builtin_popcountll(selm);
+  uint64_t* gathered = L.list + qi * kMListRow;
+  if (sel)
+    gathered[__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(selm >> 32),
+                                       __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(selm), 0u))] = kj;
+  wave_sync();
   int rank = 0;
-  for (uint64_t rest = __builtin_amdgcn_ballot_w64(sel); rest != 0; rest &= rest - 1) {
-    const int k = static_cast<int>(__builtin_ctzll(rest));
-    const uint64_t kk =
-        (static_cast<uint64_t>(__builtin_amdgcn_readlane(static_cast<int>(kj >> 32), k)) << 32) |
-        static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(kj), k));
-    rank += kk > kj;
+#pragma unroll
+  for (int f = 0; f < kMultiTileMaxTop; f += 2) {
+    const uint4 kk = *reinterpret_cast<const uint4*>(gathered + f);
+    rank += (f < nsel && ((static_cast<uint64_t>(kk.y) << 32) | kk.x) > kj) +
+            (f + 1 < nsel && ((static_cast<uint64_t>(kk.w) << 32) | kk.z) > kj);
   }
   wave_sync();  // the pick slots are cleared
   const bool valid = sel && key_score(kj) > -1.0e30f && R.on != 0;
@@ -404,16 +416,15 @@ __device__ int exact_select(const MultiTileParams& p, const MLds& L, int qi, int
     if (c >= 0) sc[c] = -INFINITY;
   }
   wave_sync();
-  // The list in quads: lane l reads candidates 256 j + 4 l + e (e < 4); those
-  // past CAP (the trash slot, padding) read -inf.
-  const int nquad = (p.CAP + 255) >> 8;
+  // The list in quads: lane l reads candidates 256 j + 4 l + e (e < 4); the
+  // padding past CAP reads -inf.
+  const int nquad = list_trash(p.CAP) >> 8;
   auto quad = [&](int j, float (&x)[4]) {
-    const int c = 256 * j + 4 * lane;
-    const float4 v = *reinterpret_cast<const float4*>(sc + (c < p.CAP ? c : 0));
-    x[0] = c < p.CAP ? v.x : -INFINITY;
-    x[1] = c + 1 < p.CAP ? v.y : -INFINITY;
-    x[2] = c + 2 < p.CAP ? v.z : -INFINITY;
-    x[3] = c + 3 < p.CAP ? v.w : -INFINITY;
+    const float4 v = *reinterpret_cast<const float4*>(sc + 256 * j + 4 * lane);
+    x[0] = v.x;
+    x[1] = v.y;
+    x[2] = v.z;
+    x[3] = v.w;
   };
   float lm = -INFINITY;
   for (int j = 0; j < nquad; ++j) {
@@ -602,6 +613,7 @@ __device__ uint32_t score_tiles(const MultiTileParams& p, const MLds& L, rsrc_t 
   const int lq = R.ls;
   const signed char* rank = L.rank + c16 * p.NB;
   float* sc = L.sc + c16 * (p.q_bytes >> 2);
+  const int trash = list_trash(p.CAP);
   u16x2_t km = {0, 0};
   const int ntiles = (u.hi + 16) >> 4;
   // The union's tiles numbered in position order, 64 tiles per group; tile
@@ -653,18 +665,17 @@ __device__ uint32_t score_tiles(const MultiTileParams& p, const MLds& L, rsrc_t 
       if (PAIR) acc = mfma_bf16(b0[v], al0, acc);
       acc = mfma_bf16(b1[v], ah1, acc);
       if (PAIR) acc = mfma_bf16(b1[v], al1, acc);
-      // Candidate lane of each position: local window, else the block's pick;
-      // positions that are not a candidate store to the trash slot.
+      // Candidate lane of position pb + e: local window from e >= lq - pb on,
+      // else the block's pick (an unpicked block: the trash slots after the
+      // list); past tq, the trash slot.
       const int pb = p0 + 4 * g4;
       const int r = rank[p0 >> p.BS_log2];
       const int local0 = pb - (tq - p.L + 1);
-      const int pick0 = r >= 0 ? p.L + r * p.BS + (pb & (p.BS - 1)) : -1;
+      const int pick0 = r >= 0 ? p.L + r * p.BS + (pb & (p.BS - 1)) : trash;
+      const int dl = lq - pb, dv = tq - pb;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int pos = pb + e;
-        const int c = pos >= lq ? local0 + e : (pick0 >= 0 ? pick0 + e : -1);
-        sc[pos <= tq && c >= 0 ? c : p.CAP] = acc[e];
-      }
+      for (int e = 0; e < 4; ++e)
+        sc[e <= dv ? (e >= dl ? local0 : pick0) + e : trash] = acc[e];
     }
   }
   return wave_max_u32(umax32(km.x, km.y));
@@ -853,7 +864,7 @@ bool multi_tile_layout(MultiTileParams& p) {
   };
   p.off_stats = take(2 * p.NB * kMStatRow * 4);
   // Per query: its per-head block scores, then its candidate list.
-  const int sc_bytes = sc_row(p.CAP) * 4;
+  const int sc_bytes = list_floats(p.CAP) * 4;
   const int sh_bytes = p.H * p.NB * 8;
   p.q_bytes = ((sc_bytes > sh_bytes ? sc_bytes : sh_bytes) + 15) & ~15;
   p.off_sc = take(kMQ * p.q_bytes);
