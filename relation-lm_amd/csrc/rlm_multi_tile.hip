@@ -795,21 +795,33 @@ __global__ void __launch_bounds__(kMThreads) multi_tile_kernel(const MultiTilePa
   }
 
   // ---- Partner routing of each active slot. ----
+  // Partner query of slot s (wave w's query w): the fp32 sum of its query-side
+  // row and the anchor's cached row.  Lane l holds elements l and 64 + l of
+  // both rows; slot s + 1's are loaded while slot s runs.
+  static_assert(kMQ == kMWaves, "one query per wave");
+  bool pactive;
+  const int64_t prow = query_row(wave, pactive);
+  auto partner_rows = [&](int s, bf16 (&v)[4]) {
+    const bool on = pactive && s < L.qr[wave].nact;
+    const int anchor = on ? L.qr[wave].taken[s] : 0;
+    const bf16* pb = p.pbase + (prow * p.S + s) * 128;
+    const bf16* pc = p.pcache + ((b * p.T + anchor) * p.S + s) * 128;
+    v[0] = pb[lane];
+    v[1] = pc[lane];
+    v[2] = pb[64 + lane];
+    v[3] = pc[64 + lane];
+  };
   __syncthreads();  // every wave is done with the anchor side's LDS
+  bf16 next_rows[4];
+  partner_rows(0, next_rows);
   stage_side_stats<TS>(p, L, 1, b, tid);
   for (int s = 0; s < p.S; ++s) {
-    for (int h = 0; h < kMQ / kMWaves; ++h) {
-      const int qi = wave + kMWaves * h;
-      bool active;
-      const int64_t qrow = query_row(qi, active);
-      const bool on = active && s < L.qr[qi].nact;
-      const int anchor = on ? L.qr[qi].taken[s] : 0;
-      // Partner query: fp32 sum of the query-side row and the anchor's cached row.
-      const bf16* pb = p.pbase + (qrow * p.S + s) * 128;
-      const bf16* pc = p.pcache + ((b * p.T + anchor) * p.S + s) * 128;
-      L.eq[qi * kMQRow + lane] = static_cast<double>(to_f32(pb[lane]) + to_f32(pc[lane]));
-      L.rq[qi * kMQRow + lane] = static_cast<double>(to_f32(pb[64 + lane]) + to_f32(pc[64 + lane]));
-      if (lane == 0) L.qr[qi].on = on ? 1 : 0;
+    {
+      const bf16 rows[4] = {next_rows[0], next_rows[1], next_rows[2], next_rows[3]};
+      if (s + 1 < p.S) partner_rows(s + 1, next_rows);
+      L.eq[wave * kMQRow + lane] = static_cast<double>(to_f32(rows[0]) + to_f32(rows[1]));
+      L.rq[wave * kMQRow + lane] = static_cast<double>(to_f32(rows[2]) + to_f32(rows[3]));
+      if (lane == 0) L.qr[wave].on = pactive && s < L.qr[wave].nact ? 1 : 0;
     }
     __syncthreads();  // query rows, statistics; previous slot's lists done
     head_scores(p, L, 1, wave, lane);
