@@ -6,7 +6,8 @@ The relation MLP's second Linear of the multi-anchor block (cfg5:
 [98304, 3072] x [3072, 768], bf16) and the reference's second linear G3
 (benchmark_relation_reduce.py:63) run here.  Shapes cover both tile sizes,
 edges in M and N, a row-strided input, fp16 weights, fp32 and bf16 outputs
-and the bias in the epilogue.  fp32 outputs: within fp32 accumulation of the
+and the bias in the epilogue; the small-K kernel (K <= 128, the expanded-cache
+projection) on its own shapes.  fp32 outputs: within fp32 accumulation of the
 exact products (1e-5 of sum |a w|); 16-bit outputs: that plus half an ulp of
 the output type.
 """
@@ -69,6 +70,50 @@ def test_relation_linear_dma_path(device, m, n, k, wdt, odt, with_bias, pad):
     torch.cuda.synchronize()
     assert got.shape == (m, n) and got.dtype == odt
     check(got, a, w, bias)
+
+
+SMALLK_CASES = [
+    # (M, N, K, weight dtype, out dtype, bias, input row padding): K <= 128, the
+    # expanded-cache projection's kernel (smallk_kernel)
+    (4096, 1024, 128, torch.bfloat16, torch.bfloat16, True, 0),   # cfg2 expanded projection
+    (4096, 1024, 128, torch.bfloat16, torch.float32, False, 0),
+    (1000, 256, 32, torch.bfloat16, torch.bfloat16, True, 0),     # a partial last tile in M
+    (777, 384, 96, torch.float16, torch.bfloat16, True, 16),      # fp16, row-strided input
+    (300, 128, 64, torch.bfloat16, torch.float32, True, 0),
+    (520, 200, 128, torch.bfloat16, torch.bfloat16, True, 0),     # a partial last tile in N
+]
+
+
+@pytest.mark.parametrize("m,n,k,wdt,odt,with_bias,pad", SMALLK_CASES)
+def test_relation_linear_small_k(device, m, n, k, wdt, odt, with_bias, pad):
+    g = torch.Generator().manual_seed(m + n + k + 7)
+    base = torch.randn(m, k + pad, generator=g).to(wdt)
+    a = base[:, :k]
+    w = (torch.randn(n, k, generator=g) / np.sqrt(k)).to(wdt)
+    bias = (0.5 * torch.randn(n, generator=g)).to(wdt) if with_bias else None
+    print(f"relation_linear small K: M={m} N={n} K={k} {wdt} -> {odt} bias={with_bias} "
+          f"pad={pad}", flush=True)
+    got = ops.relation_linear(base.to(device)[:, :k], w.to(device),
+                              None if bias is None else bias.to(device), odt)
+    torch.cuda.synchronize()
+    assert got.shape == (m, n) and got.dtype == odt
+    check(got, a, w, bias)
+
+
+@pytest.mark.parametrize("odt", [torch.bfloat16, torch.float32])
+def test_relation_linear_small_k_edge_tiles_equal_full_tiles(device, odt):
+    # N = 1024 is whole 128-column tiles (vector stores), N = 1000 ends in an
+    # edge tile (element stores); every output takes the same k-steps, so the
+    # bits agree.
+    g = torch.Generator().manual_seed(31)
+    a = torch.randn(4096, 128, generator=g).to(torch.bfloat16).to(device)
+    w = (torch.randn(1024, 128, generator=g) / np.sqrt(128)).to(torch.bfloat16).to(device)
+    b = (0.5 * torch.randn(1024, generator=g)).to(torch.bfloat16).to(device)
+    print(f"relation_linear small K, full vs edge tiles -> {odt}", flush=True)
+    full = ops.relation_linear(a, w, b, odt)
+    part = ops.relation_linear(a, w[:1000].contiguous(), b[:1000].contiguous(), odt)
+    torch.cuda.synchronize()
+    assert torch.equal(full[:, :1000], part)
 
 
 def test_relation_linear_dma_repeat_identical(device):
