@@ -60,7 +60,8 @@ CPU_SAMPLES = 9                 # CPU baseline: timed calls per shape (median)
 # Kernel-name prefixes (as rocprofv3 reports them) of the timed kernels.
 KERNEL_SYMBOLS = {
     "expanded_projection": "smallk_kernel<rlm::bf16, rlm::bf16, rlm::bf16",
-    "relation_select": "select_tile_kernel<",
+    "relation_select": "select_tile_kernel<float, false>",
+    "relation_select_expand": "select_tile_kernel<float, true>",
     "relation_reduce_fused": "fused_reduce_kernel<",
     "relation_hidden": "hidden_tile_kernel<",
     "second_linear": "tile_kernel<float, rlm::bf16, float",
@@ -174,6 +175,7 @@ def main() -> int:
     from relation_lm.kernels.relation_select import (
         multi_relation_select_seq,
         relation_select_packed_seq,
+        relation_select_packed_seq_expand,
     )
     from relation_lm.workloads import (
         CONFIGS,
@@ -631,6 +633,19 @@ def main() -> int:
         a, s, p, ps = run_select()
         return run_fused(expanded, a, p, ps)
 
+    # The selection launch also projecting the whole expanded cache
+    # (relation_select_packed_seq_expand: the same cache bits as relation_linear).
+    expanded_buf = torch.empty(cfg.batch, cfg.context, red["expanded_weight"].shape[0],
+                               dtype=red["operand_cache"].dtype, device=device)
+
+    def run_select_expand():
+        return relation_select_packed_seq_expand(*sargs, operand, red["expanded_weight"],
+                                                 red["expanded_bias"], expanded_buf)
+
+    def step_xp():
+        a, s, p, ps = run_select_expand()
+        return run_fused(expanded_buf, a, p, ps)
+
     # The headline schedule: the selection and the expanded projection do not
     # depend on each other, so the selection runs on a second stream beside the
     # projection and the fused reduce waits for both (replayed as one HIP graph;
@@ -657,6 +672,7 @@ def main() -> int:
 
     for _ in range(args.warmup):
         step()
+        step_xp()
         step_unfused()
     torch.cuda.synchronize()
     expanded = run_expanded()
@@ -666,6 +682,7 @@ def main() -> int:
     kernels = {
         "expanded_projection": run_expanded,
         "relation_select": run_select,
+        "relation_select_expand": run_select_expand,
         "relation_reduce_fused": lambda: run_fused(expanded, a, p, ps),
         "relation_hidden": lambda: run_hidden(expanded, a, p),
         "second_linear": lambda: run_second(hidden),
@@ -741,9 +758,13 @@ def main() -> int:
     if not torch.equal(graph_out, reference_out):
         print("forked graph step differs from the eager step", file=sys.stderr)
         return 1
+    if not torch.equal(step_xp(), reference_out):
+        print("the one-launch projection step differs from the eager step", file=sys.stderr)
+        return 1
     ms_forked_graph = timed(step_graph.replay, args.steps)
     ms_serial_graph = timed(serial_graph.replay, args.steps)
     ms_serial = timed(step, args.steps)
+    ms_xp = timed(step_xp, args.steps)
     # The step's schedule is picked by measurement, as a kernel variant would
     # be: the forked graph when it is faster, else the serial eager launches
     # (both measured above over the same K steps; same output bits).
@@ -752,6 +773,9 @@ def main() -> int:
                          "fused reduce after both", ms_forked_graph),
         "serial_eager": ("eager launches on one stream: expanded projection, select, fused "
                          "reduce", ms_serial),
+        "serial_eager_projection_in_select": (
+            "eager launches on one stream: select with the expanded projection in the same "
+            "launch (relation_select_packed_seq_expand), fused reduce", ms_xp),
     }
     chosen = min(schedules, key=lambda k: schedules[k][1])
     ms_per_step = schedules[chosen][1]
@@ -818,6 +842,19 @@ def main() -> int:
     torch.cuda.synchronize()
     in_step_us = {name: statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1e3 for ev in marks)
                   for i, name in enumerate(headline)}
+    marks_xp = [[torch.cuda.Event(enable_timing=True) for _ in range(3)]
+                for _ in range(args.kernel_repeats)]
+    torch.cuda.synchronize()
+    for ev in marks_xp:
+        ev[0].record()
+        xa, _, xp, xps = run_select_expand()
+        ev[1].record()
+        run_fused(expanded_buf, xa, xp, xps)
+        ev[2].record()
+    torch.cuda.synchronize()
+    in_step_xp_us = {name: statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1e3
+                                             for ev in marks_xp)
+                     for i, name in enumerate(("relation_select_expand", "relation_reduce_fused"))}
     nbytes = algorithmic_bytes(cfg)
     nflops = algorithmic_flops(cfg)
     dominant = max(headline, key=in_step_us.get)
@@ -884,12 +921,15 @@ def main() -> int:
         "roofline": roof,
         "rooflines": rooflines,
         "per_kernel_in_step_us": {k: round(v, 2) for k, v in in_step_us.items()},
+        "per_kernel_in_step_us_projection_in_select": {k: round(v, 2)
+                                                       for k, v in in_step_xp_us.items()},
         "per_kernel_us": {k: round(v, 2) for k, v in per_kernel_us.items()},
         "settle": {"seconds": round(settle_s, 2), "steps": settle_steps,
                    "floor_s": SETTLE_S},
         "schedule": schedules[chosen][0],
         "schedules_ms_per_step": {"forked_graph": round(ms_forked_graph, 5),
                                   "serial_eager": round(ms_serial, 5),
+                                  "serial_eager_projection_in_select": round(ms_xp, 5),
                                   "serial_graph": round(ms_serial_graph, 5)},
         "hbm_frac_fused_chain": round(fused_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "residency": (f"value, roofline and hbm_frac_* are cache-resident: the same "

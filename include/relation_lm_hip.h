@@ -107,6 +107,36 @@ hipError_t rlm_relation_select_packed_seq(
     const rlm_tensor* out_partner_score, hipStream_t stream);
 
 /*
+ * rlm_relation_select_packed_seq plus the whole expanded cache: no reference op.
+ * Replaces, in one launch where the shapes allow, the sequence selection and
+ * the expanded-cache projection the reference runs as its own linear call
+ * (tests/test_relation_reduce_gpu.py:64-68: expanded = F.linear(operand_cache,
+ * W_e, b_e)): for every cache row r of every batch row b,
+ *   expanded_cache[b, r] = expanded_weight . operand_cache[b, r] + expanded_bias,
+ * in bf16 with fp32 sums, the same bits as rlm_linear on [B*T, R].  The
+ * selection is the same as rlm_relation_select_packed_seq.  operand_cache
+ * [B,T,R] bf16 (R in {32,64,96,128}), expanded_weight [N,R] bf16 (N % 16 == 0),
+ * expanded_bias [N] or NULL, expanded_cache [B,T,N] bf16.  Where the sequence
+ * selection's matrix-core kernel applies, N % 128 == 0 and T >= 4 R,
+ * its workgroups project 128 x 128 cache tiles while their own loads are in
+ * flight; otherwise the projection is a launch of its own after the selection.
+ */
+hipError_t rlm_relation_select_packed_seq_expand(
+    const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
+    const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
+    const rlm_tensor* anchor_block_std, const rlm_tensor* anchor_gamma,
+    const rlm_tensor* anchor_bias, const rlm_tensor* partner_base,
+    const rlm_tensor* partner_anchor_cache, const rlm_tensor* partner_keys,
+    const rlm_tensor* partner_block_mean, const rlm_tensor* partner_block_std,
+    const rlm_tensor* partner_gamma, const rlm_tensor* partner_bias,
+    const rlm_tensor* positions, int64_t local_window, int64_t top_blocks,
+    int64_t k_out, int32_t strict_valid, const rlm_tensor* operand_cache,
+    const rlm_tensor* expanded_weight, const rlm_tensor* expanded_bias,
+    const rlm_tensor* expanded_cache, const rlm_tensor* out_anchor,
+    const rlm_tensor* out_anchor_score, const rlm_tensor* out_partner,
+    const rlm_tensor* out_partner_score, hipStream_t stream);
+
+/*
  * rlm_relation_select_packed (decode form) plus the token's expanded-cache row:
  * no reference op.  Replaces, in one launch, relation_select_packed
  * (relation_select.py:311-382) and the reference decode's row projection

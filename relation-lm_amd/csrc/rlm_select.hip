@@ -1553,6 +1553,24 @@ hipError_t fill_expand_row(const RowArgs& a, const Geometry& g, const rlm_tensor
   return hipSuccess;
 }
 
+// The whole expanded cache as one launch of the library GEMM (rlm_linear):
+// [B*T, R] . [N, R]^T + bias -> [B*T, N] bf16.
+hipError_t expand_seq_linear(const RowArgs& a, const Geometry& g, hipStream_t stream) {
+  const int64_t R = a.operand->shape[2], N = a.weight->shape[0];
+  rlm_tensor in = *a.operand, out = *a.cache;
+  in.ndim = 2;
+  in.shape[0] = g.B * g.T;
+  in.shape[1] = R;
+  in.stride[0] = R;
+  in.stride[1] = 1;
+  out.ndim = 2;
+  out.shape[0] = g.B * g.T;
+  out.shape[1] = N;
+  out.stride[0] = N;
+  out.stride[1] = 1;
+  return rlm_linear(&in, a.weight, a.bias, &out, stream);
+}
+
 hipError_t select_packed_impl(
     bool seq, bool ring, const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
     const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
@@ -1564,7 +1582,7 @@ hipError_t select_packed_impl(
     int64_t local_window, int64_t top_blocks, int64_t k_out, int32_t strict_valid,
     const rlm_tensor* out_anchor, const rlm_tensor* out_anchor_score,
     const rlm_tensor* out_partner, const rlm_tensor* out_partner_score, hipStream_t stream,
-    const RowArgs* xrow = nullptr) {
+    const RowArgs* xrow = nullptr, const RowArgs* xseq = nullptr) {
   clear_error();
   const int qd = seq ? 3 : 2;  // rank of query-side tensors
   RLM_TRY(check_tensor(anchor_query, "anchor_query", qd));
@@ -1625,6 +1643,13 @@ hipError_t select_packed_impl(
     const hipError_t xe = fill_expand_row(*xrow, g, position, ring, xr);
     if (xe != hipSuccess) return xe;
   }
+  ExpandRowParams xs{};
+  if (xseq != nullptr) {
+    RLM_REQUIRE(seq, "the whole expanded cache is computed with the sequence form only");
+    // The row-wise checks of the decode form's expanded row (position unused).
+    const hipError_t xe = fill_expand_row(*xseq, g, position, false, xs);
+    if (xe != hipSuccess) return xe;
+  }
   hipError_t err = finish_params(p, g, local_window, top_blocks, k_out, strict_valid,
                                  act == RLM_F32 ? 4 : 2);
   if (err != hipSuccess) return err;
@@ -1650,8 +1675,28 @@ hipError_t select_packed_impl(
     if (tile_params(p, g, act, stat, position, anchor_query, anchor_router_query,
                     partner_base, partner_anchor_cache, anchor_keys, partner_keys,
                     anchor_block_mean, anchor_block_std, anchor_gamma, anchor_bias,
-                    partner_block_mean, partner_block_std, partner_gamma, partner_bias, tp))
-      return select_tile_launch(tp, stat, stream);
+                    partner_block_mean, partner_block_std, partner_gamma, partner_bias, tp)) {
+      // The whole expanded cache by the same launch when its 128 x 128 tiles
+      // fit the key rows' LDS (two tiles of 128 rows x R bf16) and N is whole
+      // tiles; otherwise a GEMM launch after the selection.
+      const bool fused = xseq != nullptr && xs.N % 128 == 0 &&
+                         2 * 128 * 32 * xs.KS * 2 <= g.T * 128;
+      if (fused) {
+        tp.x_op = xs.op;
+        tp.x_w = xs.w;
+        tp.x_bias = xs.bias;
+        tp.x_bias_dtype = xs.bias_dtype;
+        tp.x_out = xs.cache;
+        tp.x_rows = g.B * g.T;
+        tp.x_KS = xs.KS;
+        tp.x_N = xs.N;
+        tp.x_op_bytes = xs.op_bytes;
+        tp.x_w_bytes = xs.w_bytes;
+      }
+      const hipError_t te = select_tile_launch(tp, stat, stream);
+      if (te != hipSuccess || xseq == nullptr || fused) return te;
+      return expand_seq_linear(*xseq, g, stream);
+    }
   }
   if (ring) {
     RLM_REQUIRE(!seq, "ring-buffer caches are supported by the decode form only");
@@ -1678,7 +1723,9 @@ hipError_t select_packed_impl(
   }
   const hipError_t se = ring ? launch_select<kPacked, true>(p, act, stat, stream)
                              : launch_select<kPacked>(p, act, stat, stream);
-  if (se != hipSuccess || xrow == nullptr) return se;
+  if (se != hipSuccess) return se;
+  if (xseq != nullptr) return expand_seq_linear(*xseq, g, stream);
+  if (xrow == nullptr) return se;
   return expand_row_launch(xr, stream);
 }
 
@@ -1946,6 +1993,28 @@ extern "C" hipError_t rlm_relation_select_packed_seq(
                             out_anchor_score, out_partner, out_partner_score, stream);
 }
 
+extern "C" hipError_t rlm_relation_select_packed_seq_expand(
+    const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
+    const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,
+    const rlm_tensor* anchor_block_std, const rlm_tensor* anchor_gamma,
+    const rlm_tensor* anchor_bias, const rlm_tensor* partner_base,
+    const rlm_tensor* partner_anchor_cache, const rlm_tensor* partner_keys,
+    const rlm_tensor* partner_block_mean, const rlm_tensor* partner_block_std,
+    const rlm_tensor* partner_gamma, const rlm_tensor* partner_bias, const rlm_tensor* positions,
+    int64_t local_window, int64_t top_blocks, int64_t k_out, int32_t strict_valid,
+    const rlm_tensor* operand_cache, const rlm_tensor* expanded_weight,
+    const rlm_tensor* expanded_bias, const rlm_tensor* expanded_cache,
+    const rlm_tensor* out_anchor, const rlm_tensor* out_anchor_score,
+    const rlm_tensor* out_partner, const rlm_tensor* out_partner_score, hipStream_t stream) {
+  const RowArgs x{operand_cache, expanded_weight, expanded_bias, expanded_cache};
+  return select_packed_impl(true, false, anchor_query, anchor_keys, anchor_router_query,
+                            anchor_block_mean, anchor_block_std, anchor_gamma, anchor_bias,
+                            partner_base, partner_anchor_cache, partner_keys, partner_block_mean,
+                            partner_block_std, partner_gamma, partner_bias, positions,
+                            local_window, top_blocks, k_out, strict_valid, out_anchor,
+                            out_anchor_score, out_partner, out_partner_score, stream, nullptr,
+                            &x);
+}
 extern "C" hipError_t rlm_relation_select_packed_expand_row(
     const rlm_tensor* anchor_query, const rlm_tensor* anchor_keys,
     const rlm_tensor* anchor_router_query, const rlm_tensor* anchor_block_mean,

@@ -635,7 +635,97 @@ __device__ __forceinline__ float staged_kmax(const Lds& L) {
   return __uint_as_float(kb << 16) * (1.0f + 1.0f / 1024.0f);
 }
 
-template <typename TS>
+// The expanded-cache projection tiles of this workgroup, when the launch
+// carries them (no reference kernel: the reference projects the cache with its
+// own linear call): tile i of the (x_rows / 128) x (x_N / 128) grid for
+// i = wg, wg + G, ..., each a 128 x 128 output tile formed as the library's
+// small-K GEMM forms it (W . A^T per 16x16x32 k-step, k-steps in order, fp32
+// sums, + bias, rounded to bf16), so the bits equal that GEMM's.  The A and W
+// tiles are staged in `stage` (the key rows' LDS, before the keys are put
+// there); wave w forms rows 32 (w / 4) .. +31 and columns 32 (w % 4) .. +31.
+template <int KS>
+__device__ void expand_tiles(const TileParams& p, unsigned char* stage, int64_t wg, int64_t G,
+                             int tid, int lane, int wave) {
+  constexpr int K = 32 * KS;
+  constexpr int QPR = K / 8;                                       // 16-byte pieces per row
+  constexpr int SW = QPR % 16 == 0 ? 16 : (QPR % 8 == 0 ? 8 : 4);  // swizzle width
+  constexpr int kPer = (128 * QPR + kThreads - 1) / kThreads;      // pieces per thread per tile
+  unsigned char* ta = stage;
+  unsigned char* tw = stage + 128 * K * 2;
+  const rsrc_t ar = make_rsrc(p.x_op, p.x_op_bytes);
+  const rsrc_t wr = make_rsrc(p.x_w, p.x_w_bytes);
+  const int64_t tiles_n = p.x_N / 128;
+  const int64_t ntile = ((p.x_rows + 127) / 128) * tiles_n;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int wm = (wave >> 2) * 32, wn = (wave & 3) * 32;
+  for (int64_t tile = wg; tile < ntile; tile += G) {
+    const int64_t mt = (tile / tiles_n) * 128, nt = (tile % tiles_n) * 128;
+    uint4 va[kPer], vw[kPer];
+#pragma unroll
+    for (int t = 0; t < kPer; ++t) {
+      const int piece = t * kThreads + tid;
+      const bool ok = piece < 128 * QPR;
+      const int64_t row = piece / QPR, q = piece % QPR;
+      va[t] = buf_load_b128(ar, ok && mt + row < p.x_rows
+                                    ? static_cast<uint32_t>(((mt + row) * K + 8 * q) * 2)
+                                    : kNoOffset);
+      vw[t] = buf_load_b128(wr, ok ? static_cast<uint32_t>(((nt + row) * K + 8 * q) * 2) : kNoOffset);
+    }
+    float bv[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        bv[j][e] = p.x_bias != nullptr
+                       ? load_any_f(p.x_bias, p.x_bias_dtype, nt + wn + 16 * j + 4 * g + e)
+                       : 0.0f;
+#pragma unroll
+    for (int t = 0; t < kPer; ++t) {
+      const int piece = t * kThreads + tid;
+      if (piece < 128 * QPR) {
+        const int row = piece / QPR, q = piece % QPR;
+        const int at = row * (2 * K) + 16 * (q ^ (row % SW));
+        *reinterpret_cast<uint4*>(ta + at) = va[t];
+        *reinterpret_cast<uint4*>(tw + at) = vw[t];
+      }
+    }
+    __syncthreads();  // the tile's A and W rows staged
+    f32x4_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int q = 4 * s + g;
+      uint4 a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        a[i] = *reinterpret_cast<const uint4*>(ta + (wm + 16 * i + r16) * (2 * K) + 16 * (q ^ (r16 % SW)));
+        b[i] = *reinterpret_cast<const uint4*>(tw + (wn + 16 * i + r16) * (2 * K) + 16 * (q ^ (r16 % SW)));
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16(b[j], a[i], acc[i][j]);
+    }
+    // Lane (r16, g) holds row wm + 16 i + r16, columns wn + 16 j + 4 g .. + 3.
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int64_t m = mt + wm + 16 * i + r16;
+      if (m < p.x_rows)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          *reinterpret_cast<uint2*>(p.x_out + m * p.x_N + nt + wn + 16 * j + 4 * g) =
+              make_uint2(pack_bf16x2(acc[i][j][0] + bv[j][0], acc[i][j][1] + bv[j][1]),
+                         pack_bf16x2(acc[i][j][2] + bv[j][2], acc[i][j][3] + bv[j][3]));
+    }
+    __syncthreads();  // every wave is done with the staged rows
+  }
+}
+
+// XP: the launch also projects the expanded cache (TileParams::x_*).
+template <typename TS, bool XP>
 __global__ void __launch_bounds__(kThreads) select_tile_kernel(const TileParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   const Lds L = carve(p, smem);
@@ -653,6 +743,18 @@ __global__ void __launch_bounds__(kThreads) select_tile_kernel(const TileParams 
   const int T = static_cast<int>(p.T);
   const int nchunks = T * 8;
   const uint32_t side_bytes = static_cast<uint32_t>(T) * kRowBytes;
+
+  if constexpr (XP) {
+    // The expanded-cache projection first, in the key rows' LDS (free until
+    // the keys arrive); its stores drain while the selection's loads are in
+    // flight.
+    switch (p.x_KS) {
+      case 1: expand_tiles<1>(p, L.keys, wg, gridDim.x, tid, lane, wave); break;
+      case 2: expand_tiles<2>(p, L.keys, wg, gridDim.x, tid, lane, wave); break;
+      case 3: expand_tiles<3>(p, L.keys, wg, gridDim.x, tid, lane, wave); break;
+      default: expand_tiles<4>(p, L.keys, wg, gridDim.x, tid, lane, wave); break;
+    }
+  }
 
   // ---- One round of loads: the router constants, the anchor keys (every
   //      row), the query-side rows, the position and the statistics of both
@@ -821,20 +923,22 @@ hipError_t select_tile_launch(const TileParams& p, int stat_dtype, hipStream_t s
   const size_t lds = static_cast<size_t>(p.lds_total);
   // The LDS opt-in above 64 KiB is a per-process function attribute (set once
   // per instantiation, for the full 160 KiB).
-#define RLM_TILE_CASE(TS_ID, TS)                                                          \
-  if (stat_dtype == TS_ID) {                                                              \
+#define RLM_TILE_CASE(TS_ID, TS, XP)                                                      \
+  if (stat_dtype == TS_ID && (p.x_out != nullptr) == XP) {                                \
     static const hipError_t attr = hipFuncSetAttribute(                                   \
-        reinterpret_cast<const void*>(&select_tile_kernel<TS>),                           \
+        reinterpret_cast<const void*>(&select_tile_kernel<TS, XP>),                       \
         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);                          \
     if (attr != hipSuccess) {                                                             \
       set_error("relation_select (tile): cannot reserve LDS: %s", hipGetErrorString(attr)); \
       return attr;                                                                        \
     }                                                                                     \
-    hipLaunchKernelGGL((select_tile_kernel<TS>), grid, block, lds, stream, p);            \
+    hipLaunchKernelGGL((select_tile_kernel<TS, XP>), grid, block, lds, stream, p);        \
     return launch_status("relation_select (tile)");                                       \
   }
-  RLM_TILE_CASE(RLM_F32, float)
-  RLM_TILE_CASE(RLM_BF16, bf16)
+  RLM_TILE_CASE(RLM_F32, float, false)
+  RLM_TILE_CASE(RLM_BF16, bf16, false)
+  RLM_TILE_CASE(RLM_F32, float, true)
+  RLM_TILE_CASE(RLM_BF16, bf16, true)
 #undef RLM_TILE_CASE
   set_error("relation_select (tile): unsupported statistics dtype %s", dtype_name(stat_dtype));
   return hipErrorInvalidValue;

@@ -41,6 +41,17 @@ struct TileParams {
   int32_t* out_partner;
   float* out_partner_score;
   int tiles;  // workgroups per batch row
+  // Optional expanded-cache projection in the same launch (x_out != nullptr):
+  // x_out[r, :] = x_w . x_op[r, :] + x_bias for every cache row r < x_rows,
+  // bf16 with fp32 sums, x_N % 128 == 0, 2 x 128 x 32 x_KS x 2 bytes <= T x 128.
+  const bf16* x_op;   // [x_rows, 32 x_KS]
+  const bf16* x_w;    // [x_N, 32 x_KS]
+  const void* x_bias; // [x_N] or nullptr
+  int x_bias_dtype;
+  bf16* x_out;        // [x_rows, x_N]
+  int64_t x_rows;
+  int x_KS, x_N;
+  uint32_t x_op_bytes, x_w_bytes;
   int off_keys, off_sc, off_stats, off_rq, off_pq, off_blk, off_lmax, off_list, off_top,
       off_qrec, off_bias, off_sp, off_kmax, lds_total;
 };

@@ -215,6 +215,58 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> relation_select_packe
   return {out_anchor, out_anchor_score, out_partner, out_partner_score};
 }
 
+// relation_select_packed_seq with the whole expanded cache written into
+// expanded_cache by the same launch where the shapes allow (no reference op).
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> relation_select_packed_seq_expand(
+    const at::Tensor& anchor_query, const at::Tensor& anchor_keys,
+    const at::Tensor& anchor_router_query, const at::Tensor& anchor_block_mean,
+    const at::Tensor& anchor_block_std, const at::Tensor& anchor_gamma,
+    const at::Tensor& anchor_bias, const at::Tensor& partner_base,
+    const at::Tensor& partner_anchor_cache, const at::Tensor& partner_keys,
+    const at::Tensor& partner_block_mean, const at::Tensor& partner_block_std,
+    const at::Tensor& partner_gamma, const at::Tensor& partner_bias, const at::Tensor& positions,
+    int64_t local_window, int64_t top_blocks, int64_t k_out, bool strict_valid,
+    const at::Tensor& operand_cache, const at::Tensor& expanded_weight,
+    const c10::optional<at::Tensor>& expanded_bias, at::Tensor& expanded_cache) {
+  const char* op = "relation_lm::relation_select_packed_seq_expand";
+  c10::DeviceGuard guard(anchor_query.device());
+  const at::Tensor xb = expanded_bias.has_value() ? *expanded_bias : at::Tensor();
+  hipStream_t stream = device_stream(
+      op, {&anchor_query, &anchor_keys, &anchor_router_query, &anchor_block_mean,
+           &anchor_block_std, &anchor_gamma, &anchor_bias, &partner_base, &partner_anchor_cache,
+           &partner_keys, &partner_block_mean, &partner_block_std, &partner_gamma, &partner_bias,
+           &positions, &operand_cache, &expanded_weight, &xb, &expanded_cache});
+  TORCH_CHECK(anchor_query.dim() == 3, op, ": anchor_query must be [B,Tq,E]");
+  TORCH_CHECK(k_out >= 0, op, ": k_out must be non-negative");
+  const std::vector<int64_t> qshape{anchor_query.size(0), anchor_query.size(1)};
+  const std::vector<int64_t> kshape{anchor_query.size(0), anchor_query.size(1), k_out};
+  at::Tensor out_anchor = at::empty(qshape, i32(anchor_query));
+  at::Tensor out_anchor_score = at::empty(qshape, f32(anchor_query));
+  at::Tensor out_partner = at::empty(kshape, i32(anchor_query));
+  at::Tensor out_partner_score = at::empty(kshape, f32(anchor_query));
+  rlm_tensor d[23] = {
+      desc(anchor_query, "anchor_query"), desc(anchor_keys, "anchor_keys"),
+      desc(anchor_router_query, "anchor_router_query"),
+      desc(anchor_block_mean, "anchor_block_mean"), desc(anchor_block_std, "anchor_block_std"),
+      desc(anchor_gamma, "anchor_gamma"), desc(anchor_bias, "anchor_bias"),
+      desc(partner_base, "partner_base"), desc(partner_anchor_cache, "partner_anchor_cache"),
+      desc(partner_keys, "partner_keys"), desc(partner_block_mean, "partner_block_mean"),
+      desc(partner_block_std, "partner_block_std"), desc(partner_gamma, "partner_gamma"),
+      desc(partner_bias, "partner_bias"), desc(positions, "positions"),
+      desc(operand_cache, "operand_cache"), desc(expanded_weight, "expanded_weight"),
+      rlm_tensor{}, desc(expanded_cache, "expanded_cache"), desc(out_anchor, "out_anchor"),
+      desc(out_anchor_score, "out_anchor_score"), desc(out_partner, "out_partner"),
+      desc(out_partner_score, "out_partner_score")};
+  if (xb.defined()) d[17] = desc(xb, "expanded_bias");
+  check(rlm_relation_select_packed_seq_expand(
+            &d[0], &d[1], &d[2], &d[3], &d[4], &d[5], &d[6], &d[7], &d[8], &d[9], &d[10], &d[11],
+            &d[12], &d[13], &d[14], local_window, top_blocks, k_out, strict_valid ? 1 : 0, &d[15],
+            &d[16], xb.defined() ? &d[17] : nullptr, &d[18], &d[19], &d[20], &d[21], &d[22],
+            stream),
+        op);
+  return {out_anchor, out_anchor_score, out_partner, out_partner_score};
+}
+
 std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> relation_select_packed_seq(
     const at::Tensor& anchor_query, const at::Tensor& anchor_keys,
     const at::Tensor& anchor_router_query, const at::Tensor& anchor_block_mean,
@@ -1123,6 +1175,15 @@ TORCH_LIBRARY(relation_lm, m) {
       "partner_gamma, Tensor partner_bias, Tensor positions, SymInt local_window, SymInt "
       "top_blocks, SymInt k_out, bool strict_valid) -> (Tensor, Tensor, Tensor, Tensor)");
   m.def(
+      "relation_select_packed_seq_expand(Tensor anchor_query, Tensor anchor_keys, Tensor "
+      "anchor_router_query, Tensor anchor_block_mean, Tensor anchor_block_std, Tensor "
+      "anchor_gamma, Tensor anchor_bias, Tensor partner_base, Tensor partner_anchor_cache, "
+      "Tensor partner_keys, Tensor partner_block_mean, Tensor partner_block_std, Tensor "
+      "partner_gamma, Tensor partner_bias, Tensor positions, SymInt local_window, SymInt "
+      "top_blocks, SymInt k_out, bool strict_valid, Tensor operand_cache, Tensor "
+      "expanded_weight, Tensor? expanded_bias, Tensor(a!) expanded_cache) -> "
+      "(Tensor, Tensor, Tensor, Tensor)");
+  m.def(
       "relation_select_packed_expand_row(Tensor anchor_query, Tensor anchor_keys, Tensor "
       "anchor_router_query, Tensor anchor_block_mean, Tensor anchor_block_std, Tensor "
       "anchor_gamma, Tensor anchor_bias, Tensor partner_base, Tensor partner_anchor_cache, "
@@ -1265,6 +1326,7 @@ TORCH_LIBRARY_IMPL(relation_lm, CUDA, m) {
   m.impl("relation_select_packed", TORCH_FN(relation_select_packed));
   m.impl("relation_select_packed_seq", TORCH_FN(relation_select_packed_seq));
   m.impl("relation_select_packed_expand_row", TORCH_FN(relation_select_packed_expand_row));
+  m.impl("relation_select_packed_seq_expand", TORCH_FN(relation_select_packed_seq_expand));
   m.impl("multi_relation_select_seq", TORCH_FN(multi_relation_select_seq));
   m.impl("relation_hidden_cached", TORCH_FN(relation_hidden_cached));
   m.impl("relation_hidden_cached_seq", TORCH_FN(relation_hidden_cached_seq));

@@ -63,6 +63,8 @@ def _register_fakes() -> None:
     torch.library.register_fake("relation_lm::relation_select_packed_ring")(fake_select)
     torch.library.register_fake("relation_lm::relation_select_packed_expand_row")(
         lambda anchor_query, *rest: fake_select(anchor_query, *rest[:18]))
+    torch.library.register_fake("relation_lm::relation_select_packed_seq_expand")(
+        lambda anchor_query, *rest: fake_select(anchor_query, *rest[:18]))
 
     @torch.library.register_fake("relation_lm::multi_relation_select_seq")
     def _(anchor_query, *rest):

@@ -163,3 +163,49 @@ def relation_select_packed_expand_row(
         local_window, top_blocks, k_out, strict_valid, operand_cache, expanded_weight,
         expanded_bias, expanded_cache, ring)
 
+
+
+def relation_select_packed_seq_expand(
+    anchor_query: Tensor,
+    anchor_keys: Tensor,
+    anchor_router_query: Tensor,
+    anchor_block_mean: Tensor,
+    anchor_block_std: Tensor,
+    anchor_gamma: Tensor,
+    anchor_bias: Tensor,
+    partner_base: Tensor,
+    partner_anchor_cache: Tensor,
+    partner_keys: Tensor,
+    partner_block_mean: Tensor,
+    partner_block_std: Tensor,
+    partner_gamma: Tensor,
+    partner_bias: Tensor,
+    positions: Tensor,
+    local_window: int,
+    top_blocks: int,
+    k_out: int,
+    strict_valid: bool,
+    operand_cache: Tensor,
+    expanded_weight: Tensor,
+    expanded_bias: Tensor | None,
+    expanded_cache: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Sequence-form ``relation_select_packed_seq`` that also writes the whole
+    expanded cache in place:
+    ``expanded_cache = F.linear(operand_cache, expanded_weight, expanded_bias)`` in
+    bf16 with fp32 sums, the same bits as ``relation_linear`` on those operands.
+
+    The reference projects the expanded cache with its own linear call
+    (tests/test_relation_reduce_gpu.py:64-68) and selects separately.  Here the
+    selection's workgroups project 128 x 128 cache tiles while their own loads are
+    in flight, so the prefill step needs one launch less; shapes the selection's
+    matrix-core kernel does not take (or N % 128 != 0, or T < 4 R) run the
+    projection as a launch of its own after the selection.  bf16 caches and
+    weights, relation dim 32..128, width a multiple of 16.
+    """
+    return torch.ops.relation_lm.relation_select_packed_seq_expand(
+        anchor_query, anchor_keys, anchor_router_query, anchor_block_mean, anchor_block_std,
+        anchor_gamma, anchor_bias, partner_base, partner_anchor_cache, partner_keys,
+        partner_block_mean, partner_block_std, partner_gamma, partner_bias, positions,
+        local_window, top_blocks, k_out, strict_valid, operand_cache, expanded_weight,
+        expanded_bias, expanded_cache)
