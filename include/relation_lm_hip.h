@@ -117,7 +117,7 @@ hipError_t rlm_relation_select_packed_seq(
  * selection is the same as rlm_relation_select_packed_seq.  operand_cache
  * [B,T,R] bf16 (R in {32,64,96,128}), expanded_weight [N,R] bf16 (N % 16 == 0),
  * expanded_bias [N] or NULL, expanded_cache [B,T,N] bf16.  Where the sequence
- * selection's matrix-core kernel applies, N % 128 == 0 and T >= 4 R,
+ * selection's matrix-core kernel applies, N % 128 == 0 and T >= max(4 R, 272),
  * its workgroups project 128 x 128 cache tiles while their own loads are in
  * flight; otherwise the projection is a launch of its own after the selection.
  */

@@ -1677,10 +1677,11 @@ hipError_t select_packed_impl(
                     anchor_block_mean, anchor_block_std, anchor_gamma, anchor_bias,
                     partner_block_mean, partner_block_std, partner_gamma, partner_bias, tp)) {
       // The whole expanded cache by the same launch when its 128 x 128 tiles
-      // fit the key rows' LDS (two tiles of 128 rows x R bf16) and N is whole
-      // tiles; otherwise a GEMM launch after the selection.
-      const bool fused = xseq != nullptr && xs.N % 128 == 0 &&
-                         2 * 128 * 32 * xs.KS * 2 <= g.T * 128;
+      // fit the key rows' LDS (two tiles of 128 rows x R bf16, then the tile's
+      // bf16 outputs at a row stride of 136) and N is whole tiles; otherwise a
+      // GEMM launch after the selection.
+      const int64_t stage_bytes = std::max<int64_t>(2 * 128 * 32 * xs.KS * 2, 128 * 136 * 2);
+      const bool fused = xseq != nullptr && xs.N % 128 == 0 && stage_bytes <= g.T * 128;
       if (fused) {
         tp.x_op = xs.op;
         tp.x_w = xs.w;

@@ -635,92 +635,127 @@ __device__ __forceinline__ float staged_kmax(const Lds& L) {
   return __uint_as_float(kb << 16) * (1.0f + 1.0f / 1024.0f);
 }
 
-// The expanded-cache projection tiles of this workgroup, when the launch
-// carries them (no reference kernel: the reference projects the cache with its
-// own linear call): tile i of the (x_rows / 128) x (x_N / 128) grid for
-// i = wg, wg + G, ..., each a 128 x 128 output tile formed as the library's
-// small-K GEMM forms it (W . A^T per 16x16x32 k-step, k-steps in order, fp32
-// sums, + bias, rounded to bf16), so the bits equal that GEMM's.  The A and W
-// tiles are staged in `stage` (the key rows' LDS, before the keys are put
-// there); wave w forms rows 32 (w / 4) .. +31 and columns 32 (w % 4) .. +31.
+// The expanded-cache projection of this workgroup, when the launch carries it
+// (no reference kernel: the reference projects the cache with its own linear
+// call): tile i of the (x_rows / 128) x (x_N / 128) grid for i = wg, wg + G,
+// ..., each a 128 x 128 output tile formed as the library's small-K GEMM forms
+// it (W . A^T per 16x16x32 k-step, k-steps in order, fp32 sums, + bias,
+// rounded to bf16), so the bits equal that GEMM's.  The tile's A and W rows go
+// straight to LDS (`stage`, the key rows' LDS before the keys are put there) by
+// LDS-DMA: 16 KS instructions of 64 pieces per tile, KS per wave, each lane's
+// source chosen so that piece q of row r lands at q ^ (r % SW) (rows past the
+// cache read zeros; their outputs are not stored).
+// LDS byte address of a pointer into the dynamic LDS (wave-uniform).
+__device__ __forceinline__ uint32_t lds_u32(const void* ptr) {
+  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ptr)));
+}
+
 template <int KS>
-__device__ void expand_tiles(const TileParams& p, unsigned char* stage, int64_t wg, int64_t G,
-                             int tid, int lane, int wave) {
+__device__ __forceinline__ void expand_issue(const TileParams& p, uint32_t stage, int64_t tile,
+                                             int wave, int lane) {
   constexpr int K = 32 * KS;
-  constexpr int QPR = K / 8;                                       // 16-byte pieces per row
-  constexpr int SW = QPR % 16 == 0 ? 16 : (QPR % 8 == 0 ? 8 : 4);  // swizzle width
-  constexpr int kPer = (128 * QPR + kThreads - 1) / kThreads;      // pieces per thread per tile
-  unsigned char* ta = stage;
-  unsigned char* tw = stage + 128 * K * 2;
+  constexpr int QPR = K / 8;
+  constexpr int SW = QPR % 16 == 0 ? 16 : (QPR % 8 == 0 ? 8 : 4);
   const rsrc_t ar = make_rsrc(p.x_op, p.x_op_bytes);
   const rsrc_t wr = make_rsrc(p.x_w, p.x_w_bytes);
   const int64_t tiles_n = p.x_N / 128;
-  const int64_t ntile = ((p.x_rows + 127) / 128) * tiles_n;
+  const int64_t mt = (tile / tiles_n) * 128, nt = (tile % tiles_n) * 128;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);  // the resource choice stays scalar
+#pragma unroll
+  for (int k = 0; k < KS; ++k) {
+    const int ins = wv * KS + k;             // 0 .. 16 KS - 1: A's 2 QPR, then W's
+    const bool is_w = ins >= 2 * QPR;
+    const int J = is_w ? ins - 2 * QPR : ins;
+    const int pd = 64 * J + lane;            // LDS piece of this lane
+    const int row = pd / QPR, q = (pd % QPR) ^ (row % SW);
+    const int64_t src_row = (is_w ? nt : mt) + row;
+    const uint32_t off = is_w || src_row < p.x_rows
+                             ? static_cast<uint32_t>((src_row * K + 8 * q) * 2)
+                             : kNoOffset;
+    lds_dma16(is_w ? wr : ar, stage + (is_w ? 128 * K * 2 : 0) + 1024u * J, off);
+  }
+}
+
+// The products and stores of one staged tile; returns after every wave is done
+// with the staged rows.  Wave w forms rows 32 (w / 4) .. +31 and columns
+// 32 (w % 4) .. +31.
+template <int KS>
+__device__ void expand_compute(const TileParams& p, const unsigned char* stage, int64_t tile,
+                               int lane, int wave) {
+  constexpr int K = 32 * KS;
+  constexpr int QPR = K / 8;
+  constexpr int SW = QPR % 16 == 0 ? 16 : (QPR % 8 == 0 ? 8 : 4);
+  const unsigned char* ta = stage;
+  const unsigned char* tw = stage + 128 * K * 2;
+  const int64_t tiles_n = p.x_N / 128;
+  const int64_t mt = (tile / tiles_n) * 128, nt = (tile % tiles_n) * 128;
   const int r16 = lane & 15, g = lane >> 4;
   const int wm = (wave >> 2) * 32, wn = (wave & 3) * 32;
-  for (int64_t tile = wg; tile < ntile; tile += G) {
-    const int64_t mt = (tile / tiles_n) * 128, nt = (tile % tiles_n) * 128;
-    uint4 va[kPer], vw[kPer];
+  f32x4_t acc[2][2];
 #pragma unroll
-    for (int t = 0; t < kPer; ++t) {
-      const int piece = t * kThreads + tid;
-      const bool ok = piece < 128 * QPR;
-      const int64_t row = piece / QPR, q = piece % QPR;
-      va[t] = buf_load_b128(ar, ok && mt + row < p.x_rows
-                                    ? static_cast<uint32_t>(((mt + row) * K + 8 * q) * 2)
-                                    : kNoOffset);
-      vw[t] = buf_load_b128(wr, ok ? static_cast<uint32_t>(((nt + row) * K + 8 * q) * 2) : kNoOffset);
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const int q = 4 * s + g;
+    uint4 a[2], b[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      a[i] = *reinterpret_cast<const uint4*>(ta + (wm + 16 * i + r16) * (2 * K) + 16 * (q ^ (r16 % SW)));
+      b[i] = *reinterpret_cast<const uint4*>(tw + (wn + 16 * i + r16) * (2 * K) + 16 * (q ^ (r16 % SW)));
     }
-    float bv[2][4];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        bv[j][e] = p.x_bias != nullptr
-                       ? load_any_f(p.x_bias, p.x_bias_dtype, nt + wn + 16 * j + 4 * g + e)
-                       : 0.0f;
-#pragma unroll
-    for (int t = 0; t < kPer; ++t) {
-      const int piece = t * kThreads + tid;
-      if (piece < 128 * QPR) {
-        const int row = piece / QPR, q = piece % QPR;
-        const int at = row * (2 * K) + 16 * (q ^ (row % SW));
-        *reinterpret_cast<uint4*>(ta + at) = va[t];
-        *reinterpret_cast<uint4*>(tw + at) = vw[t];
-      }
-    }
-    __syncthreads();  // the tile's A and W rows staged
-    f32x4_t acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16(b[j], a[i], acc[i][j]);
+  }
+  // Lane (r16, g) holds row wm + 16 i + r16, columns wn + 16 j + 4 g .. + 3:
+  // + bias, bf16, restaged over the A tile (every wave is done with it) as
+  // [128 rows][128 + 8 columns], then stored as whole 256-byte row segments.
+  float bv[2][4];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const int q = 4 * s + g;
-      uint4 a[2], b[2];
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        a[i] = *reinterpret_cast<const uint4*>(ta + (wm + 16 * i + r16) * (2 * K) + 16 * (q ^ (r16 % SW)));
-        b[i] = *reinterpret_cast<const uint4*>(tw + (wn + 16 * i + r16) * (2 * K) + 16 * (q ^ (r16 % SW)));
-      }
+    for (int e = 0; e < 4; ++e)
+      bv[j][e] = p.x_bias != nullptr
+                     ? load_any_f(p.x_bias, p.x_bias_dtype, nt + wn + 16 * j + 4 * g + e)
+                     : 0.0f;
+  constexpr int kOut = 128 + 8;  // staged row stride (bf16); 34 KiB, within the key rows' LDS
+  bf16* st = reinterpret_cast<bf16*>(const_cast<unsigned char*>(stage));
+  __syncthreads();  // every wave is done reading the A and W tiles
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16(b[j], a[i], acc[i][j]);
-    }
-    // Lane (r16, g) holds row wm + 16 i + r16, columns wn + 16 j + 4 g .. + 3.
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<uint2*>(st + (wm + 16 * i + r16) * kOut + wn + 16 * j + 4 * g) =
+          make_uint2(pack_bf16x2(acc[i][j][0] + bv[j][0], acc[i][j][1] + bv[j][1]),
+                     pack_bf16x2(acc[i][j][2] + bv[j][2], acc[i][j][3] + bv[j][3]));
+  __syncthreads();  // the tile's outputs staged
+  // 128 rows x 16 pieces of 16 bytes: two per thread, 16 lanes per row.
+  const int tid = wave * kWave + lane;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int64_t m = mt + wm + 16 * i + r16;
-      if (m < p.x_rows)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          *reinterpret_cast<uint2*>(p.x_out + m * p.x_N + nt + wn + 16 * j + 4 * g) =
-              make_uint2(pack_bf16x2(acc[i][j][0] + bv[j][0], acc[i][j][1] + bv[j][1]),
-                         pack_bf16x2(acc[i][j][2] + bv[j][2], acc[i][j][3] + bv[j][3]));
-    }
-    __syncthreads();  // every wave is done with the staged rows
+  for (int t = 0; t < 2; ++t) {
+    const int piece = t * kThreads + tid;
+    const int row = piece >> 4, col = 8 * (piece & 15);
+    if (mt + row < p.x_rows)
+      *reinterpret_cast<uint4*>(p.x_out + (mt + row) * p.x_N + nt + col) =
+          *reinterpret_cast<const uint4*>(st + row * kOut + col);
+  }
+  __syncthreads();  // every wave is done with the staged rows
+}
+
+// The workgroup's projection tiles after the first (issued with the kernel's
+// own loads and computed by the caller): each staged, waited for, computed.
+template <int KS>
+__device__ void expand_rest(const TileParams& p, unsigned char* stage, int64_t wg, int64_t G,
+                            int lane, int wave) {
+  const int64_t ntile = ((p.x_rows + 127) / 128) * (p.x_N / 128);
+  for (int64_t tile = wg + G; tile < ntile; tile += G) {
+    expand_issue<KS>(p, lds_u32(stage), tile, wave, lane);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();  // the tile's rows in LDS
+    expand_compute<KS>(p, stage, tile, lane, wave);
   }
 }
 
@@ -743,18 +778,6 @@ __global__ void __launch_bounds__(kThreads) select_tile_kernel(const TileParams 
   const int T = static_cast<int>(p.T);
   const int nchunks = T * 8;
   const uint32_t side_bytes = static_cast<uint32_t>(T) * kRowBytes;
-
-  if constexpr (XP) {
-    // The expanded-cache projection first, in the key rows' LDS (free until
-    // the keys arrive); its stores drain while the selection's loads are in
-    // flight.
-    switch (p.x_KS) {
-      case 1: expand_tiles<1>(p, L.keys, wg, gridDim.x, tid, lane, wave); break;
-      case 2: expand_tiles<2>(p, L.keys, wg, gridDim.x, tid, lane, wave); break;
-      case 3: expand_tiles<3>(p, L.keys, wg, gridDim.x, tid, lane, wave); break;
-      default: expand_tiles<4>(p, L.keys, wg, gridDim.x, tid, lane, wave); break;
-    }
-  }
 
   // ---- One round of loads: the router constants, the anchor keys (every
   //      row), the query-side rows, the position and the statistics of both
@@ -780,6 +803,29 @@ __global__ void __launch_bounds__(kThreads) select_tile_kernel(const TileParams 
   const float arqe = to_f32(p.arq[qrow * 64 + lane]);
   StatGroup<TS> sg;
   issue_stats<TS>(p, b, wave, lane, sg);
+  if constexpr (XP) {
+    // The expanded-cache projection: the workgroup's first tile goes to the key
+    // rows' LDS (free until the keys are put there) by LDS-DMA together with
+    // the loads above, one wait covers both, and the tile is formed and stored
+    // before the keys are staged; further tiles follow one by one.
+    const int64_t ntile = ((p.x_rows + 127) / 128) * (p.x_N / 128);
+    if (wg < ntile) {
+      switch (p.x_KS) {
+        case 1: expand_issue<1>(p, lds_u32(L.keys), wg, wave, lane); break;
+        case 2: expand_issue<2>(p, lds_u32(L.keys), wg, wave, lane); break;
+        case 3: expand_issue<3>(p, lds_u32(L.keys), wg, wave, lane); break;
+        default: expand_issue<4>(p, lds_u32(L.keys), wg, wave, lane); break;
+      }
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      __syncthreads();  // the first tile's rows in LDS
+      switch (p.x_KS) {
+        case 1: expand_compute<1>(p, L.keys, wg, lane, wave); expand_rest<1>(p, L.keys, wg, gridDim.x, lane, wave); break;
+        case 2: expand_compute<2>(p, L.keys, wg, lane, wave); expand_rest<2>(p, L.keys, wg, gridDim.x, lane, wave); break;
+        case 3: expand_compute<3>(p, L.keys, wg, lane, wave); expand_rest<3>(p, L.keys, wg, gridDim.x, lane, wave); break;
+        default: expand_compute<4>(p, L.keys, wg, lane, wave); expand_rest<4>(p, L.keys, wg, gridDim.x, lane, wave); break;
+      }
+    }
+  }
   put_router_consts(p, L, tid, rw);
   put_stats<TS>(p, L, wave, lane, sg);
 

@@ -199,7 +199,7 @@ def relation_select_packed_seq_expand(
     (tests/test_relation_reduce_gpu.py:64-68) and selects separately.  Here the
     selection's workgroups project 128 x 128 cache tiles while their own loads are
     in flight, so the prefill step needs one launch less; shapes the selection's
-    matrix-core kernel does not take (or N % 128 != 0, or T < 4 R) run the
+    matrix-core kernel does not take (or N % 128 != 0, or T < max(4 R, 272)) run the
     projection as a launch of its own after the selection.  bf16 caches and
     weights, relation dim 32..128, width a multiple of 16.
     """

@@ -11,7 +11,7 @@ the same k-steps on the matrix cores, so the bits agree), on the path where
 the selection's workgroups project the cache tiles (cfg2: one 128 x 128 tile
 per workgroup; wider caches: several; narrower: fewer tiles than workgroups;
 relation dim 64) and on the two-launch fallbacks (width not a multiple of 128,
-cache shorter than 4 x the relation dim).  The selection itself is pinned to
+cache too short for the staged tiles).  The selection itself is pinned to
 the float64 oracle by test_select_tile_gpu.py / test_relation_select_gpu.py.
 """
 from __future__ import annotations
@@ -58,6 +58,7 @@ def test_cfg2_one_tile_per_workgroup(device):
     (2048, 128, True),   # two cache tiles per workgroup
     (256, 128, False),   # fewer tiles than workgroups, no bias
     (1024, 64, True),    # relation dim 64
+    (1024, 32, True),    # relation dim 32: the output staging is larger than the two tiles
     (1008, 128, True),   # width not a multiple of 128: the GEMM launch after the selection
 ])
 def test_cfg2_shapes(device, width, rdim, with_bias):
