@@ -172,6 +172,10 @@ def op_cases(device):
     cases.append(("relation_select_packed_seq", ops.relation_select_packed_seq.default,
                   seq_args))
     xcache = relation_linear(red["operand_cache"], red["expanded_weight"], red["expanded_bias"])
+    cases.append(("relation_select_packed_seq_expand",
+                  ops.relation_select_packed_seq_expand.default,
+                  seq_args + (red["operand_cache"], red["expanded_weight"], red["expanded_bias"],
+                              torch.empty_like(xcache))))
     cases.append(("relation_select_packed_expand_row",
                   ops.relation_select_packed_expand_row.default,
                   dec_args + (red["operand_cache"], red["expanded_weight"], red["expanded_bias"],
@@ -307,7 +311,7 @@ def op_cases(device):
 
 
 OP_NAMES = ("relation_select_packed", "relation_select_packed_seq",
-            "relation_select_packed_expand_row", "relation_select_packed_ring", "anchor_select", "partner_topk",
+            "relation_select_packed_seq_expand", "relation_select_packed_expand_row", "relation_select_packed_ring", "anchor_select", "partner_topk",
             "multi_relation_select_seq", "relation_hidden_cached", "relation_hidden_cached_seq",
             "relation_hidden_cached_seq_out", "relation_hidden_linear_seq_out", "mfma_fragments",
             "relation_hidden_cached_ring", "relation_hidden_cache_update",
