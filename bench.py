@@ -108,7 +108,7 @@ def algorithmic_bytes(cfg):
     q = b * t
     s = 2  # bf16 activations
     nb = cfg.blocks
-    return {
+    out = {
         "expanded_projection": q * r * s + 2 * h * r * s + 2 * h * s + q * 2 * h * s,
         "relation_select": (q * (2 * e + 2 * rd) * s + b * (t * (3 * e + rd) * s + 4 * nb * rd * 4)
                             + q * (8 + 8 * k)),
@@ -118,6 +118,9 @@ def algorithmic_bytes(cfg):
         "relation_reduce_fused": (b * t * (2 * h + r) * s + h * r * s + d * h * s + d * s
                                   + q * (1 + k) * 4 + q * k * 4 + 2 * d * s + q * d * 4),
     }
+    # The selection launch that also projects the expanded cache: both contracts.
+    out["relation_select_expand"] = out["relation_select"] + out["expanded_projection"]
+    return out
 
 
 def multi_select_bytes(cfg):
@@ -880,7 +883,7 @@ def main() -> int:
         return entry
 
     roof = roofline_of(dominant)
-    rooflines = {name: roofline_of(name) for name in headline}
+    rooflines = {name: roofline_of(name) for name in headline + ("relation_select_expand",)}
     trio = ("relation_select", "relation_hidden", "norm_reduce")
     trio_bytes = sum(nbytes[k] for k in trio)
     trio_us = sum(per_kernel_us[k] for k in trio)
