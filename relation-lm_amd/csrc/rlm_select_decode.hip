@@ -10,14 +10,15 @@
 // candidate lane: local window first, then picked blocks in pick order).
 //
 // The decode step is latency bound: a single query's chain of dependent
-// steps is the whole kernel.  One workgroup of four waves per batch row, and
+// steps is the whole kernel.  One workgroup of eight waves per batch row (two
+// candidate passes of 128 instead of four of 64), and
 // the chain is shortened three ways:
 //   * one burst of loads at the start -- position, bias tables, gammas, both
 //     streams' query vectors and block statistics -- then, as soon as t is
 //     known, both streams' local-window key rows; the picked blocks' rows are
 //     loaded right after each stream's picks (from L2, while the local rows'
 //     dots run), and the anchor's cached partner row right after the anchor;
-//   * every step is spread over the 256 lanes: lane (block, head) pairs for
+//   * every step is spread over the 512 lanes: lane (block, head) pairs for
 //     the block scores, four lanes per candidate (16 dims each, four partial
 //     sums) for the exact dots, one lane per block for the pick ranks (read
 //     from LDS);
@@ -31,7 +32,7 @@
 namespace rlm {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kRowBytes = 128;  // one key row: 64 16-bit values
 constexpr int kHeads = 4;
 constexpr int kHeadDim = 16;
@@ -120,6 +121,7 @@ struct Shared {
 __device__ void expand_row_group(const ExpandRowParams& x, int grp, int tid) {
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
+  if (wave >= kExpandCols / 32) return;  // four waves of two 16-column tiles each; the rest idle
   const int r16 = lane & 15, g = lane >> 4;
   const int64_t t = index_at(x.pos, x.pos_dtype, 0);
   if (t < 0 || (!x.ring && t >= x.T)) return;  // no row to write (uniform)

@@ -13,7 +13,7 @@ constexpr int kDecodeMaxCap = 256;   // candidates per stream (4 per lane of one
 // The token's expanded-cache row (decode): for every batch row b,
 // cache[b, row, :] = W . op[b, row, :] + bias in bf16, row = t (linear caches)
 // or t mod T (ring caches) for the step's position t, read on the device.
-// Each workgroup of four waves projects kExpandCols columns.
+// Each workgroup projects kExpandCols columns on its first four waves.
 constexpr int kExpandCols = 128;
 struct ExpandRowParams {
   const bf16* op;     // [B, T, R] operand cache, R = 32 * KS
