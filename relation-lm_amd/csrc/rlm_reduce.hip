@@ -1323,18 +1323,23 @@ __device__ __forceinline__ float4 chunk4_decode(const Chunk4& v, int dtype) {
 }
 
 // NP > 0: the raw rows are the sum of NP split-K partial products plus b2.
-// Query q on threads 0 .. 4*64-1 of the workgroup (any further waves of the
+// Query q on threads 0 .. NW*64-1 of the workgroup (any further waves of the
 // workgroup must have exited: the barriers below count the threads that remain).
+// Row k is wave k mod NW's row k / NW.  With NW = 8 the rows' weighted sum keeps
+// the four-wave grouping: wave w < 4 of a four-wave run adds rows w and w + 4,
+// and the eight-wave run adds waves w and w + 4 in the same place.
 // Cache policy of a device-coherent access (SC1): what agent-scope atomic loads and
 // stores use, so data another workgroup (on any XCD) publishes this way is read
 // without stale cache lines, with no whole-cache writeback or invalidation.
 constexpr int kCpolDevice = 16;
 
-template <int RPW, int GI, int NP, bool COHERENT = false>
+template <int RPW, int GI, int NP, bool COHERENT = false, int NW = kQWaves>
 __device__ __forceinline__ void norm_query(const NormParams& p, int64_t q) {
-  __shared__ float4 par[5][kQMaxD / 4];         // w, b, query, ow, ob as fp32
-  __shared__ float4 part[kQWaves][kQMaxD / 4];  // each wave's sum_k p_k xhat_k
-  __shared__ float red[2][kQWaves];
+  static_assert(NW == kQWaves || NW == 2 * kQWaves, "four or eight waves");
+  static_assert(NW == kQWaves || RPW == 1, "eight waves take one row each");
+  __shared__ float4 par[5][kQMaxD / 4];    // w, b, query, ow, ob as fp32
+  __shared__ float4 part[NW][kQMaxD / 4];  // each wave's sum_k p_k xhat_k
+  __shared__ float red[2][kQWaves];        // columns live on waves 0..3 (D <= 1024)
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -1376,7 +1381,7 @@ __device__ __forceinline__ void norm_query(const NormParams& p, int64_t q) {
     for (int r = 0; r < RPW; ++r)
 #pragma unroll
       for (int i = 0; i < GI; ++i) {
-        const int k = wave + kQWaves * r;
+        const int k = wave + NW * r;
         const int g = lane + kWave * i;
         const bool in = k < p.K && g < groups;
         // Lanes past the row and rows past K read nothing.
@@ -1392,7 +1397,7 @@ __device__ __forceinline__ void norm_query(const NormParams& p, int64_t q) {
     for (int r = 0; r < RPW; ++r)
 #pragma unroll
       for (int i = 0; i < GI; ++i) {
-        const int k = wave + kQWaves * r;
+        const int k = wave + NW * r;
         const int g = lane + kWave * i;
         const bool in = k < p.K && g < groups;
         float4 v = make_float4(__uint_as_float(w[r][i][0].x), __uint_as_float(w[r][i][0].y),
@@ -1414,7 +1419,7 @@ __device__ __forceinline__ void norm_query(const NormParams& p, int64_t q) {
     for (int r = 0; r < RPW; ++r)
 #pragma unroll
       for (int i = 0; i < GI; ++i) {
-        const int k = wave + kQWaves * r;
+        const int k = wave + NW * r;
         const int g = lane + kWave * i;
         const bool in = k < p.K && g < groups;
         const float4 v = *reinterpret_cast<const float4*>(raw + static_cast<int64_t>(in ? k : 0) * p.D +
@@ -1458,7 +1463,7 @@ __device__ __forceinline__ void norm_query(const NormParams& p, int64_t q) {
   for (int i = 0; i < GI; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
-    const int k = wave + kQWaves * r;
+    const int k = wave + NW * r;
     const float pk = __uint_as_float(
         __builtin_amdgcn_readlane(__float_as_uint(prob), k < p.K ? k : 0));
     const bool use = k < p.K && pk != 0.0f;
@@ -1486,10 +1491,19 @@ __device__ __forceinline__ void norm_query(const NormParams& p, int64_t q) {
   // ---- Column phase: thread tid owns columns 4 tid .. 4 tid + 3.
   float4 ctx = make_float4(0.f, 0.f, 0.f, 0.f);
   if (cl) {
-    float4 s = part[0][tid];
+    // Wave w's rows of a four-wave run: rows w and w + 4.
+    auto rows_of = [&](int w) {
+      float4 v = part[w][tid];
+      if constexpr (NW > kQWaves) {
+        const float4 o = part[w + kQWaves][tid];
+        v = make_float4(v.x + o.x, v.y + o.y, v.z + o.z, v.w + o.w);
+      }
+      return v;
+    };
+    float4 s = rows_of(0);
 #pragma unroll
     for (int w = 1; w < kQWaves; ++w) {
-      const float4 o = part[w][tid];
+      const float4 o = rows_of(w);
       s.x += o.x;
       s.y += o.y;
       s.z += o.z;
@@ -1510,13 +1524,13 @@ __device__ __forceinline__ void norm_query(const NormParams& p, int64_t q) {
                     fmaf(gate, ctx.w, qv.w));
   }
   float s = wave_sum_f32((y.x + y.y) + (y.z + y.w));
-  if (lane == 0) red[0][wave] = s;
+  if (lane == 0 && wave < kQWaves) red[0][wave] = s;
   __syncthreads();
   const float ymean = ((red[0][0] + red[0][1]) + (red[0][2] + red[0][3])) * inv_d;
   const float4 dy = cl ? make_float4(y.x - ymean, y.y - ymean, y.z - ymean, y.w - ymean)
                        : make_float4(0.f, 0.f, 0.f, 0.f);
   s = wave_sum_f32((dy.x * dy.x + dy.y * dy.y) + (dy.z * dy.z + dy.w * dy.w));
-  if (lane == 0) red[1][wave] = s;
+  if (lane == 0 && wave < kQWaves) red[1][wave] = s;
   __syncthreads();
   const float yrstd =
       rsqrtf(((red[1][0] + red[1][1]) + (red[1][2] + red[1][3])) * inv_d + p.out_eps);
@@ -1557,8 +1571,8 @@ norm_reduce_query_kernel(const NormParams p) {
 //      invalidation, which every workgroup would otherwise pay) and sums the
 //      group's partials in slice order into gsum[group], then
 //      counts on the query's counter; the last group's workgroup runs the
-//      per-query norm-reduce and output head (norm_query) on the group sums
-//      plus b2, in group order.  Every sum has a fixed order: the result does
+//      per-query norm-reduce and output head (norm_query, on all eight waves:
+//      one partner row each) on the group sums plus b2, in group order.  Every sum has a fixed order: the result does
 //      not depend on which workgroup arrives last.  Nothing waits for another
 //      workgroup; the last arrival of each level does the next step.  Each
 //      counter is reset to zero by that last arrival, so the next launch (and a
@@ -1568,12 +1582,13 @@ constexpr int kDecSlice = 64;                  // hidden columns per workgroup
 constexpr int kDecWaves = 8;
 constexpr int kDecThreads = kDecWaves * kWave;
 constexpr int kDecMaxK = 8;                    // partner rows per query (rows of one 16-row tile)
-constexpr int kDecMaxD = 768;                  // d_model: norm_query with RPW <= 2, GI <= 3
+constexpr int kDecMaxD = 768;                  // d_model: norm_query with GI <= 3
 constexpr int kDecMaxDT = 6;                   // 16-row tiles of D per wave (D <= 768)
 constexpr int kDecMaxSpg = 12;                 // slices per group
 constexpr int kDecGroups = kMaxParts;          // groups per query (norm_query's NP)
 constexpr int kDecHidLd = kDecSlice + 8;       // bf16 per hidden row in LDS (conflict-free b128)
 constexpr int kDecSumBatch = 3;                // float4 elements per thread per level-1 round
+static_assert(kDecMaxK <= kDecWaves, "norm_query takes one partner row per wave");
 
 struct DecodeParams {
   NormParams n;            // level 2: parts = gsum, nparts = groups, b2, output head
@@ -1594,7 +1609,7 @@ struct DecodeParams {
   uint32_t expanded_bytes, operand_bytes, wm_bytes, w2_bytes, partials_bytes, gsum_bytes;
 };
 
-template <int KS, int RPW, int GI>
+template <int KS, int GI>
 __global__ void __launch_bounds__(kDecThreads) decode_relation_kernel(const DecodeParams p) {
   __shared__ __align__(16) uint16_t hid[16][kDecHidLd];
   __shared__ int last;
@@ -1772,8 +1787,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_relation_kernel(const Deco
   __syncthreads();
   if (!last) return;  // uniform
   if (tid == 0) __hip_atomic_store(p.counters + p.B * p.G + q, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (wave >= kQWaves) return;  // norm_query runs on four waves
-  norm_query<RPW, GI, kDecGroups, true>(p.n, q);
+  norm_query<1, GI, kDecGroups, true, kDecWaves>(p.n, q);
 }
 
 // Slices, groups and slices per group for hidden dim H (a multiple of 64).
@@ -1791,24 +1805,21 @@ inline bool decode_fits_shape(int64_t B, int64_t K, int64_t R, int64_t H, int64_
          D <= kDecMaxD && decode_shape(H).spg <= kDecMaxSpg;
 }
 
-template <int KS, int RPW>
-hipError_t launch_decode_rpw(const DecodeParams& p, hipStream_t stream) {
+template <int KS>
+hipError_t launch_decode_ks(const DecodeParams& p, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.S), static_cast<unsigned>(p.B));
   const int gi = (p.D / 4 + kWave - 1) / kWave;
   if (gi <= 1)
-    hipLaunchKernelGGL((decode_relation_kernel<KS, RPW, 1>), grid, dim3(kDecThreads), 0, stream, p);
+    hipLaunchKernelGGL((decode_relation_kernel<KS, 1>), grid, dim3(kDecThreads), 0, stream, p);
   else if (gi <= 2)
-    hipLaunchKernelGGL((decode_relation_kernel<KS, RPW, 2>), grid, dim3(kDecThreads), 0, stream, p);
+    hipLaunchKernelGGL((decode_relation_kernel<KS, 2>), grid, dim3(kDecThreads), 0, stream, p);
   else
-    hipLaunchKernelGGL((decode_relation_kernel<KS, RPW, 3>), grid, dim3(kDecThreads), 0, stream, p);
+    hipLaunchKernelGGL((decode_relation_kernel<KS, 3>), grid, dim3(kDecThreads), 0, stream, p);
   return launch_status("relation_hidden_linear_norm_reduce_output");
 }
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
-  const bool one_row = p.K <= kQWaves;  // one partner row per wave in norm_query
-  if (p.R == 128)
-    return one_row ? launch_decode_rpw<4, 1>(p, stream) : launch_decode_rpw<4, 2>(p, stream);
-  return one_row ? launch_decode_rpw<2, 1>(p, stream) : launch_decode_rpw<2, 2>(p, stream);
+  return p.R == 128 ? launch_decode_ks<4>(p, stream) : launch_decode_ks<2>(p, stream);
 }
 
 template <typename TR, int VPL>

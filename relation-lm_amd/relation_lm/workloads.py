@@ -309,8 +309,10 @@ def decode_state(cfg: RelationConfig, *, device: torch.device | str, position: i
     return st
 
 
-# Workgroups the GPU runs in one round (one per CU on MI355X at the one-launch decode
-# tail's size); beyond this the tail's latency chain runs twice.
+# Grid size up to which the one-launch decode tail is the faster form on MI355X.  Two
+# of its workgroups fit a CU (122 VGPRs a lane, 55.6 KB of LDS), so cfg3 at B=8 (288
+# workgroups) is resident at once, yet its tail takes 24.6 us there against 18.9 us
+# for the three launches of the split form; at B=1 (36 workgroups) it takes 14.8 us.
 ONE_ROUND_WORKGROUPS = 256
 
 
@@ -323,12 +325,13 @@ def decode_step(st: dict, cfg: RelationConfig) -> tuple:
       2. relation_select_packed with the token's expanded-cache row projected by
          extra workgroups of the same launch;
       3. the relation tail: while its grid (one workgroup per query and 64 hidden
-         columns) fits one round of the chip's 256 CUs, one launch -- the cached
-         relation hidden, the second linear over slices of the hidden dim and the
-         norm-reduce with the output-head preparation
-         (relation_hidden_linear_norm_reduce_output); beyond that (cfg3 at B=8) the
-         two-launch form is faster on MI355X: relation_hidden_cached(_ring), then
-         relation_linear_norm_reduce_output (the split-K linear and the norm-reduce).
+         columns; 36 per query at cfg3) stays within ONE_ROUND_WORKGROUPS, one
+         launch -- the cached relation hidden, the second linear over slices of the
+         hidden dim and the norm-reduce with the output-head preparation
+         (relation_hidden_linear_norm_reduce_output); beyond that (cfg3 at B=8)
+         the two-launch form is faster on MI355X: relation_hidden_cached(_ring),
+         then relation_linear_norm_reduce_output (the split-K linear and the
+         norm-reduce).
     The caches are updated in place at the state's position (ring: mod T).
     Returns (anchor, anchor_score, partner, partner_score, context, final)."""
     from relation_lm.kernels.relation_reduce import (
