@@ -356,4 +356,8 @@ def test_cfg5_stack(device):
     final = stack.final_norm
     expected = omb.layer_norm(host(h[rows_b, rows_t]), host(final.weight), host(final.bias),
                               final.eps)
-    np.testing.assert_allclose(host(out[rows_b, rows_t]), bf16_round(expected), rtol=0, atol=0.03)
+    # The final LayerNorm of the device's own last-layer output: the bf16 result is
+    # the oracle's value rounded to bf16, or its neighbour (one step, at most 2^-7
+    # of the value) where the fp32 statistics fall near a rounding boundary.
+    np.testing.assert_allclose(host(out[rows_b, rows_t]), bf16_round(expected), rtol=2.0**-7,
+                               atol=1e-4)
